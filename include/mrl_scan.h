@@ -1,0 +1,262 @@
+/*
+ * mrl_scan.h -- C ABI of the MI355X (gfx950) PaxBlock64 bitplane scan.
+ *
+ * Drop-in backend for the reference crate's scan path
+ * (tcondello/mrl-index-rust-vector, src/scan.rs + src/pipeline.rs).  Plain C
+ * types only: a Rust `extern "C"` block, ctypes or any other FFI binds it.
+ *
+ * Conventions
+ *  - Every function returns an mrl_status; MRL_OK == 0.  On error the calling
+ *    thread's mrl_last_error() holds a message.  Nothing panics or throws
+ *    across the boundary (the reference panics on bad plan input and on a NaN
+ *    score in Shortlist::into_sorted, src/scan.rs:113-124,392; here those are
+ *    MRL_ERR_INVALID_ARG and MRL_ERR_NAN).
+ *  - A context owns one HIP stream on one device.  Calls on one context are
+ *    serialised by a context mutex, so a host wrapper may be Send + Sync.
+ *  - Blocks are raw 4096-byte little-endian PaxBlock64 records
+ *    (src/block.rs:130-147).  They are uploaded to HBM once and re-laid out
+ *    on the device (see mrl_index_upload); mrl_index_download restores the
+ *    original bytes exactly.
+ *  - Hit ids use VectorId::as_u64: block << 16 | slot (src/block.rs:213-215).
+ *  - Results per query are sorted by score descending (ties: smaller id first)
+ *    and hold min(K, #scored vectors) entries, the same set the reference's
+ *    scan_blocks returns apart from the choice among exactly tied scores at
+ *    the K boundary.
+ */
+#ifndef MRL_SCAN_H
+#define MRL_SCAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MRL_ABI_VERSION 1
+#define MRL_BLOCK_BYTES 4096
+#define MRL_VECTORS_PER_BLOCK 64
+#define MRL_MAX_SHORTLIST 4096
+#define MRL_MAX_DIMS 8192
+
+typedef enum mrl_status {
+  MRL_OK = 0,
+  MRL_ERR_INVALID_ARG = 1,
+  MRL_ERR_HIP = 2,
+  MRL_ERR_NAN = 3,
+  MRL_ERR_OUT_OF_MEMORY = 4,
+  MRL_ERR_NO_DEVICE = 5,
+  MRL_ERR_CORRUPT = 6,
+  MRL_ERR_IO = 7
+} mrl_status;
+
+/* src/config.rs:10-16 */
+typedef enum mrl_prefix_codec { MRL_PREFIX_MINMAX4 = 0, MRL_PREFIX_EDEN_PROD = 1 } mrl_prefix_codec;
+/* src/config.rs:21-28 */
+typedef enum mrl_mid_codec { MRL_MID_RABITQ = 0, MRL_MID_EDEN_B1 = 1 } mrl_mid_codec;
+/* src/config.rs:36-67 */
+typedef enum mrl_strata_depth {
+  MRL_STRATA_L0_ONLY = 0,
+  MRL_STRATA_L1_RABITQ = 1,
+  MRL_STRATA_FULL64B = 2
+} mrl_strata_depth;
+
+/* EdenFit (src/eden.rs:386-395).  `mean` has `dim` floats. */
+typedef struct mrl_eden_fit {
+  uint32_t dim;
+  uint32_t bits;
+  uint64_t seed;
+  const float *mean;
+  uint64_t n_observed;
+} mrl_eden_fit;
+
+/* ScanConfig (src/config.rs:81-114) plus one build-specific switch.
+ * Like the reference's scan_blocks, values are not range-checked except K:
+ * shortlist_cand 0 behaves as 1 (Shortlist::new, src/scan.rs:321-329) and
+ * values above MRL_MAX_SHORTLIST are rejected. */
+typedef struct mrl_scan_config {
+  uint32_t shortlist_cand;          /* K_cand */
+  float cs_tolerance;               /* alpha, admissible-bound multiplier */
+  float stratum4_weight;            /* w_s4 */
+  int32_t strata_depth;             /* mrl_strata_depth */
+  int32_t temporal_filter_enable;
+  int32_t numa_sharding;            /* accepted for API parity; the GPU result does not depend on it */
+  int32_t exhaustive;               /* 1: score every active vector through every gated stage (no bound pruning) */
+  int32_t reserved;
+} mrl_scan_config;
+
+/* Temporal filter bounds: the Option<u32> pair of scan_blocks (src/scan.rs:802-810). */
+typedef struct mrl_time_range {
+  int32_t has_lo;
+  uint32_t lo;
+  int32_t has_hi;
+  uint32_t hi;
+} mrl_time_range;
+
+/* ScanStats (src/scan.rs:270-278), summed over all queries of a call.  The
+ * GPU prunes against its own running threshold, so prune counts are
+ * reported, not compared; the per-stage masks of mrl_scan_fixed_tau are the
+ * tau-independent comparison. */
+typedef struct mrl_scan_stats {
+  uint64_t blocks;
+  uint64_t active_vecs;
+  uint64_t after_prefix;
+  uint64_t after_s1;
+  uint64_t after_s4_budget;
+  uint64_t pushed;
+} mrl_scan_stats;
+
+/* QueryPlan (src/scan.rs:20-71) with every reference field, followed by the
+ * values the reference recomputes from the plan inside the stages:
+ * prefix_weight (scan.rs:457-461) and the EdenB1 base/deltas (scan.rs:523-532). */
+typedef struct mrl_query_plan {
+  uint32_t dims;
+  int32_t prefix_codec;
+  int32_t mid_codec;
+  uint32_t has_tail_fold;
+  float prefix[64];
+  float bit_weights[64][4];
+  float rabitq_q[128];
+  float rabitq_scale;
+  float rabitq_weights2[128];
+  float rabitq_base;
+  float rabitq_lut[32][16];
+  float tail_fold_q[64];
+  float tail_fold_weights2[64];
+  float tail_fold_base;
+  float q_tail_norm;
+  float q_mid_norm;
+  float q_after_prefix;
+  float q_after_s1;
+  float s4_abs_budget;
+  float prefix_l1;
+  float prefix_sum;
+  float eden_q_rot[64];
+  float eden_mean_ip;
+  float eden_inv_sqrt_d;
+  float eden_codebook[16];
+  float eden_mid_q_rot[128];
+  float eden_mid_mean_ip;
+  float eden_mid_inv_sqrt_d;
+  float eden_mid_codebook[2];
+  float prefix_weight[64];
+  float eden_mid_base;
+  float eden_mid_deltas[128];
+  float pad[27];
+} mrl_query_plan;
+
+typedef struct mrl_ctx mrl_ctx;
+typedef struct mrl_index mrl_index;
+typedef struct mrl_plans mrl_plans;
+typedef struct mrl_results mrl_results;
+
+/* ---------------------------------------------------------------- */
+/* library / context                                                */
+/* ---------------------------------------------------------------- */
+int mrl_abi_version(void);
+/* Message for the last failing call on this thread ("" if none). */
+const char *mrl_last_error(void);
+size_t mrl_query_plan_size(void);
+
+/* No reference counterpart (the reference scan runs on the global Rayon pool). */
+int mrl_ctx_create(int device, mrl_ctx **out);
+void mrl_ctx_destroy(mrl_ctx *ctx);
+int mrl_ctx_synchronize(mrl_ctx *ctx);
+
+/* ---------------------------------------------------------------- */
+/* index: a device-resident slab of blocks                          */
+/* ---------------------------------------------------------------- */
+/* Replaces the `&[PaxBlock64]` slab handed to scan_blocks
+ * (src/scan.rs:802-810, src/pipeline.rs:77-98, src/segment.rs:187-193).
+ * Copies n_blocks * 4096 bytes to HBM once.  verify_crc=1 checks every block
+ * like PaxBlock64::verify_crc (src/block.rs:192-197) and fails with
+ * MRL_ERR_CORRUPT on a mismatch. */
+int mrl_index_upload(mrl_ctx *ctx, const void *blocks, uint64_t n_blocks, int verify_crc,
+                     mrl_index **out);
+/* Same, from a segments/NNNNNN.pax file (SegmentReader::open, src/segment.rs:89-162):
+ * a size that is not a multiple of 4096 is MRL_ERR_CORRUPT
+ * (SegmentError::CorruptSize); a missing file gives an empty index. */
+int mrl_index_open_segment(mrl_ctx *ctx, const char *path, int verify_crc, mrl_index **out);
+int mrl_index_block_count(const mrl_index *index, uint64_t *out);
+/* Inverse of the device re-layout: writes the original n_blocks*4096 bytes. */
+int mrl_index_download(mrl_ctx *ctx, const mrl_index *index, void *out_blocks);
+void mrl_index_destroy(mrl_index *index);
+
+/* ---------------------------------------------------------------- */
+/* query plans (batched HIP kernel)                                 */
+/* ---------------------------------------------------------------- */
+/* QueryPlan::from_query_codec (src/scan.rs:105-266) for n_queries row-major
+ * queries of `dims` floats (host memory).  Errors where the reference
+ * asserts: dims < 192, EdenProd without a 64-d 4-bit fit, EdenB1 without a
+ * 128-d 1-bit fit.  Pipeline selection (src/pipeline.rs:63-74) is the
+ * caller's choice of codecs and fits. */
+int mrl_plans_build(mrl_ctx *ctx, const float *queries, uint32_t n_queries, uint32_t dims,
+                    int prefix_codec, int mid_codec, const mrl_eden_fit *eden,
+                    const mrl_eden_fit *eden_mid, mrl_plans **out);
+/* Same, with the queries already in device memory (no copy, no sync). */
+int mrl_plans_build_device(mrl_ctx *ctx, const float *d_queries, uint32_t n_queries, uint32_t dims,
+                           int prefix_codec, int mid_codec, const mrl_eden_fit *eden,
+                           const mrl_eden_fit *eden_mid, mrl_plans **out);
+/* Rebuild an existing plan set from new device queries of the same shape,
+ * codecs and fits (used by the benchmark loop; no allocation). */
+int mrl_plans_rebuild_device(mrl_ctx *ctx, mrl_plans *plans, const float *d_queries);
+int mrl_plans_count(const mrl_plans *plans, uint32_t *out);
+/* Copies plans [first, first+count) to host. */
+int mrl_plans_export(mrl_ctx *ctx, const mrl_plans *plans, uint32_t first, uint32_t count,
+                     mrl_query_plan *out);
+void mrl_plans_destroy(mrl_plans *plans);
+
+/* ---------------------------------------------------------------- */
+/* scan                                                             */
+/* ---------------------------------------------------------------- */
+/* scan_blocks_stats (src/scan.rs:813-886) for every plan at once.
+ * out_ids / out_scores: n_queries * K entries (K = max(shortlist_cand,1)),
+ * row q at offset q*K; out_counts[q] = hits for query q.  stats may be NULL.
+ * time may be NULL (no bounds). */
+int mrl_scan(mrl_ctx *ctx, const mrl_index *index, const mrl_plans *plans,
+             const mrl_scan_config *cfg, const mrl_time_range *time, uint64_t *out_ids,
+             float *out_scores, uint32_t *out_counts, mrl_scan_stats *stats);
+
+/* Device-resident results for callers that keep outputs in HBM. */
+int mrl_results_create(mrl_ctx *ctx, uint32_t n_queries, uint32_t k, mrl_results **out);
+void mrl_results_destroy(mrl_results *res);
+/* Enqueue a scan on the context stream; returns without waiting. */
+int mrl_scan_async(mrl_ctx *ctx, const mrl_index *index, const mrl_plans *plans,
+                   const mrl_scan_config *cfg, const mrl_time_range *time, mrl_results *res);
+/* Waits for the stream, then copies results (any pointer may be NULL). */
+int mrl_results_fetch(mrl_ctx *ctx, mrl_results *res, uint64_t *out_ids, float *out_scores,
+                      uint32_t *out_counts, mrl_scan_stats *stats);
+
+/* Diagnostic scan at a fixed threshold per query: the stage functions of
+ * src/scan.rs:453-634 composed as scan_block_stats does (709-799) with
+ * tau[q] in place of shortlist.threshold().  Outputs, per (query, block):
+ *   masks[5]   active, after prefix, after S1+CS, after S4 budget, pushed
+ *   prefix_ip[64]  stage-1 score of every active slot
+ *   scores[64]     block state scores after the stages (valid where pushed)
+ * Array layout is [query][block][...].  Skipped blocks report zero masks. */
+int mrl_scan_fixed_tau(mrl_ctx *ctx, const mrl_index *index, const mrl_plans *plans,
+                       const mrl_scan_config *cfg, const mrl_time_range *time, const float *tau,
+                       uint64_t *out_masks, float *out_prefix_ip, float *out_scores);
+
+/* ---------------------------------------------------------------- */
+/* ingest-side helpers (host C++, multi-threaded)                   */
+/* ---------------------------------------------------------------- */
+/* encode_block_with_fits (src/quantize.rs:36-96): n <= 64 vectors of `dims`
+ * floats into one 4096-byte block.  eden selects the EDEN-prod prefix,
+ * eden_mid the EdenB1 mid-band. */
+int mrl_encode_block(const float *vectors, uint32_t n, uint32_t dims, const uint32_t *timestamps,
+                     const uint32_t *sources, const mrl_eden_fit *eden,
+                     const mrl_eden_fit *eden_mid, void *out_block);
+/* encode_f32_corpus_par (src/encoder.rs:195-219): n rows -> ceil(n/64)
+ * blocks, timestamp = row index, source = default_source. */
+int mrl_encode_corpus(const float *matrix, uint64_t n, uint32_t dims, uint32_t default_source,
+                      const mrl_eden_fit *eden, const mrl_eden_fit *eden_mid, int n_threads,
+                      void *out_blocks);
+/* EdenFit::fit_band (src/eden.rs:130-159): mean of row[start..start+dim]. */
+int mrl_eden_fit_band(const float *rows, uint64_t n_rows, uint32_t row_stride, uint32_t start,
+                      uint32_t dim, float *out_mean);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MRL_SCAN_H */

@@ -1,0 +1,905 @@
+// mrl_api.cpp -- C ABI runtime of the MI355X scan (contexts, device index,
+// plans, the multi-pass scan driver, diagnostics, ingest helpers).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <atomic>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/mrl_scan.h"
+#include "../../include/mrl_synth.h"
+#include "mrl_codec.h"
+#include "mrl_internal.h"
+
+using namespace mrl;
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+static thread_local std::string g_err;
+
+static int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                          \
+  do {                                                                                         \
+    hipError_t e_ = (expr);                                                                    \
+    if (e_ != hipSuccess) return fail(MRL_ERR_HIP, std::string(#expr ": ") + hipGetErrorString(e_)); \
+  } while (0)
+
+extern "C" const char* mrl_last_error(void) { return g_err.c_str(); }
+extern "C" int mrl_abi_version(void) { return MRL_ABI_VERSION; }
+extern "C" size_t mrl_query_plan_size(void) { return sizeof(mrl_query_plan); }
+
+// ---------------------------------------------------------------------------
+// objects
+// ---------------------------------------------------------------------------
+struct LevelPlan {
+  uint32_t* d_order = nullptr;
+  std::vector<std::pair<uint32_t, uint32_t>> passes;  // (start, size) into d_order
+  uint32_t cap = 0;                                     // candidate slots per query
+};
+
+struct mrl_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  float* d_flag_tabs = nullptr;
+  PlanConsts consts;
+};
+
+struct mrl_index {
+  mrl_ctx* ctx = nullptr;
+  uint8_t* d_blocks = nullptr;
+  uint64_t n_blocks = 0;
+  std::map<uint32_t, LevelPlan> levels;
+};
+
+struct mrl_plans {
+  mrl_ctx* ctx = nullptr;
+  mrl_query_plan* d_plans = nullptr;
+  uint32_t n_q = 0;
+  uint32_t dims = 0;
+  int prefix_codec = 0;
+  int mid_codec = 0;
+  float* d_eden_mean = nullptr;
+  uint64_t eden_seed = 0;
+  float* d_mid_mean = nullptr;
+  uint64_t mid_seed = 0;
+};
+
+struct mrl_results {
+  mrl_ctx* ctx = nullptr;
+  uint32_t n_q = 0, k = 0, cap = 0;
+  uint64_t* d_ids = nullptr;
+  float* d_scores = nullptr;
+  uint32_t* d_counts = nullptr;
+  float* d_cand_score = nullptr;
+  uint32_t* d_cand_row = nullptr;
+  uint32_t* d_cand_count = nullptr;
+  float* d_tau = nullptr;
+  uint32_t* d_overflow = nullptr;
+  unsigned long long* d_stats = nullptr;
+  uint32_t* d_err = nullptr;
+  // the last enqueued scan, re-run densely for queries whose candidate list overflowed
+  const mrl_index* last_index = nullptr;
+  const mrl_plans* last_plans = nullptr;
+  mrl_scan_config last_cfg{};
+  mrl_time_range last_time{};
+  bool pending = false;
+};
+
+static void dev_free(void* p) {
+  if (p) (void)hipFree(p);
+}
+
+// ---------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------
+extern "C" int mrl_ctx_create(int device, mrl_ctx** out) {
+  if (!out) return fail(MRL_ERR_INVALID_ARG, "out is null");
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(MRL_ERR_NO_DEVICE, "no HIP device");
+  if (device < 0 || device >= n) return fail(MRL_ERR_INVALID_ARG, "device index out of range");
+  HIP_TRY(hipSetDevice(device));
+  std::unique_ptr<mrl_ctx> c(new mrl_ctx());
+  c->device = device;
+  HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+  // IEEE constants the reference computes with the same f32 operations.
+  c->consts.inv_sqrt64 = 1.0f / sqrtf(64.0f);
+  c->consts.inv_sqrt128 = 1.0f / sqrtf(128.0f);
+  c->consts.rabitq_scale = sqrtf(2.0f / (float)M_PI) / sqrtf(128.0f);    // rotate.rs:46-49
+  c->consts.tail_fold_scale = sqrtf(2.0f / (float)M_PI) / sqrtf(64.0f);  // rotate.rs:124-126
+  int nb;
+  const float* cb4 = lloyd_max(4, &nb);
+  for (int i = 0; i < 16; ++i) c->consts.eden_codebook[i] = cb4[i];
+  const float* cb1 = lloyd_max(1, &nb);
+  c->consts.eden_mid_codebook[0] = cb1[0];
+  c->consts.eden_mid_codebook[1] = cb1[1];
+  // VectorMeta::rho_ratio and the sqrt factor of mid_norm_f32 per flags byte (block.rs:74-84)
+  float tabs[512];
+  for (int f = 0; f < 256; ++f) {
+    float r = (float)f / 255.0f;
+    tabs[f] = r;
+    float rc = r < 0.0f ? 0.0f : (r > 1.0f ? 1.0f : r);
+    tabs[256 + f] = sqrtf(fmaxf(1.0f - rc * rc, 0.0f));
+  }
+  HIP_TRY(hipMalloc(&c->d_flag_tabs, sizeof(tabs)));
+  HIP_TRY(hipMemcpy(c->d_flag_tabs, tabs, sizeof(tabs), hipMemcpyHostToDevice));
+  *out = c.release();
+  return MRL_OK;
+}
+
+extern "C" void mrl_ctx_destroy(mrl_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  dev_free(ctx->d_flag_tabs);
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+extern "C" int mrl_ctx_synchronize(mrl_ctx* ctx) {
+  if (!ctx) return fail(MRL_ERR_INVALID_ARG, "ctx is null");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return MRL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// index
+// ---------------------------------------------------------------------------
+static int verify_crcs(const uint8_t* blocks, uint64_t n_blocks) {
+  std::atomic<int64_t> bad{-1};
+  parallel_for(n_blocks, 0, [&](uint64_t b0, uint64_t b1) {
+    for (uint64_t b = b0; b < b1; ++b)
+      if (!block_crc_ok(blocks + b * kBlockBytes)) {
+        int64_t expect = -1;
+        bad.compare_exchange_strong(expect, (int64_t)b);
+      }
+  });
+  return bad.load() < 0 ? MRL_OK : fail(MRL_ERR_CORRUPT, "crc32 mismatch in block " + std::to_string(bad.load()));
+}
+
+extern "C" int mrl_index_upload(mrl_ctx* ctx, const void* blocks, uint64_t n_blocks, int verify_crc,
+                                mrl_index** out) {
+  if (!ctx || !out || (n_blocks && !blocks)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (n_blocks > (1ull << 26)) return fail(MRL_ERR_INVALID_ARG, "n_blocks exceeds 2^26 (32-bit row ids)");
+  *out = nullptr;
+  const uint8_t* src = static_cast<const uint8_t*>(blocks);
+  if (verify_crc) {
+    int rc = verify_crcs(src, n_blocks);
+    if (rc) return rc;
+  }
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  std::unique_ptr<mrl_index> ix(new mrl_index());
+  ix->ctx = ctx;
+  ix->n_blocks = n_blocks;
+  if (n_blocks) {
+    const size_t bytes = (size_t)n_blocks * kBlockBytes;
+    uint8_t* staging = nullptr;
+    if (hipMalloc(&ix->d_blocks, bytes) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc index");
+    // stage in chunks of at most 256 MiB so the transient copy stays small
+    const uint64_t chunk = std::min<uint64_t>(n_blocks, 65536);
+    if (hipMalloc(&staging, chunk * kBlockBytes) != hipSuccess) {
+      dev_free(ix->d_blocks);
+      return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc staging");
+    }
+    for (uint64_t b = 0; b < n_blocks; b += chunk) {
+      uint64_t nb = std::min(chunk, n_blocks - b);
+      hipError_t e = hipMemcpyAsync(staging, src + b * kBlockBytes, nb * kBlockBytes, hipMemcpyHostToDevice,
+                                    ctx->stream);
+      if (e == hipSuccess) e = launch_relayout(staging, ix->d_blocks + b * kBlockBytes, nb, true, ctx->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+      if (e != hipSuccess) {
+        dev_free(staging);
+        dev_free(ix->d_blocks);
+        return fail(MRL_ERR_HIP, std::string("upload: ") + hipGetErrorString(e));
+      }
+    }
+    dev_free(staging);
+  }
+  *out = ix.release();
+  return MRL_OK;
+}
+
+extern "C" int mrl_index_open_segment(mrl_ctx* ctx, const char* path, int verify_crc, mrl_index** out) {
+  if (!ctx || !path || !out) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  FILE* f = fopen(path, "rb");
+  if (!f) return mrl_index_upload(ctx, nullptr, 0, 0, out);  // segment.rs:94-101: absent file = empty
+  if (fseek(f, 0, SEEK_END) != 0) {
+    fclose(f);
+    return fail(MRL_ERR_IO, "seek failed");
+  }
+  long len = ftell(f);
+  if (len < 0) {
+    fclose(f);
+    return fail(MRL_ERR_IO, "ftell failed");
+  }
+  if (len % kBlockBytes != 0) {  // segment.rs:101-103
+    fclose(f);
+    return fail(MRL_ERR_CORRUPT, "corrupt segment size " + std::to_string(len) + " (not multiple of 4096)");
+  }
+  std::vector<uint8_t> buf((size_t)len);
+  fseek(f, 0, SEEK_SET);
+  size_t got = len ? fread(buf.data(), 1, (size_t)len, f) : 0;
+  fclose(f);
+  if (got != (size_t)len) return fail(MRL_ERR_IO, "short read");
+  return mrl_index_upload(ctx, buf.data(), (uint64_t)len / kBlockBytes, verify_crc, out);
+}
+
+extern "C" int mrl_index_block_count(const mrl_index* index, uint64_t* out) {
+  if (!index || !out) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  *out = index->n_blocks;
+  return MRL_OK;
+}
+
+extern "C" int mrl_index_download(mrl_ctx* ctx, const mrl_index* index, void* out_blocks) {
+  if (!ctx || !index || (index->n_blocks && !out_blocks)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (index->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "index belongs to another context");
+  if (!index->n_blocks) return MRL_OK;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  uint8_t* staging = nullptr;
+  const uint64_t chunk = std::min<uint64_t>(index->n_blocks, 65536);
+  if (hipMalloc(&staging, chunk * kBlockBytes) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc staging");
+  uint8_t* dst = static_cast<uint8_t*>(out_blocks);
+  for (uint64_t b = 0; b < index->n_blocks; b += chunk) {
+    uint64_t nb = std::min(chunk, index->n_blocks - b);
+    hipError_t e = launch_relayout(index->d_blocks + b * kBlockBytes, staging, nb, false, ctx->stream);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(dst + b * kBlockBytes, staging, nb * kBlockBytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+      dev_free(staging);
+      return fail(MRL_ERR_HIP, std::string("download: ") + hipGetErrorString(e));
+    }
+  }
+  dev_free(staging);
+  return MRL_OK;
+}
+
+extern "C" void mrl_index_destroy(mrl_index* index) {
+  if (!index) return;
+  (void)hipSetDevice(index->ctx->device);
+  (void)hipStreamSynchronize(index->ctx->stream);
+  for (auto& kv : index->levels) dev_free(kv.second.d_order);
+  dev_free(index->d_blocks);
+  delete index;
+}
+
+// Pass schedule for one K.  Pass 0 scores a spread sample of up to 256 blocks
+// with no threshold; every later pass prunes against the K-th best score of
+// all earlier passes (a lower bound of the final K-th score, so pruning and
+// filtering stay exact) and grows the covered set by at most
+// (16384/K - 1)x, which keeps each pass near 16K candidates per query.  The
+// last pass covers the remaining blocks in ascending order.
+static const uint32_t kPassTarget = 16384;
+static const uint32_t kDefaultCap = 65536;
+
+static int get_levels(mrl_index* ix, uint32_t K, LevelPlan** out) {
+  auto it = ix->levels.find(K);
+  if (it != ix->levels.end()) {
+    *out = &it->second;
+    return MRL_OK;
+  }
+  const uint64_t B = ix->n_blocks;
+  LevelPlan lp;
+  std::vector<uint32_t> sizes;
+  uint64_t first = std::min<uint64_t>(B, (kPassTarget + 63) / 64);
+  sizes.push_back((uint32_t)first);
+  uint64_t cum = first;
+  const uint64_t ratio = std::max<uint64_t>(1, kPassTarget / std::max<uint32_t>(K, 1) - 1);
+  while (cum < B) {
+    uint64_t nxt = std::min<uint64_t>(B - cum, cum * ratio);
+    sizes.push_back((uint32_t)nxt);
+    cum += nxt;
+  }
+  std::vector<uint32_t> order(B);
+  const uint64_t sampled = B - (sizes.size() > 1 ? sizes.back() : 0);
+  if (sizes.size() == 1) {
+    for (uint64_t i = 0; i < B; ++i) order[i] = (uint32_t)i;
+  } else {
+    uint64_t step = (uint64_t)((double)B * 0.6180339887498949) | 1;
+    auto gcd = [](uint64_t a, uint64_t b) {
+      while (b) {
+        uint64_t t = a % b;
+        a = b;
+        b = t;
+      }
+      return a;
+    };
+    while (gcd(step, B) != 1) ++step;
+    std::vector<uint8_t> used(B, 0);
+    for (uint64_t i = 0; i < sampled; ++i) {
+      uint64_t b = (i * step) % B;
+      order[i] = (uint32_t)b;
+      used[b] = 1;
+    }
+    uint64_t w = sampled;
+    for (uint64_t b = 0; b < B; ++b)
+      if (!used[b]) order[w++] = (uint32_t)b;
+  }
+  uint32_t start = 0, maxsz = 0;
+  for (uint32_t s : sizes) {
+    lp.passes.push_back({start, s});
+    start += s;
+    maxsz = std::max(maxsz, s);
+  }
+  lp.cap = (uint32_t)std::min<uint64_t>(kDefaultCap, std::max<uint64_t>((uint64_t)maxsz * 64 + K, 1024));
+  if (B) {
+    if (hipMalloc(&lp.d_order, B * sizeof(uint32_t)) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "order");
+    if (hipMemcpy(lp.d_order, order.data(), B * sizeof(uint32_t), hipMemcpyHostToDevice) != hipSuccess)
+      return fail(MRL_ERR_HIP, "order upload");
+  }
+  auto res = ix->levels.emplace(K, std::move(lp));
+  *out = &res.first->second;
+  return MRL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// plans
+// ---------------------------------------------------------------------------
+static int check_fit(const mrl_eden_fit* f, uint32_t dim, uint32_t bits, const char* what) {
+  if (!f) return fail(MRL_ERR_INVALID_ARG, std::string(what) + " requires an EdenFit");
+  if (f->dim != dim || f->bits != bits || !f->mean)
+    return fail(MRL_ERR_INVALID_ARG, std::string(what) + " fit must have dim " + std::to_string(dim) + ", bits " +
+                                         std::to_string(bits));
+  return MRL_OK;
+}
+
+static int plans_build_impl(mrl_ctx* ctx, const float* queries, bool on_device, uint32_t n_q, uint32_t dims,
+                            int prefix_codec, int mid_codec, const mrl_eden_fit* eden, const mrl_eden_fit* eden_mid,
+                            mrl_plans** out) {
+  if (!ctx || !out || (n_q && !queries)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  *out = nullptr;
+  if (dims < (uint32_t)(kPrefixDims + kRabitqDims)) return fail(MRL_ERR_INVALID_ARG, "dims must be >= 192");  // scan.rs:114
+  if (dims > MRL_MAX_DIMS) return fail(MRL_ERR_INVALID_ARG, "dims above MRL_MAX_DIMS");
+  if (prefix_codec != MRL_PREFIX_MINMAX4 && prefix_codec != MRL_PREFIX_EDEN_PROD)
+    return fail(MRL_ERR_INVALID_ARG, "unknown prefix codec");
+  if (mid_codec != MRL_MID_RABITQ && mid_codec != MRL_MID_EDEN_B1) return fail(MRL_ERR_INVALID_ARG, "unknown mid codec");
+  int rc;
+  if (prefix_codec == MRL_PREFIX_EDEN_PROD && (rc = check_fit(eden, 64, 4, "EdenProd"))) return rc;  // scan.rs:115-119
+  if (mid_codec == MRL_MID_EDEN_B1 && (rc = check_fit(eden_mid, 128, 1, "EdenB1 mid"))) return rc;  // scan.rs:120-124
+  if (eden && (rc = check_fit(eden, 64, 4, "prefix"))) return rc;
+  if (eden_mid && (rc = check_fit(eden_mid, 128, 1, "mid"))) return rc;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  std::unique_ptr<mrl_plans> p(new mrl_plans());
+  p->ctx = ctx;
+  p->n_q = n_q;
+  p->dims = dims;
+  p->prefix_codec = prefix_codec;
+  p->mid_codec = mid_codec;
+  auto cleanup = [&]() {
+    dev_free(p->d_plans);
+    dev_free(p->d_eden_mean);
+    dev_free(p->d_mid_mean);
+  };
+  if (hipMalloc(&p->d_plans, sizeof(mrl_query_plan) * std::max<uint32_t>(n_q, 1)) != hipSuccess)
+    return fail(MRL_ERR_OUT_OF_MEMORY, "plans");
+  if (eden) {
+    p->eden_seed = eden->seed;
+    if (hipMalloc(&p->d_eden_mean, 64 * sizeof(float)) != hipSuccess ||
+        hipMemcpy(p->d_eden_mean, eden->mean, 64 * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+      cleanup();
+      return fail(MRL_ERR_HIP, "eden mean upload");
+    }
+  }
+  if (eden_mid) {
+    p->mid_seed = eden_mid->seed;
+    if (hipMalloc(&p->d_mid_mean, 128 * sizeof(float)) != hipSuccess ||
+        hipMemcpy(p->d_mid_mean, eden_mid->mean, 128 * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+      cleanup();
+      return fail(MRL_ERR_HIP, "eden mid mean upload");
+    }
+  }
+  const float* dq = queries;
+  float* tmp = nullptr;
+  if (!on_device && n_q) {
+    if (hipMalloc(&tmp, (size_t)n_q * dims * sizeof(float)) != hipSuccess) {
+      cleanup();
+      return fail(MRL_ERR_OUT_OF_MEMORY, "queries");
+    }
+    if (hipMemcpyAsync(tmp, queries, (size_t)n_q * dims * sizeof(float), hipMemcpyHostToDevice, ctx->stream) !=
+        hipSuccess) {
+      dev_free(tmp);
+      cleanup();
+      return fail(MRL_ERR_HIP, "query upload");
+    }
+    dq = tmp;
+  }
+  PlanArgs a;
+  a.queries = dq;
+  a.n_q = n_q;
+  a.dims = dims;
+  a.prefix_codec = prefix_codec;
+  a.mid_codec = mid_codec;
+  a.eden_mean = p->d_eden_mean;
+  a.eden_seed = p->eden_seed;
+  a.mid_mean = p->d_mid_mean;
+  a.mid_seed = p->mid_seed;
+  a.c = ctx->consts;
+  a.out = p->d_plans;
+  hipError_t e = launch_plan(a, ctx->stream);
+  if (tmp) {
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    dev_free(tmp);
+  }
+  if (e != hipSuccess) {
+    cleanup();
+    return fail(MRL_ERR_HIP, std::string("plan kernel: ") + hipGetErrorString(e));
+  }
+  *out = p.release();
+  return MRL_OK;
+}
+
+extern "C" int mrl_plans_build(mrl_ctx* ctx, const float* queries, uint32_t n_q, uint32_t dims, int prefix_codec,
+                               int mid_codec, const mrl_eden_fit* eden, const mrl_eden_fit* eden_mid,
+                               mrl_plans** out) {
+  return plans_build_impl(ctx, queries, false, n_q, dims, prefix_codec, mid_codec, eden, eden_mid, out);
+}
+
+extern "C" int mrl_plans_build_device(mrl_ctx* ctx, const float* d_queries, uint32_t n_q, uint32_t dims,
+                                      int prefix_codec, int mid_codec, const mrl_eden_fit* eden,
+                                      const mrl_eden_fit* eden_mid, mrl_plans** out) {
+  return plans_build_impl(ctx, d_queries, true, n_q, dims, prefix_codec, mid_codec, eden, eden_mid, out);
+}
+
+extern "C" int mrl_plans_rebuild_device(mrl_ctx* ctx, mrl_plans* plans, const float* d_queries) {
+  if (!ctx || !plans || (plans->n_q && !d_queries)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (plans->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "plans belong to another context");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  PlanArgs a;
+  a.queries = d_queries;
+  a.n_q = plans->n_q;
+  a.dims = plans->dims;
+  a.prefix_codec = plans->prefix_codec;
+  a.mid_codec = plans->mid_codec;
+  a.eden_mean = plans->d_eden_mean;
+  a.eden_seed = plans->eden_seed;
+  a.mid_mean = plans->d_mid_mean;
+  a.mid_seed = plans->mid_seed;
+  a.c = ctx->consts;
+  a.out = plans->d_plans;
+  HIP_TRY(launch_plan(a, ctx->stream));
+  return MRL_OK;
+}
+
+extern "C" int mrl_plans_count(const mrl_plans* plans, uint32_t* out) {
+  if (!plans || !out) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  *out = plans->n_q;
+  return MRL_OK;
+}
+
+extern "C" int mrl_plans_export(mrl_ctx* ctx, const mrl_plans* plans, uint32_t first, uint32_t count,
+                                mrl_query_plan* out) {
+  if (!ctx || !plans || (count && !out)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if ((uint64_t)first + count > plans->n_q) return fail(MRL_ERR_INVALID_ARG, "plan range out of bounds");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  if (count) HIP_TRY(hipMemcpy(out, plans->d_plans + first, sizeof(mrl_query_plan) * count, hipMemcpyDeviceToHost));
+  return MRL_OK;
+}
+
+extern "C" void mrl_plans_destroy(mrl_plans* plans) {
+  if (!plans) return;
+  (void)hipSetDevice(plans->ctx->device);
+  (void)hipStreamSynchronize(plans->ctx->stream);
+  dev_free(plans->d_plans);
+  dev_free(plans->d_eden_mean);
+  dev_free(plans->d_mid_mean);
+  delete plans;
+}
+
+// ---------------------------------------------------------------------------
+// scan
+// ---------------------------------------------------------------------------
+static int check_cfg(const mrl_scan_config* cfg, uint32_t* k_eff) {
+  if (!cfg) return fail(MRL_ERR_INVALID_ARG, "cfg is null");
+  if (cfg->strata_depth < MRL_STRATA_L0_ONLY || cfg->strata_depth > MRL_STRATA_FULL64B)
+    return fail(MRL_ERR_INVALID_ARG, "unknown strata_depth");
+  if (cfg->shortlist_cand > MRL_MAX_SHORTLIST) return fail(MRL_ERR_INVALID_ARG, "shortlist_cand above 4096");
+  *k_eff = std::max<uint32_t>(cfg->shortlist_cand, 1);  // Shortlist::new: capacity.max(1)
+  return MRL_OK;
+}
+
+static ScanParams make_params(const mrl_scan_config* cfg, const mrl_time_range* t) {
+  ScanParams sp{};
+  sp.alpha = cfg->cs_tolerance;
+  sp.w_s4 = cfg->stratum4_weight;
+  sp.strata = cfg->strata_depth;
+  sp.temporal = cfg->temporal_filter_enable ? 1 : 0;
+  sp.has_lo = t && t->has_lo;
+  sp.lo = t ? t->lo : 0;
+  sp.has_hi = t && t->has_hi;
+  sp.hi = t ? t->hi : 0;
+  sp.exhaustive = cfg->exhaustive ? 1 : 0;
+  return sp;
+}
+
+static void results_free(mrl_results* r) {
+  dev_free(r->d_ids);
+  dev_free(r->d_scores);
+  dev_free(r->d_counts);
+  dev_free(r->d_cand_score);
+  dev_free(r->d_cand_row);
+  dev_free(r->d_cand_count);
+  dev_free(r->d_tau);
+  dev_free(r->d_overflow);
+  dev_free(r->d_stats);
+  dev_free(r->d_err);
+}
+
+extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_results** out) {
+  if (!ctx || !out) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (k == 0 || k > MRL_MAX_SHORTLIST) return fail(MRL_ERR_INVALID_ARG, "k must be in [1, 4096]");
+  *out = nullptr;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  std::unique_ptr<mrl_results> r(new mrl_results());
+  r->ctx = ctx;
+  r->n_q = n_q;
+  r->k = k;
+  r->cap = kDefaultCap;
+  const size_t nq = std::max<uint32_t>(n_q, 1);
+  bool ok = hipMalloc(&r->d_ids, nq * k * sizeof(uint64_t)) == hipSuccess &&
+            hipMalloc(&r->d_scores, nq * k * sizeof(float)) == hipSuccess &&
+            hipMalloc(&r->d_counts, nq * sizeof(uint32_t)) == hipSuccess &&
+            hipMalloc(&r->d_cand_score, nq * r->cap * sizeof(float)) == hipSuccess &&
+            hipMalloc(&r->d_cand_row, nq * r->cap * sizeof(uint32_t)) == hipSuccess &&
+            hipMalloc(&r->d_cand_count, nq * sizeof(uint32_t)) == hipSuccess &&
+            hipMalloc(&r->d_tau, nq * sizeof(float)) == hipSuccess &&
+            hipMalloc(&r->d_overflow, nq * sizeof(uint32_t)) == hipSuccess &&
+            hipMalloc(&r->d_stats, kStatCount * sizeof(unsigned long long)) == hipSuccess &&
+            hipMalloc(&r->d_err, sizeof(uint32_t)) == hipSuccess;
+  if (!ok) {
+    results_free(r.get());
+    return fail(MRL_ERR_OUT_OF_MEMORY, "results buffers");
+  }
+  *out = r.release();
+  return MRL_OK;
+}
+
+extern "C" void mrl_results_destroy(mrl_results* res) {
+  if (!res) return;
+  (void)hipSetDevice(res->ctx->device);
+  (void)hipStreamSynchronize(res->ctx->stream);
+  results_free(res);
+  delete res;
+}
+
+// Enqueue all passes for queries [q_first, q_first+n_q) of `plans` into the
+// result rows starting at q_first.  Caller holds the context lock.
+static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t q_first, uint32_t n_q,
+                        const ScanParams& sp, uint32_t K, mrl_results* r, const LevelPlan& lp, uint32_t cap,
+                        float* cand_score, uint32_t* cand_row) {
+  hipStream_t s = ctx->stream;
+  HIP_TRY(launch_reset(n_q, r->d_cand_count + q_first, r->d_tau + q_first, r->d_overflow + q_first,
+                       q_first == 0 ? r->d_stats : nullptr, r->d_err, s));
+  for (size_t pi = 0; pi < lp.passes.size(); ++pi) {
+    ScanArgs a{};
+    a.idx = ix->d_blocks;
+    a.n_blocks = ix->n_blocks;
+    a.order = lp.d_order ? lp.d_order + lp.passes[pi].first : nullptr;
+    a.n_order = lp.passes[pi].second;
+    a.plans = plans->d_plans + q_first;
+    a.n_q = n_q;
+    a.flag_tabs = ctx->d_flag_tabs;
+    a.sp = sp;
+    a.tau = r->d_tau + q_first;
+    a.cand_score = cand_score;
+    a.cand_row = cand_row;
+    a.cand_count = r->d_cand_count + q_first;
+    a.cand_cap = cap;
+    a.stats = r->d_stats;
+    a.err = r->d_err;
+    HIP_TRY(launch_scan(a, false, s));
+    SelectArgs sa{};
+    sa.cand_score = cand_score;
+    sa.cand_row = cand_row;
+    sa.cand_count = r->d_cand_count + q_first;
+    sa.cand_cap = cap;
+    sa.k = K;
+    sa.tau = r->d_tau + q_first;
+    sa.overflow = r->d_overflow + q_first;
+    sa.final_pass = pi + 1 == lp.passes.size();
+    sa.out_ids = r->d_ids + (size_t)q_first * K;
+    sa.out_scores = r->d_scores + (size_t)q_first * K;
+    sa.out_counts = r->d_counts + q_first;
+    HIP_TRY(launch_select(sa, n_q, s));
+  }
+  return MRL_OK;
+}
+
+extern "C" int mrl_scan_async(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* plans,
+                              const mrl_scan_config* cfg, const mrl_time_range* time, mrl_results* res) {
+  if (!ctx || !index || !plans || !res) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (index->ctx != ctx || plans->ctx != ctx || res->ctx != ctx)
+    return fail(MRL_ERR_INVALID_ARG, "objects belong to another context");
+  uint32_t K;
+  int rc = check_cfg(cfg, &K);
+  if (rc) return rc;
+  if (K != res->k) return fail(MRL_ERR_INVALID_ARG, "results were created for another K");
+  if (plans->n_q > res->n_q) return fail(MRL_ERR_INVALID_ARG, "results hold fewer queries than plans");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  mrl_index* ix = const_cast<mrl_index*>(index);
+  const ScanParams sp = make_params(cfg, time);
+  res->last_index = index;
+  res->last_plans = plans;
+  res->last_cfg = *cfg;
+  res->last_time = time ? *time : mrl_time_range{0, 0, 0, 0};
+  res->pending = true;
+  if (plans->n_q == 0) return MRL_OK;
+  if (ix->n_blocks == 0) {
+    HIP_TRY(launch_reset(plans->n_q, res->d_counts, res->d_tau, res->d_overflow, res->d_stats, res->d_err,
+                         ctx->stream));
+    return MRL_OK;
+  }
+  LevelPlan* lp;
+  if ((rc = get_levels(ix, K, &lp))) return rc;
+  return enqueue_scan(ctx, ix, plans, 0, plans->n_q, sp, K, res, *lp, std::min(lp->cap, res->cap),
+                      res->d_cand_score, res->d_cand_row);
+}
+
+// Exhaustive single pass for one query whose candidate list overflowed
+// (massive score ties or a threshold that could not tighten): every scored
+// vector becomes a candidate, then one exact selection.
+static int dense_rerun(mrl_ctx* ctx, mrl_results* r, uint32_t q) {
+  mrl_index* ix = const_cast<mrl_index*>(r->last_index);
+  const uint64_t n_vec = ix->n_blocks * 64;
+  if (n_vec > 0xffffffffull) return fail(MRL_ERR_INVALID_ARG, "index too large for the dense fallback");
+  float* sc = nullptr;
+  uint32_t* rw = nullptr;
+  if (hipMalloc(&sc, n_vec * sizeof(float)) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "dense scores");
+  if (hipMalloc(&rw, n_vec * sizeof(uint32_t)) != hipSuccess) {
+    dev_free(sc);
+    return fail(MRL_ERR_OUT_OF_MEMORY, "dense rows");
+  }
+  LevelPlan lp;
+  lp.passes.push_back({0u, (uint32_t)ix->n_blocks});
+  lp.d_order = nullptr;
+  ScanParams sp = make_params(&r->last_cfg, &r->last_time);
+  int rc = enqueue_scan(ctx, ix, r->last_plans, q, 1, sp, r->k, r, lp, (uint32_t)n_vec, sc, rw);
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  dev_free(sc);
+  dev_free(rw);
+  if (rc) return rc;
+  if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("dense rerun: ") + hipGetErrorString(e));
+  return MRL_OK;
+}
+
+extern "C" int mrl_results_fetch(mrl_ctx* ctx, mrl_results* res, uint64_t* out_ids, float* out_scores,
+                                 uint32_t* out_counts, mrl_scan_stats* stats) {
+  if (!ctx || !res) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  const uint32_t n_q = res->last_plans ? res->last_plans->n_q : 0;
+  if (res->pending && n_q && res->last_index && res->last_index->n_blocks) {
+    uint32_t err = 0;
+    HIP_TRY(hipMemcpy(&err, res->d_err, sizeof(err), hipMemcpyDeviceToHost));
+    std::vector<uint32_t> ovf(n_q);
+    HIP_TRY(hipMemcpy(ovf.data(), res->d_overflow, n_q * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    for (uint32_t q = 0; q < n_q; ++q) {
+      if (!ovf[q]) continue;
+      int rc = dense_rerun(ctx, res, q);
+      if (rc) return rc;
+      uint32_t e2 = 0;
+      HIP_TRY(hipMemcpy(&e2, res->d_err, sizeof(e2), hipMemcpyDeviceToHost));
+      err |= e2;
+    }
+    res->pending = false;
+    if (err & 1u) return fail(MRL_ERR_NAN, "NaN score among scan survivors (Shortlist::into_sorted would panic)");
+  }
+  const size_t K = res->k;
+  if (out_ids && n_q) HIP_TRY(hipMemcpy(out_ids, res->d_ids, n_q * K * sizeof(uint64_t), hipMemcpyDeviceToHost));
+  if (out_scores && n_q) HIP_TRY(hipMemcpy(out_scores, res->d_scores, n_q * K * sizeof(float), hipMemcpyDeviceToHost));
+  if (out_counts && n_q) HIP_TRY(hipMemcpy(out_counts, res->d_counts, n_q * sizeof(uint32_t), hipMemcpyDeviceToHost));
+  if (stats) {
+    unsigned long long st[kStatCount] = {0};
+    if (n_q) HIP_TRY(hipMemcpy(st, res->d_stats, sizeof(st), hipMemcpyDeviceToHost));
+    stats->blocks = st[kStatBlocks];
+    stats->active_vecs = st[kStatActive];
+    stats->after_prefix = st[kStatPrefix];
+    stats->after_s1 = st[kStatS1];
+    stats->after_s4_budget = st[kStatS4Budget];
+    stats->pushed = st[kStatPushed];
+  }
+  return MRL_OK;
+}
+
+extern "C" int mrl_scan(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* plans, const mrl_scan_config* cfg,
+                        const mrl_time_range* time, uint64_t* out_ids, float* out_scores, uint32_t* out_counts,
+                        mrl_scan_stats* stats) {
+  if (!ctx || !index || !plans) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  uint32_t K;
+  int rc = check_cfg(cfg, &K);
+  if (rc) return rc;
+  mrl_results* res = nullptr;
+  if ((rc = mrl_results_create(ctx, plans->n_q, K, &res))) return rc;
+  rc = mrl_scan_async(ctx, index, plans, cfg, time, res);
+  if (!rc) rc = mrl_results_fetch(ctx, res, out_ids, out_scores, out_counts, stats);
+  std::string msg = g_err;
+  mrl_results_destroy(res);
+  g_err = msg;
+  return rc;
+}
+
+extern "C" int mrl_scan_fixed_tau(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* plans,
+                                  const mrl_scan_config* cfg, const mrl_time_range* time, const float* tau,
+                                  uint64_t* out_masks, float* out_prefix_ip, float* out_scores) {
+  if (!ctx || !index || !plans || !tau) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  uint32_t K;
+  int rc = check_cfg(cfg, &K);
+  if (rc) return rc;
+  const uint64_t nq = plans->n_q, B = index->n_blocks;
+  if (!nq || !B) return MRL_OK;
+  if (!out_masks || !out_prefix_ip || !out_scores) return fail(MRL_ERR_INVALID_ARG, "null output");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  float* d_tau = nullptr;
+  uint64_t* d_masks = nullptr;
+  float *d_prefix = nullptr, *d_score = nullptr;
+  auto cleanup = [&]() {
+    dev_free(d_tau);
+    dev_free(d_masks);
+    dev_free(d_prefix);
+    dev_free(d_score);
+  };
+  if (hipMalloc(&d_tau, nq * sizeof(float)) != hipSuccess || hipMalloc(&d_masks, nq * B * 5 * 8) != hipSuccess ||
+      hipMalloc(&d_prefix, nq * B * 64 * 4) != hipSuccess || hipMalloc(&d_score, nq * B * 64 * 4) != hipSuccess) {
+    cleanup();
+    return fail(MRL_ERR_OUT_OF_MEMORY, "diagnostic buffers");
+  }
+  ScanArgs a{};
+  a.idx = index->d_blocks;
+  a.n_blocks = B;
+  a.order = nullptr;
+  a.n_order = (uint32_t)B;
+  a.plans = plans->d_plans;
+  a.n_q = (uint32_t)nq;
+  a.flag_tabs = ctx->d_flag_tabs;
+  a.sp = make_params(cfg, time);
+  a.tau = d_tau;
+  a.d_masks = d_masks;
+  a.d_prefix = d_prefix;
+  a.d_score = d_score;
+  hipError_t e = hipMemcpyAsync(d_tau, tau, nq * sizeof(float), hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = launch_scan(a, true, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(out_masks, d_masks, nq * B * 5 * 8, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(out_prefix_ip, d_prefix, nq * B * 64 * 4, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(out_scores, d_score, nq * B * 64 * 4, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  cleanup();
+  if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("fixed-tau scan: ") + hipGetErrorString(e));
+  return MRL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// ingest helpers
+// ---------------------------------------------------------------------------
+static bool fit_view(const mrl_eden_fit* f, EdenFitView* v) {
+  if (!f) return false;
+  v->dim = f->dim;
+  v->bits = f->bits;
+  v->seed = f->seed;
+  v->mean = f->mean;
+  return true;
+}
+
+extern "C" int mrl_encode_block(const float* vectors, uint32_t n, uint32_t dims, const uint32_t* timestamps,
+                                const uint32_t* sources, const mrl_eden_fit* eden, const mrl_eden_fit* eden_mid,
+                                void* out_block) {
+  if (!vectors || !timestamps || !sources || !out_block) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  EdenFitView e, m;
+  int rc = encode_block(vectors, n, dims, timestamps, sources, fit_view(eden, &e) ? &e : nullptr,
+                        fit_view(eden_mid, &m) ? &m : nullptr, static_cast<uint8_t*>(out_block));
+  return rc ? fail(rc, "encode_block: invalid arguments (n in 1..64, dims >= 192, fit shapes)") : MRL_OK;
+}
+
+extern "C" int mrl_encode_corpus(const float* matrix, uint64_t n, uint32_t dims, uint32_t default_source,
+                                 const mrl_eden_fit* eden, const mrl_eden_fit* eden_mid, int n_threads,
+                                 void* out_blocks) {
+  if ((n && (!matrix || !out_blocks))) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  EdenFitView e, m;
+  int rc = encode_corpus(matrix, n, dims, default_source, fit_view(eden, &e) ? &e : nullptr,
+                         fit_view(eden_mid, &m) ? &m : nullptr, n_threads, static_cast<uint8_t*>(out_blocks));
+  return rc ? fail(rc, "encode_corpus: invalid arguments") : MRL_OK;
+}
+
+extern "C" int mrl_eden_fit_band(const float* rows, uint64_t n_rows, uint32_t row_stride, uint32_t start, uint32_t dim,
+                                 float* out_mean) {
+  if (!rows || !out_mean) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (start + dim > row_stride) return fail(MRL_ERR_INVALID_ARG, "band exceeds the row");
+  int rc = eden_fit_band(rows, n_rows, row_stride, start, dim, out_mean);
+  return rc ? fail(rc, "empty corpus for EdenFit") : MRL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// synthetic workloads (benchmark inputs)
+// ---------------------------------------------------------------------------
+static SynthSpec to_spec(const mrl_synth_spec* s) {
+  SynthSpec o;
+  o.n_docs = s->n_docs;
+  o.dims = s->dims;
+  o.mean_offset = s->mean_offset;
+  o.seed = s->seed;
+  o.n_centroids = s->n_centroids;
+  o.seed_centroids = s->seed_centroids;
+  o.seed_assign = s->seed_assign;
+  o.noise_sigma = s->noise_sigma;
+  return o;
+}
+
+extern "C" int mrl_synth_docs(const mrl_synth_spec* spec, uint64_t first_row, uint64_t n_rows, int n_threads,
+                              float* out) {
+  if (!spec || (n_rows && !out)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  SynthSpec s = to_spec(spec);
+  parallel_for(n_rows, n_threads, [&](uint64_t r0, uint64_t r1) {
+    for (uint64_t r = r0; r < r1; ++r) synth_doc(s, first_row + r, out + r * s.dims);
+  });
+  return MRL_OK;
+}
+
+extern "C" int mrl_synth_queries(const mrl_synth_spec* spec, uint64_t seed_q, float noise_sigma, int fresh,
+                                 uint32_t n_q, float* out, uint64_t* out_src_rows) {
+  if (!spec || (n_q && !out)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  SynthSpec s = to_spec(spec);
+  for (uint32_t q = 0; q < n_q; ++q)
+    synth_query(s, seed_q, noise_sigma, fresh, q, out + (size_t)q * s.dims, out_src_rows ? out_src_rows + q : nullptr);
+  return MRL_OK;
+}
+
+extern "C" int mrl_synth_eden_fit(const mrl_synth_spec* spec, uint64_t n_rows, float* out_mean64) {
+  if (!spec || !out_mean64) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  SynthSpec s = to_spec(spec);
+  n_rows = std::min<uint64_t>(n_rows, s.n_docs);
+  if (!n_rows) return fail(MRL_ERR_INVALID_ARG, "empty corpus for EdenFit");
+  std::vector<float> rows(n_rows * s.dims);
+  parallel_for(n_rows, 0, [&](uint64_t r0, uint64_t r1) {
+    for (uint64_t r = r0; r < r1; ++r) synth_doc(s, r, rows.data() + r * s.dims);
+  });
+  return eden_fit_band(rows.data(), n_rows, s.dims, 0, 64, out_mean64);
+}
+
+extern "C" int mrl_synth_encode(const mrl_synth_spec* spec, const mrl_eden_fit* eden, const mrl_eden_fit* eden_mid,
+                                uint32_t default_source, int n_threads, void* out_blocks) {
+  if (!spec || !out_blocks) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  SynthSpec s = to_spec(spec);
+  EdenFitView e, m;
+  const EdenFitView* ep = fit_view(eden, &e) ? &e : nullptr;
+  const EdenFitView* mp = fit_view(eden_mid, &m) ? &m : nullptr;
+  const uint64_t n_blocks = (s.n_docs + 63) / 64;
+  std::atomic<int> status{MRL_OK};
+  uint8_t* out = static_cast<uint8_t*>(out_blocks);
+  parallel_for(n_blocks, n_threads, [&](uint64_t b0, uint64_t b1) {
+    std::vector<float> rows(64 * (size_t)s.dims);
+    uint32_t ts[64], src[64];
+    for (uint64_t b = b0; b < b1; ++b) {
+      const uint64_t start = b * 64, end = std::min(s.n_docs, start + 64);
+      for (uint64_t r = start; r < end; ++r) {
+        synth_doc(s, r, rows.data() + (r - start) * s.dims);
+        ts[r - start] = (uint32_t)r;
+        src[r - start] = default_source;
+      }
+      int rc = encode_block(rows.data(), (uint32_t)(end - start), s.dims, ts, src, ep, mp, out + b * kBlockBytes);
+      if (rc) status.store(rc);
+    }
+  });
+  return status.load() ? fail(status.load(), "synth encode failed") : MRL_OK;
+}

@@ -1,0 +1,140 @@
+// mrl_internal.h -- definitions shared by the HIP kernels and the host runtime.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/mrl_scan.h"
+
+namespace mrl {
+
+constexpr int kBlockBytes = 4096;
+constexpr int kVecs = 64;
+constexpr int kPrefixDims = 64;
+constexpr int kRabitqDims = 128;
+constexpr int kTailStart = 192;
+constexpr int kTailFoldDims = 64;
+constexpr int kTailFoldBlocks = 9;
+
+// Reference PaxBlock64 layout (src/block.rs:34-44,133-142).
+constexpr int kOrigMinTs = 0;
+constexpr int kOrigMaxTs = 4;
+constexpr int kOrigTombstone = 16;
+constexpr int kOrigCrc = 24;
+constexpr int kOrigMeta = 64;  // 64 x 7 bytes: scale f16, offset f16, tail_norm f16, flags u8
+constexpr int kOrigS0 = 512;   // bit 3 of each 4-bit prefix level
+constexpr int kOrigS1 = 1024;  // RaBitQ / EdenB1 plane, 128 x u64
+constexpr int kOrigS2 = 2048;  // bit 2
+constexpr int kOrigS3 = 2560;  // bit 1
+constexpr int kOrigS4 = 3072;  // folded tail, 64 x u64
+constexpr int kOrigS5 = 3584;  // bit 0
+
+// Device-resident layout of one block (same 4096 bytes, same information).
+// The header is kept verbatim.  Per-vector fields become structure-of-arrays
+// so lane v of a wave reads slot v with one coalesced load, and the four
+// prefix bitplanes become per-vector 4-bit levels: u32 word (j, v) at
+// kDevNibbles + 4*(64*j + v) holds the levels of dims 8j..8j+7 of slot v,
+// dim 8j+i in bits 4i..4i+3.  S1 and S4 stay bit-transposed (bit v of word d
+// is slot v), which is exactly a wave64 lane mask.
+constexpr int kDevHeader = 0;
+constexpr int kDevScale = 64;     // u16[64]
+constexpr int kDevOffset = 192;   // u16[64]
+constexpr int kDevTail = 320;     // u16[64]
+constexpr int kDevFlags = 448;    // u8[64]
+constexpr int kDevNibbles = 512;  // u32[8][64]
+constexpr int kDevS1 = 2560;      // u64[128]
+constexpr int kDevS4 = 3584;      // u64[64]
+static_assert(kDevS4 + 64 * 8 == kBlockBytes, "device layout fills the block");
+
+static_assert(sizeof(mrl_query_plan) == 1664 * 4, "mrl_query_plan layout");
+
+// Scan-time parameters passed by value to the kernels.
+struct ScanParams {
+  float alpha;        // cs_tolerance
+  float w_s4;         // stratum4_weight
+  int32_t strata;     // mrl_strata_depth
+  int32_t temporal;   // temporal_filter_enable
+  int32_t has_lo;
+  int32_t has_hi;
+  uint32_t lo;
+  uint32_t hi;
+  int32_t exhaustive;
+  int32_t pad;
+};
+
+// Host-computed IEEE constants for the plan kernel (each is the exact f32
+// value the reference computes with the same operations).
+struct PlanConsts {
+  float inv_sqrt64;       // 1.0 / sqrt(64)  (fwht_inplace, n = 64)
+  float inv_sqrt128;      // 1.0 / sqrt(128) (fwht_inplace, n = 128)
+  float rabitq_scale;     // rabitq_bit_scale()
+  float tail_fold_scale;  // tail_fold_bit_scale()
+  float eden_codebook[16];
+  float eden_mid_codebook[2];
+};
+
+// Per-query statistic counters (ScanStats) accumulated on the device.
+enum { kStatBlocks = 0, kStatActive, kStatPrefix, kStatS1, kStatS4Budget, kStatPushed, kStatCount };
+
+// Kernel argument blocks (passed by value as kernarg segments).
+struct PlanArgs {
+  const float* queries;
+  uint32_t n_q;
+  uint32_t dims;
+  int32_t prefix_codec;
+  int32_t mid_codec;
+  const float* eden_mean;  // 64 floats or null
+  uint64_t eden_seed;
+  const float* mid_mean;   // 128 floats or null
+  uint64_t mid_seed;
+  PlanConsts c;
+  mrl_query_plan* out;
+};
+
+struct ScanArgs {
+  const uint8_t* idx;          // device-layout blocks
+  uint64_t n_blocks;
+  const uint32_t* order;       // block ids of this pass (null: 0..n_order-1)
+  uint32_t n_order;
+  const mrl_query_plan* plans;
+  uint32_t n_q;
+  const float* flag_tabs;      // [0,256) rho = f/255, [256,512) sqrt(max(1-rho^2,0))
+  ScanParams sp;
+  const float* tau;            // per query: pruning threshold and candidate floor
+  float* cand_score;           // [n_q][cand_cap]
+  uint32_t* cand_row;
+  uint32_t* cand_count;        // [n_q]
+  uint32_t cand_cap;
+  unsigned long long* stats;   // kStatCount counters, or null
+  uint32_t* err;               // bit 0: NaN score among pushed survivors
+  uint64_t* d_masks;           // diagnostic outputs, [n_q][n_blocks][5]
+  float* d_prefix;             // [n_q][n_blocks][64]
+  float* d_score;              // [n_q][n_blocks][64]
+};
+
+struct SelectArgs {
+  float* cand_score;
+  uint32_t* cand_row;
+  uint32_t* cand_count;
+  uint32_t cand_cap;
+  uint32_t k;
+  float* tau;             // out: K-th best score (or -inf) for the next pass
+  uint32_t* overflow;     // out: per query, set when the candidate list overflowed
+  int32_t final_pass;
+  uint64_t* out_ids;      // final pass: [n_q][k]
+  float* out_scores;
+  uint32_t* out_counts;
+};
+
+// Launchers (mrl_kernels.hip).
+hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device, hipStream_t s);
+hipError_t launch_plan(const PlanArgs& a, hipStream_t s);
+hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s);
+hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s);
+hipError_t launch_reset(uint32_t n_q, uint32_t* cand_count, float* tau, uint32_t* overflow,
+                        unsigned long long* stats, uint32_t* err, hipStream_t s);
+hipError_t launch_fill(float* p, uint64_t n, float v, hipStream_t s);
+
+}  // namespace mrl
