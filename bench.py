@@ -1,0 +1,196 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X PaxBlock64 bitplane scan (prints one JSON line).
+
+A step is one pass of the hot path over one batch of queries: the batched
+query-plan kernel on the resident queries, then every scan pass + top-K
+selection, all enqueued on the library's stream with the index already in
+HBM.  Default workload: BASELINE configs[1] (1M x 768, EDEN-prod prefix,
+batch 1, K_cand 256).  --config 1..5 selects another BASELINE workload.
+
+`roofline` uses the dominant kernel's HIP-event durations recorded during the
+timed steps; `cpu_baseline` times the C restatement of the reference's
+scan_blocks (oracle/, Rayon-equivalent sharding on host threads) on query 0
+of the same index, which also cross-checks the GPU top-K for that query.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mrl-index-rust-vector_amd"))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU; runs across several GPUs are not part of it "
+              "(the scan shards by block range, see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import mrl_index_amd as m
+    from mrl_index_amd import _lib, synth
+
+    w = synth.CONFIGS[args.config]
+    n_threads = min(os.cpu_count() or 1, 16)
+    t0 = time.time()
+    fit = synth.eden_fit(w)
+    log(f"generating + encoding {w.name}: {w.n_docs} x {w.dims} on {n_threads} threads")
+    blocks = synth.encode(w, fit, n_threads)
+    queries, _ = synth.queries(w)
+    log(f"corpus ready in {time.time() - t0:.1f}s ({blocks.nbytes / 1e6:.1f} MB of codes)")
+
+    dev = m.default_device()
+    ix = m.DeviceIndex.upload(blocks, dev)
+    plan = m.QueryPlan.from_query_codec(queries, w.dims, w.prefix_codec, m.MidCodec.RABITQ, fit, None, dev)
+    cfg = m.ScanConfig(shortlist_cand=w.k, strata_depth=w.strata, exhaustive=w.exhaustive)
+    ccfg = cfg.to_c()
+    tr = _lib.TimeRangeC(0, 0, 0, 0)
+    nq = w.n_queries
+    res = C.c_void_p()
+    _lib.check(_lib.lib.mrl_results_create(dev.handle, nq, w.k, C.byref(res)))
+    L = _lib.lib
+
+    def step():
+        _lib.check(L.mrl_plans_rebuild(dev.handle, plan.handle))
+        _lib.check(L.mrl_scan_async(dev.handle, ix.handle, plan.handle, C.byref(ccfg), C.byref(tr), res))
+
+    ids = np.zeros((nq, w.k), dtype=np.uint64)
+    scores = np.zeros((nq, w.k), dtype=np.float32)
+    counts = np.zeros(nq, dtype=np.uint32)
+    st = _lib.ScanStatsC()
+
+    log(f"warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        step()
+    _lib.check(L.mrl_results_fetch(dev.handle, res, _lib.u64ptr(ids), _lib.fptr(scores), _lib.u32ptr(counts),
+                                   C.byref(st)))
+
+    log(f"timed {args.steps} steps")
+    _lib.check(L.mrl_ctx_set_profiling(dev.handle, 1))
+    dev.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dev.synchronize()
+    t_end = time.perf_counter()
+    _lib.check(L.mrl_ctx_set_profiling(dev.handle, 0))
+    cap = 64 * args.steps + 64
+    kt = (_lib.KernelTimeC * cap)()
+    nrec = C.c_uint32()
+    _lib.check(L.mrl_ctx_profile_collect(dev.handle, kt, cap, C.byref(nrec)))
+    _lib.check(L.mrl_results_fetch(dev.handle, res, _lib.u64ptr(ids), _lib.fptr(scores), _lib.u32ptr(counts),
+                                   C.byref(st)))
+
+    ms_step = (t_end - t_start) * 1000.0 / args.steps
+    vec_per_s = w.n_docs / (ms_step / 1000.0)
+
+    # per-kernel durations over the timed steps
+    groups = {}
+    for i in range(min(nrec.value, cap)):
+        r = kt[i]
+        key = ({0: "plan", 1: "scan", 2: "select"}[r.kind], r.pass_)
+        g = groups.setdefault(key, {"ms": [], "n_blocks": r.n_blocks, "n_queries": r.n_queries})
+        g["ms"].append(r.ms)
+    kernels = {}
+    for (kind, p), g in sorted(groups.items()):
+        avg = float(np.mean(g["ms"]))
+        kernels[f"{kind}[{p}]"] = {"avg_ms": avg, "launches": len(g["ms"]), "n_blocks": g["n_blocks"],
+                                   "total_ms": float(np.sum(g["ms"]))}
+    dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["total_ms"])
+    if dom_name.startswith("scan"):
+        dom_bytes = 4096.0 * dom["n_blocks"]
+        achieved = dom_bytes / (dom["avg_ms"] / 1000.0) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_scan " + dom_name,
+                    "kernel_avg_ms": round(dom["avg_ms"], 5), "algorithmic_bytes_per_launch": dom_bytes}
+    else:
+        roofline = {"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None,
+                    "traffic": None, "kernel": dom_name}
+
+    out = {
+        "metric": "scan Mvec/s (vectors scored per second per query batch pass)",
+        "value": round(vec_per_s / 1e6, 2),
+        "unit": "Mvec/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": w.name, "baseline_config": args.config, "n_vectors": w.n_docs, "dims": w.dims,
+                   "blocks": int(blocks.shape[0]), "queries_per_step": nq, "k_cand": w.k,
+                   "prefix_codec": w.prefix_codec.name.lower(), "strata": w.strata.name.lower(),
+                   "pruning": "off (exhaustive)" if w.exhaustive else "on",
+                   "query_noise": f"isotropic, norm {w.query_noise}" if not w.fresh_queries else "fresh draw"},
+        "queries_per_s": round(nq / (ms_step / 1000.0), 1),
+        "pairs_per_s": round(w.n_docs * nq / (ms_step / 1000.0), 1),
+        "step_algorithmic_gb_s": round((4096.0 * blocks.shape[0] + 4 * w.dims * nq + 12 * w.k * nq)
+                                       / (ms_step / 1000.0) / 1e9, 1),
+        "roofline": roofline,
+        "kernels": kernels,
+        "scan_stats_per_step": {f: getattr(st, f) // args.steps for f, _ in _lib.ScanStatsC._fields_},
+    }
+
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"], out["parity_query0"] = cpu_baseline(w, blocks, queries, fit, ids[0], scores[0],
+                                                                 int(counts[0]), args.cpu_seconds, n_threads)
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(w, blocks, queries, fit, gpu_ids, gpu_scores, gpu_count, seconds, n_threads):
+    """The oracle's scan_blocks (restated reference, sharded like Rayon) on
+    query 0; also the parity check of the GPU top-K for that query."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ora
+    fitc = ora.Fit(fit.mean, 4, fit.seed, fit.n_observed) if fit is not None else None
+    op = ora.plan_build(queries[0], w.dims, int(w.prefix_codec), 0, fitc, None)
+    cfg = ora.scan_config(w.k, depth=int(w.strata), sharding=True, threads=n_threads)
+    times = []
+    t_end = time.time() + seconds
+    ref = None
+    while time.time() < t_end or len(times) < 2:
+        t = time.perf_counter()
+        ref = ora.scan_blocks(blocks, op, cfg)
+        times.append(time.perf_counter() - t)
+        if len(times) >= 50:
+            break
+    t_med = float(np.median(times[1:] if len(times) > 1 else times))
+    ref_ids, ref_scores = ref
+    # tie-aware top-K comparison (scores bit-exact)
+    n = gpu_count
+    ok = n == len(ref_ids)
+    if ok and n:
+        gs, rs = gpu_scores[:n], ref_scores
+        ok = np.array_equal(np.sort(gs).view(np.uint32), np.sort(rs).view(np.uint32))
+        kth = np.sort(rs)[0] if len(rs) >= w.k else -np.inf
+        ok = ok and set(gpu_ids[:n][gs > kth].tolist()) == set(ref_ids[rs > kth].tolist())
+    base = {"value": round(w.n_docs / t_med / 1e6, 2), "unit": "Mvec/s", "cores": n_threads, "kind": "port",
+            "sample": f"query 0 of this workload over the full index, {len(times)} runs of the oracle's "
+                      f"sharded scan_blocks, median {t_med * 1000:.1f} ms"}
+    return base, {"checked": True, "identical_topk": bool(ok)}
+
+
+if __name__ == "__main__":
+    main()

@@ -197,9 +197,10 @@ int mrl_plans_build(mrl_ctx *ctx, const float *queries, uint32_t n_queries, uint
 int mrl_plans_build_device(mrl_ctx *ctx, const float *d_queries, uint32_t n_queries, uint32_t dims,
                            int prefix_codec, int mid_codec, const mrl_eden_fit *eden,
                            const mrl_eden_fit *eden_mid, mrl_plans **out);
-/* Rebuild an existing plan set from new device queries of the same shape,
- * codecs and fits (used by the benchmark loop; no allocation). */
-int mrl_plans_rebuild_device(mrl_ctx *ctx, mrl_plans *plans, const float *d_queries);
+/* Plans keep a device copy of their queries.  Re-run the plan kernel on it,
+ * enqueued on the context stream (no copy, no allocation, no sync): the
+ * query-side half of one scan step with its input resident in HBM. */
+int mrl_plans_rebuild(mrl_ctx *ctx, mrl_plans *plans);
 int mrl_plans_count(const mrl_plans *plans, uint32_t *out);
 /* Copies plans [first, first+count) to host. */
 int mrl_plans_export(mrl_ctx *ctx, const mrl_plans *plans, uint32_t first, uint32_t count,
@@ -237,6 +238,28 @@ int mrl_results_fetch(mrl_ctx *ctx, mrl_results *res, uint64_t *out_ids, float *
 int mrl_scan_fixed_tau(mrl_ctx *ctx, const mrl_index *index, const mrl_plans *plans,
                        const mrl_scan_config *cfg, const mrl_time_range *time, const float *tau,
                        uint64_t *out_masks, float *out_prefix_ip, float *out_scores);
+
+/* ---------------------------------------------------------------- */
+/* kernel timing (no reference counterpart; the reference times     */
+/* scans with Instant, src/pipeline.rs:85-95)                       */
+/* ---------------------------------------------------------------- */
+typedef enum mrl_kernel_kind { MRL_KERNEL_PLAN = 0, MRL_KERNEL_SCAN = 1, MRL_KERNEL_SELECT = 2 } mrl_kernel_kind;
+
+typedef struct mrl_kernel_time {
+  int32_t kind;      /* mrl_kernel_kind */
+  int32_t pass;      /* pass index within its scan (0 for plans) */
+  uint32_t n_blocks; /* blocks this launch scanned */
+  uint32_t n_queries;
+  float ms;          /* hipEventElapsedTime around the launch on the context stream */
+  uint32_t reserved;
+} mrl_kernel_time;
+
+/* While enabled, every plan / scan-pass / select launch on the context is
+ * bracketed by HIP events on the context stream. */
+int mrl_ctx_set_profiling(mrl_ctx *ctx, int enable);
+/* Waits for the stream, returns up to max recorded launches (oldest first),
+ * total count in *n_recorded, and clears the record. */
+int mrl_ctx_profile_collect(mrl_ctx *ctx, mrl_kernel_time *out, uint32_t max, uint32_t *n_recorded);
 
 /* ---------------------------------------------------------------- */
 /* ingest-side helpers (host C++, multi-threaded)                   */

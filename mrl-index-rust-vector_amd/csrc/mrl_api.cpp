@@ -46,7 +46,11 @@ extern "C" size_t mrl_query_plan_size(void) { return sizeof(mrl_query_plan); }
 struct LevelPlan {
   uint32_t* d_order = nullptr;
   std::vector<std::pair<uint32_t, uint32_t>> passes;  // (start, size) into d_order
-  uint32_t cap = 0;                                     // candidate slots per query
+};
+
+struct ProfRecord {
+  hipEvent_t start, stop;
+  mrl_kernel_time info;
 };
 
 struct mrl_ctx {
@@ -55,6 +59,38 @@ struct mrl_ctx {
   std::mutex mu;
   float* d_flag_tabs = nullptr;
   PlanConsts consts;
+  bool profiling = false;
+  std::vector<ProfRecord> prof;       // recorded, not yet collected
+  std::vector<hipEvent_t> event_pool; // reusable events
+};
+
+static hipEvent_t pool_event(mrl_ctx* c) {
+  if (!c->event_pool.empty()) {
+    hipEvent_t e = c->event_pool.back();
+    c->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Brackets one launch with events when profiling is on.
+struct ProfScope {
+  mrl_ctx* c;
+  ProfRecord r{};
+  bool on;
+  ProfScope(mrl_ctx* ctx, int kind, int pass, uint32_t n_blocks, uint32_t n_q) : c(ctx), on(ctx->profiling) {
+    if (!on) return;
+    r.start = pool_event(c);
+    r.stop = pool_event(c);
+    r.info = mrl_kernel_time{kind, pass, n_blocks, n_q, 0.0f, 0u};
+    if (!r.start || !r.stop || hipEventRecord(r.start, c->stream) != hipSuccess) on = false;
+  }
+  ~ProfScope() {
+    if (!on) return;
+    if (hipEventRecord(r.stop, c->stream) == hipSuccess) c->prof.push_back(r);
+  }
 };
 
 struct mrl_index {
@@ -75,21 +111,24 @@ struct mrl_plans {
   uint64_t eden_seed = 0;
   float* d_mid_mean = nullptr;
   uint64_t mid_seed = 0;
+  float* d_queries = nullptr;  // owned copy, n_q * dims
+  float* d_luts = nullptr;     // n_q * 1024 prefix LUT written by the plan kernel
 };
 
 struct mrl_results {
   mrl_ctx* ctx = nullptr;
-  uint32_t n_q = 0, k = 0, cap = 0;
+  uint32_t n_q = 0, k = 0, seg_cap = 0;
   uint64_t* d_ids = nullptr;
   float* d_scores = nullptr;
   uint32_t* d_counts = nullptr;
-  float* d_cand_score = nullptr;
+  float* d_cand_score = nullptr;   // [n_q][kSegs][seg_cap]
   uint32_t* d_cand_row = nullptr;
-  uint32_t* d_cand_count = nullptr;
+  uint32_t* d_seg_count = nullptr; // [n_q][kSegs], zero between scans
   float* d_tau = nullptr;
-  uint32_t* d_overflow = nullptr;
+  uint32_t* d_err = nullptr;       // [n_q], zero between scans
+  uint32_t* d_status = nullptr;    // [n_q]
   unsigned long long* d_stats = nullptr;
-  uint32_t* d_err = nullptr;
+  unsigned long long stats_seen[kStatCount] = {0};
   // the last enqueued scan, re-run densely for queries whose candidate list overflowed
   const mrl_index* last_index = nullptr;
   const mrl_plans* last_plans = nullptr;
@@ -145,6 +184,11 @@ extern "C" void mrl_ctx_destroy(mrl_ctx* ctx) {
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
   dev_free(ctx->d_flag_tabs);
+  for (auto& r : ctx->prof) {
+    (void)hipEventDestroy(r.start);
+    (void)hipEventDestroy(r.stop);
+  }
+  for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -154,6 +198,35 @@ extern "C" int mrl_ctx_synchronize(mrl_ctx* ctx) {
   std::lock_guard<std::mutex> g(ctx->mu);
   HIP_TRY(hipSetDevice(ctx->device));
   HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return MRL_OK;
+}
+
+extern "C" int mrl_ctx_set_profiling(mrl_ctx* ctx, int enable) {
+  if (!ctx) return fail(MRL_ERR_INVALID_ARG, "ctx is null");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  ctx->profiling = enable != 0;
+  return MRL_OK;
+}
+
+extern "C" int mrl_ctx_profile_collect(mrl_ctx* ctx, mrl_kernel_time* out, uint32_t max, uint32_t* n_recorded) {
+  if (!ctx || (max && !out)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  uint32_t i = 0;
+  for (auto& r : ctx->prof) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess) ms = -1.0f;
+    if (i < max) {
+      out[i] = r.info;
+      out[i].ms = ms;
+    }
+    ++i;
+    ctx->event_pool.push_back(r.start);
+    ctx->event_pool.push_back(r.stop);
+  }
+  if (n_recorded) *n_recorded = (uint32_t)ctx->prof.size();
+  ctx->prof.clear();
   return MRL_OK;
 }
 
@@ -287,7 +360,6 @@ extern "C" void mrl_index_destroy(mrl_index* index) {
 // (16384/K - 1)x, which keeps each pass near 16K candidates per query.  The
 // last pass covers the remaining blocks in ascending order.
 static const uint32_t kPassTarget = 16384;
-static const uint32_t kDefaultCap = 65536;
 
 static int get_levels(mrl_index* ix, uint32_t K, LevelPlan** out) {
   auto it = ix->levels.find(K);
@@ -338,7 +410,7 @@ static int get_levels(mrl_index* ix, uint32_t K, LevelPlan** out) {
     start += s;
     maxsz = std::max(maxsz, s);
   }
-  lp.cap = (uint32_t)std::min<uint64_t>(kDefaultCap, std::max<uint64_t>((uint64_t)maxsz * 64 + K, 1024));
+  (void)maxsz;
   if (B) {
     if (hipMalloc(&lp.d_order, B * sizeof(uint32_t)) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "order");
     if (hipMemcpy(lp.d_order, order.data(), B * sizeof(uint32_t), hipMemcpyHostToDevice) != hipSuccess)
@@ -357,6 +429,27 @@ static int check_fit(const mrl_eden_fit* f, uint32_t dim, uint32_t bits, const c
   if (f->dim != dim || f->bits != bits || !f->mean)
     return fail(MRL_ERR_INVALID_ARG, std::string(what) + " fit must have dim " + std::to_string(dim) + ", bits " +
                                          std::to_string(bits));
+  return MRL_OK;
+}
+
+// Plan kernel over the plan set's resident queries.  Caller holds the lock.
+static int enqueue_plan(mrl_ctx* ctx, mrl_plans* p) {
+  if (!p->n_q) return MRL_OK;
+  PlanArgs a;
+  a.queries = p->d_queries;
+  a.n_q = p->n_q;
+  a.dims = p->dims;
+  a.prefix_codec = p->prefix_codec;
+  a.mid_codec = p->mid_codec;
+  a.eden_mean = p->d_eden_mean;
+  a.eden_seed = p->eden_seed;
+  a.mid_mean = p->d_mid_mean;
+  a.mid_seed = p->mid_seed;
+  a.c = ctx->consts;
+  a.out = p->d_plans;
+  a.luts = p->d_luts;
+  ProfScope ps(ctx, MRL_KERNEL_PLAN, 0, 0, p->n_q);
+  HIP_TRY(launch_plan(a, ctx->stream));
   return MRL_OK;
 }
 
@@ -385,11 +478,16 @@ static int plans_build_impl(mrl_ctx* ctx, const float* queries, bool on_device, 
   p->mid_codec = mid_codec;
   auto cleanup = [&]() {
     dev_free(p->d_plans);
+    dev_free(p->d_luts);
     dev_free(p->d_eden_mean);
     dev_free(p->d_mid_mean);
+    dev_free(p->d_queries);
   };
-  if (hipMalloc(&p->d_plans, sizeof(mrl_query_plan) * std::max<uint32_t>(n_q, 1)) != hipSuccess)
+  if (hipMalloc(&p->d_plans, sizeof(mrl_query_plan) * std::max<uint32_t>(n_q, 1)) != hipSuccess ||
+      hipMalloc(&p->d_luts, sizeof(float) * 1024 * std::max<uint32_t>(n_q, 1)) != hipSuccess) {
+    cleanup();
     return fail(MRL_ERR_OUT_OF_MEMORY, "plans");
+  }
   if (eden) {
     p->eden_seed = eden->seed;
     if (hipMalloc(&p->d_eden_mean, 64 * sizeof(float)) != hipSuccess ||
@@ -406,41 +504,26 @@ static int plans_build_impl(mrl_ctx* ctx, const float* queries, bool on_device, 
       return fail(MRL_ERR_HIP, "eden mid mean upload");
     }
   }
-  const float* dq = queries;
-  float* tmp = nullptr;
-  if (!on_device && n_q) {
-    if (hipMalloc(&tmp, (size_t)n_q * dims * sizeof(float)) != hipSuccess) {
+  if (n_q) {
+    const size_t qbytes = (size_t)n_q * dims * sizeof(float);
+    if (hipMalloc(&p->d_queries, qbytes) != hipSuccess) {
       cleanup();
       return fail(MRL_ERR_OUT_OF_MEMORY, "queries");
     }
-    if (hipMemcpyAsync(tmp, queries, (size_t)n_q * dims * sizeof(float), hipMemcpyHostToDevice, ctx->stream) !=
-        hipSuccess) {
-      dev_free(tmp);
+    if (hipMemcpyAsync(p->d_queries, queries, qbytes, on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                       ctx->stream) != hipSuccess) {
       cleanup();
-      return fail(MRL_ERR_HIP, "query upload");
+      return fail(MRL_ERR_HIP, "query copy");
     }
-    dq = tmp;
   }
-  PlanArgs a;
-  a.queries = dq;
-  a.n_q = n_q;
-  a.dims = dims;
-  a.prefix_codec = prefix_codec;
-  a.mid_codec = mid_codec;
-  a.eden_mean = p->d_eden_mean;
-  a.eden_seed = p->eden_seed;
-  a.mid_mean = p->d_mid_mean;
-  a.mid_seed = p->mid_seed;
-  a.c = ctx->consts;
-  a.out = p->d_plans;
-  hipError_t e = launch_plan(a, ctx->stream);
-  if (tmp) {
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    dev_free(tmp);
-  }
-  if (e != hipSuccess) {
+  int rc2 = enqueue_plan(ctx, p.get());
+  if (rc2) {
     cleanup();
-    return fail(MRL_ERR_HIP, std::string("plan kernel: ") + hipGetErrorString(e));
+    return rc2;
+  }
+  if (!on_device && hipStreamSynchronize(ctx->stream) != hipSuccess) {  // host buffer may be released after return
+    cleanup();
+    return fail(MRL_ERR_HIP, "plan build");
   }
   *out = p.release();
   return MRL_OK;
@@ -458,24 +541,12 @@ extern "C" int mrl_plans_build_device(mrl_ctx* ctx, const float* d_queries, uint
   return plans_build_impl(ctx, d_queries, true, n_q, dims, prefix_codec, mid_codec, eden, eden_mid, out);
 }
 
-extern "C" int mrl_plans_rebuild_device(mrl_ctx* ctx, mrl_plans* plans, const float* d_queries) {
-  if (!ctx || !plans || (plans->n_q && !d_queries)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+extern "C" int mrl_plans_rebuild(mrl_ctx* ctx, mrl_plans* plans) {
+  if (!ctx || !plans) return fail(MRL_ERR_INVALID_ARG, "null argument");
   if (plans->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "plans belong to another context");
   std::lock_guard<std::mutex> g(ctx->mu);
-  PlanArgs a;
-  a.queries = d_queries;
-  a.n_q = plans->n_q;
-  a.dims = plans->dims;
-  a.prefix_codec = plans->prefix_codec;
-  a.mid_codec = plans->mid_codec;
-  a.eden_mean = plans->d_eden_mean;
-  a.eden_seed = plans->eden_seed;
-  a.mid_mean = plans->d_mid_mean;
-  a.mid_seed = plans->mid_seed;
-  a.c = ctx->consts;
-  a.out = plans->d_plans;
-  HIP_TRY(launch_plan(a, ctx->stream));
-  return MRL_OK;
+  HIP_TRY(hipSetDevice(ctx->device));
+  return enqueue_plan(ctx, plans);
 }
 
 extern "C" int mrl_plans_count(const mrl_plans* plans, uint32_t* out) {
@@ -500,8 +571,10 @@ extern "C" void mrl_plans_destroy(mrl_plans* plans) {
   (void)hipSetDevice(plans->ctx->device);
   (void)hipStreamSynchronize(plans->ctx->stream);
   dev_free(plans->d_plans);
+  dev_free(plans->d_luts);
   dev_free(plans->d_eden_mean);
   dev_free(plans->d_mid_mean);
+  dev_free(plans->d_queries);
   delete plans;
 }
 
@@ -537,12 +610,14 @@ static void results_free(mrl_results* r) {
   dev_free(r->d_counts);
   dev_free(r->d_cand_score);
   dev_free(r->d_cand_row);
-  dev_free(r->d_cand_count);
+  dev_free(r->d_seg_count);
   dev_free(r->d_tau);
-  dev_free(r->d_overflow);
-  dev_free(r->d_stats);
   dev_free(r->d_err);
+  dev_free(r->d_status);
+  dev_free(r->d_stats);
 }
+
+static const uint32_t kSegCap = 4096;  // kSegs * kSegCap = 65536 candidates per query and scan
 
 extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_results** out) {
   if (!ctx || !out) return fail(MRL_ERR_INVALID_ARG, "null argument");
@@ -554,21 +629,33 @@ extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_re
   r->ctx = ctx;
   r->n_q = n_q;
   r->k = k;
-  r->cap = kDefaultCap;
+  r->seg_cap = kSegCap;
   const size_t nq = std::max<uint32_t>(n_q, 1);
+  const size_t cands = nq * kSegs * (size_t)kSegCap;
   bool ok = hipMalloc(&r->d_ids, nq * k * sizeof(uint64_t)) == hipSuccess &&
             hipMalloc(&r->d_scores, nq * k * sizeof(float)) == hipSuccess &&
             hipMalloc(&r->d_counts, nq * sizeof(uint32_t)) == hipSuccess &&
-            hipMalloc(&r->d_cand_score, nq * r->cap * sizeof(float)) == hipSuccess &&
-            hipMalloc(&r->d_cand_row, nq * r->cap * sizeof(uint32_t)) == hipSuccess &&
-            hipMalloc(&r->d_cand_count, nq * sizeof(uint32_t)) == hipSuccess &&
+            hipMalloc(&r->d_cand_score, cands * sizeof(float)) == hipSuccess &&
+            hipMalloc(&r->d_cand_row, cands * sizeof(uint32_t)) == hipSuccess &&
+            hipMalloc(&r->d_seg_count, nq * kSegs * sizeof(uint32_t)) == hipSuccess &&
             hipMalloc(&r->d_tau, nq * sizeof(float)) == hipSuccess &&
-            hipMalloc(&r->d_overflow, nq * sizeof(uint32_t)) == hipSuccess &&
-            hipMalloc(&r->d_stats, kStatCount * sizeof(unsigned long long)) == hipSuccess &&
-            hipMalloc(&r->d_err, sizeof(uint32_t)) == hipSuccess;
+            hipMalloc(&r->d_err, nq * sizeof(uint32_t)) == hipSuccess &&
+            hipMalloc(&r->d_status, nq * sizeof(uint32_t)) == hipSuccess &&
+            hipMalloc(&r->d_stats, kStatCount * sizeof(unsigned long long)) == hipSuccess;
   if (!ok) {
     results_free(r.get());
     return fail(MRL_ERR_OUT_OF_MEMORY, "results buffers");
+  }
+  // Pass state starts zeroed; each final selection leaves it zeroed again.
+  ok = hipMemset(r->d_seg_count, 0, nq * kSegs * sizeof(uint32_t)) == hipSuccess &&
+       hipMemset(r->d_err, 0, nq * sizeof(uint32_t)) == hipSuccess &&
+       hipMemset(r->d_status, 0, nq * sizeof(uint32_t)) == hipSuccess &&
+       hipMemset(r->d_counts, 0, nq * sizeof(uint32_t)) == hipSuccess &&
+       hipMemset(r->d_stats, 0, kStatCount * sizeof(unsigned long long)) == hipSuccess &&
+       hipDeviceSynchronize() == hipSuccess;
+  if (!ok) {
+    results_free(r.get());
+    return fail(MRL_ERR_HIP, "results init");
   }
   *out = r.release();
   return MRL_OK;
@@ -582,47 +669,89 @@ extern "C" void mrl_results_destroy(mrl_results* res) {
   delete res;
 }
 
-// Enqueue all passes for queries [q_first, q_first+n_q) of `plans` into the
-// result rows starting at q_first.  Caller holds the context lock.
-static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t q_first, uint32_t n_q,
-                        const ScanParams& sp, uint32_t K, mrl_results* r, const LevelPlan& lp, uint32_t cap,
-                        float* cand_score, uint32_t* cand_row) {
+// Buffers one scan writes its candidates into.
+struct PassBuffers {
+  float* cand_score;
+  uint32_t* cand_row;
+  uint32_t* seg_count;
+  uint32_t nseg;
+  uint32_t seg_cap;
+  uint32_t* err;
+  float* tau;
+  uint32_t* status;
+  uint64_t* out_ids;
+  float* out_scores;
+  uint32_t* out_counts;
+};
+
+// Enqueue all passes for n_q plans starting at plans_first.  Pass 0 runs
+// with no threshold; after every pass but the last, the histogram threshold
+// becomes the floor of the next; the final selection emits the top K.
+// Caller holds the context lock.
+static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t plans_first, uint32_t n_q,
+                        const ScanParams& sp, uint32_t K, const LevelPlan& lp, const PassBuffers& pb,
+                        unsigned long long* stats) {
   hipStream_t s = ctx->stream;
-  HIP_TRY(launch_reset(n_q, r->d_cand_count + q_first, r->d_tau + q_first, r->d_overflow + q_first,
-                       q_first == 0 ? r->d_stats : nullptr, r->d_err, s));
   for (size_t pi = 0; pi < lp.passes.size(); ++pi) {
     ScanArgs a{};
     a.idx = ix->d_blocks;
     a.n_blocks = ix->n_blocks;
     a.order = lp.d_order ? lp.d_order + lp.passes[pi].first : nullptr;
     a.n_order = lp.passes[pi].second;
-    a.plans = plans->d_plans + q_first;
+    a.plans = plans->d_plans + plans_first;
+    a.luts = plans->d_luts + (size_t)plans_first * 1024;
     a.n_q = n_q;
     a.flag_tabs = ctx->d_flag_tabs;
     a.sp = sp;
-    a.tau = r->d_tau + q_first;
-    a.cand_score = cand_score;
-    a.cand_row = cand_row;
-    a.cand_count = r->d_cand_count + q_first;
-    a.cand_cap = cap;
-    a.stats = r->d_stats;
-    a.err = r->d_err;
-    HIP_TRY(launch_scan(a, false, s));
-    SelectArgs sa{};
-    sa.cand_score = cand_score;
-    sa.cand_row = cand_row;
-    sa.cand_count = r->d_cand_count + q_first;
-    sa.cand_cap = cap;
-    sa.k = K;
-    sa.tau = r->d_tau + q_first;
-    sa.overflow = r->d_overflow + q_first;
-    sa.final_pass = pi + 1 == lp.passes.size();
-    sa.out_ids = r->d_ids + (size_t)q_first * K;
-    sa.out_scores = r->d_scores + (size_t)q_first * K;
-    sa.out_counts = r->d_counts + q_first;
-    HIP_TRY(launch_select(sa, n_q, s));
+    a.tau = pi == 0 ? nullptr : pb.tau;
+    a.cand_score = pb.cand_score;
+    a.cand_row = pb.cand_row;
+    a.seg_count = pb.seg_count;
+    a.nseg = pb.nseg;
+    a.seg_cap = pb.seg_cap;
+    a.stats = stats;
+    a.err = pb.err;
+    {
+      ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)pi, a.n_order, n_q);
+      HIP_TRY(launch_scan(a, false, s));
+    }
+    if (pi + 1 < lp.passes.size()) {
+      ThreshArgs ta{pb.cand_score, pb.seg_count, pb.nseg, pb.seg_cap, pb.tau, K, n_q};
+      ProfScope ps(ctx, MRL_KERNEL_SELECT, (int)pi, a.n_order, n_q);
+      HIP_TRY(launch_thresh(ta, s));
+    }
   }
+  SelectArgs sa{};
+  sa.cand_score = pb.cand_score;
+  sa.cand_row = pb.cand_row;
+  sa.seg_count = pb.seg_count;
+  sa.nseg = pb.nseg;
+  sa.seg_cap = pb.seg_cap;
+  sa.err = pb.err;
+  sa.k = K;
+  sa.status = pb.status;
+  sa.out_ids = pb.out_ids;
+  sa.out_scores = pb.out_scores;
+  sa.out_counts = pb.out_counts;
+  ProfScope ps(ctx, MRL_KERNEL_SELECT, (int)lp.passes.size() - 1, 0, n_q);
+  HIP_TRY(launch_select(sa, n_q, s));
   return MRL_OK;
+}
+
+static PassBuffers results_buffers(mrl_results* r) {
+  PassBuffers pb;
+  pb.cand_score = r->d_cand_score;
+  pb.cand_row = r->d_cand_row;
+  pb.seg_count = r->d_seg_count;
+  pb.nseg = kSegs;
+  pb.seg_cap = r->seg_cap;
+  pb.err = r->d_err;
+  pb.tau = r->d_tau;
+  pb.status = r->d_status;
+  pb.out_ids = r->d_ids;
+  pb.out_scores = r->d_scores;
+  pb.out_counts = r->d_counts;
+  return pb;
 }
 
 extern "C" int mrl_scan_async(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* plans,
@@ -646,41 +775,61 @@ extern "C" int mrl_scan_async(mrl_ctx* ctx, const mrl_index* index, const mrl_pl
   res->pending = true;
   if (plans->n_q == 0) return MRL_OK;
   if (ix->n_blocks == 0) {
-    HIP_TRY(launch_reset(plans->n_q, res->d_counts, res->d_tau, res->d_overflow, res->d_stats, res->d_err,
-                         ctx->stream));
+    HIP_TRY(hipMemsetAsync(res->d_counts, 0, plans->n_q * sizeof(uint32_t), ctx->stream));
+    HIP_TRY(hipMemsetAsync(res->d_status, 0, plans->n_q * sizeof(uint32_t), ctx->stream));
     return MRL_OK;
   }
   LevelPlan* lp;
   if ((rc = get_levels(ix, K, &lp))) return rc;
-  return enqueue_scan(ctx, ix, plans, 0, plans->n_q, sp, K, res, *lp, std::min(lp->cap, res->cap),
-                      res->d_cand_score, res->d_cand_row);
+  return enqueue_scan(ctx, ix, plans, 0, plans->n_q, sp, K, *lp, results_buffers(res), res->d_stats);
 }
 
 // Exhaustive single pass for one query whose candidate list overflowed
 // (massive score ties or a threshold that could not tighten): every scored
-// vector becomes a candidate, then one exact selection.
+// vector becomes a candidate in one large segment, then one exact selection
+// written into the query's result row.
 static int dense_rerun(mrl_ctx* ctx, mrl_results* r, uint32_t q) {
   mrl_index* ix = const_cast<mrl_index*>(r->last_index);
   const uint64_t n_vec = ix->n_blocks * 64;
   if (n_vec > 0xffffffffull) return fail(MRL_ERR_INVALID_ARG, "index too large for the dense fallback");
   float* sc = nullptr;
-  uint32_t* rw = nullptr;
-  if (hipMalloc(&sc, n_vec * sizeof(float)) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "dense scores");
-  if (hipMalloc(&rw, n_vec * sizeof(uint32_t)) != hipSuccess) {
+  uint32_t *rw = nullptr, *small = nullptr;
+  if (hipMalloc(&sc, n_vec * sizeof(float)) != hipSuccess || hipMalloc(&rw, n_vec * sizeof(uint32_t)) != hipSuccess ||
+      hipMalloc(&small, (kHistBins + 4) * sizeof(uint32_t)) != hipSuccess) {
     dev_free(sc);
-    return fail(MRL_ERR_OUT_OF_MEMORY, "dense rows");
+    dev_free(rw);
+    dev_free(small);
+    return fail(MRL_ERR_OUT_OF_MEMORY, "dense fallback buffers");
   }
   LevelPlan lp;
   lp.passes.push_back({0u, (uint32_t)ix->n_blocks});
   lp.d_order = nullptr;
+  PassBuffers pb;
+  pb.cand_score = sc;
+  pb.cand_row = rw;
+  pb.seg_count = small + kHistBins;
+  pb.err = small + kHistBins + 1;
+  pb.status = small + kHistBins + 2;
+  pb.nseg = 1;
+  pb.seg_cap = (uint32_t)n_vec;
+  pb.tau = r->d_tau + q;
+  pb.out_ids = r->d_ids + (size_t)q * r->k;
+  pb.out_scores = r->d_scores + (size_t)q * r->k;
+  pb.out_counts = r->d_counts + q;
   ScanParams sp = make_params(&r->last_cfg, &r->last_time);
-  int rc = enqueue_scan(ctx, ix, r->last_plans, q, 1, sp, r->k, r, lp, (uint32_t)n_vec, sc, rw);
-  hipError_t e = hipStreamSynchronize(ctx->stream);
+  uint32_t st = 0;
+  hipError_t e = hipMemsetAsync(small, 0, (kHistBins + 4) * sizeof(uint32_t), ctx->stream);
+  int rc = e == hipSuccess ? enqueue_scan(ctx, ix, r->last_plans, q, 1, sp, r->k, lp, pb, nullptr) : MRL_ERR_HIP;
+  if (e == hipSuccess) e = hipMemcpyAsync(&st, pb.status, sizeof(st), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   dev_free(sc);
   dev_free(rw);
+  dev_free(small);
   if (rc) return rc;
   if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("dense rerun: ") + hipGetErrorString(e));
-  return MRL_OK;
+  if (st & 2u) return fail(MRL_ERR_HIP, "dense rerun overflowed");
+  return (st & 1u) ? fail(MRL_ERR_NAN, "NaN score among scan survivors (Shortlist::into_sorted would panic)")
+                   : MRL_OK;
 }
 
 extern "C" int mrl_results_fetch(mrl_ctx* ctx, mrl_results* res, uint64_t* out_ids, float* out_scores,
@@ -690,36 +839,36 @@ extern "C" int mrl_results_fetch(mrl_ctx* ctx, mrl_results* res, uint64_t* out_i
   HIP_TRY(hipSetDevice(ctx->device));
   HIP_TRY(hipStreamSynchronize(ctx->stream));
   const uint32_t n_q = res->last_plans ? res->last_plans->n_q : 0;
+  bool nan = false;
   if (res->pending && n_q && res->last_index && res->last_index->n_blocks) {
-    uint32_t err = 0;
-    HIP_TRY(hipMemcpy(&err, res->d_err, sizeof(err), hipMemcpyDeviceToHost));
-    std::vector<uint32_t> ovf(n_q);
-    HIP_TRY(hipMemcpy(ovf.data(), res->d_overflow, n_q * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    std::vector<uint32_t> status(n_q);
+    HIP_TRY(hipMemcpy(status.data(), res->d_status, n_q * sizeof(uint32_t), hipMemcpyDeviceToHost));
     for (uint32_t q = 0; q < n_q; ++q) {
-      if (!ovf[q]) continue;
-      int rc = dense_rerun(ctx, res, q);
-      if (rc) return rc;
-      uint32_t e2 = 0;
-      HIP_TRY(hipMemcpy(&e2, res->d_err, sizeof(e2), hipMemcpyDeviceToHost));
-      err |= e2;
+      if (status[q] & 1u) nan = true;
+      if (status[q] & 2u) {
+        int rc = dense_rerun(ctx, res, q);
+        if (rc == MRL_ERR_NAN) nan = true;
+        else if (rc) return rc;
+      }
     }
-    res->pending = false;
-    if (err & 1u) return fail(MRL_ERR_NAN, "NaN score among scan survivors (Shortlist::into_sorted would panic)");
   }
+  res->pending = false;
+  if (nan) return fail(MRL_ERR_NAN, "NaN score among scan survivors (Shortlist::into_sorted would panic)");
   const size_t K = res->k;
   if (out_ids && n_q) HIP_TRY(hipMemcpy(out_ids, res->d_ids, n_q * K * sizeof(uint64_t), hipMemcpyDeviceToHost));
   if (out_scores && n_q) HIP_TRY(hipMemcpy(out_scores, res->d_scores, n_q * K * sizeof(float), hipMemcpyDeviceToHost));
   if (out_counts && n_q) HIP_TRY(hipMemcpy(out_counts, res->d_counts, n_q * sizeof(uint32_t), hipMemcpyDeviceToHost));
-  if (stats) {
-    unsigned long long st[kStatCount] = {0};
-    if (n_q) HIP_TRY(hipMemcpy(st, res->d_stats, sizeof(st), hipMemcpyDeviceToHost));
-    stats->blocks = st[kStatBlocks];
-    stats->active_vecs = st[kStatActive];
-    stats->after_prefix = st[kStatPrefix];
-    stats->after_s1 = st[kStatS1];
-    stats->after_s4_budget = st[kStatS4Budget];
-    stats->pushed = st[kStatPushed];
+  unsigned long long st[kStatCount] = {0};
+  HIP_TRY(hipMemcpy(st, res->d_stats, sizeof(st), hipMemcpyDeviceToHost));
+  if (stats) {  // counters accumulated since the previous fetch
+    stats->blocks = st[kStatBlocks] - res->stats_seen[kStatBlocks];
+    stats->active_vecs = st[kStatActive] - res->stats_seen[kStatActive];
+    stats->after_prefix = st[kStatPrefix] - res->stats_seen[kStatPrefix];
+    stats->after_s1 = st[kStatS1] - res->stats_seen[kStatS1];
+    stats->after_s4_budget = st[kStatS4Budget] - res->stats_seen[kStatS4Budget];
+    stats->pushed = st[kStatPushed] - res->stats_seen[kStatPushed];
   }
+  memcpy(res->stats_seen, st, sizeof(st));
   return MRL_OK;
 }
 
@@ -772,10 +921,12 @@ extern "C" int mrl_scan_fixed_tau(mrl_ctx* ctx, const mrl_index* index, const mr
   a.order = nullptr;
   a.n_order = (uint32_t)B;
   a.plans = plans->d_plans;
+  a.luts = plans->d_luts;
   a.n_q = (uint32_t)nq;
   a.flag_tabs = ctx->d_flag_tabs;
   a.sp = make_params(cfg, time);
   a.tau = d_tau;
+  a.nseg = 1;
   a.d_masks = d_masks;
   a.d_prefix = d_prefix;
   a.d_score = d_score;

@@ -91,7 +91,16 @@ struct PlanArgs {
   uint64_t mid_seed;
   PlanConsts c;
   mrl_query_plan* out;
+  float* luts;  // [n_q][1024] prefix LUT for the scan
 };
+
+// Candidate lists: per query, kSegs segments with their own counters.  A
+// workgroup stages its appends in LDS and flushes them with one atomic on
+// its segment.  The threshold and select kernels histogram the appended
+// scores, bin = trunc(clamp((s + 2) * 512, 0, 2047)); the lower edge of the
+// bin holding the K-th best appended score is <= the final K-th score.
+constexpr int kSegs = 16;
+constexpr int kHistBins = 2048;
 
 struct ScanArgs {
   const uint8_t* idx;          // device-layout blocks
@@ -99,31 +108,43 @@ struct ScanArgs {
   const uint32_t* order;       // block ids of this pass (null: 0..n_order-1)
   uint32_t n_order;
   const mrl_query_plan* plans;
+  const float* luts;           // [n_q][64][16] prefix LUT (codebook[level] * weight[d])
   uint32_t n_q;
   const float* flag_tabs;      // [0,256) rho = f/255, [256,512) sqrt(max(1-rho^2,0))
   ScanParams sp;
-  const float* tau;            // per query: pruning threshold and candidate floor
-  float* cand_score;           // [n_q][cand_cap]
+  const float* tau;            // per query: pruning threshold and candidate floor (null: -inf)
+  float* cand_score;           // [n_q][nseg][seg_cap]
   uint32_t* cand_row;
-  uint32_t* cand_count;        // [n_q]
-  uint32_t cand_cap;
+  uint32_t* seg_count;         // [n_q][nseg]
+  uint32_t nseg;
+  uint32_t seg_cap;
   unsigned long long* stats;   // kStatCount counters, or null
-  uint32_t* err;               // bit 0: NaN score among pushed survivors
+  uint32_t* err;               // [n_q] bit 0: NaN score among pushed survivors
   uint64_t* d_masks;           // diagnostic outputs, [n_q][n_blocks][5]
   float* d_prefix;             // [n_q][n_blocks][64]
   float* d_score;              // [n_q][n_blocks][64]
 };
 
-struct SelectArgs {
-  float* cand_score;
-  uint32_t* cand_row;
-  uint32_t* cand_count;
-  uint32_t cand_cap;
+struct ThreshArgs {
+  const float* cand_score;  // [n_q][nseg][seg_cap]
+  const uint32_t* seg_count;
+  uint32_t nseg;
+  uint32_t seg_cap;
+  float* tau;               // out [n_q]
   uint32_t k;
-  float* tau;             // out: K-th best score (or -inf) for the next pass
-  uint32_t* overflow;     // out: per query, set when the candidate list overflowed
-  int32_t final_pass;
-  uint64_t* out_ids;      // final pass: [n_q][k]
+  uint32_t n_q;
+};
+
+struct SelectArgs {
+  const float* cand_score;
+  const uint32_t* cand_row;
+  uint32_t* seg_count;    // consumed and zeroed
+  uint32_t nseg;
+  uint32_t seg_cap;
+  uint32_t* err;          // consumed and zeroed
+  uint32_t k;
+  uint32_t* status;       // out per query: bit 0 NaN seen, bit 1 a segment overflowed
+  uint64_t* out_ids;      // [n_q][k]
   float* out_scores;
   uint32_t* out_counts;
 };
@@ -132,9 +153,7 @@ struct SelectArgs {
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device, hipStream_t s);
 hipError_t launch_plan(const PlanArgs& a, hipStream_t s);
 hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s);
+hipError_t launch_thresh(const ThreshArgs& a, hipStream_t s);
 hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s);
-hipError_t launch_reset(uint32_t n_q, uint32_t* cand_count, float* tau, uint32_t* overflow,
-                        unsigned long long* stats, uint32_t* err, hipStream_t s);
-hipError_t launch_fill(float* p, uint64_t n, float v, hipStream_t s);
 
 }  // namespace mrl

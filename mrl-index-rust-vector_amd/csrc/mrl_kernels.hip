@@ -62,6 +62,73 @@ __device__ __forceinline__ float mix_sign(uint64_t a, uint64_t i) {
   return (x & 1ull) == 0 ? 1.0f : -1.0f;
 }
 
+// Read-only views in the constant address space: uniform loads through them
+// become scalar (SMEM) loads.  Only memory no kernel writes during a scan
+// (device blocks, query plans) is read this way.
+#define CONST_AS __attribute__((address_space(4)))
+template <typename T>
+__device__ __forceinline__ const CONST_AS T* cview(const void* p) {
+  return (const CONST_AS T*)(p);
+}
+
+struct Chunk8 {
+  uint64_t p[8];
+  float w[8];
+};
+
+__device__ __forceinline__ Chunk8 load_chunk8(const CONST_AS uint64_t* pl, const CONST_AS float* w) {
+  Chunk8 c;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c.p[i] = pl[i];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c.w[i] = w[i];
+  return c;
+}
+
+// s += w[i] on the lanes whose bit is set in p[i] & m, for i = 0..7 in order:
+// the reference's set-bit accumulation (scan.rs:553-562, 534-542, 618-627)
+// with the bitplane word used directly as the wavefront's execution mask.
+// Lanes not set keep s unchanged.  m is first restricted to the incoming
+// exec mask, so no lane that was inactive on entry is ever enabled.
+__device__ __forceinline__ float masked_add8(float s, uint64_t m, const Chunk8& c) {
+  uint64_t sv, mm;
+  asm volatile(
+      "s_mov_b64 %[sv], exec\n\t"
+      "s_and_b64 %[mm], %[m], %[sv]\n\t"
+      "s_and_b64 exec, %[p0], %[mm]\n\tv_add_f32 %[s], %[w0], %[s]\n\t"
+      "s_and_b64 exec, %[p1], %[mm]\n\tv_add_f32 %[s], %[w1], %[s]\n\t"
+      "s_and_b64 exec, %[p2], %[mm]\n\tv_add_f32 %[s], %[w2], %[s]\n\t"
+      "s_and_b64 exec, %[p3], %[mm]\n\tv_add_f32 %[s], %[w3], %[s]\n\t"
+      "s_and_b64 exec, %[p4], %[mm]\n\tv_add_f32 %[s], %[w4], %[s]\n\t"
+      "s_and_b64 exec, %[p5], %[mm]\n\tv_add_f32 %[s], %[w5], %[s]\n\t"
+      "s_and_b64 exec, %[p6], %[mm]\n\tv_add_f32 %[s], %[w6], %[s]\n\t"
+      "s_and_b64 exec, %[p7], %[mm]\n\tv_add_f32 %[s], %[w7], %[s]\n\t"
+      "s_mov_b64 exec, %[sv]"
+      : [s] "+v"(s), [sv] "=&s"(sv), [mm] "=&s"(mm)
+      : [m] "s"(m), [p0] "s"(c.p[0]), [p1] "s"(c.p[1]), [p2] "s"(c.p[2]), [p3] "s"(c.p[3]), [p4] "s"(c.p[4]),
+        [p5] "s"(c.p[5]), [p6] "s"(c.p[6]), [p7] "s"(c.p[7]), [w0] "s"(c.w[0]), [w1] "s"(c.w[1]),
+        [w2] "s"(c.w[2]), [w3] "s"(c.w[3]), [w4] "s"(c.w[4]), [w5] "s"(c.w[5]), [w6] "s"(c.w[6]),
+        [w7] "s"(c.w[7])
+      : "scc");
+  return s;
+}
+
+// Sum over NCHUNK*8 dims with the next chunk's scalar loads issued before
+// the current chunk's adds.
+template <int NCHUNK>
+__device__ __forceinline__ float masked_accumulate(float s, uint64_t m, const CONST_AS uint64_t* planes,
+                                                   const CONST_AS float* w) {
+  Chunk8 cur = load_chunk8(planes, w);
+#pragma unroll
+  for (int c = 0; c < NCHUNK; ++c) {
+    Chunk8 nxt;
+    if (c + 1 < NCHUNK) nxt = load_chunk8(planes + 8 * (c + 1), w + 8 * (c + 1));
+    s = masked_add8(s, m, cur);
+    if (c + 1 < NCHUNK) cur = nxt;
+  }
+  return s;
+}
+
 // ---------------------------------------------------------------------------
 // block re-layout (upload) and its inverse (download)
 // one 64-lane workgroup per block; lane v owns slot v
@@ -255,6 +322,17 @@ __global__ __launch_bounds__(128) void k_plan(PlanArgs a) {
     float v3 = (mask & 8) ? p3 : -p3;
     p->rabitq_lut[g][mask] = v0 + v1 + v2 + v3;
   }
+  // Prefix LUT for the scan: lut[d*16 + level] = codebook[level] * weight[d]
+  // (or level * weight[d]), the product scan.rs:476-484 forms per (d, level).
+  {
+    float* lut = a.luts + (uint64_t)q * 1024;
+    for (int e = t; e < 1024; e += 128) {
+      const int d = e >> 4, l = e & 15;
+      const float w = eden_codec ? s_eden[d] * a.c.inv_sqrt64 : s_q[d];
+      const float cb = eden_codec ? a.c.eden_codebook[l] : (float)l;
+      lut[e] = cb * w;
+    }
+  }
   if (t < 16) p->eden_codebook[t] = has_eden ? a.c.eden_codebook[t] : 0.0f;
   if (t < 27) p->pad[t] = 0.0f;
 
@@ -282,9 +360,17 @@ __global__ __launch_bounds__(128) void k_plan(PlanArgs a) {
     p->eden_mid_inv_sqrt_d = a.c.inv_sqrt128;
     p->eden_mid_codebook[0] = has_mid ? a.c.eden_mid_codebook[0] : 0.0f;
     p->eden_mid_codebook[1] = has_mid ? a.c.eden_mid_codebook[1] : 0.0f;
-  } else if (t == 3) {  // q_tail_sq (203-206)
+  } else if (t == 3) {  // q_tail_sq (203-206); loads batched ahead, adds in order
     float s = zero_acc();
-    for (uint32_t i = kTailStart; i < dims; ++i) s += s_q[i] * s_q[i];
+    uint32_t i = kTailStart;
+    for (; i + 16 <= dims; i += 16) {
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = s_q[i + j];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s += v[j] * v[j];
+    }
+    for (; i < dims; ++i) s += s_q[i] * s_q[i];
     s_sums[0] = s;
   } else if (t == 4) {  // q_mid_sq (209-212)
     float s = zero_acc();
@@ -343,9 +429,9 @@ struct LaneBlock {
 // One (block, query) evaluation: the stage functions of src/scan.rs:453-634
 // composed as run_default_scan_kernel (654-691) / the L0Only branch (753-790).
 // Returns the pushed-survivor mask; score/prefix_ip are this lane's values.
-__device__ __forceinline__ uint64_t eval_block(const uint8_t* __restrict__ blk, uint64_t active,
+__device__ __forceinline__ uint64_t eval_block(const CONST_AS uint8_t* blk, uint64_t active,
                                               const LaneBlock& m, const float* __restrict__ lut,
-                                              const mrl_query_plan* __restrict__ p, const ScanParams& sp,
+                                              const CONST_AS mrl_query_plan* p, const ScanParams& sp,
                                               float tau, float& prefix_ip_out, float& score_out,
                                               uint64_t* masks) {
   const float alpha = sp.alpha;
@@ -392,14 +478,10 @@ __device__ __forceinline__ uint64_t eval_block(const uint8_t* __restrict__ blk, 
   const bool full = sp.strata == MRL_STRATA_FULL64B;
   if (surv != 0 && rabitq) {
     // Stage: mid-band 1-bit IP (scan.rs:520-569), set bits added in d order.
-    const uint64_t* __restrict__ s1p = reinterpret_cast<const uint64_t*>(blk + kDevS1);
+    const CONST_AS uint64_t* s1p = (const CONST_AS uint64_t*)(blk + kDevS1);
     const bool b1 = p->mid_codec == MRL_MID_EDEN_B1;
-    const float* __restrict__ w2 = b1 ? p->eden_mid_deltas : p->rabitq_weights2;
-    float s1 = b1 ? p->eden_mid_base : p->rabitq_base;
-#pragma unroll 16
-    for (int d = 0; d < 128; ++d) {
-      if (lane_in(s1p[d] & surv)) s1 = s1 + w2[d];
-    }
+    const CONST_AS float* w2 = b1 ? p->eden_mid_deltas : p->rabitq_weights2;
+    float s1 = masked_accumulate<16>(b1 ? p->eden_mid_base : p->rabitq_base, surv, s1p, w2);
     score = b1 ? score + (p->eden_mid_mean_ip + m.offset * s1) : score + s1 * m.mid_n;
     // Stage: post-S1 CS (scan.rs:572-584)
     float ub2 = score + alpha * p->q_after_s1 * m.high_n;
@@ -417,12 +499,8 @@ __device__ __forceinline__ uint64_t eval_block(const uint8_t* __restrict__ blk, 
     masks[3] = surv;
     // Stage: folded-tail 1-bit IP (scan.rs:610-634)
     if (surv != 0 && p->has_tail_fold) {
-      const uint64_t* __restrict__ s4p = reinterpret_cast<const uint64_t*>(blk + kDevS4);
-      float s4 = p->tail_fold_base;
-#pragma unroll 16
-      for (int d = 0; d < 64; ++d) {
-        if (lane_in(s4p[d] & surv)) s4 = s4 + p->tail_fold_weights2[d];
-      }
+      const CONST_AS uint64_t* s4p = (const CONST_AS uint64_t*)(blk + kDevS4);
+      float s4 = masked_accumulate<8>(p->tail_fold_base, surv, s4p, p->tail_fold_weights2);
       score = score + s4 * hn * w_s4;
     }
   }
@@ -431,24 +509,111 @@ __device__ __forceinline__ uint64_t eval_block(const uint8_t* __restrict__ blk, 
   return surv;
 }
 
+// Histogram bin of an appended score (monotone non-decreasing in s).
+__device__ __forceinline__ uint32_t hist_bin(float s) {
+  float x = (s + 2.0f) * 512.0f;
+  x = fminf(fmaxf(x, 0.0f), (float)(kHistBins - 1));
+  return (uint32_t)x;
+}
+
+// A float t with: hist_bin(s) >= b  implies  s >= t.  (For b >= 1, the
+// rounding of s + 2 near the edge is below 2^-22, far inside the 1e-6 margin.)
+__device__ __forceinline__ float bin_floor(uint32_t b) {
+  if (b == 0) return -INFINITY;
+  const double t = (double)b / 512.0 - 2.0 - 1e-6;
+  float f = (float)t;
+  if ((double)f > t) {  // one ulp toward -inf
+    uint32_t u = __float_as_uint(f);
+    if (f > 0.0f) u -= 1u;
+    else if (f == 0.0f) u = 0x80000001u;
+    else u += 1u;
+    f = __uint_as_float(u);
+  }
+  return f;
+}
+
+// Per-lane raw inputs of one block, loaded one block ahead.
+struct RawLane {
+  uint16_t scale, offset, tail;
+  uint32_t flags;
+  uint32_t nib[8];
+  uint32_t hdr_lo, hdr_hi, min_ts, max_ts;  // header words (same value in every lane)
+  uint32_t touch;                           // xor of this lane's S1/S4 words (L2 warm-up only)
+};
+
+__device__ __forceinline__ RawLane load_raw(const uint8_t* blk) {
+  RawLane r;
+  const uint32_t lane = __lane_id();
+  r.scale = reinterpret_cast<const uint16_t*>(blk + kDevScale)[lane];
+  r.offset = reinterpret_cast<const uint16_t*>(blk + kDevOffset)[lane];
+  r.tail = reinterpret_cast<const uint16_t*>(blk + kDevTail)[lane];
+  r.flags = blk[kDevFlags + lane];
+  const uint32_t* nibp = reinterpret_cast<const uint32_t*>(blk + kDevNibbles);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r.nib[j] = nibp[64 * j + lane];
+  const uint32_t* h = reinterpret_cast<const uint32_t*>(blk);
+  r.min_ts = h[kOrigMinTs / 4];
+  r.max_ts = h[kOrigMaxTs / 4];
+  r.hdr_lo = h[kOrigTombstone / 4];
+  r.hdr_hi = h[kOrigTombstone / 4 + 1];
+  const uint32_t* s14 = reinterpret_cast<const uint32_t*>(blk + kDevS1);  // S1 then S4: 384 dwords
+  r.touch = s14[lane] ^ s14[lane + 64] ^ s14[lane + 128] ^ s14[lane + 192] ^ s14[lane + 256] ^ s14[lane + 320];
+  return r;
+}
+
+// Appends of one workgroup are staged here per query and flushed at the end.
+template <int QT>
+struct Staging {
+  static constexpr int kCap = QT == 1 ? 1024 : 256;
+  float score[QT][kCap];
+  uint32_t row[QT][kCap];
+  uint32_t n[QT];
+  uint32_t gbase[QT];
+};
+
+// Appends (score, row) for the lanes in pm: into the LDS staging area while
+// it has room, directly into the query's global segment otherwise.
+template <int QT>
+__device__ __forceinline__ void stage_append(Staging<QT>& st, const ScanArgs& a, int qi, uint32_t q, uint32_t seg,
+                                             uint64_t pm, float score, uint32_t row) {
+  const uint32_t lane = __lane_id();
+  const uint32_t lead = (uint32_t)__ffsll((long long)pm) - 1;
+  uint32_t base = 0;
+  if (lane == lead) base = atomicAdd(&st.n[qi], (uint32_t)__popcll(pm));
+  base = __shfl(base, (int)lead);
+  if ((pm >> lane) & 1ull) {
+    const uint32_t slot = base + lanes_below(pm);
+    if (slot < (uint32_t)Staging<QT>::kCap) {
+      st.score[qi][slot] = score;
+      st.row[qi][slot] = row;
+    } else {
+      const uint64_t sq = (uint64_t)q * a.nseg + seg;
+      const uint32_t g = atomicAdd(a.seg_count + sq, 1u);
+      if (g < a.seg_cap) {
+        a.cand_score[sq * a.seg_cap + g] = score;
+        a.cand_row[sq * a.seg_cap + g] = row;
+      }
+    }
+  }
+}
+
 template <int QT, bool DIAG>
 __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   __shared__ float s_lut[QT * 1024];
   __shared__ float s_rho[256];
   __shared__ float s_midf[256];
+  __shared__ unsigned int s_stats[kStatCount];
+  __shared__ Staging<DIAG ? 1 : QT> s_app;
 
   const int tid = threadIdx.x;
   const uint32_t q0 = blockIdx.y * QT;
   const int nq = (int)min((uint32_t)QT, a.n_q - q0);
-
-  for (int e = tid; e < QT * 1024; e += 256) {
-    int qi = e >> 10;
-    if (qi < nq) {
-      const mrl_query_plan* p = a.plans + q0 + qi;
-      int d = (e >> 4) & 63, l = e & 15;
-      float cb = p->prefix_codec == MRL_PREFIX_EDEN_PROD ? p->eden_codebook[l] : (float)l;
-      s_lut[e] = cb * p->prefix_weight[d];
-    }
+  if (tid < kStatCount) s_stats[tid] = 0u;
+  if (tid < QT) s_app.n[tid] = 0u;
+  {
+    const float4* src = reinterpret_cast<const float4*>(a.luts + (uint64_t)q0 * 1024);
+    float4* dst = reinterpret_cast<float4*>(s_lut);
+    for (int e = tid; e < nq * 256; e += 256) dst[e] = src[e];
   }
   s_rho[tid] = a.flag_tabs[tid];
   s_midf[tid] = a.flag_tabs[256 + tid];
@@ -457,14 +622,40 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t lane = lane_id();
   const ScanParams sp = a.sp;
-  uint64_t st_blocks = 0, st_active = 0, st_prefix = 0, st_s1 = 0, st_s4 = 0, st_pushed = 0;
+  const uint32_t seg = blockIdx.x % a.nseg;
 
-  for (uint32_t pos = blockIdx.x * 4 + wave; pos < a.n_order; pos += gridDim.x * 4) {
-    const uint32_t b = a.order ? a.order[pos] : pos;
-    const uint8_t* __restrict__ blk = a.idx + (uint64_t)b * kBlockBytes;
-    const uint32_t min_ts = *reinterpret_cast<const uint32_t*>(blk + kOrigMinTs);
-    const uint32_t max_ts = *reinterpret_cast<const uint32_t*>(blk + kOrigMaxTs);
-    const uint64_t tomb = *reinterpret_cast<const uint64_t*>(blk + kOrigTombstone);
+  // Block ids for this wave's iterations k (pos = first + k*stride), 64 at a time.
+  const uint32_t stride = gridDim.x * 4;
+  const uint32_t first = blockIdx.x * 4 + wave;
+  auto load_ids = [&](uint32_t k0) -> uint32_t {
+    const uint32_t pos = first + (k0 + lane) * stride;
+    if (pos >= a.n_order) return 0u;
+    return a.order ? a.order[pos] : pos;
+  };
+  uint32_t ids = load_ids(0);
+  uint32_t k = 0;
+  uint32_t pos = first;
+  RawLane cur, nxt;
+  uint32_t b_cur = 0;
+  if (pos < a.n_order) {
+    b_cur = __builtin_amdgcn_readlane(ids, 0);
+    cur = load_raw(a.idx + (uint64_t)b_cur * kBlockBytes);
+  }
+  for (; pos < a.n_order; pos += stride, ++k) {
+    // prefetch the next block of this wave
+    const uint32_t npos = pos + stride;
+    uint32_t b_nxt = 0;
+    if (npos < a.n_order) {
+      if (((k + 1) & 63) == 0) ids = load_ids(k + 1);
+      b_nxt = __builtin_amdgcn_readlane(ids, (k + 1) & 63);
+      nxt = load_raw(a.idx + (uint64_t)b_nxt * kBlockBytes);
+    }
+    const uint32_t b = b_cur;
+    const CONST_AS uint8_t* blk = cview<uint8_t>(a.idx + (uint64_t)b * kBlockBytes);
+    const uint32_t min_ts = __builtin_amdgcn_readfirstlane(cur.min_ts);
+    const uint32_t max_ts = __builtin_amdgcn_readfirstlane(cur.max_ts);
+    const uint64_t tomb = ((uint64_t)__builtin_amdgcn_readfirstlane(cur.hdr_hi) << 32) |
+                          (uint64_t)__builtin_amdgcn_readfirstlane(cur.hdr_lo);
     bool skip = false;
     if (sp.temporal) {  // scan.rs:719-730
       if (sp.has_lo && max_ts < sp.lo) skip = true;
@@ -480,83 +671,214 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
           a.d_score[o * 64 + lane] = 0.0f;
         }
       }
-      continue;
-    }
-    // per-lane meta decode (block.rs:61-99)
-    LaneBlock m;
-    m.scale = h2f(reinterpret_cast<const uint16_t*>(blk + kDevScale)[lane]);
-    m.offset = h2f(reinterpret_cast<const uint16_t*>(blk + kDevOffset)[lane]);
-    m.tail = h2f(reinterpret_cast<const uint16_t*>(blk + kDevTail)[lane]);
-    const uint32_t fl = blk[kDevFlags + lane];
-    const float t = fmaxf(m.tail, 0.0f);
-    m.mid_n = fmaxf(s_midf[fl] * t, 1e-6f);
-    m.high_n = fmaxf(s_rho[fl] * t, 0.0f);
-    const uint32_t* nibp = reinterpret_cast<const uint32_t*>(blk + kDevNibbles);
+    } else {
+      // per-lane meta decode (block.rs:61-99)
+      LaneBlock m;
+      m.scale = h2f(cur.scale);
+      m.offset = h2f(cur.offset);
+      m.tail = h2f(cur.tail);
+      const float t = fmaxf(m.tail, 0.0f);
+      m.mid_n = fmaxf(s_midf[cur.flags] * t, 1e-6f);
+      m.high_n = fmaxf(s_rho[cur.flags] * t, 0.0f);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) m.nib[j] = nibp[64 * j + lane];
+      for (int j = 0; j < 8; ++j) m.nib[j] = cur.nib[j];
 
-    const uint32_t n_active = (uint32_t)__popcll(active);
-    for (int qi = 0; qi < nq; ++qi) {
-      const uint32_t q = q0 + qi;
-      const mrl_query_plan* __restrict__ p = a.plans + q;
-      const float tq = a.tau[q];
-      const float tau = sp.exhaustive ? -INFINITY : tq;
-      uint64_t masks[5];
-      masks[0] = active;
-      float prefix_ip, score;
-      uint64_t surv = eval_block(blk, active, m, s_lut + qi * 1024, p, sp, tau, prefix_ip, score, masks);
-      if (DIAG) {
-        uint64_t o = ((uint64_t)q * a.n_blocks + b);
-        if (lane < 5) {
-          uint64_t mv = lane == 0 ? masks[0] : lane == 1 ? masks[1] : lane == 2 ? masks[2] : lane == 3 ? masks[3] : masks[4];
-          a.d_masks[o * 5 + lane] = mv;
-        }
-        a.d_prefix[o * 64 + lane] = prefix_ip;
-        a.d_score[o * 64 + lane] = score;
-      } else {
-        st_blocks += 1;
-        st_active += n_active;
-        st_prefix += (uint64_t)__popcll(masks[1]);
-        st_s1 += (uint64_t)__popcll(masks[2]);
-        st_s4 += (uint64_t)__popcll(masks[3]);
-        st_pushed += (uint64_t)__popcll(surv);
-        const bool mine = (surv >> lane) & 1ull;
-        if (ballot(mine && score != score) != 0 && lane == 0) atomicOr(a.err, 1u);
-        const uint64_t pm = ballot(mine && score >= tq);
-        if (pm != 0) {
-          const uint32_t first = (uint32_t)__ffsll((long long)pm) - 1;
-          uint32_t base = 0;
-          if (lane == first) base = atomicAdd(a.cand_count + q, (uint32_t)__popcll(pm));
-          base = __shfl(base, (int)first);
-          if ((pm >> lane) & 1ull) {
-            uint32_t slot = base + lanes_below(pm);
-            if (slot < a.cand_cap) {
-              a.cand_score[(uint64_t)q * a.cand_cap + slot] = score;
-              a.cand_row[(uint64_t)q * a.cand_cap + slot] = b * 64u + lane;
-            }
+      const uint32_t n_active = (uint32_t)__popcll(active);
+#pragma unroll 1
+      for (int qi = 0; qi < nq; ++qi) {
+        const uint32_t q = q0 + qi;
+        const CONST_AS mrl_query_plan* p = cview<mrl_query_plan>(a.plans + q);
+        const float tq = a.tau ? cview<float>(a.tau)[q] : -INFINITY;
+        const float tau = sp.exhaustive ? -INFINITY : tq;
+        uint64_t masks[5];
+        masks[0] = active;
+        float prefix_ip, score;
+        // Re-derive the block pointer opaquely per query so the plane-word
+        // loads stay inside this loop (hoisted, 192 words would not fit in SGPRs).
+        uint64_t blk_bits = (uint64_t)blk;
+        asm volatile("" : "+s"(blk_bits));
+        const CONST_AS uint8_t* blk_q = (const CONST_AS uint8_t*)blk_bits;
+        uint64_t surv = eval_block(blk_q, active, m, s_lut + qi * 1024, p, sp, tau, prefix_ip, score, masks);
+        if constexpr (DIAG) {
+          uint64_t o = ((uint64_t)q * a.n_blocks + b);
+          if (lane < 5) {
+            uint64_t mv = lane == 0 ? masks[0] : lane == 1 ? masks[1] : lane == 2 ? masks[2] : lane == 3 ? masks[3] : masks[4];
+            a.d_masks[o * 5 + lane] = mv;
           }
+          a.d_prefix[o * 64 + lane] = prefix_ip;
+          a.d_score[o * 64 + lane] = score;
+        } else {
+          if (a.stats && lane == 0) {
+            atomicAdd(&s_stats[kStatBlocks], 1u);
+            atomicAdd(&s_stats[kStatActive], n_active);
+            atomicAdd(&s_stats[kStatPrefix], (unsigned)__popcll(masks[1]));
+            atomicAdd(&s_stats[kStatS1], (unsigned)__popcll(masks[2]));
+            atomicAdd(&s_stats[kStatS4Budget], (unsigned)__popcll(masks[3]));
+            atomicAdd(&s_stats[kStatPushed], (unsigned)__popcll(surv));
+          }
+          const bool mine = (surv >> lane) & 1ull;
+          if (ballot(mine && score != score) != 0 && lane == 0) atomicOr(a.err + q, 1u);
+          // Append survivors whose score can still reach the top K.
+          const uint64_t pm = ballot(mine && score >= tq);
+          if (pm != 0) stage_append<QT>(s_app, a, qi, q, seg, pm, score, b * 64u + lane);
+        }
+      }
+    }
+    // the touch loads only warm L2; consume them here, long after they landed
+    asm volatile("" ::"v"(cur.touch));
+    cur = nxt;
+    b_cur = b_nxt;
+  }
+  if constexpr (!DIAG) {
+    // flush the staged appends: one global atomic per (workgroup, query)
+    __syncthreads();
+    if (tid < nq) {
+      const uint32_t n = min(s_app.n[tid], (uint32_t)Staging<QT>::kCap);
+      s_app.gbase[tid] = n ? atomicAdd(a.seg_count + (uint64_t)(q0 + tid) * a.nseg + seg, n) : 0u;
+    }
+    if (a.stats && tid < kStatCount && s_stats[tid]) atomicAdd(a.stats + tid, (unsigned long long)s_stats[tid]);
+    __syncthreads();
+    for (int qi = 0; qi < nq; ++qi) {
+      const uint32_t n = min(s_app.n[qi], (uint32_t)Staging<QT>::kCap);
+      const uint32_t g0 = s_app.gbase[qi];
+      const uint64_t sq = (uint64_t)(q0 + qi) * a.nseg + seg;
+      for (uint32_t i = tid; i < n; i += 256) {
+        const uint32_t g = g0 + i;
+        if (g < a.seg_cap) {
+          a.cand_score[sq * a.seg_cap + g] = s_app.score[qi][i];
+          a.cand_row[sq * a.seg_cap + g] = s_app.row[qi][i];
         }
       }
     }
   }
-  if (!DIAG && lane == 0 && a.stats) {
-    atomicAdd(a.stats + kStatBlocks, (unsigned long long)st_blocks);
-    atomicAdd(a.stats + kStatActive, (unsigned long long)st_active);
-    atomicAdd(a.stats + kStatPrefix, (unsigned long long)st_prefix);
-    atomicAdd(a.stats + kStatS1, (unsigned long long)st_s1);
-    atomicAdd(a.stats + kStatS4Budget, (unsigned long long)st_s4);
-    atomicAdd(a.stats + kStatPushed, (unsigned long long)st_pushed);
-  }
 }
 
 // ---------------------------------------------------------------------------
-// top-K selection over per-query candidate lists
-// Order: score descending, then row ascending (a total order, so keeping the
-// best K after every pass yields the global best K).
+// thresholds and top-K selection
+// Order: score descending, then row ascending (a total order, so the best K
+// under it is unique and can be assembled from any superset).
 // ---------------------------------------------------------------------------
 constexpr int kSortCap = 8192;
 constexpr int kSelThreads = 1024;
 
+// One wave: bin holding the need-th largest entry of a descending scan over
+// `hist` (nb = 64 * per bins).  Returns the bin and the count strictly above
+// it through LDS outputs; bin 0 when the histogram holds fewer than `need`.
+__device__ void find_boundary(const uint32_t* hist, uint32_t nb, uint32_t need, bool desc,
+                              uint32_t* out_bin, uint32_t* out_before) {
+  if (threadIdx.x >= 64) return;
+  const uint32_t lane = threadIdx.x;
+  const uint32_t per = nb / 64;
+  uint32_t part = 0;
+  for (uint32_t i = 0; i < per; ++i) {
+    uint32_t bin = desc ? (nb - 1 - (lane * per + i)) : (lane * per + i);
+    part += hist[bin];
+  }
+  uint32_t incl = part;
+  for (int off = 1; off < 64; off <<= 1) {
+    uint32_t o = __shfl_up(incl, off);
+    if ((int)lane >= off) incl += o;
+  }
+  const uint32_t excl = incl - part;
+  const bool hit = excl < need && incl >= need;
+  const uint64_t hm = __ballot(hit);
+  const uint32_t total = __shfl(incl, 63);
+  if (hm == 0) {  // fewer than need entries in total
+    if (lane == 0) {
+      *out_bin = desc ? 0u : nb - 1;
+      *out_before = total;
+    }
+    return;
+  }
+  const uint32_t src = (uint32_t)__ffsll((long long)hm) - 1;
+  if (lane == src) {
+    uint32_t before = excl;
+    for (uint32_t i = 0; i < per; ++i) {
+      uint32_t bin = desc ? (nb - 1 - (lane * per + i)) : (lane * per + i);
+      uint32_t c = hist[bin];
+      if (before + c >= need) {
+        *out_bin = bin;
+        *out_before = before;
+        break;
+      }
+      before += c;
+    }
+  }
+}
+
+// Flattened walk over a query's candidate segments: entry i of the
+// concatenation lives in segment s with off[s] <= i < off[s+1].  Each thread
+// walks i = tid, tid + blockDim.x, ... and keeps its segment cursor, loading
+// four entries ahead so the reads of different segments overlap.
+struct CandView {
+  const float* sc;
+  const uint32_t* rw;
+  uint32_t seg_cap;
+  uint32_t nseg;
+  const uint32_t* off;  // LDS, nseg + 1 prefix offsets
+};
+
+template <typename F>
+__device__ __forceinline__ void for_each_cand(const CandView& v, F&& fn) {
+  const uint32_t total = v.off[v.nseg];
+  uint32_t s = 0;
+  for (uint32_t i0 = threadIdx.x; i0 < total; i0 += 4 * blockDim.x) {
+    float sc[4];
+    uint32_t idx[4];
+    bool ok[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t i = i0 + u * blockDim.x;
+      ok[u] = i < total;
+      if (ok[u]) {
+        while (v.off[s + 1] <= i) ++s;
+        idx[u] = s * v.seg_cap + (i - v.off[s]);
+        sc[u] = v.sc[idx[u]];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (ok[u]) fn(sc[u], idx[u]);
+  }
+}
+
+// Prefix offsets of the (capped) segment counts into off[0..nseg].
+__device__ void seg_offsets(const uint32_t* seg_count, uint32_t nseg, uint32_t seg_cap, uint32_t* off) {
+  if (threadIdx.x == 0) {
+    uint32_t acc = 0;
+    for (uint32_t s = 0; s < nseg; ++s) {
+      off[s] = acc;
+      const uint32_t c = seg_count[s];
+      acc += c < seg_cap ? c : seg_cap;
+    }
+    off[nseg] = acc;
+  }
+  __syncthreads();
+}
+
+// LDS histogram of the appended scores of one query (all segments).
+__device__ void build_hist(uint32_t* hist, const CandView& v) {
+  for (int i = threadIdx.x; i < kHistBins; i += blockDim.x) hist[i] = 0u;
+  __syncthreads();
+  for_each_cand(v, [&](float sc, uint32_t) { atomicAdd(&hist[hist_bin(sc)], 1u); });
+  __syncthreads();
+}
+
+// Threshold after a pass: the lower edge of the bin holding the K-th best
+// score appended so far.  Those scores belong to real vectors, so the K-th
+// best of all vectors is at least this edge.  One workgroup per query.
+__global__ __launch_bounds__(1024) void k_thresh(ThreshArgs a) {
+  __shared__ uint32_t s_hist[kHistBins];
+  __shared__ uint32_t s_off[kSegs + 1];
+  __shared__ uint32_t s_out[2];
+  const uint32_t q = blockIdx.x;
+  seg_offsets(a.seg_count + (uint64_t)q * a.nseg, a.nseg, a.seg_cap, s_off);
+  const CandView v{a.cand_score + (uint64_t)q * a.nseg * a.seg_cap, nullptr, a.seg_cap, a.nseg, s_off};
+  build_hist(s_hist, v);
+  find_boundary(s_hist, kHistBins, a.k, true, &s_out[0], &s_out[1]);
+  __syncthreads();
+  if (threadIdx.x == 0) a.tau[q] = bin_floor(s_out[0]);
+}
 
 __device__ __forceinline__ uint64_t composite(uint32_t key, uint32_t row) {
   return ((uint64_t)key << 32) | (uint64_t)(~row);
@@ -582,143 +904,101 @@ __device__ void bitonic_desc(uint64_t* s, int n2) {
   }
 }
 
-// Wave 0 finds the histogram bin holding the need-th entry, counting from
-// the top bin down (desc) or from bin 0 up (asc).  Writes bin / count beyond.
-__device__ void find_boundary(const uint32_t* hist, uint32_t nb, uint32_t need, bool desc,
-                              uint32_t* out_bin, uint32_t* out_before) {
-  if (threadIdx.x >= 64) return;
-  const uint32_t lane = threadIdx.x;
-  const uint32_t per = nb / 64;  // nb is 1024 or 2048
-  uint32_t part = 0;
-  for (uint32_t i = 0; i < per; ++i) {
-    uint32_t bin = desc ? (nb - 1 - (lane * per + i)) : (lane * per + i);
-    part += hist[bin];
-  }
-  // inclusive prefix over lanes
-  uint32_t incl = part;
-  for (int off = 1; off < 64; off <<= 1) {
-    uint32_t o = __shfl_up(incl, off);
-    if ((int)lane >= off) incl += o;
-  }
-  const uint32_t excl = incl - part;
-  const bool hit = excl < need && incl >= need;
-  const uint64_t hm = __ballot(hit);
-  const uint32_t src = (uint32_t)__ffsll((long long)hm) - 1;
-  if (lane == src) {
-    uint32_t before = excl;
-    for (uint32_t i = 0; i < per; ++i) {
-      uint32_t bin = desc ? (nb - 1 - (lane * per + i)) : (lane * per + i);
-      uint32_t c = hist[bin];
-      if (before + c >= need) {
-        *out_bin = bin;
-        *out_before = before;
-        break;
-      }
-      before += c;
-    }
-  }
-}
-
+// Final selection for one query: threshold from the histogram, gather the
+// appended candidates at or above it (typically K plus one bin), sort, emit.
+// Falls back to an exact radix select on the score key (then on the row for
+// exact ties) when the gathered set exceeds the sort buffer.  Leaves the
+// query's counters, histogram and error flag zeroed for the next scan.
 __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   __shared__ uint64_t s_buf[kSortCap];
   __shared__ uint32_t s_hist[2048];
-  __shared__ uint32_t s_misc[4];
+  __shared__ uint32_t s_misc[8];
+  __shared__ uint32_t s_off[kSegs + 1];
 
   const uint32_t q = blockIdx.x;
   const int tid = threadIdx.x;
-  const uint32_t raw = a.cand_count[q];
-  const uint32_t n = raw < a.cand_cap ? raw : a.cand_cap;
-  const float* sc = a.cand_score + (uint64_t)q * a.cand_cap;
-  const uint32_t* rw = a.cand_row + (uint64_t)q * a.cand_cap;
   const uint32_t K = a.k;
-  if (tid == 0 && raw > a.cand_cap) a.overflow[q] = 1u;
+  const uint32_t* qcount = a.seg_count + (uint64_t)q * a.nseg;
+  if (tid == 0) s_misc[7] = 0;
+  __syncthreads();
+  if (tid < (int)a.nseg && qcount[tid] > a.seg_cap) atomicOr(&s_misc[7], 2u);
+  seg_offsets(qcount, a.nseg, a.seg_cap, s_off);
+  const CandView v{a.cand_score + (uint64_t)q * a.nseg * a.seg_cap, a.cand_row + (uint64_t)q * a.nseg * a.seg_cap,
+                   a.seg_cap, a.nseg, s_off};
+  build_hist(s_hist, v);
+  find_boundary(s_hist, kHistBins, K, true, &s_misc[0], &s_misc[1]);
+  __syncthreads();
+  const float floor_t = bin_floor(s_misc[0]);
 
-  const int shifts[3] = {21, 10, 0};
-  const int widths[3] = {11, 11, 10};
-
-  // gather mode: 0 all entries; 1 (key >> sel_shift) >= sel_prefix;
-  // 2 key > tie_key, plus the tie_need smallest rows among key == tie_key.
-  int mode = 0;
-  uint32_t sel_shift = 0, sel_prefix = 0, tie_key = 0, tie_need = 0;
-  if (n > (uint32_t)kSortCap) {
-    // MSB-first radix select on the score key, stopping once everything at or
-    // above the boundary prefix fits in the sort buffer.
-    uint32_t prefix = 0, need = K;
-    mode = 2;
-    for (int pass = 0; pass < 3; ++pass) {
-      const int sh = shifts[pass], wd = widths[pass];
-      const uint32_t nb = 1u << wd;
-      for (int i = tid; i < 2048; i += kSelThreads) s_hist[i] = 0;
-      __syncthreads();
-      for (uint32_t i = tid; i < n; i += kSelThreads) {
-        uint32_t key = score_key(sc[i]);
-        if (pass == 0 || (key >> (sh + wd)) == prefix) atomicAdd(&s_hist[(key >> sh) & (nb - 1)], 1u);
-      }
-      __syncthreads();
-      find_boundary(s_hist, nb, need, true, &s_misc[0], &s_misc[1]);
-      __syncthreads();
-      const uint32_t bsel = s_misc[0], above = s_misc[1], inbin = s_hist[bsel];
-      __syncthreads();
-      const uint32_t definite = (K - need) + above;
-      need -= above;
-      prefix = (prefix << wd) | bsel;
-      if (definite + inbin <= (uint32_t)kSortCap) {
-        mode = 1;
-        sel_shift = (uint32_t)sh;
-        sel_prefix = prefix;
-        break;
-      }
-    }
-    if (mode == 2) {
-      tie_key = prefix;  // exact K-th key; more exact ties than the buffer holds
-      tie_need = need;
-    }
-  }
-
+  // entries >= floor_t, as (score key, row) composites
   if (tid == 0) s_misc[2] = 0;
   __syncthreads();
-  for (uint32_t i = tid; i < n; i += kSelThreads) {
-    uint32_t key = score_key(sc[i]);
-    bool take = mode == 0 ? true : mode == 1 ? ((key >> sel_shift) >= sel_prefix) : (key > tie_key);
-    if (take) {
-      uint32_t slot = atomicAdd(&s_misc[2], 1u);
-      if (slot < (uint32_t)kSortCap) s_buf[slot] = composite(key, rw[i]);
+  for_each_cand(v, [&](float sc, uint32_t idx) {
+    if (sc >= floor_t) {
+      const uint32_t slot = atomicAdd(&s_misc[2], 1u);
+      if (slot < (uint32_t)kSortCap) s_buf[slot] = composite(score_key(sc), v.rw[idx]);
     }
-  }
+  });
   __syncthreads();
-  if (mode == 2) {
-    // Keep the tie_need smallest rows among entries whose key equals tie_key
-    // (radix select over the 32 row bits, ascending).  Rows are unique.
-    uint32_t prefix = 0, need = tie_need;
+  uint32_t m = s_misc[2];
+  if (m > (uint32_t)kSortCap) {
+    // Radix select: the exact K-th key among entries >= floor_t, then the
+    // smallest rows among its exact ties.
+    const int shifts[3] = {21, 10, 0};
+    const int widths[3] = {11, 11, 10};
+    uint32_t prefix = 0, need = K;
     for (int pass = 0; pass < 3; ++pass) {
       const int sh = shifts[pass], wd = widths[pass];
       const uint32_t nb = 1u << wd;
       for (int i = tid; i < 2048; i += kSelThreads) s_hist[i] = 0;
       __syncthreads();
-      for (uint32_t i = tid; i < n; i += kSelThreads) {
-        if (score_key(sc[i]) != tie_key) continue;
-        uint32_t r = rw[i];
-        if (pass == 0 || (r >> (sh + wd)) == prefix) atomicAdd(&s_hist[(r >> sh) & (nb - 1)], 1u);
-      }
+      for_each_cand(v, [&](float sc, uint32_t) {
+        if (!(sc >= floor_t)) return;
+        const uint32_t key = score_key(sc);
+        if (pass == 0 || (key >> (sh + wd)) == prefix) atomicAdd(&s_hist[(key >> sh) & (nb - 1)], 1u);
+      });
       __syncthreads();
-      find_boundary(s_hist, nb, need, false, &s_misc[0], &s_misc[1]);
+      find_boundary(s_hist, nb, need, true, &s_misc[3], &s_misc[4]);
       __syncthreads();
-      need -= s_misc[1];
-      prefix = (prefix << wd) | s_misc[0];
+      need -= s_misc[4];
+      prefix = (prefix << wd) | s_misc[3];
       __syncthreads();
     }
-    const uint32_t row_max = prefix;
-    for (uint32_t i = tid; i < n; i += kSelThreads) {
-      uint32_t key = score_key(sc[i]);
-      if (key == tie_key && rw[i] <= row_max) {
-        uint32_t slot = atomicAdd(&s_misc[2], 1u);
-        if (slot < (uint32_t)kSortCap) s_buf[slot] = composite(key, rw[i]);
-      }
+    const uint32_t tie_key = prefix;  // exact K-th key; `need` of its ties are kept
+    uint32_t rprefix = 0, rneed = need;
+    for (int pass = 0; pass < 3; ++pass) {
+      const int sh = shifts[pass], wd = widths[pass];
+      const uint32_t nb = 1u << wd;
+      for (int i = tid; i < 2048; i += kSelThreads) s_hist[i] = 0;
+      __syncthreads();
+      for_each_cand(v, [&](float sc, uint32_t idx) {
+        if (!(sc >= floor_t) || score_key(sc) != tie_key) return;
+        const uint32_t r = v.rw[idx];
+        if (pass == 0 || (r >> (sh + wd)) == rprefix) atomicAdd(&s_hist[(r >> sh) & (nb - 1)], 1u);
+      });
+      __syncthreads();
+      find_boundary(s_hist, nb, rneed, false, &s_misc[3], &s_misc[4]);
+      __syncthreads();
+      rneed -= s_misc[4];
+      rprefix = (rprefix << wd) | s_misc[3];
+      __syncthreads();
     }
+    const uint32_t row_max = rprefix;
+    if (tid == 0) s_misc[2] = 0;
     __syncthreads();
+    for_each_cand(v, [&](float sc, uint32_t idx) {
+      if (!(sc >= floor_t)) return;
+      const uint32_t key = score_key(sc);
+      const uint32_t r = v.rw[idx];
+      if (key > tie_key || (key == tie_key && r <= row_max)) {
+        const uint32_t slot = atomicAdd(&s_misc[2], 1u);
+        if (slot < (uint32_t)kSortCap) s_buf[slot] = composite(key, r);
+      }
+    });
+    __syncthreads();
+    m = s_misc[2];  // == K
+    if (m > (uint32_t)kSortCap) m = kSortCap;
   }
-  uint32_t m = s_misc[2];
-  if (m > (uint32_t)kSortCap) m = kSortCap;  // cannot happen: the boundary search bounds m
   int n2 = 1;
   while ((uint32_t)n2 < m) n2 <<= 1;
   for (int i = (int)m + tid; i < n2; i += kSelThreads) s_buf[i] = 0ull;
@@ -726,45 +1006,20 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   bitonic_desc(s_buf, n2);
 
   const uint32_t keep = m < K ? m : K;
-  if (a.final_pass) {
-    for (uint32_t i = tid; i < keep; i += kSelThreads) {
-      uint64_t c = s_buf[i];
-      uint32_t row = ~(uint32_t)c;
-      a.out_ids[(uint64_t)q * K + i] = ((uint64_t)(row >> 6) << 16) | (uint64_t)(row & 63u);
-      a.out_scores[(uint64_t)q * K + i] = key_score((uint32_t)(c >> 32));
-    }
-    if (tid == 0) a.out_counts[q] = keep;
-  } else {
-    float* wsc = a.cand_score + (uint64_t)q * a.cand_cap;
-    uint32_t* wrw = a.cand_row + (uint64_t)q * a.cand_cap;
-    for (uint32_t i = tid; i < keep; i += kSelThreads) {
-      uint64_t c = s_buf[i];
-      wsc[i] = key_score((uint32_t)(c >> 32));
-      wrw[i] = ~(uint32_t)c;
-    }
-    if (tid == 0) {
-      a.cand_count[q] = keep;
-      a.tau[q] = keep >= K ? key_score((uint32_t)(s_buf[K - 1] >> 32)) : -INFINITY;
-    }
+  for (uint32_t i = tid; i < keep; i += kSelThreads) {
+    const uint64_t c = s_buf[i];
+    const uint32_t row = ~(uint32_t)c;
+    a.out_ids[(uint64_t)q * K + i] = ((uint64_t)(row >> 6) << 16) | (uint64_t)(row & 63u);
+    a.out_scores[(uint64_t)q * K + i] = key_score((uint32_t)(c >> 32));
   }
-}
-
-// Resets per-query pass state without hipMemsetAsync (safe under graph capture).
-__global__ void k_reset(uint32_t n_q, uint32_t* cand_count, float* tau, uint32_t* overflow,
-                        unsigned long long* stats, uint32_t* err) {
-  uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n_q) {
-    cand_count[i] = 0;
-    tau[i] = -INFINITY;
-    overflow[i] = 0;
+  __syncthreads();
+  // leave this query's pass state clean for the next scan
+  if (tid < (int)a.nseg) a.seg_count[(uint64_t)q * a.nseg + tid] = 0u;
+  if (tid == 0) {
+    a.out_counts[q] = keep;
+    a.status[q] = (a.err[q] & 1u) | s_misc[7];
+    a.err[q] = 0u;
   }
-  if (stats && i < kStatCount) stats[i] = 0;
-  if (i == 0) *err = 0;
-}
-
-__global__ void k_fill_f32(float* p, uint64_t n, float v) {
-  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -791,8 +1046,7 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s) {
   if (a.n_order == 0 || a.n_q == 0) return hipSuccess;
   const int qt = scan_query_tile(a.n_q);
   const uint32_t tiles = (a.n_q + qt - 1) / qt;
-  uint32_t waves_needed = a.n_order;
-  uint32_t grid = (waves_needed + 3) / 4;
+  uint32_t grid = (a.n_order + 3) / 4;
   const uint32_t max_grid = tiles >= 64 ? 256 : (tiles >= 8 ? 1024 : 2048);
   if (grid > max_grid) grid = max_grid;
   dim3 g(grid, tiles);
@@ -806,23 +1060,15 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s) {
   return hipGetLastError();
 }
 
+hipError_t launch_thresh(const ThreshArgs& a, hipStream_t s) {
+  if (a.n_q == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_thresh, dim3(a.n_q), dim3(1024), 0, s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s) {
   if (n_q == 0) return hipSuccess;
   hipLaunchKernelGGL(k_select, dim3(n_q), dim3(kSelThreads), 0, s, a);
-  return hipGetLastError();
-}
-
-hipError_t launch_reset(uint32_t n_q, uint32_t* cand_count, float* tau, uint32_t* overflow,
-                        unsigned long long* stats, uint32_t* err, hipStream_t s) {
-  uint32_t n = n_q > (uint32_t)kStatCount ? n_q : (uint32_t)kStatCount;
-  hipLaunchKernelGGL(k_reset, dim3((n + 255) / 256), dim3(256), 0, s, n_q, cand_count, tau, overflow, stats,
-                     err);
-  return hipGetLastError();
-}
-
-hipError_t launch_fill(float* p, uint64_t n, float v, hipStream_t s) {
-  if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_fill_f32, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, p, n, v);
   return hipGetLastError();
 }
 

@@ -118,6 +118,20 @@ class QueryPlanC(C.Structure):
     _fields_ = PLAN_FIELDS
 
 
+class KernelTimeC(C.Structure):
+    _fields_ = [
+        ("kind", C.c_int32),
+        ("pass_", C.c_int32),
+        ("n_blocks", C.c_uint32),
+        ("n_queries", C.c_uint32),
+        ("ms", C.c_float),
+        ("reserved", C.c_uint32),
+    ]
+
+
+KERNEL_PLAN, KERNEL_SCAN, KERNEL_SELECT = 0, 1, 2
+
+
 class SynthSpecC(C.Structure):
     _fields_ = [
         ("n_docs", C.c_uint64),
@@ -154,7 +168,7 @@ SIGNATURES = {
                                    C.POINTER(EdenFitC), C.POINTER(EdenFitC), _PP]),
     "mrl_plans_build_device": (C.c_int, [_P, _P, C.c_uint32, C.c_uint32, C.c_int, C.c_int,
                                           C.POINTER(EdenFitC), C.POINTER(EdenFitC), _PP]),
-    "mrl_plans_rebuild_device": (C.c_int, [_P, _P, _P]),
+    "mrl_plans_rebuild": (C.c_int, [_P, _P]),
     "mrl_plans_count": (C.c_int, [_P, _U32]),
     "mrl_plans_export": (C.c_int, [_P, _P, C.c_uint32, C.c_uint32, C.POINTER(QueryPlanC)]),
     "mrl_plans_destroy": (None, [_P]),
@@ -166,6 +180,8 @@ SIGNATURES = {
     "mrl_results_fetch": (C.c_int, [_P, _P, _U64, _F, _U32, C.POINTER(ScanStatsC)]),
     "mrl_scan_fixed_tau": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), C.POINTER(TimeRangeC), _F, _U64,
                                      _F, _F]),
+    "mrl_ctx_set_profiling": (C.c_int, [_P, C.c_int]),
+    "mrl_ctx_profile_collect": (C.c_int, [_P, C.POINTER(KernelTimeC), C.c_uint32, _U32]),
     "mrl_encode_block": (C.c_int, [_F, C.c_uint32, C.c_uint32, _U32, _U32, C.POINTER(EdenFitC),
                                    C.POINTER(EdenFitC), _P]),
     "mrl_encode_corpus": (C.c_int, [_F, C.c_uint64, C.c_uint32, C.c_uint32, C.POINTER(EdenFitC),
