@@ -638,7 +638,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   RawLane cur, nxt;
   uint32_t b_cur = 0;
   if (pos < a.n_order) {
-    b_cur = __builtin_amdgcn_readlane(ids, 0);
+    b_cur = (uint32_t)__builtin_amdgcn_readlane(ids, 0);
     cur = load_raw(a.idx + (uint64_t)b_cur * kBlockBytes);
   }
   for (; pos < a.n_order; pos += stride, ++k) {
@@ -647,15 +647,16 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     uint32_t b_nxt = 0;
     if (npos < a.n_order) {
       if (((k + 1) & 63) == 0) ids = load_ids(k + 1);
-      b_nxt = __builtin_amdgcn_readlane(ids, (k + 1) & 63);
+      b_nxt = (uint32_t)__builtin_amdgcn_readlane(ids, (k + 1) & 63);
       nxt = load_raw(a.idx + (uint64_t)b_nxt * kBlockBytes);
     }
     const uint32_t b = b_cur;
     const CONST_AS uint8_t* blk = cview<uint8_t>(a.idx + (uint64_t)b * kBlockBytes);
-    const uint32_t min_ts = __builtin_amdgcn_readfirstlane(cur.min_ts);
-    const uint32_t max_ts = __builtin_amdgcn_readfirstlane(cur.max_ts);
-    const uint64_t tomb = ((uint64_t)__builtin_amdgcn_readfirstlane(cur.hdr_hi) << 32) |
-                          (uint64_t)__builtin_amdgcn_readfirstlane(cur.hdr_lo);
+    // readfirstlane returns int: widen through uint32_t (no sign extension)
+    const uint32_t min_ts = (uint32_t)__builtin_amdgcn_readfirstlane(cur.min_ts);
+    const uint32_t max_ts = (uint32_t)__builtin_amdgcn_readfirstlane(cur.max_ts);
+    const uint64_t tomb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(cur.hdr_hi) << 32) |
+                          (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(cur.hdr_lo);
     bool skip = false;
     if (sp.temporal) {  // scan.rs:719-730
       if (sp.has_lo && max_ts < sp.lo) skip = true;
