@@ -7,10 +7,14 @@ selection, all enqueued on the library's stream with the index already in
 HBM.  Default workload: BASELINE configs[1] (1M x 768, EDEN-prod prefix,
 batch 1, K_cand 256).  --config 1..5 selects another BASELINE workload.
 
-`roofline` uses the dominant kernel's HIP-event durations recorded during the
-timed steps; `cpu_baseline` times the C restatement of the reference's
-scan_blocks (oracle/, Rayon-equivalent sharding on host threads) on query 0
-of the same index, which also cross-checks the GPU top-K for that query.
+`roofline` uses the dominant kernel's (k_scan) durations from HIP events that
+each dispatch records at its own start and end (hipExtLaunchKernelGGL) during
+the timed steps, on the library's stream; `traffic` is the committed
+rocprofv3 FETCH_SIZE + WRITE_SIZE reading for the same workload.
+`cpu_baseline` times the C restatement of the reference's scan_blocks
+(oracle/, Rayon-equivalent sharding on host threads) on query 0 of the same
+index, which also cross-checks the GPU top-K for that query.  `host_boundary`
+is the PCIe-inclusive rate of the synchronous host-buffer calls.
 """
 import argparse
 import ctypes as C
@@ -37,12 +41,17 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (PMC byte-counter calibration) and exit")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU; runs across several GPUs are not part of it "
-              "(the scan shards by block range, see DESIGN.md).", file=sys.stderr)
+              "(the scan would shard by contiguous block range, one top-K merge per query).", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
 
     import numpy as np
     import mrl_index_amd as m
@@ -106,24 +115,30 @@ def main():
     groups = {}
     for i in range(min(nrec.value, cap)):
         r = kt[i]
-        key = ({0: "plan", 1: "scan", 2: "select"}[r.kind], r.pass_)
-        g = groups.setdefault(key, {"ms": [], "n_blocks": r.n_blocks, "n_queries": r.n_queries})
+        key = ({0: "plan", 1: "scan", 2: "select", 3: "thresh"}[r.kind], r.pass_)
+        g = groups.setdefault(key, {"ms": [], "blocks": []})
         g["ms"].append(r.ms)
+        g["blocks"].append(r.n_blocks)
     kernels = {}
     for (kind, p), g in sorted(groups.items()):
-        avg = float(np.mean(g["ms"]))
-        kernels[f"{kind}[{p}]"] = {"avg_ms": avg, "launches": len(g["ms"]), "n_blocks": g["n_blocks"],
-                                   "total_ms": float(np.sum(g["ms"]))}
-    dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["total_ms"])
-    if dom_name.startswith("scan"):
-        dom_bytes = 4096.0 * dom["n_blocks"]
-        achieved = dom_bytes / (dom["avg_ms"] / 1000.0) / 1e9
-        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_scan " + dom_name,
-                    "kernel_avg_ms": round(dom["avg_ms"], 5), "algorithmic_bytes_per_launch": dom_bytes}
-    else:
-        roofline = {"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None,
-                    "traffic": None, "kernel": dom_name}
+        kernels[f"{kind}[{p}]"] = {"avg_ms": float(np.mean(g["ms"])), "launches": len(g["ms"]),
+                                   "avg_blocks": float(np.mean(g["blocks"])), "total_ms": float(np.sum(g["ms"]))}
+    # The dominant kernel is k_scan (every pass launches it); its roofline is
+    # taken over all of its launches, as rocprofv3's per-kernel average is:
+    # algorithmic bytes per launch = 4096 B x blocks scanned by that launch.
+    scan_ms = [ms for (kind, _), g in groups.items() if kind == "scan" for ms in g["ms"]]
+    scan_blk = [b for (kind, _), g in groups.items() if kind == "scan" for b in g["blocks"]]
+    avg_ms = float(np.mean(scan_ms))
+    bytes_per_launch = 4096.0 * float(np.mean(scan_blk))
+    achieved = bytes_per_launch / (avg_ms / 1000.0) / 1e9
+    traffic = committed_traffic(w.name)
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": traffic["bytes_per_launch"] if traffic else None,
+                "kernel": "k_scan", "launches_per_step": len(scan_ms) / args.steps,
+                "kernel_avg_ms": round(avg_ms, 5), "algorithmic_bytes_per_launch": bytes_per_launch}
+    if traffic:
+        roofline["traffic_source"] = traffic["source"]
 
     out = {
         "metric": "scan Mvec/s (vectors scored per second per query batch pass)",
@@ -152,10 +167,67 @@ def main():
         "scan_stats_per_step": {f: getattr(st, f) // args.steps for f, _ in _lib.ScanStatsC._fields_},
     }
 
+    out["host_boundary"] = host_boundary_rate(L, _lib, dev, ix, queries, fit, w, ccfg, tr)
+
     if not args.no_cpu_baseline:
         out["cpu_baseline"], out["parity_query0"] = cpu_baseline(w, blocks, queries, fit, ids[0], scores[0],
                                                                  int(counts[0]), args.cpu_seconds, n_threads)
     print(json.dumps(out), flush=True)
+
+
+def host_boundary_rate(L, _lib, dev, ix, queries, fit, w, ccfg, tr, reps=20):
+    """PCIe-inclusive rate of the synchronous host-buffer calls: queries copied
+    from host memory (mrl_plans_build), scan, results copied back (mrl_scan).
+    Reported beside `value`, never as it."""
+    import numpy as np
+    nq, k = w.n_queries, w.k
+    ids = np.zeros((nq, k), dtype=np.uint64)
+    scores = np.zeros((nq, k), dtype=np.float32)
+    counts = np.zeros(nq, dtype=np.uint32)
+    fitc = fit.to_c() if fit is not None else None
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    times = []
+    for i in range(reps + 2):
+        plans = C.c_void_p()
+        dev.synchronize()
+        t = time.perf_counter()
+        _lib.check(L.mrl_plans_build(dev.handle, _lib.fptr(q), nq, w.dims, int(w.prefix_codec), 0,
+                                     C.byref(fitc) if fitc is not None else None, None, C.byref(plans)))
+        _lib.check(L.mrl_scan(dev.handle, ix.handle, plans, C.byref(ccfg), C.byref(tr), _lib.u64ptr(ids),
+                              _lib.fptr(scores), _lib.u32ptr(counts), None))
+        times.append(time.perf_counter() - t)
+        L.mrl_plans_destroy(plans)
+    t_med = float(np.median(times[2:]))
+    return {"ms_per_call": round(t_med * 1000.0, 4), "value": round(w.n_docs / t_med / 1e6, 2), "unit": "Mvec/s",
+            "calls": "mrl_plans_build (host queries) + mrl_scan (host results), synchronous, median of "
+                     f"{reps}"}
+
+
+def copy_calibration(mib):
+    """A plain device-to-device copy of known size: under rocprofv3 --pmc its
+    FETCH_SIZE / WRITE_SIZE per dispatch give the counters' scale factor."""
+    import torch
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_dispatch": n, "dispatches": 5}), flush=True)
+
+
+def committed_traffic(workload):
+    """HBM bytes per k_scan launch for this workload, from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the same
+    counters' reading on a copy of known size); None when not measured."""
+    path = os.path.join(ROOT, "profiles", "k_scan_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == workload:
+            return {"bytes_per_launch": float(f[2]), "source": "profiles/k_scan_traffic.txt"}
+    return None
 
 
 def cpu_baseline(w, blocks, queries, fit, gpu_ids, gpu_scores, gpu_count, seconds, n_threads):

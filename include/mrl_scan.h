@@ -243,19 +243,24 @@ int mrl_scan_fixed_tau(mrl_ctx *ctx, const mrl_index *index, const mrl_plans *pl
 /* kernel timing (no reference counterpart; the reference times     */
 /* scans with Instant, src/pipeline.rs:85-95)                       */
 /* ---------------------------------------------------------------- */
-typedef enum mrl_kernel_kind { MRL_KERNEL_PLAN = 0, MRL_KERNEL_SCAN = 1, MRL_KERNEL_SELECT = 2 } mrl_kernel_kind;
+typedef enum mrl_kernel_kind {
+  MRL_KERNEL_PLAN = 0,   /* batched query plan + LUT build */
+  MRL_KERNEL_SCAN = 1,   /* one scan pass over a block range */
+  MRL_KERNEL_SELECT = 2, /* final top-K selection */
+  MRL_KERNEL_THRESH = 3  /* per-query threshold between passes */
+} mrl_kernel_kind;
 
 typedef struct mrl_kernel_time {
   int32_t kind;      /* mrl_kernel_kind */
   int32_t pass;      /* pass index within its scan (0 for plans) */
   uint32_t n_blocks; /* blocks this launch scanned */
   uint32_t n_queries;
-  float ms;          /* hipEventElapsedTime around the launch on the context stream */
+  float ms;          /* kernel duration from events recorded by the dispatch itself */
   uint32_t reserved;
 } mrl_kernel_time;
 
-/* While enabled, every plan / scan-pass / select launch on the context is
- * bracketed by HIP events on the context stream. */
+/* While enabled, every plan / scan-pass / threshold / select launch on the
+ * context records its kernel start and end (events written by the dispatch). */
 int mrl_ctx_set_profiling(mrl_ctx *ctx, int enable);
 /* Waits for the stream, returns up to max recorded launches (oldest first),
  * total count in *n_recorded, and clears the record. */

@@ -75,7 +75,8 @@ static hipEvent_t pool_event(mrl_ctx* c) {
   return e;
 }
 
-// Brackets one launch with events when profiling is on.
+// Supplies dispatch-recorded start/stop events to one launch when profiling
+// is on; the record is kept once the launch was enqueued (commit()).
 struct ProfScope {
   mrl_ctx* c;
   ProfRecord r{};
@@ -85,11 +86,37 @@ struct ProfScope {
     r.start = pool_event(c);
     r.stop = pool_event(c);
     r.info = mrl_kernel_time{kind, pass, n_blocks, n_q, 0.0f, 0u};
-    if (!r.start || !r.stop || hipEventRecord(r.start, c->stream) != hipSuccess) on = false;
+    if (!r.start || !r.stop) {
+      if (r.start) c->event_pool.push_back(r.start);
+      if (r.stop) c->event_pool.push_back(r.stop);
+      on = false;
+    }
+  }
+  LaunchEvents ev() const {
+    LaunchEvents e;
+    if (on) {
+      e.start = r.start;
+      e.stop = r.stop;
+    }
+    return e;
+  }
+  // Called after a successful enqueue; events of a launch that was skipped
+  // (empty work) are returned to the pool instead.
+  void commit(bool launched) {
+    if (!on) return;
+    if (launched) {
+      c->prof.push_back(r);
+    } else {
+      c->event_pool.push_back(r.start);
+      c->event_pool.push_back(r.stop);
+    }
+    on = false;
   }
   ~ProfScope() {
-    if (!on) return;
-    if (hipEventRecord(r.stop, c->stream) == hipSuccess) c->prof.push_back(r);
+    if (on) {  // enqueue failed: recycle the events
+      c->event_pool.push_back(r.start);
+      c->event_pool.push_back(r.stop);
+    }
   }
 };
 
@@ -449,7 +476,8 @@ static int enqueue_plan(mrl_ctx* ctx, mrl_plans* p) {
   a.out = p->d_plans;
   a.luts = p->d_luts;
   ProfScope ps(ctx, MRL_KERNEL_PLAN, 0, 0, p->n_q);
-  HIP_TRY(launch_plan(a, ctx->stream));
+  HIP_TRY(launch_plan(a, ctx->stream, ps.ev()));
+  ps.commit(p->n_q != 0);
   return MRL_OK;
 }
 
@@ -713,12 +741,14 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
     a.err = pb.err;
     {
       ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)pi, a.n_order, n_q);
-      HIP_TRY(launch_scan(a, false, s));
+      HIP_TRY(launch_scan(a, false, s, ps.ev()));
+      ps.commit(a.n_order != 0 && n_q != 0);
     }
     if (pi + 1 < lp.passes.size()) {
       ThreshArgs ta{pb.cand_score, pb.seg_count, pb.nseg, pb.seg_cap, pb.tau, K, n_q};
-      ProfScope ps(ctx, MRL_KERNEL_SELECT, (int)pi, a.n_order, n_q);
-      HIP_TRY(launch_thresh(ta, s));
+      ProfScope ps(ctx, MRL_KERNEL_THRESH, (int)pi, a.n_order, n_q);
+      HIP_TRY(launch_thresh(ta, s, ps.ev()));
+      ps.commit(n_q != 0);
     }
   }
   SelectArgs sa{};
@@ -734,7 +764,8 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
   sa.out_scores = pb.out_scores;
   sa.out_counts = pb.out_counts;
   ProfScope ps(ctx, MRL_KERNEL_SELECT, (int)lp.passes.size() - 1, 0, n_q);
-  HIP_TRY(launch_select(sa, n_q, s));
+  HIP_TRY(launch_select(sa, n_q, s, ps.ev()));
+  ps.commit(n_q != 0);
   return MRL_OK;
 }
 

@@ -150,10 +150,17 @@ struct SelectArgs {
 };
 
 // Launchers (mrl_kernels.hip).
+// Optional start/stop events written by the dispatch itself (kernel-only
+// duration, the same interval a kernel-trace profiler reports).
+struct LaunchEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device, hipStream_t s);
-hipError_t launch_plan(const PlanArgs& a, hipStream_t s);
-hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s);
-hipError_t launch_thresh(const ThreshArgs& a, hipStream_t s);
-hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s);
+hipError_t launch_plan(const PlanArgs& a, hipStream_t s, const LaunchEvents& ev = {});
+hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev = {});
+hipError_t launch_thresh(const ThreshArgs& a, hipStream_t s, const LaunchEvents& ev = {});
+hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
 
 }  // namespace mrl

@@ -5,6 +5,7 @@
 // division/sqrt and IEEE denormals, so per-vector scores are bit-identical to
 // src/scan.rs.  Wave64 is the natural unit: the 64 slots of a PaxBlock64 map
 // to the 64 lanes of a wavefront and a bitplane word is a lane mask.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -1035,15 +1036,22 @@ hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, 
   return hipGetLastError();
 }
 
-hipError_t launch_plan(const PlanArgs& a, hipStream_t s) {
+// Launch with the dispatch-recorded events when profiling, plainly otherwise.
+template <typename K, typename... Args>
+static void launch(K kernel, dim3 grid, dim3 block, hipStream_t s, const LaunchEvents& ev, Args... args) {
+  if (ev.start) hipExtLaunchKernelGGL(kernel, grid, block, 0, s, ev.start, ev.stop, 0u, args...);
+  else hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
+}
+
+hipError_t launch_plan(const PlanArgs& a, hipStream_t s, const LaunchEvents& ev) {
   if (a.n_q == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_plan, dim3(a.n_q), dim3(128), 0, s, a);
+  launch(k_plan, dim3(a.n_q), dim3(128), s, ev, a);
   return hipGetLastError();
 }
 
 int scan_query_tile(uint32_t n_q) { return n_q >= 8 ? 8 : 1; }
 
-hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s) {
+hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev) {
   if (a.n_order == 0 || a.n_q == 0) return hipSuccess;
   const int qt = scan_query_tile(a.n_q);
   const uint32_t tiles = (a.n_q + qt - 1) / qt;
@@ -1052,24 +1060,24 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s) {
   if (grid > max_grid) grid = max_grid;
   dim3 g(grid, tiles);
   if (qt == 8) {
-    if (diag) hipLaunchKernelGGL((k_scan<8, true>), g, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((k_scan<8, false>), g, dim3(256), 0, s, a);
+    if (diag) launch(k_scan<8, true>, g, dim3(256), s, ev, a);
+    else launch(k_scan<8, false>, g, dim3(256), s, ev, a);
   } else {
-    if (diag) hipLaunchKernelGGL((k_scan<1, true>), g, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((k_scan<1, false>), g, dim3(256), 0, s, a);
+    if (diag) launch(k_scan<1, true>, g, dim3(256), s, ev, a);
+    else launch(k_scan<1, false>, g, dim3(256), s, ev, a);
   }
   return hipGetLastError();
 }
 
-hipError_t launch_thresh(const ThreshArgs& a, hipStream_t s) {
+hipError_t launch_thresh(const ThreshArgs& a, hipStream_t s, const LaunchEvents& ev) {
   if (a.n_q == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_thresh, dim3(a.n_q), dim3(1024), 0, s, a);
+  launch(k_thresh, dim3(a.n_q), dim3(1024), s, ev, a);
   return hipGetLastError();
 }
 
-hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s) {
+hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev) {
   if (n_q == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_select, dim3(n_q), dim3(kSelThreads), 0, s, a);
+  launch(k_select, dim3(n_q), dim3(kSelThreads), s, ev, a);
   return hipGetLastError();
 }
 

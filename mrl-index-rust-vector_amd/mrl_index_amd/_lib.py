@@ -129,7 +129,7 @@ class KernelTimeC(C.Structure):
     ]
 
 
-KERNEL_PLAN, KERNEL_SCAN, KERNEL_SELECT = 0, 1, 2
+KERNEL_PLAN, KERNEL_SCAN, KERNEL_SELECT, KERNEL_THRESH = 0, 1, 2, 3
 
 
 class SynthSpecC(C.Structure):

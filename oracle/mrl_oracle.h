@@ -9,6 +9,27 @@
  * in plain C with the same IEEE-754 single-precision operations in the same
  * order (build with -ffp-contract=off, no fast-math; x86-64 SSE arithmetic).
  * Citations are path:line into the reference tree.
+ *
+ * How each part is pinned (the reference holds no golden vectors and cannot
+ * be built here: no Rust toolchain):
+ *  - f16 decode/encode: all 65536 patterns against numpy's IEEE binary16.
+ *  - CRC-32: the "123456789" known answer and zlib.crc32.
+ *  - FWHT, mid-band and tail-fold rotations: the Sylvester Hadamard matrix and
+ *    the operator's Gram structure (float64).
+ *  - Plan fields, encoder fields and every per-vector stage score: float64
+ *    closed forms recomputed from the inputs; hand-built blocks whose scores
+ *    follow from single set bits; the pruned scan against the exhaustive
+ *    top-K (admissibility); stage-mask monotonicity and stats consistency.
+ *  - EDEN nearest_centroid: brute force incl. the lower-index tie rule.
+ * Parity unpinned (no independent check fixes the exact bits):
+ *  - ora_rademacher_diag / ora_tail_rademacher (eden.rs:357-370,
+ *    rotate.rs:53-67): the SplitMix-style sign sequence is checked only
+ *    against a second restatement, for balance, and through the rotations'
+ *    orthogonality, which any sign sequence satisfies.
+ *  - ora_lloyd_max_normal (eden.rs:27-44): each level is within 2e-6 of the
+ *    N(0,1) Lloyd-Max centroid; the literal f32 bits are as read.
+ *  - ora_scan_blocks with sharding on: which of several exactly tied scores
+ *    survive at the K boundary (Rayon's merge order, scan.rs:846-865).
  */
 #ifndef MRL_ORACLE_H
 #define MRL_ORACLE_H
