@@ -232,12 +232,13 @@ __device__ __forceinline__ void fwht_stage(float* a, int n, int h, int i) {
 }
 
 __global__ __launch_bounds__(128) void k_plan(PlanArgs a) {
-  __shared__ float s_q[MRL_MAX_DIMS];
+  __shared__ __align__(16) float s_q[MRL_MAX_DIMS];
   __shared__ float s_mid[128];
   __shared__ float s_emid[128];
   __shared__ float s_eden[64];
   __shared__ float s_tail[64];
-  __shared__ float s_sums[4];
+  __shared__ __align__(16) float s_terms[10][128];
+  __shared__ float s_sums[10];
 
   const uint32_t q = blockIdx.x;
   const int t = threadIdx.x;
@@ -336,81 +337,93 @@ __global__ __launch_bounds__(128) void k_plan(PlanArgs a) {
   }
   if (t < 16) p->eden_codebook[t] = has_eden ? a.c.eden_codebook[t] : 0.0f;
   if (t < 27) p->pad[t] = 0.0f;
-
-  // sequential reductions, one chain per thread, in the reference's order
-  if (t == 0) {  // prefix_l1, prefix_sum (132-140)
-    float l1 = zero_acc(), sum = zero_acc();
-    for (int d = 0; d < 64; ++d) {
-      float v = s_q[d];
-      l1 += fabsf(v);
-      sum += v;
-    }
-    p->prefix_l1 = l1;
-    p->prefix_sum = sum;
-  } else if (t == 1) {  // eden_mean_ip (149-151)
-    float s = zero_acc();
-    if (has_eden)
-      for (int d = 0; d < 64; ++d) s += s_q[d] * a.eden_mean[d];
-    p->eden_mean_ip = s;
-    p->eden_inv_sqrt_d = a.c.inv_sqrt64;
-  } else if (t == 2) {  // eden_mid_mean_ip (167-169)
-    float s = zero_acc();
-    if (has_mid)
-      for (int d = 0; d < 128; ++d) s += s_q[64 + d] * a.mid_mean[d];
-    p->eden_mid_mean_ip = s;
-    p->eden_mid_inv_sqrt_d = a.c.inv_sqrt128;
-    p->eden_mid_codebook[0] = has_mid ? a.c.eden_mid_codebook[0] : 0.0f;
-    p->eden_mid_codebook[1] = has_mid ? a.c.eden_mid_codebook[1] : 0.0f;
-  } else if (t == 3) {  // q_tail_sq (203-206); loads batched ahead, adds in order
-    float s = zero_acc();
-    uint32_t i = kTailStart;
-    for (; i + 16 <= dims; i += 16) {
-      float v[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] = s_q[i + j];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) s += v[j] * v[j];
-    }
-    for (; i < dims; ++i) s += s_q[i] * s_q[i];
-    s_sums[0] = s;
-  } else if (t == 4) {  // q_mid_sq (209-212)
-    float s = zero_acc();
-    for (int i = 0; i < 128; ++i) {
-      float v = s_q[64 + i];
-      s += v * v;
-    }
-    s_sums[1] = s;
-  } else if (t == 5) {  // rabitq_base (182-186)
-    float base = zero_acc();
-    for (int d = 0; d < 128; ++d) base -= s_mid[d] * rs;
-    p->rabitq_base = base;
-    p->rabitq_scale = rs;
-  } else if (t == 6) {  // tail_fold_base, s4_abs_budget (226-233)
-    float base = zero_acc(), budget = zero_acc();
-    if (has_tail) {
-      for (int d = 0; d < 64; ++d) {
-        float pos = s_tail[d] * ts;
-        base -= pos;
-        budget += fabsf(pos);
-      }
-    }
-    p->tail_fold_base = base;
-    p->s4_abs_budget = budget;
-  } else if (t == 7) {  // EdenB1 base (scan.rs:528-531)
-    float base = zero_acc();
-    float c0 = has_mid ? a.c.eden_mid_codebook[0] : 0.0f;
-    for (int d = 0; d < 128; ++d) base += c0 * (s_emid[d] * a.c.inv_sqrt128);
-    p->eden_mid_base = base;
-  } else if (t == 8) {
+  if (t == 0) {
     p->dims = dims;
     p->prefix_codec = a.prefix_codec;
     p->mid_codec = a.mid_codec;
     p->has_tail_fold = has_tail ? 1u : 0u;
+    p->eden_inv_sqrt_d = a.c.inv_sqrt64;
+    p->eden_mid_inv_sqrt_d = a.c.inv_sqrt128;
+    p->eden_mid_codebook[0] = has_mid ? a.c.eden_mid_codebook[0] : 0.0f;
+    p->eden_mid_codebook[1] = has_mid ? a.c.eden_mid_codebook[1] : 0.0f;
+    p->rabitq_scale = rs;
+  }
+
+  // Sequential reductions (scan.rs:132-233, 528-531).  Each one is a chain of
+  // f32 additions in the reference's order; the terms (each a single rounded
+  // f32 operation of the reference, formed before its addition) are written
+  // to LDS in parallel, then lane c of wave 0 runs chain c (all in lockstep,
+  // 128 terms each) while wave 1 runs the long q_tail_sq chain.  `x -= y` is
+  // accumulated as `x + (-y)`, which IEEE-754 defines to be the same
+  // operation.  Past its length a chain adds +0.0, a no-op for a sum that
+  // starts at +0 (such a sum is never -0).
+  const int tail_n = has_tail ? (int)dims - kTailStart : 0;
+  {
+    const int i = t;  // 0..127
+    const float c0 = has_mid ? a.c.eden_mid_codebook[0] : 0.0f;
+    if (i < 64) {
+      const float v = s_q[i];
+      s_terms[0][i] = fabsf(v);                                         // prefix_l1
+      s_terms[1][i] = v;                                                // prefix_sum
+      s_terms[2][i] = has_eden ? v * a.eden_mean[i] : 0.0f;             // eden_mean_ip
+      const float pos = s_tail[i] * ts;
+      s_terms[7][i] = has_tail ? -pos : 0.0f;                           // tail_fold_base
+      s_terms[8][i] = has_tail ? fabsf(pos) : 0.0f;                     // s4_abs_budget
+    } else {
+      s_terms[0][i] = s_terms[1][i] = s_terms[2][i] = s_terms[7][i] = s_terms[8][i] = 0.0f;
+    }
+    const float mv = s_q[64 + i];
+    s_terms[3][i] = has_mid ? mv * a.mid_mean[i] : 0.0f;                // eden_mid_mean_ip
+    s_terms[5][i] = mv * mv;                                            // q_mid_sq
+    s_terms[6][i] = -(s_mid[i] * rs);                                   // rabitq_base
+    s_terms[9][i] = c0 * (s_emid[i] * a.c.inv_sqrt128);                 // eden_mid_base
+  }
+  __syncthreads();
+  // q_tail_sq terms, squared in place (s_q[192..] has no other reader now)
+  for (int i = t; i < tail_n; i += 128) s_q[kTailStart + i] = s_q[kTailStart + i] * s_q[kTailStart + i];
+  __syncthreads();
+  if (t < 10 && t != 4) {
+    // chains 0..9 except 4: 128 terms each (shorter chains are padded with +0)
+    const float4* src = reinterpret_cast<const float4*>(&s_terms[t][0]);
+    float acc = zero_acc();
+#pragma unroll 1
+    for (int i = 0; i < 32; i += 4) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = src[i + u];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc = ((((acc + v[u].x) + v[u].y) + v[u].z) + v[u].w);
+    }
+    s_sums[t] = acc;
+  } else if (t == 64) {
+    // chain 4, q_tail_sq: dims - 192 terms, on a wave of its own
+    const float* src = s_q + kTailStart;
+    float acc = zero_acc();
+    int i = 0;
+#pragma unroll 1
+    for (; i + 16 <= tail_n; i += 16) {
+      const float4* s4 = reinterpret_cast<const float4*>(src + i);
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = s4[u];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc = ((((acc + v[u].x) + v[u].y) + v[u].z) + v[u].w);
+    }
+    for (; i < tail_n; ++i) acc = acc + src[i];
+    s_sums[4] = acc;
   }
   __syncthreads();
   if (t == 0) {
-    float tail_sq = s_sums[0], mid_sq = s_sums[1];
-    float qt = sqrtf(tail_sq);
+    p->prefix_l1 = s_sums[0];
+    p->prefix_sum = s_sums[1];
+    p->eden_mean_ip = s_sums[2];
+    p->eden_mid_mean_ip = s_sums[3];
+    p->rabitq_base = s_sums[6];
+    p->tail_fold_base = s_sums[7];
+    p->s4_abs_budget = s_sums[8];
+    p->eden_mid_base = s_sums[9];
+    const float tail_sq = s_sums[4], mid_sq = s_sums[5];
+    const float qt = sqrtf(tail_sq);
     p->q_tail_norm = qt;
     p->q_mid_norm = sqrtf(mid_sq);
     p->q_after_prefix = sqrtf(mid_sq + tail_sq);
@@ -427,45 +440,59 @@ struct LaneBlock {
   uint32_t nib[8];
 };
 
+// L0Only (src/scan.rs:753-790): the sign plane alone (bit 3 of every level),
+// then the MinMax4 prefix formula whatever the codec.  accum_plane skips
+// weight == 0, and adding a zero weight never changes a sum that started at +0.
+__device__ __forceinline__ uint64_t eval_block_l0(uint64_t active, const LaneBlock& m,
+                                                 const CONST_AS mrl_query_plan* p, const ScanParams& sp,
+                                                 float tau, float& prefix_ip_out, float& score_out,
+                                                 uint64_t* masks) {
+  float cd = zero_acc();
+#pragma unroll
+  for (int d = 0; d < 64; ++d) {
+    float w = p->bit_weights[d][3];
+    bool bit = (m.nib[d >> 3] >> (4 * (d & 7) + 3)) & 1u;
+    float nx = cd + w;
+    cd = bit ? nx : cd;
+  }
+  float prefix_ip = cd * m.scale + m.offset * p->prefix_sum;
+  float x_rest = fmaxf(m.tail, 0.0f);
+  float ub = prefix_ip + sp.alpha * p->q_after_prefix * x_rest;
+  uint64_t surv = ballot(ub >= tau) & active;
+  masks[1] = masks[2] = masks[3] = masks[4] = surv;
+  prefix_ip_out = prefix_ip;
+  score_out = prefix_ip;
+  return surv;
+}
+
+// Byte offset of the LUT entry of dim 8j+i inside dim-group j's 16 entries:
+// level * 4.  From w2 = w << 2 and w3 = w >> 2, byte k of w2 holds level 2k
+// in bits 2..5 and byte k of w3 holds level 2k+1 there, so each offset is one
+// byte extract and mask.
+__device__ __forceinline__ uint32_t lut_off(uint32_t w2, uint32_t w3, int i) {
+  return (((i & 1) ? w3 : w2) >> (8 * (i >> 1))) & 0x3Cu;
+}
+
 // One (block, query) evaluation: the stage functions of src/scan.rs:453-634
-// composed as run_default_scan_kernel (654-691) / the L0Only branch (753-790).
-// Returns the pushed-survivor mask; score/prefix_ip are this lane's values.
+// composed as run_default_scan_kernel (654-691).  Returns the pushed-survivor
+// mask; score/prefix_ip are this lane's values.
 __device__ __forceinline__ uint64_t eval_block(const CONST_AS uint8_t* blk, uint64_t active,
                                               const LaneBlock& m, const float* __restrict__ lut,
                                               const CONST_AS mrl_query_plan* p, const ScanParams& sp,
                                               float tau, float& prefix_ip_out, float& score_out,
                                               uint64_t* masks) {
   const float alpha = sp.alpha;
-  if (sp.strata == MRL_STRATA_L0_ONLY) {
-    // sign plane = bit 3 of every level; accum_plane skips weight == 0, and
-    // adding a zero weight never changes a sum that started at +0.
-    float cd = zero_acc();
-#pragma unroll
-    for (int d = 0; d < 64; ++d) {
-      float w = p->bit_weights[d][3];
-      bool bit = (m.nib[d >> 3] >> (4 * (d & 7) + 3)) & 1u;
-      float nx = cd + w;
-      cd = bit ? nx : cd;
-    }
-    float prefix_ip = cd * m.scale + m.offset * p->prefix_sum;
-    float x_rest = fmaxf(m.tail, 0.0f);
-    float ub = prefix_ip + alpha * p->q_after_prefix * x_rest;
-    uint64_t surv = ballot(ub >= tau) & active;
-    masks[1] = masks[2] = masks[3] = masks[4] = surv;
-    prefix_ip_out = prefix_ip;
-    score_out = prefix_ip;
-    return surv;
-  }
-
   // Stage: 4-bit prefix IP (scan.rs:453-517).  lut[d*16 + level] holds the
   // reference's product codebook[level] * weight (or level * weight), so the
   // per-vector sum over d is the same sequence of f32 additions.
   float acc = zero_acc();
+  const char* lutb = reinterpret_cast<const char*>(lut);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const uint32_t w = m.nib[j];
+    const uint32_t w2 = m.nib[j] << 2, w3 = m.nib[j] >> 2;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc = acc + lut[(8 * j + i) * 16 + ((w >> (4 * i)) & 15u)];
+    for (int i = 0; i < 8; ++i)
+      acc = acc + *reinterpret_cast<const float*>(lutb + (8 * j + i) * 64 + lut_off(w2, w3, i));
   }
   const bool eden = p->prefix_codec == MRL_PREFIX_EDEN_PROD;
   float prefix_ip = eden ? p->eden_mean_ip + m.scale * acc : acc * m.scale + m.offset * p->prefix_sum;
@@ -533,13 +560,18 @@ __device__ __forceinline__ float bin_floor(uint32_t b) {
   return f;
 }
 
-// Per-lane raw inputs of one block, loaded one block ahead.
+// Per-lane raw inputs of one block, loaded one block ahead.  Lane l < 4 of
+// `hdr` holds header dword {0, 1, 4, 5}[l]: min_ts, max_ts and the two halves
+// of the tombstone mask.  t14 holds this lane's 24 bytes of the S1/S4 planes;
+// the scan reads those planes with scalar loads, the vector loads here only
+// bring them into L2 ahead of use.
 struct RawLane {
   uint16_t scale, offset, tail;
   uint32_t flags;
   uint32_t nib[8];
-  uint32_t hdr_lo, hdr_hi, min_ts, max_ts;  // header words (same value in every lane)
-  uint32_t touch;                           // xor of this lane's S1/S4 words (L2 warm-up only)
+  uint32_t hdr;
+  uint4 t1;
+  uint2 t4;
 };
 
 __device__ __forceinline__ RawLane load_raw(const uint8_t* blk) {
@@ -552,14 +584,16 @@ __device__ __forceinline__ RawLane load_raw(const uint8_t* blk) {
   const uint32_t* nibp = reinterpret_cast<const uint32_t*>(blk + kDevNibbles);
 #pragma unroll
   for (int j = 0; j < 8; ++j) r.nib[j] = nibp[64 * j + lane];
-  const uint32_t* h = reinterpret_cast<const uint32_t*>(blk);
-  r.min_ts = h[kOrigMinTs / 4];
-  r.max_ts = h[kOrigMaxTs / 4];
-  r.hdr_lo = h[kOrigTombstone / 4];
-  r.hdr_hi = h[kOrigTombstone / 4 + 1];
-  const uint32_t* s14 = reinterpret_cast<const uint32_t*>(blk + kDevS1);  // S1 then S4: 384 dwords
-  r.touch = s14[lane] ^ s14[lane + 64] ^ s14[lane + 128] ^ s14[lane + 192] ^ s14[lane + 256] ^ s14[lane + 320];
+  const uint32_t hw = lane < 2 ? lane : (lane < 4 ? lane + 2 : 0);
+  r.hdr = reinterpret_cast<const uint32_t*>(blk)[hw];
+  r.t1 = reinterpret_cast<const uint4*>(blk + kDevS1)[lane];
+  r.t4 = reinterpret_cast<const uint2*>(blk + kDevS4)[lane];
   return r;
+}
+
+// Keeps the L2 warm-up loads alive without using their values.
+__device__ __forceinline__ void retire_touch(const RawLane& r) {
+  asm volatile("" ::"v"(r.t1.x), "v"(r.t1.y), "v"(r.t1.z), "v"(r.t1.w), "v"(r.t4.x), "v"(r.t4.y));
 }
 
 // Appends of one workgroup are staged here per query and flushed at the end.
@@ -598,9 +632,41 @@ __device__ __forceinline__ void stage_append(Staging<QT>& st, const ScanArgs& a,
   }
 }
 
+// End of a scan workgroup: one global atomic per (workgroup, query) reserves
+// space in the query's segment, then the staged appends are copied out.
 template <int QT, bool DIAG>
+__device__ __forceinline__ void flush_appends(Staging<DIAG ? 1 : QT>& st, const ScanArgs& a, uint32_t q0, int nq,
+                                              uint32_t seg, const unsigned int* s_stats) {
+  if constexpr (!DIAG) {
+    const int tid = threadIdx.x;
+    __syncthreads();
+    if (tid < nq) {
+      const uint32_t n = min(st.n[tid], (uint32_t)Staging<QT>::kCap);
+      st.gbase[tid] = n ? atomicAdd(a.seg_count + (uint64_t)(q0 + tid) * a.nseg + seg, n) : 0u;
+    }
+    if (a.stats && tid < kStatCount && s_stats[tid]) atomicAdd(a.stats + tid, (unsigned long long)s_stats[tid]);
+    __syncthreads();
+    for (int qi = 0; qi < nq; ++qi) {
+      const uint32_t n = min(st.n[qi], (uint32_t)Staging<QT>::kCap);
+      const uint32_t g0 = st.gbase[qi];
+      const uint64_t sq = (uint64_t)(q0 + qi) * a.nseg + seg;
+      for (uint32_t i = tid; i < n; i += 256) {
+        const uint32_t g = g0 + i;
+        if (g < a.seg_cap) {
+          a.cand_score[sq * a.seg_cap + g] = st.score[qi][i];
+          a.cand_row[sq * a.seg_cap + g] = st.row[qi][i];
+        }
+      }
+    }
+  }
+}
+
+// One pass of the strata scan.  Workgroup = 4 waves; wave = one block at a
+// time (lane v = slot v), blocks pos = first + k * stride of the pass order.
+// QT queries share each block's loads.  L0 selects the L0Only stage set.
+template <int QT, bool DIAG, bool L0>
 __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
-  __shared__ float s_lut[QT * 1024];
+  __shared__ float s_lut[L0 ? 1 : QT * 1024];
   __shared__ float s_rho[256];
   __shared__ float s_midf[256];
   __shared__ unsigned int s_stats[kStatCount];
@@ -611,7 +677,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   const int nq = (int)min((uint32_t)QT, a.n_q - q0);
   if (tid < kStatCount) s_stats[tid] = 0u;
   if (tid < QT) s_app.n[tid] = 0u;
-  {
+  if (!L0) {
     const float4* src = reinterpret_cast<const float4*>(a.luts + (uint64_t)q0 * 1024);
     float4* dst = reinterpret_cast<float4*>(s_lut);
     for (int e = tid; e < nq * 256; e += 256) dst[e] = src[e];
@@ -633,31 +699,31 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     if (pos >= a.n_order) return 0u;
     return a.order ? a.order[pos] : pos;
   };
-  uint32_t ids = load_ids(0);
-  uint32_t k = 0;
-  uint32_t pos = first;
-  RawLane cur, nxt;
-  uint32_t b_cur = 0;
-  if (pos < a.n_order) {
+  // Every wave reaches the flush barrier below, also one with no block.
+  uint32_t ids = 0, b_cur = 0;
+  RawLane cur;
+  if (first < a.n_order) {
+    ids = load_ids(0);
     b_cur = (uint32_t)__builtin_amdgcn_readlane(ids, 0);
     cur = load_raw(a.idx + (uint64_t)b_cur * kBlockBytes);
   }
-  for (; pos < a.n_order; pos += stride, ++k) {
-    // prefetch the next block of this wave
-    const uint32_t npos = pos + stride;
-    uint32_t b_nxt = 0;
-    if (npos < a.n_order) {
-      if (((k + 1) & 63) == 0) ids = load_ids(k + 1);
-      b_nxt = (uint32_t)__builtin_amdgcn_readlane(ids, (k + 1) & 63);
-      nxt = load_raw(a.idx + (uint64_t)b_nxt * kBlockBytes);
-    }
+  uint32_t k = 0;
+  for (uint32_t pos = first; pos < a.n_order; pos += stride, ++k) {
+    // Prefetch the next block of this wave.  Past the end the current block
+    // is loaded again, so the loads are unconditional and the wait before
+    // this block's compute covers only this block's own loads.
+    const bool more = pos + stride < a.n_order;
+    if (more && ((k + 1) & 63) == 0) ids = load_ids(k + 1);
+    const uint32_t b_nxt = more ? (uint32_t)__builtin_amdgcn_readlane(ids, (k + 1) & 63) : b_cur;
+    const RawLane nxt = load_raw(a.idx + (uint64_t)b_nxt * kBlockBytes);
+
     const uint32_t b = b_cur;
     const CONST_AS uint8_t* blk = cview<uint8_t>(a.idx + (uint64_t)b * kBlockBytes);
-    // readfirstlane returns int: widen through uint32_t (no sign extension)
-    const uint32_t min_ts = (uint32_t)__builtin_amdgcn_readfirstlane(cur.min_ts);
-    const uint32_t max_ts = (uint32_t)__builtin_amdgcn_readfirstlane(cur.max_ts);
-    const uint64_t tomb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(cur.hdr_hi) << 32) |
-                          (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(cur.hdr_lo);
+    // readlane returns int: widen through uint32_t (no sign extension)
+    const uint32_t min_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 0);
+    const uint32_t max_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 1);
+    const uint64_t tomb = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(cur.hdr, 3) << 32) |
+                          (uint64_t)(uint32_t)__builtin_amdgcn_readlane(cur.hdr, 2);
     bool skip = false;
     if (sp.temporal) {  // scan.rs:719-730
       if (sp.has_lo && max_ts < sp.lo) skip = true;
@@ -695,12 +761,17 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
         uint64_t masks[5];
         masks[0] = active;
         float prefix_ip, score;
-        // Re-derive the block pointer opaquely per query so the plane-word
-        // loads stay inside this loop (hoisted, 192 words would not fit in SGPRs).
-        uint64_t blk_bits = (uint64_t)blk;
-        asm volatile("" : "+s"(blk_bits));
-        const CONST_AS uint8_t* blk_q = (const CONST_AS uint8_t*)blk_bits;
-        uint64_t surv = eval_block(blk_q, active, m, s_lut + qi * 1024, p, sp, tau, prefix_ip, score, masks);
+        uint64_t surv;
+        if constexpr (L0) {
+          surv = eval_block_l0(active, m, p, sp, tau, prefix_ip, score, masks);
+        } else {
+          // Re-derive the block pointer opaquely per query so the plane-word
+          // loads stay inside this loop (hoisted, 192 words would not fit in SGPRs).
+          uint64_t blk_bits = (uint64_t)blk;
+          asm volatile("" : "+s"(blk_bits));
+          const CONST_AS uint8_t* blk_q = (const CONST_AS uint8_t*)blk_bits;
+          surv = eval_block(blk_q, active, m, s_lut + qi * 1024, p, sp, tau, prefix_ip, score, masks);
+        }
         if constexpr (DIAG) {
           uint64_t o = ((uint64_t)q * a.n_blocks + b);
           if (lane < 5) {
@@ -726,33 +797,11 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
         }
       }
     }
-    // the touch loads only warm L2; consume them here, long after they landed
-    asm volatile("" ::"v"(cur.touch));
+    retire_touch(cur);
     cur = nxt;
     b_cur = b_nxt;
   }
-  if constexpr (!DIAG) {
-    // flush the staged appends: one global atomic per (workgroup, query)
-    __syncthreads();
-    if (tid < nq) {
-      const uint32_t n = min(s_app.n[tid], (uint32_t)Staging<QT>::kCap);
-      s_app.gbase[tid] = n ? atomicAdd(a.seg_count + (uint64_t)(q0 + tid) * a.nseg + seg, n) : 0u;
-    }
-    if (a.stats && tid < kStatCount && s_stats[tid]) atomicAdd(a.stats + tid, (unsigned long long)s_stats[tid]);
-    __syncthreads();
-    for (int qi = 0; qi < nq; ++qi) {
-      const uint32_t n = min(s_app.n[qi], (uint32_t)Staging<QT>::kCap);
-      const uint32_t g0 = s_app.gbase[qi];
-      const uint64_t sq = (uint64_t)(q0 + qi) * a.nseg + seg;
-      for (uint32_t i = tid; i < n; i += 256) {
-        const uint32_t g = g0 + i;
-        if (g < a.seg_cap) {
-          a.cand_score[sq * a.seg_cap + g] = s_app.score[qi][i];
-          a.cand_row[sq * a.seg_cap + g] = s_app.row[qi][i];
-        }
-      }
-    }
-  }
+  flush_appends<QT, DIAG>(s_app, a, q0, nq, seg, s_stats);
 }
 
 // ---------------------------------------------------------------------------
@@ -762,6 +811,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kSortCap = 8192;
 constexpr int kSelThreads = 1024;
+constexpr int kRankMax = 512;  // up to this many gathered entries are rank-sorted
 
 // One wave: bin holding the need-th largest entry of a descending scan over
 // `hist` (nb = 64 * per bins).  Returns the bin and the count strictly above
@@ -808,52 +858,71 @@ __device__ void find_boundary(const uint32_t* hist, uint32_t nb, uint32_t need, 
   }
 }
 
-// Flattened walk over a query's candidate segments: entry i of the
-// concatenation lives in segment s with off[s] <= i < off[s+1].  Each thread
-// walks i = tid, tid + blockDim.x, ... and keeps its segment cursor, loading
-// four entries ahead so the reads of different segments overlap.
+// Walk over a query's candidate segments in work items of kChunk entries of
+// one segment: item c lies in segment s with coff[s] <= c < coff[s+1].  A
+// wave takes items c = wave, wave + nwaves, ...; lane l loads entries
+// base + 64u + l (u < kWalk) of its item, all before any is used, so the
+// loads are coalesced and kWalk of them are in flight per lane.
+constexpr int kWalk = 16;
+constexpr uint32_t kChunk = 64u * kWalk;
 struct CandView {
   const float* sc;
   const uint32_t* rw;
   uint32_t seg_cap;
   uint32_t nseg;
-  const uint32_t* off;  // LDS, nseg + 1 prefix offsets
+  const uint32_t* off;   // LDS, nseg + 1 prefix offsets of the capped counts
+  const uint32_t* coff;  // LDS, nseg + 1 prefix offsets of the item counts
 };
 
 template <typename F>
 __device__ __forceinline__ void for_each_cand(const CandView& v, F&& fn) {
-  const uint32_t total = v.off[v.nseg];
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  const uint32_t items = v.coff[v.nseg];
   uint32_t s = 0;
-  for (uint32_t i0 = threadIdx.x; i0 < total; i0 += 4 * blockDim.x) {
-    float sc[4];
-    uint32_t idx[4];
-    bool ok[4];
+  for (uint32_t c = wave; c < items; c += nwaves) {
+    while (v.coff[s + 1] <= c) ++s;
+    const uint32_t base = (c - v.coff[s]) * kChunk;
+    const uint32_t cnt = v.off[s + 1] - v.off[s];
+    float sc[kWalk];
+    uint32_t idx[kWalk];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint32_t i = i0 + u * blockDim.x;
-      ok[u] = i < total;
-      if (ok[u]) {
-        while (v.off[s + 1] <= i) ++s;
-        idx[u] = s * v.seg_cap + (i - v.off[s]);
+    for (int u = 0; u < kWalk; ++u) {
+      const uint32_t i = base + 64u * u + lane;
+      idx[u] = 0xFFFFFFFFu;
+      if (i < cnt) {
+        idx[u] = s * v.seg_cap + i;
         sc[u] = v.sc[idx[u]];
       }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (ok[u]) fn(sc[u], idx[u]);
+    for (int u = 0; u < kWalk; ++u)
+      if (idx[u] != 0xFFFFFFFFu) fn(sc[u], idx[u]);
   }
 }
 
-// Prefix offsets of the (capped) segment counts into off[0..nseg].
-__device__ void seg_offsets(const uint32_t* seg_count, uint32_t nseg, uint32_t seg_cap, uint32_t* off) {
-  if (threadIdx.x == 0) {
-    uint32_t acc = 0;
-    for (uint32_t s = 0; s < nseg; ++s) {
+// Prefix offsets of the (capped) segment counts into off[0..nseg] and of
+// their item counts into coff[0..nseg]: the counters are loaded by nseg
+// threads at once, then summed in LDS.
+__device__ void seg_offsets(const uint32_t* seg_count, uint32_t nseg, uint32_t seg_cap, uint32_t* off,
+                            uint32_t* coff) {
+  const uint32_t t = threadIdx.x;
+  if (t < nseg) {
+    const uint32_t c = seg_count[t];
+    off[t + 1] = c < seg_cap ? c : seg_cap;
+  }
+  __syncthreads();
+  if (t == 0) {
+    uint32_t acc = 0, cacc = 0;
+    off[0] = 0;
+    coff[0] = 0;
+    for (uint32_t s = 1; s <= nseg; ++s) {
+      const uint32_t c = off[s];
+      acc += c;
+      cacc += (c + kChunk - 1) / kChunk;
       off[s] = acc;
-      const uint32_t c = seg_count[s];
-      acc += c < seg_cap ? c : seg_cap;
+      coff[s] = cacc;
     }
-    off[nseg] = acc;
   }
   __syncthreads();
 }
@@ -872,10 +941,11 @@ __device__ void build_hist(uint32_t* hist, const CandView& v) {
 __global__ __launch_bounds__(1024) void k_thresh(ThreshArgs a) {
   __shared__ uint32_t s_hist[kHistBins];
   __shared__ uint32_t s_off[kSegs + 1];
+  __shared__ uint32_t s_coff[kSegs + 1];
   __shared__ uint32_t s_out[2];
   const uint32_t q = blockIdx.x;
-  seg_offsets(a.seg_count + (uint64_t)q * a.nseg, a.nseg, a.seg_cap, s_off);
-  const CandView v{a.cand_score + (uint64_t)q * a.nseg * a.seg_cap, nullptr, a.seg_cap, a.nseg, s_off};
+  seg_offsets(a.seg_count + (uint64_t)q * a.nseg, a.nseg, a.seg_cap, s_off, s_coff);
+  const CandView v{a.cand_score + (uint64_t)q * a.nseg * a.seg_cap, nullptr, a.seg_cap, a.nseg, s_off, s_coff};
   build_hist(s_hist, v);
   find_boundary(s_hist, kHistBins, a.k, true, &s_out[0], &s_out[1]);
   __syncthreads();
@@ -916,6 +986,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   __shared__ uint32_t s_hist[2048];
   __shared__ uint32_t s_misc[8];
   __shared__ uint32_t s_off[kSegs + 1];
+  __shared__ uint32_t s_coff[kSegs + 1];
 
   const uint32_t q = blockIdx.x;
   const int tid = threadIdx.x;
@@ -924,9 +995,9 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   if (tid == 0) s_misc[7] = 0;
   __syncthreads();
   if (tid < (int)a.nseg && qcount[tid] > a.seg_cap) atomicOr(&s_misc[7], 2u);
-  seg_offsets(qcount, a.nseg, a.seg_cap, s_off);
+  seg_offsets(qcount, a.nseg, a.seg_cap, s_off, s_coff);
   const CandView v{a.cand_score + (uint64_t)q * a.nseg * a.seg_cap, a.cand_row + (uint64_t)q * a.nseg * a.seg_cap,
-                   a.seg_cap, a.nseg, s_off};
+                   a.seg_cap, a.nseg, s_off, s_coff};
   build_hist(s_hist, v);
   find_boundary(s_hist, kHistBins, K, true, &s_misc[0], &s_misc[1]);
   __syncthreads();
@@ -1001,18 +1072,29 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     m = s_misc[2];  // == K
     if (m > (uint32_t)kSortCap) m = kSortCap;
   }
-  int n2 = 1;
-  while ((uint32_t)n2 < m) n2 <<= 1;
-  for (int i = (int)m + tid; i < n2; i += kSelThreads) s_buf[i] = 0ull;
-  __syncthreads();
-  bitonic_desc(s_buf, n2);
-
   const uint32_t keep = m < K ? m : K;
-  for (uint32_t i = tid; i < keep; i += kSelThreads) {
-    const uint64_t c = s_buf[i];
+  auto emit = [&](uint32_t r, uint64_t c) {
     const uint32_t row = ~(uint32_t)c;
-    a.out_ids[(uint64_t)q * K + i] = ((uint64_t)(row >> 6) << 16) | (uint64_t)(row & 63u);
-    a.out_scores[(uint64_t)q * K + i] = key_score((uint32_t)(c >> 32));
+    a.out_ids[(uint64_t)q * K + r] = ((uint64_t)(row >> 6) << 16) | (uint64_t)(row & 63u);
+    a.out_scores[(uint64_t)q * K + r] = key_score((uint32_t)(c >> 32));
+  };
+  if (m <= (uint32_t)kRankMax) {
+    // Rank sort: the composite keys are distinct, so an entry's position in
+    // the descending order is the number of larger keys.  Every lane of a
+    // wave reads the same key j at the same time (an LDS broadcast).
+    for (uint32_t i = tid; i < m; i += kSelThreads) {
+      const uint64_t key = s_buf[i];
+      uint32_t r = 0;
+      for (uint32_t j = 0; j < m; ++j) r += s_buf[j] > key ? 1u : 0u;
+      if (r < keep) emit(r, key);
+    }
+  } else {
+    int n2 = 1;
+    while ((uint32_t)n2 < m) n2 <<= 1;
+    for (int i = (int)m + tid; i < n2; i += kSelThreads) s_buf[i] = 0ull;
+    __syncthreads();
+    bitonic_desc(s_buf, n2);
+    for (uint32_t i = tid; i < keep; i += kSelThreads) emit(i, s_buf[i]);
   }
   __syncthreads();
   // leave this query's pass state clean for the next scan
@@ -1059,12 +1141,23 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const Launch
   const uint32_t max_grid = tiles >= 64 ? 256 : (tiles >= 8 ? 1024 : 2048);
   if (grid > max_grid) grid = max_grid;
   dim3 g(grid, tiles);
+  const bool l0 = a.sp.strata == MRL_STRATA_L0_ONLY;
   if (qt == 8) {
-    if (diag) launch(k_scan<8, true>, g, dim3(256), s, ev, a);
-    else launch(k_scan<8, false>, g, dim3(256), s, ev, a);
+    if (l0) {
+      if (diag) launch(k_scan<8, true, true>, g, dim3(256), s, ev, a);
+      else launch(k_scan<8, false, true>, g, dim3(256), s, ev, a);
+    } else {
+      if (diag) launch(k_scan<8, true, false>, g, dim3(256), s, ev, a);
+      else launch(k_scan<8, false, false>, g, dim3(256), s, ev, a);
+    }
   } else {
-    if (diag) launch(k_scan<1, true>, g, dim3(256), s, ev, a);
-    else launch(k_scan<1, false>, g, dim3(256), s, ev, a);
+    if (l0) {
+      if (diag) launch(k_scan<1, true, true>, g, dim3(256), s, ev, a);
+      else launch(k_scan<1, false, true>, g, dim3(256), s, ev, a);
+    } else {
+      if (diag) launch(k_scan<1, true, false>, g, dim3(256), s, ev, a);
+      else launch(k_scan<1, false, false>, g, dim3(256), s, ev, a);
+    }
   }
   return hipGetLastError();
 }
