@@ -77,12 +77,16 @@ struct Chunk8 {
   float w[8];
 };
 
-__device__ __forceinline__ Chunk8 load_chunk8(const CONST_AS uint64_t* pl, const CONST_AS float* w) {
+// Plane words come from the block (scalar loads); weights from the LDS copy
+// of the query's plan (every lane reads the same address).
+__device__ __forceinline__ Chunk8 load_chunk8(const CONST_AS uint64_t* pl, const float* w) {
   Chunk8 c;
 #pragma unroll
   for (int i = 0; i < 8; ++i) c.p[i] = pl[i];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) c.w[i] = w[i];
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  const float4 a = w4[0], b = w4[1];
+  c.w[0] = a.x; c.w[1] = a.y; c.w[2] = a.z; c.w[3] = a.w;
+  c.w[4] = b.x; c.w[5] = b.y; c.w[6] = b.z; c.w[7] = b.w;
   return c;
 }
 
@@ -107,18 +111,18 @@ __device__ __forceinline__ float masked_add8(float s, uint64_t m, const Chunk8& 
       "s_mov_b64 exec, %[sv]"
       : [s] "+v"(s), [sv] "=&s"(sv), [mm] "=&s"(mm)
       : [m] "s"(m), [p0] "s"(c.p[0]), [p1] "s"(c.p[1]), [p2] "s"(c.p[2]), [p3] "s"(c.p[3]), [p4] "s"(c.p[4]),
-        [p5] "s"(c.p[5]), [p6] "s"(c.p[6]), [p7] "s"(c.p[7]), [w0] "s"(c.w[0]), [w1] "s"(c.w[1]),
-        [w2] "s"(c.w[2]), [w3] "s"(c.w[3]), [w4] "s"(c.w[4]), [w5] "s"(c.w[5]), [w6] "s"(c.w[6]),
-        [w7] "s"(c.w[7])
+        [p5] "s"(c.p[5]), [p6] "s"(c.p[6]), [p7] "s"(c.p[7]), [w0] "v"(c.w[0]), [w1] "v"(c.w[1]),
+        [w2] "v"(c.w[2]), [w3] "v"(c.w[3]), [w4] "v"(c.w[4]), [w5] "v"(c.w[5]), [w6] "v"(c.w[6]),
+        [w7] "v"(c.w[7])
       : "scc");
   return s;
 }
 
-// Sum over NCHUNK*8 dims with the next chunk's scalar loads issued before
-// the current chunk's adds.
+// Sum over NCHUNK*8 dims with the next chunk's loads issued before the
+// current chunk's adds.
 template <int NCHUNK>
 __device__ __forceinline__ float masked_accumulate(float s, uint64_t m, const CONST_AS uint64_t* planes,
-                                                   const CONST_AS float* w) {
+                                                   const float* w) {
   Chunk8 cur = load_chunk8(planes, w);
 #pragma unroll
   for (int c = 0; c < NCHUNK; ++c) {
@@ -469,8 +473,28 @@ __device__ __forceinline__ uint64_t eval_block_l0(uint64_t active, const LaneBlo
 // level * 4.  From w2 = w << 2 and w3 = w >> 2, byte k of w2 holds level 2k
 // in bits 2..5 and byte k of w3 holds level 2k+1 there, so each offset is one
 // byte extract and mask.
-__device__ __forceinline__ uint32_t lut_off(uint32_t w2, uint32_t w3, int i) {
-  return (((i & 1) ? w3 : w2) >> (8 * (i >> 1))) & 0x3Cu;
+// byte B of w, masked with m: one SDWA v_and_b32 (byte select of src0).
+template <int B>
+__device__ __forceinline__ uint32_t and_byte(uint32_t w, uint32_t m) {
+  uint32_t r;
+  if constexpr (B == 0)
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
+        : "=v"(r) : "v"(w), "v"(m));
+  else if constexpr (B == 1)
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:DWORD"
+        : "=v"(r) : "v"(w), "v"(m));
+  else if constexpr (B == 2)
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2 src1_sel:DWORD"
+        : "=v"(r) : "v"(w), "v"(m));
+  else
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3 src1_sel:DWORD"
+        : "=v"(r) : "v"(w), "v"(m));
+  return r;
+}
+
+template <int I>
+__device__ __forceinline__ uint32_t lut_off(uint32_t w2, uint32_t w3, uint32_t m) {
+  return and_byte<I / 2>((I & 1) ? w3 : w2, m);
 }
 
 // One (block, query) evaluation: the stage functions of src/scan.rs:453-634
@@ -478,6 +502,7 @@ __device__ __forceinline__ uint32_t lut_off(uint32_t w2, uint32_t w3, int i) {
 // mask; score/prefix_ip are this lane's values.
 __device__ __forceinline__ uint64_t eval_block(const CONST_AS uint8_t* blk, uint64_t active,
                                               const LaneBlock& m, const float* __restrict__ lut,
+                                              const float* __restrict__ w_mid, const float* __restrict__ w_tail,
                                               const CONST_AS mrl_query_plan* p, const ScanParams& sp,
                                               float tau, float& prefix_ip_out, float& score_out,
                                               uint64_t* masks) {
@@ -487,12 +512,19 @@ __device__ __forceinline__ uint64_t eval_block(const CONST_AS uint8_t* blk, uint
   // per-vector sum over d is the same sequence of f32 additions.
   float acc = zero_acc();
   const char* lutb = reinterpret_cast<const char*>(lut);
+  const uint32_t mask = 0x3Cu;
+  auto ld = [&](int d, uint32_t off) { return *reinterpret_cast<const float*>(lutb + d * 64 + off); };
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint32_t w2 = m.nib[j] << 2, w3 = m.nib[j] >> 2;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      acc = acc + *reinterpret_cast<const float*>(lutb + (8 * j + i) * 64 + lut_off(w2, w3, i));
+    acc = acc + ld(8 * j + 0, lut_off<0>(w2, w3, mask));
+    acc = acc + ld(8 * j + 1, lut_off<1>(w2, w3, mask));
+    acc = acc + ld(8 * j + 2, lut_off<2>(w2, w3, mask));
+    acc = acc + ld(8 * j + 3, lut_off<3>(w2, w3, mask));
+    acc = acc + ld(8 * j + 4, lut_off<4>(w2, w3, mask));
+    acc = acc + ld(8 * j + 5, lut_off<5>(w2, w3, mask));
+    acc = acc + ld(8 * j + 6, lut_off<6>(w2, w3, mask));
+    acc = acc + ld(8 * j + 7, lut_off<7>(w2, w3, mask));
   }
   const bool eden = p->prefix_codec == MRL_PREFIX_EDEN_PROD;
   float prefix_ip = eden ? p->eden_mean_ip + m.scale * acc : acc * m.scale + m.offset * p->prefix_sum;
@@ -508,8 +540,7 @@ __device__ __forceinline__ uint64_t eval_block(const CONST_AS uint8_t* blk, uint
     // Stage: mid-band 1-bit IP (scan.rs:520-569), set bits added in d order.
     const CONST_AS uint64_t* s1p = (const CONST_AS uint64_t*)(blk + kDevS1);
     const bool b1 = p->mid_codec == MRL_MID_EDEN_B1;
-    const CONST_AS float* w2 = b1 ? p->eden_mid_deltas : p->rabitq_weights2;
-    float s1 = masked_accumulate<16>(b1 ? p->eden_mid_base : p->rabitq_base, surv, s1p, w2);
+    float s1 = masked_accumulate<16>(b1 ? p->eden_mid_base : p->rabitq_base, surv, s1p, w_mid);
     score = b1 ? score + (p->eden_mid_mean_ip + m.offset * s1) : score + s1 * m.mid_n;
     // Stage: post-S1 CS (scan.rs:572-584)
     float ub2 = score + alpha * p->q_after_s1 * m.high_n;
@@ -528,7 +559,7 @@ __device__ __forceinline__ uint64_t eval_block(const CONST_AS uint8_t* blk, uint
     // Stage: folded-tail 1-bit IP (scan.rs:610-634)
     if (surv != 0 && p->has_tail_fold) {
       const CONST_AS uint64_t* s4p = (const CONST_AS uint64_t*)(blk + kDevS4);
-      float s4 = masked_accumulate<8>(p->tail_fold_base, surv, s4p, p->tail_fold_weights2);
+      float s4 = masked_accumulate<8>(p->tail_fold_base, surv, s4p, w_tail);
       score = score + s4 * hn * w_s4;
     }
   }
@@ -607,7 +638,8 @@ struct Staging {
 };
 
 // Appends (score, row) for the lanes in pm: into the LDS staging area while
-// it has room, directly into the query's global segment otherwise.
+// it has room, directly into the query's global segment otherwise (one
+// global atomic per wave for the lanes that overflow).
 template <int QT>
 __device__ __forceinline__ void stage_append(Staging<QT>& st, const ScanArgs& a, int qi, uint32_t q, uint32_t seg,
                                              uint64_t pm, float score, uint32_t row) {
@@ -616,18 +648,23 @@ __device__ __forceinline__ void stage_append(Staging<QT>& st, const ScanArgs& a,
   uint32_t base = 0;
   if (lane == lead) base = atomicAdd(&st.n[qi], (uint32_t)__popcll(pm));
   base = __shfl(base, (int)lead);
-  if ((pm >> lane) & 1ull) {
-    const uint32_t slot = base + lanes_below(pm);
-    if (slot < (uint32_t)Staging<QT>::kCap) {
-      st.score[qi][slot] = score;
-      st.row[qi][slot] = row;
-    } else {
-      const uint64_t sq = (uint64_t)q * a.nseg + seg;
-      const uint32_t g = atomicAdd(a.seg_count + sq, 1u);
-      if (g < a.seg_cap) {
-        a.cand_score[sq * a.seg_cap + g] = score;
-        a.cand_row[sq * a.seg_cap + g] = row;
-      }
+  const bool mine = (pm >> lane) & 1ull;
+  const uint32_t slot = base + lanes_below(pm);
+  if (mine && slot < (uint32_t)Staging<QT>::kCap) {
+    st.score[qi][slot] = score;
+    st.row[qi][slot] = row;
+  }
+  const uint64_t om = ballot(mine && slot >= (uint32_t)Staging<QT>::kCap);
+  if (om != 0) {
+    const uint64_t sq = (uint64_t)q * a.nseg + seg;
+    const uint32_t olead = (uint32_t)__ffsll((long long)om) - 1;
+    uint32_t g0 = 0;
+    if (lane == olead) g0 = atomicAdd(a.seg_count + sq, (uint32_t)__popcll(om));
+    g0 = __shfl(g0, (int)olead);
+    const uint32_t g = g0 + lanes_below(om);
+    if (((om >> lane) & 1ull) && g < a.seg_cap) {
+      a.cand_score[sq * a.seg_cap + g] = score;
+      a.cand_row[sq * a.seg_cap + g] = row;
     }
   }
 }
@@ -666,7 +703,9 @@ __device__ __forceinline__ void flush_appends(Staging<DIAG ? 1 : QT>& st, const 
 // QT queries share each block's loads.  L0 selects the L0Only stage set.
 template <int QT, bool DIAG, bool L0>
 __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
-  __shared__ float s_lut[L0 ? 1 : QT * 1024];
+  __shared__ __align__(16) float s_lut[L0 ? 1 : QT * 1024];
+  __shared__ __align__(16) float s_wmid[L0 ? 1 : QT * 128];  // S1 weights: rabitq_weights2 or eden_mid_deltas
+  __shared__ __align__(16) float s_wtail[L0 ? 1 : QT * 64];  // S4 weights: tail_fold_weights2
   __shared__ float s_rho[256];
   __shared__ float s_midf[256];
   __shared__ unsigned int s_stats[kStatCount];
@@ -681,6 +720,12 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     const float4* src = reinterpret_cast<const float4*>(a.luts + (uint64_t)q0 * 1024);
     float4* dst = reinterpret_cast<float4*>(s_lut);
     for (int e = tid; e < nq * 256; e += 256) dst[e] = src[e];
+    for (int e = tid; e < nq * 192; e += 256) {
+      const int qi = e / 192, d = e % 192;
+      const mrl_query_plan* pq = a.plans + q0 + qi;
+      if (d < 128) s_wmid[qi * 128 + d] = pq->mid_codec == MRL_MID_EDEN_B1 ? pq->eden_mid_deltas[d] : pq->rabitq_weights2[d];
+      else s_wtail[qi * 64 + d - 128] = pq->tail_fold_weights2[d - 128];
+    }
   }
   s_rho[tid] = a.flag_tabs[tid];
   s_midf[tid] = a.flag_tabs[256 + tid];
@@ -770,7 +815,8 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
           uint64_t blk_bits = (uint64_t)blk;
           asm volatile("" : "+s"(blk_bits));
           const CONST_AS uint8_t* blk_q = (const CONST_AS uint8_t*)blk_bits;
-          surv = eval_block(blk_q, active, m, s_lut + qi * 1024, p, sp, tau, prefix_ip, score, masks);
+          surv = eval_block(blk_q, active, m, s_lut + qi * 1024, s_wmid + qi * 128, s_wtail + qi * 64, p, sp, tau,
+                            prefix_ip, score, masks);
         }
         if constexpr (DIAG) {
           uint64_t o = ((uint64_t)q * a.n_blocks + b);
@@ -863,7 +909,7 @@ __device__ void find_boundary(const uint32_t* hist, uint32_t nb, uint32_t need, 
 // wave takes items c = wave, wave + nwaves, ...; lane l loads entries
 // base + 64u + l (u < kWalk) of its item, all before any is used, so the
 // loads are coalesced and kWalk of them are in flight per lane.
-constexpr int kWalk = 16;
+constexpr int kWalk = 32;
 constexpr uint32_t kChunk = 64u * kWalk;
 struct CandView {
   const float* sc;
@@ -1003,18 +1049,25 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   __syncthreads();
   const float floor_t = bin_floor(s_misc[0]);
 
-  // entries >= floor_t, as (score key, row) composites
+  // entries >= floor_t as (score key, candidate index); the rows of the
+  // gathered entries are then loaded all at once
   if (tid == 0) s_misc[2] = 0;
   __syncthreads();
   for_each_cand(v, [&](float sc, uint32_t idx) {
     if (sc >= floor_t) {
       const uint32_t slot = atomicAdd(&s_misc[2], 1u);
-      if (slot < (uint32_t)kSortCap) s_buf[slot] = composite(score_key(sc), v.rw[idx]);
+      if (slot < (uint32_t)kSortCap) s_buf[slot] = ((uint64_t)score_key(sc) << 32) | idx;
     }
   });
   __syncthreads();
   uint32_t m = s_misc[2];
-  if (m > (uint32_t)kSortCap) {
+  if (m <= (uint32_t)kSortCap) {
+    for (uint32_t i = tid; i < m; i += kSelThreads) {
+      const uint64_t c = s_buf[i];
+      s_buf[i] = composite((uint32_t)(c >> 32), v.rw[(uint32_t)c]);
+    }
+    __syncthreads();
+  } else {
     // Radix select: the exact K-th key among entries >= floor_t, then the
     // smallest rows among its exact ties.
     const int shifts[3] = {21, 10, 0};
@@ -1084,8 +1137,15 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     // wave reads the same key j at the same time (an LDS broadcast).
     for (uint32_t i = tid; i < m; i += kSelThreads) {
       const uint64_t key = s_buf[i];
-      uint32_t r = 0;
-      for (uint32_t j = 0; j < m; ++j) r += s_buf[j] > key ? 1u : 0u;
+      uint32_t r = 0, j = 0;
+      for (; j + 8 <= m; j += 8) {
+        uint64_t k8[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) k8[u] = s_buf[j + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) r += k8[u] > key ? 1u : 0u;
+      }
+      for (; j < m; ++j) r += s_buf[j] > key ? 1u : 0u;
       if (r < keep) emit(r, key);
     }
   } else {
@@ -1133,12 +1193,28 @@ hipError_t launch_plan(const PlanArgs& a, hipStream_t s, const LaunchEvents& ev)
 
 int scan_query_tile(uint32_t n_q) { return n_q >= 8 ? 8 : 1; }
 
+// Workgroups of `kernel` resident at once on the current device.
+template <typename K>
+static uint32_t resident_groups(K kernel) {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1024;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 1024;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu < 1) per_cu = 1;
+  return (uint32_t)(cus * per_cu);
+}
+
 hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev) {
   if (a.n_order == 0 || a.n_q == 0) return hipSuccess;
   const int qt = scan_query_tile(a.n_q);
   const uint32_t tiles = (a.n_q + qt - 1) / qt;
+  // One round of resident workgroups (each wave then loops over blocks),
+  // but at least one workgroup per candidate segment of a query.
+  static const uint32_t res1 = resident_groups(k_scan<1, false, false>);
+  static const uint32_t res8 = resident_groups(k_scan<8, false, false>);
+  const uint32_t res = qt == 8 ? res8 : res1;
   uint32_t grid = (a.n_order + 3) / 4;
-  const uint32_t max_grid = tiles >= 64 ? 256 : (tiles >= 8 ? 1024 : 2048);
+  uint32_t max_grid = res / tiles;
+  if (max_grid < a.nseg) max_grid = a.nseg;
   if (grid > max_grid) grid = max_grid;
   dim3 g(grid, tiles);
   const bool l0 = a.sp.strata == MRL_STRATA_L0_ONLY;
