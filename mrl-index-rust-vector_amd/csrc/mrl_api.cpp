@@ -43,9 +43,16 @@ extern "C" size_t mrl_query_plan_size(void) { return sizeof(mrl_query_plan); }
 // ---------------------------------------------------------------------------
 // objects
 // ---------------------------------------------------------------------------
+// Pass p scans blocks b = pos << shift (pos < n_pos) that no earlier pass
+// scanned (b not a multiple of 1 << prev_shift); n_new of them.
+struct Pass {
+  uint32_t shift;
+  int32_t prev_shift;
+  uint32_t n_pos;
+  uint32_t n_new;
+};
 struct LevelPlan {
-  uint32_t* d_order = nullptr;
-  std::vector<std::pair<uint32_t, uint32_t>> passes;  // (start, size) into d_order
+  std::vector<Pass> passes;
 };
 
 struct ProfRecord {
@@ -375,19 +382,18 @@ extern "C" void mrl_index_destroy(mrl_index* index) {
   if (!index) return;
   (void)hipSetDevice(index->ctx->device);
   (void)hipStreamSynchronize(index->ctx->stream);
-  for (auto& kv : index->levels) dev_free(kv.second.d_order);
   dev_free(index->d_blocks);
   delete index;
 }
 
-// Pass schedule for one K.  Pass 0 scores a spread sample of up to 256 blocks
-// with no threshold; every later pass prunes against the K-th best score of
-// all earlier passes (a lower bound of the final K-th score, so pruning and
-// filtering stay exact) and grows the covered set by at most
-// (16384/K - 1)x, which keeps each pass near 16K candidates per query.  The
-// last pass covers the remaining blocks in ascending order.
-static const uint32_t kPassTarget = 16384;
-
+// Pass schedule for one K.  Pass 0 scores every S0-th block (S0 the
+// smallest power of two leaving at most 256 blocks) with no threshold; pass p
+// scores the multiples of S0 / r^p not scored before, pruning against the K-th
+// best score of all earlier passes (a lower bound of the final K-th score, so
+// pruning and filtering stay exact); the last pass has stride 1.  r is the
+// power of two nearest 16384/K - 1 (at least 2): each pass then grows the
+// scored set so that about 16K candidates per query pass the threshold.
+// Block ids are arithmetic, so a pass needs no index list.
 static int get_levels(mrl_index* ix, uint32_t K, LevelPlan** out) {
   auto it = ix->levels.find(K);
   if (it != ix->levels.end()) {
@@ -396,52 +402,23 @@ static int get_levels(mrl_index* ix, uint32_t K, LevelPlan** out) {
   }
   const uint64_t B = ix->n_blocks;
   LevelPlan lp;
-  std::vector<uint32_t> sizes;
-  uint64_t first = std::min<uint64_t>(B, (kPassTarget + 63) / 64);
-  sizes.push_back((uint32_t)first);
-  uint64_t cum = first;
-  const uint64_t ratio = std::max<uint64_t>(1, kPassTarget / std::max<uint32_t>(K, 1) - 1);
-  while (cum < B) {
-    uint64_t nxt = std::min<uint64_t>(B - cum, cum * ratio);
-    sizes.push_back((uint32_t)nxt);
-    cum += nxt;
-  }
-  std::vector<uint32_t> order(B);
-  const uint64_t sampled = B - (sizes.size() > 1 ? sizes.back() : 0);
-  if (sizes.size() == 1) {
-    for (uint64_t i = 0; i < B; ++i) order[i] = (uint32_t)i;
-  } else {
-    uint64_t step = (uint64_t)((double)B * 0.6180339887498949) | 1;
-    auto gcd = [](uint64_t a, uint64_t b) {
-      while (b) {
-        uint64_t t = a % b;
-        a = b;
-        b = t;
-      }
-      return a;
-    };
-    while (gcd(step, B) != 1) ++step;
-    std::vector<uint8_t> used(B, 0);
-    for (uint64_t i = 0; i < sampled; ++i) {
-      uint64_t b = (i * step) % B;
-      order[i] = (uint32_t)b;
-      used[b] = 1;
-    }
-    uint64_t w = sampled;
-    for (uint64_t b = 0; b < B; ++b)
-      if (!used[b]) order[w++] = (uint32_t)b;
-  }
-  uint32_t start = 0, maxsz = 0;
-  for (uint32_t s : sizes) {
-    lp.passes.push_back({start, s});
-    start += s;
-    maxsz = std::max(maxsz, s);
-  }
-  (void)maxsz;
-  if (B) {
-    if (hipMalloc(&lp.d_order, B * sizeof(uint32_t)) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "order");
-    if (hipMemcpy(lp.d_order, order.data(), B * sizeof(uint32_t), hipMemcpyHostToDevice) != hipSuccess)
-      return fail(MRL_ERR_HIP, "order upload");
+  uint32_t s0 = 0;
+  while (((B + (1ull << s0) - 1) >> s0) > 256) ++s0;
+  const uint64_t want = std::max<uint64_t>(2, 16384 / std::max<uint32_t>(K, 1) - 1);
+  uint32_t lr = 1;
+  while ((1ull << (lr + 1)) <= want) ++lr;
+  if ((1ull << (lr + 1)) - want < want - (1ull << lr)) ++lr;  // nearest power of two
+  int32_t prev = -1;
+  for (int32_t sh = (int32_t)s0;; sh -= (int32_t)lr) {
+    if (sh < 0) sh = 0;
+    Pass p;
+    p.shift = (uint32_t)sh;
+    p.prev_shift = prev;
+    p.n_pos = (uint32_t)((B + (1ull << sh) - 1) >> sh);
+    p.n_new = p.n_pos - (prev < 0 ? 0u : (uint32_t)((B + (1ull << prev) - 1) >> prev));
+    lp.passes.push_back(p);
+    prev = sh;
+    if (sh == 0) break;
   }
   auto res = ix->levels.emplace(K, std::move(lp));
   *out = &res.first->second;
@@ -724,8 +701,9 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
     ScanArgs a{};
     a.idx = ix->d_blocks;
     a.n_blocks = ix->n_blocks;
-    a.order = lp.d_order ? lp.d_order + lp.passes[pi].first : nullptr;
-    a.n_order = lp.passes[pi].second;
+    a.n_pos = lp.passes[pi].n_pos;
+    a.shift = lp.passes[pi].shift;
+    a.prev_shift = lp.passes[pi].prev_shift;
     a.plans = plans->d_plans + plans_first;
     a.luts = plans->d_luts + (size_t)plans_first * 1024;
     a.n_q = n_q;
@@ -740,13 +718,13 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
     a.stats = stats;
     a.err = pb.err;
     {
-      ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)pi, a.n_order, n_q);
+      ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)pi, lp.passes[pi].n_new, n_q);
       HIP_TRY(launch_scan(a, false, s, ps.ev()));
-      ps.commit(a.n_order != 0 && n_q != 0);
+      ps.commit(a.n_pos != 0 && n_q != 0);
     }
     if (pi + 1 < lp.passes.size()) {
       ThreshArgs ta{pb.cand_score, pb.seg_count, pb.nseg, pb.seg_cap, pb.tau, K, n_q};
-      ProfScope ps(ctx, MRL_KERNEL_THRESH, (int)pi, a.n_order, n_q);
+      ProfScope ps(ctx, MRL_KERNEL_THRESH, (int)pi, lp.passes[pi].n_new, n_q);
       HIP_TRY(launch_thresh(ta, s, ps.ev()));
       ps.commit(n_q != 0);
     }
@@ -833,8 +811,7 @@ static int dense_rerun(mrl_ctx* ctx, mrl_results* r, uint32_t q) {
     return fail(MRL_ERR_OUT_OF_MEMORY, "dense fallback buffers");
   }
   LevelPlan lp;
-  lp.passes.push_back({0u, (uint32_t)ix->n_blocks});
-  lp.d_order = nullptr;
+  lp.passes.push_back(Pass{0u, -1, (uint32_t)ix->n_blocks, (uint32_t)ix->n_blocks});
   PassBuffers pb;
   pb.cand_score = sc;
   pb.cand_row = rw;
@@ -949,8 +926,9 @@ extern "C" int mrl_scan_fixed_tau(mrl_ctx* ctx, const mrl_index* index, const mr
   ScanArgs a{};
   a.idx = index->d_blocks;
   a.n_blocks = B;
-  a.order = nullptr;
-  a.n_order = (uint32_t)B;
+  a.n_pos = (uint32_t)B;
+  a.shift = 0;
+  a.prev_shift = -1;
   a.plans = plans->d_plans;
   a.luts = plans->d_luts;
   a.n_q = (uint32_t)nq;

@@ -105,8 +105,11 @@ constexpr int kHistBins = 2048;
 struct ScanArgs {
   const uint8_t* idx;          // device-layout blocks
   uint64_t n_blocks;
-  const uint32_t* order;       // block ids of this pass (null: 0..n_order-1)
-  uint32_t n_order;
+  // Blocks of this pass: b = pos << shift for pos < n_pos, except those an
+  // earlier pass covered (prev_shift >= 0 and b a multiple of 1 << prev_shift).
+  uint32_t n_pos;
+  uint32_t shift;
+  int32_t prev_shift;
   const mrl_query_plan* plans;
   const float* luts;           // [n_q][64][16] prefix LUT (codebook[level] * weight[d])
   uint32_t n_q;

@@ -714,6 +714,22 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   const int tid = threadIdx.x;
   const uint32_t q0 = blockIdx.y * QT;
   const int nq = (int)min((uint32_t)QT, a.n_q - q0);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t lane = lane_id();
+
+  // This wave's blocks: positions pos = first + k * stride of the pass.  The
+  // stride is odd (one wave of the grid stays idle), so the positions of a
+  // wave run through every residue modulo the power-of-two pass ratio and the
+  // blocks an earlier pass already scored are spread evenly over the waves.
+  // The first block's loads are issued before the LDS set-up below.
+  const uint32_t stride = gridDim.x * 4 - 1;
+  const uint32_t first = blockIdx.x * 4 + wave;
+  const uint32_t cover = a.prev_shift >= 0 ? (1u << a.prev_shift) - 1u : 0u;
+  uint32_t b_cur = first << a.shift;
+  RawLane cur;
+  const uint32_t n_pos = first < stride ? a.n_pos : 0u;
+  if (first < n_pos) cur = load_raw(a.idx + (uint64_t)b_cur * kBlockBytes);
+
   if (tid < kStatCount) s_stats[tid] = 0u;
   if (tid < QT) s_app.n[tid] = 0u;
   if (!L0) {
@@ -731,35 +747,15 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   s_midf[tid] = a.flag_tabs[256 + tid];
   __syncthreads();
 
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t lane = lane_id();
   const ScanParams sp = a.sp;
   const uint32_t seg = blockIdx.x % a.nseg;
 
-  // Block ids for this wave's iterations k (pos = first + k*stride), 64 at a time.
-  const uint32_t stride = gridDim.x * 4;
-  const uint32_t first = blockIdx.x * 4 + wave;
-  auto load_ids = [&](uint32_t k0) -> uint32_t {
-    const uint32_t pos = first + (k0 + lane) * stride;
-    if (pos >= a.n_order) return 0u;
-    return a.order ? a.order[pos] : pos;
-  };
   // Every wave reaches the flush barrier below, also one with no block.
-  uint32_t ids = 0, b_cur = 0;
-  RawLane cur;
-  if (first < a.n_order) {
-    ids = load_ids(0);
-    b_cur = (uint32_t)__builtin_amdgcn_readlane(ids, 0);
-    cur = load_raw(a.idx + (uint64_t)b_cur * kBlockBytes);
-  }
-  uint32_t k = 0;
-  for (uint32_t pos = first; pos < a.n_order; pos += stride, ++k) {
+  for (uint32_t pos = first; pos < n_pos; pos += stride) {
     // Prefetch the next block of this wave.  Past the end the current block
     // is loaded again, so the loads are unconditional and the wait before
     // this block's compute covers only this block's own loads.
-    const bool more = pos + stride < a.n_order;
-    if (more && ((k + 1) & 63) == 0) ids = load_ids(k + 1);
-    const uint32_t b_nxt = more ? (uint32_t)__builtin_amdgcn_readlane(ids, (k + 1) & 63) : b_cur;
+    const uint32_t b_nxt = pos + stride < n_pos ? (pos + stride) << a.shift : b_cur;
     const RawLane nxt = load_raw(a.idx + (uint64_t)b_nxt * kBlockBytes);
 
     const uint32_t b = b_cur;
@@ -775,7 +771,10 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
       if (sp.has_hi && min_ts > sp.hi) skip = true;
     }
     const uint64_t active = ~tomb;
-    if (skip || active == 0) {
+    const bool covered = a.prev_shift >= 0 && (b & cover) == 0u;  // scanned by an earlier pass
+    if (covered) {
+      // the block belongs to an earlier pass
+    } else if (skip || active == 0) {
       if (DIAG) {
         for (int qi = 0; qi < nq; ++qi) {
           uint64_t o = ((uint64_t)(q0 + qi) * a.n_blocks + b);
@@ -848,6 +847,322 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     b_cur = b_nxt;
   }
   flush_appends<QT, DIAG>(s_app, a, q0, nq, seg, s_stats);
+}
+
+// ---------------------------------------------------------------------------
+// batched scan: one block against a tile of 8 queries at a time
+// ---------------------------------------------------------------------------
+// The stages of src/scan.rs:453-634 for 8 queries per block, ordered dim
+// outer / query inner so that each per-lane load or mask is shared by the 8
+// queries.  Every sum keeps the reference's order per (vector, query):
+//  - prefix: one byte extract gives the level offset of a dim; the LUT holds
+//    the 8 queries' products of that (dim, level) side by side, read as two
+//    16-byte LDS loads;
+//  - S1/S4: the plane word of a dim (from the block's prefetched plane words)
+//    becomes the execution mask and the 8 queries' weights are added under
+//    it.  These sums run for every active lane; a lane takes part in a
+//    query's stage only through that query's survivor mask, so a survivor's
+//    sum is the reference's and other lanes are never pushed.
+constexpr int kTileQ = 8;
+
+// s[i] += w[i] (i = 0..7) on the lanes set in p & mm, where mm is the
+// incoming execution mask.
+__device__ __forceinline__ void masked_add_tile(float (&s)[kTileQ], uint64_t p, const float4& wa,
+                                                const float4& wb) {
+  uint64_t sv;
+  asm volatile(
+      "s_mov_b64 %[sv], exec\n\t"
+      "s_and_b64 exec, %[p], %[sv]\n\t"
+      "v_add_f32 %[s0], %[w0], %[s0]\n\t"
+      "v_add_f32 %[s1], %[w1], %[s1]\n\t"
+      "v_add_f32 %[s2], %[w2], %[s2]\n\t"
+      "v_add_f32 %[s3], %[w3], %[s3]\n\t"
+      "v_add_f32 %[s4], %[w4], %[s4]\n\t"
+      "v_add_f32 %[s5], %[w5], %[s5]\n\t"
+      "v_add_f32 %[s6], %[w6], %[s6]\n\t"
+      "v_add_f32 %[s7], %[w7], %[s7]\n\t"
+      "s_mov_b64 exec, %[sv]"
+      : [s0] "+v"(s[0]), [s1] "+v"(s[1]), [s2] "+v"(s[2]), [s3] "+v"(s[3]), [s4] "+v"(s[4]), [s5] "+v"(s[5]),
+        [s6] "+v"(s[6]), [s7] "+v"(s[7]), [sv] "=&s"(sv)
+      : [p] "s"(p), [w0] "v"(wa.x), [w1] "v"(wa.y), [w2] "v"(wa.z), [w3] "v"(wa.w), [w4] "v"(wb.x),
+        [w5] "v"(wb.y), [w6] "v"(wb.z), [w7] "v"(wb.w)
+      : "scc");
+}
+
+// Plane word d of a 128-word plane held as uint4 per lane (lane l: dwords
+// 4l..4l+3), or of a 64-word plane held as uint2 per lane.
+__device__ __forceinline__ uint64_t plane_word128(const uint4& t, int d) {
+  const int l = d >> 1;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((d & 1) ? t.z : t.x, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((d & 1) ? t.w : t.y, l);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t plane_word64(const uint2& t, int d) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane(t.x, d);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane(t.y, d);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Per-query constants of the tile kernel, one 16-float record per query in
+// LDS (read as broadcasts, so they occupy no scalar registers).
+enum {
+  kQcEden = 0,      // prefix codec is EdenProd (1.0) or MinMax4 (0.0)
+  kQcMeanIp,        // eden_mean_ip
+  kQcPrefixSum,     // prefix_sum
+  kQcMidNorm,       // q_mid_norm
+  kQcTailNorm,      // q_tail_norm
+  kQcTauPrune,      // pruning threshold (-inf when exhaustive)
+  kQcTauPush,       // candidate floor
+  kQcB1,            // mid codec is EdenB1 (1.0)
+  kQcS1Base,        // eden_mid_base or rabitq_base
+  kQcMidMeanIp,     // eden_mid_mean_ip
+  kQcAfterS1,       // q_after_s1
+  kQcHasTail,       // has_tail_fold (1.0)
+  kQcBudget,        // s4_abs_budget
+  kQcTailBase,      // tail_fold_base
+  kQcCount = 16
+};
+
+template <bool FULL>
+__global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
+  constexpr int QT = kTileQ;
+  // LUT: ((g * 64 + d) * 16 + level) * 4 + j holds query 4g + j's entry of (d, level)
+  __shared__ __align__(16) float s_lut[QT * 1024];
+  __shared__ __align__(16) float s_w1[128 * QT];  // [d][q]: rabitq_weights2 or eden_mid_deltas
+  __shared__ __align__(16) float s_w4[64 * QT];   // [d][q]: tail_fold_weights2
+  __shared__ __align__(16) float s_qc[QT * kQcCount];
+  __shared__ float s_rho[256];
+  __shared__ float s_midf[256];
+  __shared__ unsigned int s_stats[kStatCount];
+  __shared__ Staging<QT> s_app;
+
+  const int tid = threadIdx.x;
+  const uint32_t q0 = blockIdx.y * QT;
+  const int nq = (int)min((uint32_t)QT, a.n_q - q0);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t lane = lane_id();
+
+  const uint32_t stride = gridDim.x * 4 - 1;  // odd: see k_scan
+  const uint32_t first = blockIdx.x * 4 + wave;
+  const uint32_t cover = a.prev_shift >= 0 ? (1u << a.prev_shift) - 1u : 0u;
+  const uint32_t n_pos = first < stride ? a.n_pos : 0u;
+  uint32_t b_cur = first << a.shift;
+  RawLane cur;
+  if (first < n_pos) cur = load_raw(a.idx + (uint64_t)b_cur * kBlockBytes);
+
+  const ScanParams sp = a.sp;
+  if (tid < kStatCount) s_stats[tid] = 0u;
+  if (tid < QT) s_app.n[tid] = 0u;
+  for (int e = tid; e < QT * 1024; e += 256) {
+    const int j = e & 3, l = (e >> 2) & 15, d = (e >> 6) & 63, g = e >> 12;
+    const int qi = 4 * g + j;
+    s_lut[e] = qi < nq ? a.luts[(uint64_t)(q0 + qi) * 1024 + d * 16 + l] : 0.0f;
+  }
+  for (int e = tid; e < 192 * QT; e += 256) {
+    const int qi = e % QT, d = e / QT;
+    float w = 0.0f;
+    if (qi < nq) {
+      const mrl_query_plan* pq = a.plans + q0 + qi;
+      if (d < 128) w = pq->mid_codec == MRL_MID_EDEN_B1 ? pq->eden_mid_deltas[d] : pq->rabitq_weights2[d];
+      else w = pq->tail_fold_weights2[d - 128];
+    }
+    if (d < 128) s_w1[e] = w;
+    else s_w4[e - 128 * QT] = w;
+  }
+  if (tid < QT) {
+    const int qi = tid;
+    float* c = s_qc + qi * kQcCount;
+    for (int i = 0; i < kQcCount; ++i) c[i] = 0.0f;
+    c[kQcTauPrune] = __builtin_nanf("");  // absent query: no lane ever survives
+    if (qi < nq) {
+      const mrl_query_plan* pq = a.plans + q0 + qi;
+      const float tq = a.tau ? a.tau[q0 + qi] : -INFINITY;
+      const bool b1 = pq->mid_codec == MRL_MID_EDEN_B1;
+      c[kQcEden] = pq->prefix_codec == MRL_PREFIX_EDEN_PROD ? 1.0f : 0.0f;
+      c[kQcMeanIp] = pq->eden_mean_ip;
+      c[kQcPrefixSum] = pq->prefix_sum;
+      c[kQcMidNorm] = pq->q_mid_norm;
+      c[kQcTailNorm] = pq->q_tail_norm;
+      c[kQcTauPrune] = sp.exhaustive ? -INFINITY : tq;
+      c[kQcTauPush] = tq;
+      c[kQcB1] = b1 ? 1.0f : 0.0f;
+      c[kQcS1Base] = b1 ? pq->eden_mid_base : pq->rabitq_base;
+      c[kQcMidMeanIp] = pq->eden_mid_mean_ip;
+      c[kQcAfterS1] = pq->q_after_s1;
+      c[kQcHasTail] = pq->has_tail_fold ? 1.0f : 0.0f;
+      c[kQcBudget] = pq->s4_abs_budget;
+      c[kQcTailBase] = pq->tail_fold_base;
+    }
+  }
+  s_rho[tid] = a.flag_tabs[tid];
+  s_midf[tid] = a.flag_tabs[256 + tid];
+  __syncthreads();
+
+  const float alpha = sp.alpha;
+  const uint32_t seg = blockIdx.x % a.nseg;
+  const char* lutb = reinterpret_cast<const char*>(s_lut);
+  const float4* w1 = reinterpret_cast<const float4*>(s_w1);
+  const float4* w4 = reinterpret_cast<const float4*>(s_w4);
+  const float4* qc4 = reinterpret_cast<const float4*>(s_qc);
+  // ScanStats of this wave, summed over its blocks and the tile's queries
+  uint32_t c_blocks = 0, c_active = 0, c_prefix = 0, c_s1 = 0, c_s4b = 0;
+
+  for (uint32_t pos = first; pos < n_pos; pos += stride) {
+    const uint32_t b_nxt = pos + stride < n_pos ? (pos + stride) << a.shift : b_cur;
+    const RawLane nxt = load_raw(a.idx + (uint64_t)b_nxt * kBlockBytes);
+    const uint32_t b = b_cur;
+    const uint32_t min_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 0);
+    const uint32_t max_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 1);
+    const uint64_t tomb = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(cur.hdr, 3) << 32) |
+                          (uint64_t)(uint32_t)__builtin_amdgcn_readlane(cur.hdr, 2);
+    bool skip = false;
+    if (sp.temporal) {  // scan.rs:719-730
+      if (sp.has_lo && max_ts < sp.lo) skip = true;
+      if (sp.has_hi && min_ts > sp.hi) skip = true;
+    }
+    const uint64_t active = ~tomb;
+    const bool covered = a.prev_shift >= 0 && (b & cover) == 0u;
+    if (!covered && !skip && active != 0) {
+      // per-lane meta decode (block.rs:61-99)
+      const float m_scale = h2f(cur.scale), m_offset = h2f(cur.offset), m_tail = h2f(cur.tail);
+      const float t = fmaxf(m_tail, 0.0f);
+      const float mid_n = fmaxf(s_midf[cur.flags] * t, 1e-6f);
+      const float high_n = fmaxf(s_rho[cur.flags] * t, 0.0f);
+
+      // Stage: 4-bit prefix IP (scan.rs:453-517), all queries
+      float acc[QT];
+#pragma unroll
+      for (int qi = 0; qi < QT; ++qi) acc[qi] = zero_acc();
+      const uint32_t mask = 0xF0u;
+#pragma unroll 1
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t w = cur.nib[j], w4s = w << 4;
+        const char* lj = lutb + j * 8 * 256;
+        uint32_t off[8];
+        // level * 16: even dims from w << 4, odd dims from w (high nibble of each byte)
+        off[0] = and_byte<0>(w4s, mask);
+        off[1] = and_byte<0>(w, mask);
+        off[2] = and_byte<1>(w4s, mask);
+        off[3] = and_byte<1>(w, mask);
+        off[4] = and_byte<2>(w4s, mask);
+        off[5] = and_byte<2>(w, mask);
+        off[6] = and_byte<3>(w4s, mask);
+        off[7] = and_byte<3>(w, mask);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float4 va = *reinterpret_cast<const float4*>(lj + i * 256 + off[i]);
+          const float4 vb = *reinterpret_cast<const float4*>(lj + 64 * 256 + i * 256 + off[i]);
+          acc[0] = acc[0] + va.x;
+          acc[1] = acc[1] + va.y;
+          acc[2] = acc[2] + va.z;
+          acc[3] = acc[3] + va.w;
+          acc[4] = acc[4] + vb.x;
+          acc[5] = acc[5] + vb.y;
+          acc[6] = acc[6] + vb.z;
+          acc[7] = acc[7] + vb.w;
+        }
+      }
+      // survivors: bit qi of sv = this lane survives query qi's stages so far
+      const bool act = lane_in(active);
+      float score[QT];
+      uint32_t sv = 0;
+#pragma unroll
+      for (int qi = 0; qi < QT; ++qi) {
+        const float4 c0 = qc4[qi * 4 + 0], c1 = qc4[qi * 4 + 1];
+        // c0 = {eden, mean_ip, prefix_sum, mid_norm}, c1 = {tail_norm, tau_prune, tau_push, b1}
+        const float prefix_ip = c0.x != 0.0f ? c0.y + m_scale * acc[qi] : acc[qi] * m_scale + m_offset * c0.z;
+        score[qi] = prefix_ip;
+        const float ub = prefix_ip + alpha * (c0.w * mid_n + c1.x * high_n);
+        sv |= (act && ub >= c1.y) ? (1u << qi) : 0u;
+      }
+      if (a.stats) {
+#pragma unroll
+        for (int qi = 0; qi < QT; ++qi) c_prefix += (uint32_t)__popcll(ballot((sv >> qi) & 1u));
+      }
+
+      if (ballot(sv != 0u) != 0) {
+        // Stage: mid-band 1-bit IP (scan.rs:520-569), all queries
+        float s1[QT];
+#pragma unroll
+        for (int qi = 0; qi < QT; ++qi) s1[qi] = s_qc[qi * kQcCount + kQcS1Base];
+#pragma unroll 4
+        for (int d = 0; d < 128; ++d) {
+          const uint64_t pw = plane_word128(cur.t1, d);
+          masked_add_tile(s1, pw & active, w1[2 * d], w1[2 * d + 1]);
+        }
+        bool any3 = false;
+#pragma unroll
+        for (int qi = 0; qi < QT; ++qi) {
+          const float4 c1 = qc4[qi * 4 + 1], c2 = qc4[qi * 4 + 2], c3 = qc4[qi * 4 + 3];
+          // c1 = {tail_norm, tau_prune, tau_push, b1}, c2 = {s1base, mid_mean_ip, after_s1, has_tail},
+          // c3 = {budget, tail_base, -, -}
+          const bool in = (sv >> qi) & 1u;
+          const float sc = c1.w != 0.0f ? score[qi] + (c2.y + m_offset * s1[qi]) : score[qi] + s1[qi] * mid_n;
+          score[qi] = in ? sc : score[qi];
+          // Stage: post-S1 CS (scan.rs:572-584)
+          const float ub2 = score[qi] + alpha * c2.z * high_n;
+          bool keep = in && ub2 >= c1.y;
+          if (a.stats) c_s1 += (uint32_t)__popcll(ballot(keep));
+          if (FULL) {
+            // Stage: S4 abs-budget prune (scan.rs:587-607), when has_tail_fold and budget > 0
+            const float hn = fmaxf(high_n, 1e-6f);
+            const float ub3 = score[qi] + alpha * hn * sp.w_s4 * c3.x;
+            const bool gate = c2.w != 0.0f && c3.x > 0.0f;
+            keep = keep && (!gate || ub3 >= c1.y);
+            any3 = any3 || (keep && c2.w != 0.0f);
+          }
+          sv = keep ? (sv | (1u << qi)) : (sv & ~(1u << qi));
+        }
+        if (FULL && ballot(any3) != 0) {
+          // Stage: folded-tail 1-bit IP (scan.rs:610-634), all queries
+          float s4[QT];
+#pragma unroll
+          for (int qi = 0; qi < QT; ++qi) s4[qi] = s_qc[qi * kQcCount + kQcTailBase];
+#pragma unroll 4
+          for (int d = 0; d < 64; ++d) {
+            const uint64_t pw = plane_word64(cur.t4, d);
+            masked_add_tile(s4, pw & active, w4[2 * d], w4[2 * d + 1]);
+          }
+          const float hn = fmaxf(high_n, 1e-6f);
+#pragma unroll
+          for (int qi = 0; qi < QT; ++qi) {
+            const float sc = score[qi] + s4[qi] * hn * sp.w_s4;
+            score[qi] = (s_qc[qi * kQcCount + kQcHasTail] != 0.0f && ((sv >> qi) & 1u)) ? sc : score[qi];
+          }
+        }
+      } else if (a.stats) {
+#pragma unroll
+        for (int qi = 0; qi < QT; ++qi) c_s1 += (uint32_t)__popcll(ballot((sv >> qi) & 1u));
+      }
+      // push / append, per query
+      c_blocks += (uint32_t)nq;
+      c_active += (uint32_t)nq * (uint32_t)__popcll(active);
+#pragma unroll
+      for (int qi = 0; qi < QT; ++qi) {
+        const uint32_t q = q0 + qi;
+        const bool mine = (sv >> qi) & 1u;
+        const uint64_t pushed = ballot(mine);
+        if (a.stats) c_s4b += (uint32_t)__popcll(pushed);
+        if (pushed == 0) continue;
+        const float tq = s_qc[qi * kQcCount + kQcTauPush];
+        if (ballot(mine && score[qi] != score[qi]) != 0 && lane == 0) atomicOr(a.err + q, 1u);
+        const uint64_t pm = ballot(mine && score[qi] >= tq);
+        if (pm != 0) stage_append<QT>(s_app, a, qi, q, seg, pm, score[qi], b * 64u + lane);
+      }
+    }
+    retire_touch(cur);
+    cur = nxt;
+    b_cur = b_nxt;
+  }
+  if (a.stats && lane == 0) {
+    atomicAdd(&s_stats[kStatBlocks], c_blocks);
+    atomicAdd(&s_stats[kStatActive], c_active);
+    atomicAdd(&s_stats[kStatPrefix], c_prefix);
+    atomicAdd(&s_stats[kStatS1], c_s1);
+    atomicAdd(&s_stats[kStatS4Budget], c_s4b);
+    atomicAdd(&s_stats[kStatPushed], c_s4b);
+  }
+  flush_appends<QT, false>(s_app, a, q0, nq, seg, s_stats);
 }
 
 // ---------------------------------------------------------------------------
@@ -1204,21 +1519,24 @@ static uint32_t resident_groups(K kernel) {
 }
 
 hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev) {
-  if (a.n_order == 0 || a.n_q == 0) return hipSuccess;
+  if (a.n_pos == 0 || a.n_q == 0) return hipSuccess;
   const int qt = scan_query_tile(a.n_q);
   const uint32_t tiles = (a.n_q + qt - 1) / qt;
   // One round of resident workgroups (each wave then loops over blocks),
   // but at least one workgroup per candidate segment of a query.
   static const uint32_t res1 = resident_groups(k_scan<1, false, false>);
-  static const uint32_t res8 = resident_groups(k_scan<8, false, false>);
+  static const uint32_t res8 = resident_groups(k_scan_tile<true>);
   const uint32_t res = qt == 8 ? res8 : res1;
-  uint32_t grid = (a.n_order + 3) / 4;
+  uint32_t grid = (a.n_pos + 4) / 4;  // 4 * grid - 1 >= n_pos waves carry positions
   uint32_t max_grid = res / tiles;
   if (max_grid < a.nseg) max_grid = a.nseg;
   if (grid > max_grid) grid = max_grid;
   dim3 g(grid, tiles);
   const bool l0 = a.sp.strata == MRL_STRATA_L0_ONLY;
-  if (qt == 8) {
+  if (qt == 8 && !diag && !l0) {
+    if (a.sp.strata == MRL_STRATA_FULL64B) launch(k_scan_tile<true>, g, dim3(256), s, ev, a);
+    else launch(k_scan_tile<false>, g, dim3(256), s, ev, a);
+  } else if (qt == 8) {
     if (l0) {
       if (diag) launch(k_scan<8, true, true>, g, dim3(256), s, ev, a);
       else launch(k_scan<8, false, true>, g, dim3(256), s, ev, a);
