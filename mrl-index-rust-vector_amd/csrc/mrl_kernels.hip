@@ -90,14 +90,16 @@ __device__ __forceinline__ Chunk8 load_chunk8(const CONST_AS uint64_t* pl, const
   return c;
 }
 
-// s += w[i] on the lanes whose bit is set in p[i] & m, for i = 0..7 in order:
+// s += w[i] on the lanes whose bit is set in p[i] & m, for i = 0..7 in order
+// (the asm saves and restores exec, so its only effect is its output and it
+// is not volatile: loads of later chunks may be scheduled ahead of it):
 // the reference's set-bit accumulation (scan.rs:553-562, 534-542, 618-627)
 // with the bitplane word used directly as the wavefront's execution mask.
 // Lanes not set keep s unchanged.  m is first restricted to the incoming
 // exec mask, so no lane that was inactive on entry is ever enabled.
 __device__ __forceinline__ float masked_add8(float s, uint64_t m, const Chunk8& c) {
   uint64_t sv, mm;
-  asm volatile(
+  asm(
       "s_mov_b64 %[sv], exec\n\t"
       "s_and_b64 %[mm], %[m], %[sv]\n\t"
       "s_and_b64 exec, %[p0], %[mm]\n\tv_add_f32 %[s], %[w0], %[s]\n\t"
@@ -630,7 +632,7 @@ __device__ __forceinline__ void retire_touch(const RawLane& r) {
 // Appends of one workgroup are staged here per query and flushed at the end.
 template <int QT>
 struct Staging {
-  static constexpr int kCap = QT == 1 ? 1024 : 256;
+  static constexpr int kCap = QT == 1 ? 1024 : 1024 / QT;
   float score[QT][kCap];
   uint32_t row[QT][kCap];
   uint32_t n[QT];
@@ -850,27 +852,26 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// batched scan: one block against a tile of 8 queries at a time
+// batched scan: one block against a tile of QT queries at a time
 // ---------------------------------------------------------------------------
-// The stages of src/scan.rs:453-634 for 8 queries per block, ordered dim
-// outer / query inner so that each per-lane load or mask is shared by the 8
-// queries.  Every sum keeps the reference's order per (vector, query):
+// The stages of src/scan.rs:453-634 for QT (4 or 8) queries per block,
+// ordered dim outer / query inner so that each per-lane load or mask is
+// shared by the tile's queries.  Every sum keeps the reference's order per
+// (vector, query):
 //  - prefix: one byte extract gives the level offset of a dim; the LUT holds
-//    the 8 queries' products of that (dim, level) side by side, read as two
-//    16-byte LDS loads;
+//    the tile's products of that (dim, level) side by side, read as 16-byte
+//    LDS loads of 4 queries;
 //  - S1/S4: the plane word of a dim (from the block's prefetched plane words)
-//    becomes the execution mask and the 8 queries' weights are added under
-//    it.  These sums run for every active lane; a lane takes part in a
+//    becomes the execution mask and the tile's weights are added under it.  These sums run for every active lane; a lane takes part in a
 //    query's stage only through that query's survivor mask, so a survivor's
 //    sum is the reference's and other lanes are never pushed.
-constexpr int kTileQ = 8;
+constexpr int kTileQ = 8;  // queries per tile of the batched kernel
 
-// s[i] += w[i] (i = 0..7) on the lanes set in p & mm, where mm is the
-// incoming execution mask.
-__device__ __forceinline__ void masked_add_tile(float (&s)[kTileQ], uint64_t p, const float4& wa,
-                                                const float4& wb) {
+// s[i] += w[i] on the lanes set in p (and in the incoming execution mask).
+__device__ __forceinline__ void masked_add_tile(float (&s)[8], uint64_t p, const float4* w) {
   uint64_t sv;
-  asm volatile(
+  const float4 wa = w[0], wb = w[1];
+  asm(
       "s_mov_b64 %[sv], exec\n\t"
       "s_and_b64 exec, %[p], %[sv]\n\t"
       "v_add_f32 %[s0], %[w0], %[s0]\n\t"
@@ -886,6 +887,21 @@ __device__ __forceinline__ void masked_add_tile(float (&s)[kTileQ], uint64_t p, 
         [s6] "+v"(s[6]), [s7] "+v"(s[7]), [sv] "=&s"(sv)
       : [p] "s"(p), [w0] "v"(wa.x), [w1] "v"(wa.y), [w2] "v"(wa.z), [w3] "v"(wa.w), [w4] "v"(wb.x),
         [w5] "v"(wb.y), [w6] "v"(wb.z), [w7] "v"(wb.w)
+      : "scc");
+}
+__device__ __forceinline__ void masked_add_tile(float (&s)[4], uint64_t p, const float4* w) {
+  uint64_t sv;
+  const float4 wa = w[0];
+  asm(
+      "s_mov_b64 %[sv], exec\n\t"
+      "s_and_b64 exec, %[p], %[sv]\n\t"
+      "v_add_f32 %[s0], %[w0], %[s0]\n\t"
+      "v_add_f32 %[s1], %[w1], %[s1]\n\t"
+      "v_add_f32 %[s2], %[w2], %[s2]\n\t"
+      "v_add_f32 %[s3], %[w3], %[s3]\n\t"
+      "s_mov_b64 exec, %[sv]"
+      : [s0] "+v"(s[0]), [s1] "+v"(s[1]), [s2] "+v"(s[2]), [s3] "+v"(s[3]), [sv] "=&s"(sv)
+      : [p] "s"(p), [w0] "v"(wa.x), [w1] "v"(wa.y), [w2] "v"(wa.z), [w3] "v"(wa.w)
       : "scc");
 }
 
@@ -923,16 +939,15 @@ enum {
   kQcCount = 16
 };
 
-template <bool FULL>
+template <int QT, bool FULL>
 __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
-  constexpr int QT = kTileQ;
+  static_assert(QT == 4 || QT == 8, "tile of 4 or 8 queries");
+  constexpr int NG = QT / 4;  // float4 groups per (dim, level)
   // LUT: ((g * 64 + d) * 16 + level) * 4 + j holds query 4g + j's entry of (d, level)
   __shared__ __align__(16) float s_lut[QT * 1024];
   __shared__ __align__(16) float s_w1[128 * QT];  // [d][q]: rabitq_weights2 or eden_mid_deltas
   __shared__ __align__(16) float s_w4[64 * QT];   // [d][q]: tail_fold_weights2
   __shared__ __align__(16) float s_qc[QT * kQcCount];
-  __shared__ float s_rho[256];
-  __shared__ float s_midf[256];
   __shared__ unsigned int s_stats[kStatCount];
   __shared__ Staging<QT> s_app;
 
@@ -994,8 +1009,6 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
       c[kQcTailBase] = pq->tail_fold_base;
     }
   }
-  s_rho[tid] = a.flag_tabs[tid];
-  s_midf[tid] = a.flag_tabs[256 + tid];
   __syncthreads();
 
   const float alpha = sp.alpha;
@@ -1024,10 +1037,13 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
     const bool covered = a.prev_shift >= 0 && (b & cover) == 0u;
     if (!covered && !skip && active != 0) {
       // per-lane meta decode (block.rs:61-99)
+      // rho = flags / 255 and sqrt(max(1 - rho^2, 0)) (block.rs:74-84), correctly rounded
       const float m_scale = h2f(cur.scale), m_offset = h2f(cur.offset), m_tail = h2f(cur.tail);
       const float t = fmaxf(m_tail, 0.0f);
-      const float mid_n = fmaxf(s_midf[cur.flags] * t, 1e-6f);
-      const float high_n = fmaxf(s_rho[cur.flags] * t, 0.0f);
+      const float rho = (float)cur.flags / 255.0f;
+      const float rc = rho > 1.0f ? 1.0f : rho;
+      const float mid_n = fmaxf(sqrtf(fmaxf(1.0f - rc * rc, 0.0f)) * t, 1e-6f);
+      const float high_n = fmaxf(rho * t, 0.0f);
 
       // Stage: 4-bit prefix IP (scan.rs:453-517), all queries
       float acc[QT];
@@ -1036,7 +1052,12 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
       const uint32_t mask = 0xF0u;
 #pragma unroll 1
       for (int j = 0; j < 8; ++j) {
-        const uint32_t w = cur.nib[j], w4s = w << 4;
+        // one 8-dim group per iteration; the level word is picked by selects
+        // (a run-time index into the per-lane array would place it in scratch)
+        uint32_t w = cur.nib[7];
+#pragma unroll
+        for (int u = 6; u >= 0; --u) w = j == u ? cur.nib[u] : w;
+        const uint32_t w4s = w << 4;
         const char* lj = lutb + j * 8 * 256;
         uint32_t off[8];
         // level * 16: even dims from w << 4, odd dims from w (high nibble of each byte)
@@ -1050,16 +1071,14 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
         off[7] = and_byte<3>(w, mask);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float4 va = *reinterpret_cast<const float4*>(lj + i * 256 + off[i]);
-          const float4 vb = *reinterpret_cast<const float4*>(lj + 64 * 256 + i * 256 + off[i]);
-          acc[0] = acc[0] + va.x;
-          acc[1] = acc[1] + va.y;
-          acc[2] = acc[2] + va.z;
-          acc[3] = acc[3] + va.w;
-          acc[4] = acc[4] + vb.x;
-          acc[5] = acc[5] + vb.y;
-          acc[6] = acc[6] + vb.z;
-          acc[7] = acc[7] + vb.w;
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const float4 v = *reinterpret_cast<const float4*>(lj + g * 64 * 256 + i * 256 + off[i]);
+            acc[4 * g + 0] = acc[4 * g + 0] + v.x;
+            acc[4 * g + 1] = acc[4 * g + 1] + v.y;
+            acc[4 * g + 2] = acc[4 * g + 2] + v.z;
+            acc[4 * g + 3] = acc[4 * g + 3] + v.w;
+          }
         }
       }
       // survivors: bit qi of sv = this lane survives query qi's stages so far
@@ -1088,7 +1107,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
 #pragma unroll 4
         for (int d = 0; d < 128; ++d) {
           const uint64_t pw = plane_word128(cur.t1, d);
-          masked_add_tile(s1, pw & active, w1[2 * d], w1[2 * d + 1]);
+          masked_add_tile(s1, pw & active, w1 + NG * d);
         }
         bool any3 = false;
 #pragma unroll
@@ -1121,7 +1140,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
 #pragma unroll 4
           for (int d = 0; d < 64; ++d) {
             const uint64_t pw = plane_word64(cur.t4, d);
-            masked_add_tile(s4, pw & active, w4[2 * d], w4[2 * d + 1]);
+            masked_add_tile(s4, pw & active, w4 + NG * d);
           }
           const float hn = fmaxf(high_n, 1e-6f);
 #pragma unroll
@@ -1223,9 +1242,10 @@ __device__ void find_boundary(const uint32_t* hist, uint32_t nb, uint32_t need, 
 // one segment: item c lies in segment s with coff[s] <= c < coff[s+1].  A
 // wave takes items c = wave, wave + nwaves, ...; lane l loads entries
 // base + 64u + l (u < kWalk) of its item, all before any is used, so the
-// loads are coalesced and kWalk of them are in flight per lane.
+// loads are coalesced and kWalk of them are in flight per lane (with 16
+// waves, up to 32K candidates take one round of memory latency).
 constexpr int kWalk = 32;
-constexpr uint32_t kChunk = 64u * kWalk;
+constexpr uint32_t kChunk = 64u * kWalk;  // entries of a work item
 struct CandView {
   const float* sc;
   const uint32_t* rw;
@@ -1235,7 +1255,8 @@ struct CandView {
   const uint32_t* coff;  // LDS, nseg + 1 prefix offsets of the item counts
 };
 
-template <typename F>
+// W (<= kWalk) loads per lane at a time; an item is walked in kWalk / W steps.
+template <int W = kWalk, typename F>
 __device__ __forceinline__ void for_each_cand(const CandView& v, F&& fn) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
@@ -1245,20 +1266,18 @@ __device__ __forceinline__ void for_each_cand(const CandView& v, F&& fn) {
     while (v.coff[s + 1] <= c) ++s;
     const uint32_t base = (c - v.coff[s]) * kChunk;
     const uint32_t cnt = v.off[s + 1] - v.off[s];
-    float sc[kWalk];
-    uint32_t idx[kWalk];
+    const uint32_t lim = cnt > base ? cnt - base : 0u;  // entries of the item (may exceed kChunk)
+    for (int h = 0; h < kWalk / W; ++h) {
+      const uint32_t i0 = s * v.seg_cap + base + (uint32_t)h * 64u * W + lane;
+      const uint32_t lh = lim > (uint32_t)h * 64u * W ? lim - (uint32_t)h * 64u * W : 0u;
+      float sc[W];
 #pragma unroll
-    for (int u = 0; u < kWalk; ++u) {
-      const uint32_t i = base + 64u * u + lane;
-      idx[u] = 0xFFFFFFFFu;
-      if (i < cnt) {
-        idx[u] = s * v.seg_cap + i;
-        sc[u] = v.sc[idx[u]];
-      }
+      for (int u = 0; u < W; ++u)
+        if (64u * u + lane < lh) sc[u] = v.sc[i0 + 64u * u];
+#pragma unroll
+      for (int u = 0; u < W; ++u)
+        if (64u * u + lane < lh) fn(sc[u], i0 + 64u * u);
     }
-#pragma unroll
-    for (int u = 0; u < kWalk; ++u)
-      if (idx[u] != 0xFFFFFFFFu) fn(sc[u], idx[u]);
   }
 }
 
@@ -1393,7 +1412,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
       const uint32_t nb = 1u << wd;
       for (int i = tid; i < 2048; i += kSelThreads) s_hist[i] = 0;
       __syncthreads();
-      for_each_cand(v, [&](float sc, uint32_t) {
+      for_each_cand<16>(v, [&](float sc, uint32_t) {
         if (!(sc >= floor_t)) return;
         const uint32_t key = score_key(sc);
         if (pass == 0 || (key >> (sh + wd)) == prefix) atomicAdd(&s_hist[(key >> sh) & (nb - 1)], 1u);
@@ -1412,7 +1431,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
       const uint32_t nb = 1u << wd;
       for (int i = tid; i < 2048; i += kSelThreads) s_hist[i] = 0;
       __syncthreads();
-      for_each_cand(v, [&](float sc, uint32_t idx) {
+      for_each_cand<16>(v, [&](float sc, uint32_t idx) {
         if (!(sc >= floor_t) || score_key(sc) != tie_key) return;
         const uint32_t r = v.rw[idx];
         if (pass == 0 || (r >> (sh + wd)) == rprefix) atomicAdd(&s_hist[(r >> sh) & (nb - 1)], 1u);
@@ -1427,7 +1446,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     const uint32_t row_max = rprefix;
     if (tid == 0) s_misc[2] = 0;
     __syncthreads();
-    for_each_cand(v, [&](float sc, uint32_t idx) {
+    for_each_cand<16>(v, [&](float sc, uint32_t idx) {
       if (!(sc >= floor_t)) return;
       const uint32_t key = score_key(sc);
       const uint32_t r = v.rw[idx];
@@ -1450,17 +1469,28 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     // Rank sort: the composite keys are distinct, so an entry's position in
     // the descending order is the number of larger keys.  Every lane of a
     // wave reads the same key j at the same time (an LDS broadcast).
+    // pad to a multiple of 16 with keys below every composite key
+    for (uint32_t i = m + tid; i < ((m + 15u) & ~15u); i += kSelThreads) s_buf[i] = 0ull;
+    __syncthreads();
+    const uint32_t m16 = (m + 15u) & ~15u;
+    const ulonglong2* b2 = reinterpret_cast<const ulonglong2*>(s_buf);
     for (uint32_t i = tid; i < m; i += kSelThreads) {
       const uint64_t key = s_buf[i];
-      uint32_t r = 0, j = 0;
-      for (; j + 8 <= m; j += 8) {
-        uint64_t k8[8];
+      uint32_t r = 0;
+      ulonglong2 nx[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) k8[u] = s_buf[j + u];
+      for (int u = 0; u < 4; ++u) nx[u] = b2[u];
+      for (uint32_t j = 8; j <= m16; j += 8) {
+        ulonglong2 k4[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) r += k8[u] > key ? 1u : 0u;
+        for (int u = 0; u < 4; ++u) k4[u] = nx[u];
+        if (j < m16) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) nx[u] = b2[(j >> 1) + u];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) r += (k4[u].x > key ? 1u : 0u) + (k4[u].y > key ? 1u : 0u);
       }
-      for (; j < m; ++j) r += s_buf[j] > key ? 1u : 0u;
       if (r < keep) emit(r, key);
     }
   } else {
@@ -1520,22 +1550,26 @@ static uint32_t resident_groups(K kernel) {
 
 hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev) {
   if (a.n_pos == 0 || a.n_q == 0) return hipSuccess;
-  const int qt = scan_query_tile(a.n_q);
+  const bool l0 = a.sp.strata == MRL_STRATA_L0_ONLY;
+  // batched: the tile kernel; otherwise one query per workgroup, or the
+  // 8-query workgroups of the diagnostic and L0Only paths
+  const bool tile = a.n_q >= 8 && !diag && !l0;
+  const int qt = tile ? kTileQ : scan_query_tile(a.n_q);
   const uint32_t tiles = (a.n_q + qt - 1) / qt;
   // One round of resident workgroups (each wave then loops over blocks),
   // but at least one workgroup per candidate segment of a query.
   static const uint32_t res1 = resident_groups(k_scan<1, false, false>);
-  static const uint32_t res8 = resident_groups(k_scan_tile<true>);
-  const uint32_t res = qt == 8 ? res8 : res1;
+  static const uint32_t res8 = resident_groups(k_scan<8, false, false>);
+  static const uint32_t rest = resident_groups(k_scan_tile<kTileQ, true>);
+  const uint32_t res = tile ? rest : (qt == 8 ? res8 : res1);
   uint32_t grid = (a.n_pos + 4) / 4;  // 4 * grid - 1 >= n_pos waves carry positions
   uint32_t max_grid = res / tiles;
   if (max_grid < a.nseg) max_grid = a.nseg;
   if (grid > max_grid) grid = max_grid;
   dim3 g(grid, tiles);
-  const bool l0 = a.sp.strata == MRL_STRATA_L0_ONLY;
-  if (qt == 8 && !diag && !l0) {
-    if (a.sp.strata == MRL_STRATA_FULL64B) launch(k_scan_tile<true>, g, dim3(256), s, ev, a);
-    else launch(k_scan_tile<false>, g, dim3(256), s, ev, a);
+  if (tile) {
+    if (a.sp.strata == MRL_STRATA_FULL64B) launch(k_scan_tile<kTileQ, true>, g, dim3(256), s, ev, a);
+    else launch(k_scan_tile<kTileQ, false>, g, dim3(256), s, ev, a);
   } else if (qt == 8) {
     if (l0) {
       if (diag) launch(k_scan<8, true, true>, g, dim3(256), s, ev, a);
