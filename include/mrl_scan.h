@@ -280,6 +280,22 @@ int mrl_encode_block(const float *vectors, uint32_t n, uint32_t dims, const uint
 int mrl_encode_corpus(const float *matrix, uint64_t n, uint32_t dims, uint32_t default_source,
                       const mrl_eden_fit *eden, const mrl_eden_fit *eden_mid, int n_threads,
                       void *out_blocks);
+/* encode_f32_corpus_par (src/encoder.rs:195-219) on the GPU: n rows of `dims`
+ * floats already in device memory -> ceil(n/64) records in device memory, in
+ * the reference byte layout with the CRC set, byte-identical to
+ * mrl_encode_corpus.  Returns when the records are written. */
+int mrl_encode_corpus_device(mrl_ctx *ctx, const float *d_matrix, uint64_t n, uint32_t dims,
+                             uint32_t default_source, const mrl_eden_fit *eden,
+                             const mrl_eden_fit *eden_mid, void *d_out_blocks);
+/* Device memory on the context's GPU, for callers without a HIP allocator of
+ * their own (no reference counterpart).  Copies are synchronous. */
+int mrl_device_alloc(mrl_ctx *ctx, size_t bytes, void **out);
+void mrl_device_free(mrl_ctx *ctx, void *d_ptr);
+int mrl_copy_to_device(mrl_ctx *ctx, void *d_dst, const void *src, size_t bytes);
+int mrl_copy_to_host(mrl_ctx *ctx, void *dst, const void *d_src, size_t bytes);
+/* mrl_index_upload for records already in device memory (e.g. written by
+ * mrl_encode_corpus_device); no host copy. */
+int mrl_index_from_device(mrl_ctx *ctx, const void *d_blocks, uint64_t n_blocks, mrl_index **out);
 /* EdenFit::fit_band (src/eden.rs:130-159): mean of row[start..start+dim]. */
 int mrl_eden_fit_band(const float *rows, uint64_t n_rows, uint32_t row_stride, uint32_t start,
                       uint32_t dim, float *out_mean);

@@ -69,6 +69,8 @@ struct mrl_ctx {
   bool profiling = false;
   std::vector<ProfRecord> prof;       // recorded, not yet collected
   std::vector<hipEvent_t> event_pool; // reusable events
+  uint32_t* d_crc = nullptr;          // encoder CRC tables: [256] byte table, then [64][32] carry map
+  uint32_t crc_const = 0;
 };
 
 static hipEvent_t pool_event(mrl_ctx* c) {
@@ -218,6 +220,7 @@ extern "C" void mrl_ctx_destroy(mrl_ctx* ctx) {
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
   dev_free(ctx->d_flag_tabs);
+  dev_free(ctx->d_crc);
   for (auto& r : ctx->prof) {
     (void)hipEventDestroy(r.start);
     (void)hipEventDestroy(r.stop);
@@ -980,6 +983,144 @@ extern "C" int mrl_encode_corpus(const float* matrix, uint64_t n, uint32_t dims,
   int rc = encode_corpus(matrix, n, dims, default_source, fit_view(eden, &e) ? &e : nullptr,
                          fit_view(eden_mid, &m) ? &m : nullptr, n_threads, static_cast<uint8_t*>(out_blocks));
   return rc ? fail(rc, "encode_corpus: invalid arguments") : MRL_OK;
+}
+
+
+// CRC-32 tables for the GPU encoder.  raw(c, M) is the reflected CRC register
+// after bytes M starting from register c (no initial or final xor); it is
+// linear in c and M over GF(2), so
+//   CRC(M) = raw(~0, 0^4096) ^ xor_k carry(raw(0, M_k), 64 * (63 - k)) ^ ~0
+// for the 64-byte chunks M_k, with carry(c, L) = raw(c, 0^L) = xor over the
+// set bits i of c of carry(1 << i, L).
+struct CrcTables {
+  uint32_t tab[256 + 64 * 32];
+  uint32_t konst;
+};
+static const CrcTables& crc_tables() {
+  static const CrcTables t = [] {
+    CrcTables r{};
+    for (uint32_t i = 0; i < 256; ++i) {
+      uint32_t c = i;
+      for (int k = 0; k < 8; ++k) c = (c & 1u) ? (0xEDB88320u ^ (c >> 1)) : (c >> 1);
+      r.tab[i] = c;
+    }
+    auto zeros = [&](uint32_t c, uint32_t nbytes) {
+      for (uint32_t j = 0; j < nbytes; ++j) c = r.tab[c & 0xffu] ^ (c >> 8);
+      return c;
+    };
+    for (uint32_t k = 0; k < 64; ++k)
+      for (uint32_t i = 0; i < 32; ++i) r.tab[256 + 32 * k + i] = zeros(1u << i, 64u * (63u - k));
+    r.konst = zeros(0xffffffffu, kBlockBytes) ^ 0xffffffffu;
+    return r;
+  }();
+  return t;
+}
+
+extern "C" int mrl_encode_corpus_device(mrl_ctx* ctx, const float* d_matrix, uint64_t n, uint32_t dims,
+                                        uint32_t default_source, const mrl_eden_fit* eden,
+                                        const mrl_eden_fit* eden_mid, void* d_out_blocks) {
+  if (!ctx || (n && (!d_matrix || !d_out_blocks))) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (dims < (uint32_t)(kPrefixDims + kRabitqDims)) return fail(MRL_ERR_INVALID_ARG, "dims < 192");
+  if (eden && (eden->dim != 64 || eden->bits != 4 || !eden->mean))
+    return fail(MRL_ERR_INVALID_ARG, "EdenProd prefix needs a 64-d 4-bit fit");
+  if (eden_mid && (!eden || eden_mid->dim != 128 || eden_mid->bits != 1 || !eden_mid->mean))
+    return fail(MRL_ERR_INVALID_ARG, "EdenB1 mid-band needs a 128-d 1-bit fit and an EdenProd prefix");
+  if (n == 0) return MRL_OK;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  if (!ctx->d_crc) {
+    const CrcTables& t = crc_tables();
+    if (hipMalloc(&ctx->d_crc, sizeof(t.tab)) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "crc tables");
+    HIP_TRY(hipMemcpy(ctx->d_crc, t.tab, sizeof(t.tab), hipMemcpyHostToDevice));
+    ctx->crc_const = t.konst;
+  }
+  float* d_means = nullptr;
+  if (hipMalloc(&d_means, 192 * sizeof(float)) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "fit means");
+  hipError_t e = hipSuccess;
+  if (eden) e = hipMemcpy(d_means, eden->mean, 64 * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess && eden_mid) e = hipMemcpy(d_means + 64, eden_mid->mean, 128 * sizeof(float), hipMemcpyHostToDevice);
+  EncodeArgs a{};
+  a.x = d_matrix;
+  a.n = n;
+  a.dims = dims;
+  a.source = default_source;
+  a.eden_mean = eden ? d_means : nullptr;
+  a.eden_seed = eden ? eden->seed : 0;
+  a.mid_mean = eden_mid ? d_means + 64 : nullptr;
+  a.mid_seed = eden_mid ? eden_mid->seed : 0;
+  a.crc_tab = ctx->d_crc;
+  a.crc_zt = ctx->d_crc + 256;
+  a.crc_const = ctx->crc_const;
+  a.c = ctx->consts;
+  a.sqrt64 = sqrtf(64.0f);
+  a.sqrt128 = sqrtf(128.0f);
+  a.out = static_cast<uint8_t*>(d_out_blocks);
+  a.n_blocks = (n + 63) / 64;
+  if (e == hipSuccess) e = launch_encode(a, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  dev_free(d_means);
+  if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("encode: ") + hipGetErrorString(e));
+  return MRL_OK;
+}
+
+// Device memory for callers without a HIP allocator of their own (plain
+// pointers in and out; copies are synchronous on the context stream).
+extern "C" int mrl_device_alloc(mrl_ctx* ctx, size_t bytes, void** out) {
+  if (!ctx || !out) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  *out = nullptr;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  if (bytes && hipMalloc(out, bytes) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc");
+  return MRL_OK;
+}
+
+extern "C" void mrl_device_free(mrl_ctx* ctx, void* d_ptr) {
+  if (!ctx || !d_ptr) return;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  (void)hipFree(d_ptr);
+}
+
+extern "C" int mrl_copy_to_device(mrl_ctx* ctx, void* d_dst, const void* src, size_t bytes) {
+  if (!ctx || (bytes && (!d_dst || !src))) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipMemcpyAsync(d_dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return MRL_OK;
+}
+
+extern "C" int mrl_copy_to_host(mrl_ctx* ctx, void* dst, const void* d_src, size_t bytes) {
+  if (!ctx || (bytes && (!dst || !d_src))) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipMemcpyAsync(dst, d_src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return MRL_OK;
+}
+
+extern "C" int mrl_index_from_device(mrl_ctx* ctx, const void* d_blocks, uint64_t n_blocks, mrl_index** out) {
+  if (!ctx || !out || (n_blocks && !d_blocks)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (n_blocks > (1ull << 26)) return fail(MRL_ERR_INVALID_ARG, "n_blocks exceeds 2^26 (32-bit row ids)");
+  *out = nullptr;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  std::unique_ptr<mrl_index> ix(new mrl_index());
+  ix->ctx = ctx;
+  ix->n_blocks = n_blocks;
+  if (n_blocks) {
+    if (hipMalloc(&ix->d_blocks, (size_t)n_blocks * kBlockBytes) != hipSuccess)
+      return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc index");
+    hipError_t e = launch_relayout(static_cast<const uint8_t*>(d_blocks), ix->d_blocks, n_blocks, true, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+      dev_free(ix->d_blocks);
+      return fail(MRL_ERR_HIP, std::string("index from device: ") + hipGetErrorString(e));
+    }
+  }
+  *out = ix.release();
+  return MRL_OK;
 }
 
 extern "C" int mrl_eden_fit_band(const float* rows, uint64_t n_rows, uint32_t row_stride, uint32_t start, uint32_t dim,

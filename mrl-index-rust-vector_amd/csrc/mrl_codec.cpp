@@ -200,7 +200,7 @@ static float eden_encode(const float* mean, int d, int bits, uint64_t seed, cons
     c[i] = v;
     norm_sq += v * v;
   }
-  const float cn = std::max(sqrtf(norm_sq), 1e-12f);
+  const float cn = fmaxf(sqrtf(norm_sq), 1e-12f);  // f32::max: a NaN norm yields 1e-12
   const float inv = 1.0f / cn;
   for (int i = 0; i < d; ++i) c[i] *= inv;
   for (int i = 0; i < d; ++i) c[i] *= mix_sign(seed, (uint64_t)i);
@@ -396,7 +396,7 @@ void gaussian_row(uint64_t seed, uint64_t stream, uint64_t row, uint32_t n, floa
 static void l2_normalize(float* v, uint32_t n) {
   float s = 0.0f;
   for (uint32_t i = 0; i < n; ++i) s += v[i] * v[i];
-  float nrm = std::max(sqrtf(s), 1e-12f);
+  float nrm = fmaxf(sqrtf(s), 1e-12f);
   for (uint32_t i = 0; i < n; ++i) v[i] /= nrm;
 }
 

@@ -152,6 +152,26 @@ struct SelectArgs {
   uint32_t* out_counts;
 };
 
+// GPU encoder (mrl_encode.hip): rows -> PaxBlock64 records in the reference layout.
+struct EncodeArgs {
+  const float* x;          // [n][dims] row-major, device
+  uint64_t n;
+  uint32_t dims;
+  uint32_t source;         // source id of every row
+  const float* eden_mean;  // 64 floats (device) or null: MinMax4 prefix
+  uint64_t eden_seed;
+  const float* mid_mean;   // 128 floats (device) or null: RaBitQ mid-band
+  uint64_t mid_seed;
+  const uint32_t* crc_tab; // [256] CRC-32 byte table
+  const uint32_t* crc_zt;  // [64][32]: register bit i of chunk k carried past the following 64*(63-k) bytes
+  uint32_t crc_const;      // CRC of 4096 zero bytes (initial register and final xor folded in)
+  PlanConsts c;
+  float sqrt64, sqrt128;
+  uint8_t* out;            // [n_blocks][4096], device
+  uint64_t n_blocks;
+};
+hipError_t launch_encode(const EncodeArgs& a, hipStream_t s);
+
 // Launchers (mrl_kernels.hip).
 // Optional start/stop events written by the dispatch itself (kernel-only
 // duration, the same interval a kernel-trace profiler reports).

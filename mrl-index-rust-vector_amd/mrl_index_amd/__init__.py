@@ -8,8 +8,8 @@ from .block import (BLOCK_BYTES, MRL_PREFIX_DIMS, RABITQ_DIMS, TAIL_FOLD_DIMS, T
 from .config import EngineConfig, MidCodec, PrefixCodec, ScanConfig, StrataDepth
 from .eden import EdenFit
 from .pipeline import QueryPipeline, ScanPhase, row_id_to_vector_id, scored_hits_to_row_ids
-from .quantize import encode_block, encode_corpus
-from .scan import (Device, DeviceIndex, QueryPlan, ScanResult, ScanStats, ScoredHit, StageTrace, default_device,
+from .quantize import encode_block, encode_corpus, encode_corpus_device
+from .scan import (Device, DeviceBuffer, DeviceIndex, QueryPlan, ScanResult, ScanStats, ScoredHit, StageTrace, default_device,
                    scan_batch, scan_blocks, scan_blocks_stats, scan_fixed_tau)
 from .segment import SegmentWriter, read_segment
 
@@ -17,7 +17,7 @@ __all__ = [
     "LIB_PATH", "MrlError", "BLOCK_BYTES", "MRL_PREFIX_DIMS", "RABITQ_DIMS", "TAIL_FOLD_DIMS", "TAIL_START",
     "VECTORS_PER_BLOCK", "VectorId", "source", "EngineConfig", "MidCodec", "PrefixCodec", "ScanConfig",
     "StrataDepth", "EdenFit", "QueryPipeline", "ScanPhase", "row_id_to_vector_id", "scored_hits_to_row_ids",
-    "encode_block", "encode_corpus", "Device", "DeviceIndex", "QueryPlan", "ScanResult", "ScanStats", "ScoredHit",
+    "encode_block", "encode_corpus", "encode_corpus_device", "Device", "DeviceBuffer", "DeviceIndex", "QueryPlan", "ScanResult", "ScanStats", "ScoredHit",
     "StageTrace", "default_device", "scan_batch", "scan_blocks", "scan_blocks_stats", "scan_fixed_tau",
     "SegmentWriter", "read_segment",
 ]

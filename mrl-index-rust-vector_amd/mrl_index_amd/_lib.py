@@ -187,6 +187,13 @@ SIGNATURES = {
     "mrl_encode_corpus": (C.c_int, [_F, C.c_uint64, C.c_uint32, C.c_uint32, C.POINTER(EdenFitC),
                                     C.POINTER(EdenFitC), C.c_int, _P]),
     "mrl_eden_fit_band": (C.c_int, [_F, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, _F]),
+    "mrl_encode_corpus_device": (C.c_int, [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, C.POINTER(EdenFitC),
+                                           C.POINTER(EdenFitC), _P]),
+    "mrl_index_from_device": (C.c_int, [_P, _P, C.c_uint64, _PP]),
+    "mrl_device_alloc": (C.c_int, [_P, C.c_size_t, _PP]),
+    "mrl_device_free": (None, [_P, _P]),
+    "mrl_copy_to_device": (C.c_int, [_P, _P, _P, C.c_size_t]),
+    "mrl_copy_to_host": (C.c_int, [_P, _P, _P, C.c_size_t]),
     "mrl_synth_docs": (C.c_int, [C.POINTER(SynthSpecC), C.c_uint64, C.c_uint64, C.c_int, _F]),
     "mrl_synth_queries": (C.c_int, [C.POINTER(SynthSpecC), C.c_uint64, C.c_float, C.c_int, C.c_uint32, _F,
                                     _U64]),

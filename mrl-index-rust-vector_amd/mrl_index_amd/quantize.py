@@ -42,3 +42,15 @@ def encode_corpus(matrix, default_source: int = source.DOC, eden: Optional[EdenF
     _lib.check(_lib.lib.mrl_encode_corpus(_lib.fptr(m), n, dims, default_source, C.byref(ef) if ef else None,
                                           C.byref(mf) if mf else None, n_threads, _lib.vptr(out)))
     return out
+
+
+def encode_corpus_device(d_matrix: int, n: int, dims: int, d_out: int, device, default_source: int = source.DOC,
+                         eden: Optional[EdenFit] = None, eden_mid: Optional[EdenFit] = None) -> None:
+    """encode_f32_corpus_par on the GPU: `d_matrix` is the device address of n x dims
+    float32 rows, `d_out` of ceil(n/64) * 4096 bytes; byte-identical to encode_corpus."""
+    import ctypes as C
+    ef = eden.to_c() if eden is not None else None
+    mf = eden_mid.to_c() if eden_mid is not None else None
+    _lib.check(_lib.lib.mrl_encode_corpus_device(device.handle, C.c_void_p(d_matrix), n, dims, default_source,
+                                                 C.byref(ef) if ef else None, C.byref(mf) if mf else None,
+                                                 C.c_void_p(d_out)))

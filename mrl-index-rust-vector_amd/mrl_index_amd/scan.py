@@ -57,6 +57,41 @@ _default = None
 _default_lock = threading.Lock()
 
 
+class DeviceBuffer:
+    """Device memory on `device` (mrl_device_alloc); `ptr` is its device address."""
+
+    def __init__(self, nbytes: int, device: Optional[Device] = None):
+        self._dev = device or default_device()
+        p = C.c_void_p()
+        _lib.check(_lib.lib.mrl_device_alloc(self._dev.handle, nbytes, C.byref(p)))
+        self.ptr = p.value or 0
+        self.nbytes = nbytes
+
+    @classmethod
+    def from_array(cls, a: np.ndarray, device: Optional[Device] = None) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes, device)
+        _lib.check(_lib.lib.mrl_copy_to_device(b._dev.handle, C.c_void_p(b.ptr), _lib.vptr(a), a.nbytes))
+        return b
+
+    def to_array(self, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        _lib.check(_lib.lib.mrl_copy_to_host(self._dev.handle, _lib.vptr(out), C.c_void_p(self.ptr), out.nbytes))
+        return out
+
+    def close(self):
+        if self.ptr:
+            _lib.lib.mrl_device_free(self._dev.handle, C.c_void_p(self.ptr))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def default_device() -> Device:
     global _default
     with _default_lock:
@@ -79,6 +114,14 @@ class DeviceIndex:
         h = C.c_void_p()
         _lib.check(_lib.lib.mrl_index_upload(device.handle, _lib.vptr(b), b.shape[0], int(verify_crc),
                                              C.byref(h)))
+        return cls(h, device)
+
+    @classmethod
+    def from_device(cls, d_blocks: int, n_blocks: int, device: Optional[Device] = None) -> "DeviceIndex":
+        """Index over records already in device memory (address d_blocks), e.g. from the GPU encoder."""
+        device = device or default_device()
+        h = C.c_void_p()
+        _lib.check(_lib.lib.mrl_index_from_device(device.handle, C.c_void_p(d_blocks), n_blocks, C.byref(h)))
         return cls(h, device)
 
     @classmethod

@@ -188,8 +188,14 @@ def test_product_encoder_is_byte_identical_to_oracle(dims, codec):
     rows[5] = 0.0                     # zero vector
     rows[6, 64:] = 0.0                # no residual
     rows[7, :64] = 0.25               # constant prefix
-    pf = oracle_fit(rows)
-    mf = oracle_fit_mid(rows)
+    rows[8] *= np.float32(3e4)        # large magnitude
+    rows[9] *= np.float32(1e-30)      # tiny magnitude
+    rows[10, 5] = np.nan              # NaN in the prefix (f32::max keeps 1e-12 for the norm)
+    rows[11, 100] = np.nan            # NaN in the mid band
+    rows[12, dims - 1] = np.inf       # infinity in the tail
+    rows[13, 70] = -np.inf            # infinity in the mid band
+    pf = oracle_fit(rows[16:])
+    mf = oracle_fit_mid(rows[16:])
     ef, emf = {"minmax": (None, None), "eden": (pf, None), "dual": (pf, mf)}[codec]
     ref = oracle_encode_corpus(rows, dims, ef, emf)
     P = lambda f: m.EdenFit(f.mean.shape[0], f.c.bits, f.c.seed, f.mean, f.c.n_observed) if f else None
