@@ -240,6 +240,60 @@ int mrl_scan_fixed_tau(mrl_ctx *ctx, const mrl_index *index, const mrl_plans *pl
                        uint64_t *out_masks, float *out_prefix_ip, float *out_scores);
 
 /* ---------------------------------------------------------------- */
+/* post-scan rerank (src/pipeline.rs:157-180, src/lowprec.rs:18-121) */
+/* ---------------------------------------------------------------- */
+/* RerankPrecision (src/lowprec.rs:18-23) */
+typedef enum mrl_rerank_precision {
+  MRL_RERANK_FP32 = 0, /* dot (src/embed.rs:115-124): dot_768 at 768 dims, else sequential */
+  MRL_RERANK_FP16 = 1, /* Fp16Vec768 + dot_f16_768 (lowprec.rs:43-61, embed.rs:158-180) */
+  MRL_RERANK_INT8 = 2  /* Int8Vec768 + dot_i8_768 (lowprec.rs:63-95, embed.rs:184-206) */
+} mrl_rerank_precision;
+
+typedef struct mrl_rerank_store mrl_rerank_store;
+
+/* Corpus rows resident in HBM at one rerank precision.  Replaces the
+ * corpus_row closure of rerank_exact_rows (src/pipeline.rs:160) and
+ * data.corpus_vector(i) in the precision loop (src/retrieval_bench.rs:742);
+ * the per-call Fp16Vec768::from_f32 / Int8Vec768::from_f32 of rerank_dot
+ * (src/lowprec.rs:112-119) is done once, on the GPU, with the same
+ * arithmetic.  rows: n_rows x dims f32, in host memory, or in device memory
+ * when rows_on_device (e.g. mrl_device_alloc).  FP16 and INT8 need
+ * dims == 768 (the assert_eq! of lowprec.rs:50,73). */
+int mrl_rerank_store_create(mrl_ctx *ctx, const float *rows, int rows_on_device, uint64_t n_rows,
+                            uint32_t dims, int precision, mrl_rerank_store **out);
+void mrl_rerank_store_destroy(mrl_rerank_store *store);
+/* The stored rows in the reference's form, row-major: FP32 f32[n][dims],
+ * FP16 f16 bits u16[n][768] (Fp16Vec768.data), INT8 i8[n][768] codes plus
+ * out_scales[n] f16 bits (Int8Vec768.codes / .scale).  out_scales is used
+ * only for INT8. */
+int mrl_rerank_store_download(mrl_ctx *ctx, const mrl_rerank_store *store, void *out_rows,
+                              uint16_t *out_scales);
+
+/* QueryPipeline::rerank_exact_rows (src/pipeline.rs:157-169), and the
+ * precision loop (src/retrieval_bench.rs:739-745) at the store's precision,
+ * for n_queries queries in one call.  Query q (queries + q*dims) scores its
+ * counts[q] candidate rows cand_rows[q*stride ..], which are then stably
+ * sorted by score, descending, into out_rows / out_scores row q (stride
+ * entries per row; counts[q] of them written).  Host buffers; returns when
+ * done.  stride <= MRL_MAX_SHORTLIST.  MRL_ERR_NAN where the reference's
+ * partial_cmp().unwrap() would panic, MRL_ERR_INVALID_ARG for a row >=
+ * n_rows (the reference's slice index would panic). */
+int mrl_rerank_rows(mrl_ctx *ctx, const mrl_rerank_store *store, const float *queries, uint32_t n_queries,
+                    uint32_t dims, const uint64_t *cand_rows, const uint32_t *counts, uint32_t stride,
+                    uint64_t *out_rows, float *out_scores);
+
+/* scored_hits_to_row_ids + rerank (src/pipeline.rs:157-180, the bench's
+ * scan-then-rerank, src/retrieval_bench.rs:736-745) on the device-resident
+ * shortlists of the last mrl_scan_async on res, without a host round trip.
+ * Candidates are each query's hits in hit order (row = block * 64 + slot);
+ * the queries are those the scan's plans were built from (the plans must
+ * still exist).  out_rows / out_scores: n_queries x K, out_counts n_queries
+ * (host; any may be null).  Resolves a pending scan like mrl_results_fetch
+ * first (MRL_ERR_NAN if the scan itself failed so). */
+int mrl_results_rerank(mrl_ctx *ctx, mrl_results *res, const mrl_rerank_store *store, uint64_t *out_rows,
+                       float *out_scores, uint32_t *out_counts);
+
+/* ---------------------------------------------------------------- */
 /* kernel timing (no reference counterpart; the reference times     */
 /* scans with Instant, src/pipeline.rs:85-95)                       */
 /* ---------------------------------------------------------------- */
@@ -247,7 +301,9 @@ typedef enum mrl_kernel_kind {
   MRL_KERNEL_PLAN = 0,   /* batched query plan + LUT build */
   MRL_KERNEL_SCAN = 1,   /* one scan pass over a block range */
   MRL_KERNEL_SELECT = 2, /* final top-K selection */
-  MRL_KERNEL_THRESH = 3  /* per-query threshold between passes */
+  MRL_KERNEL_THRESH = 3, /* per-query threshold between passes */
+  MRL_KERNEL_RERANK = 4, /* rerank scoring of shortlist rows */
+  MRL_KERNEL_RERANK_SORT = 5 /* stable sort of the reranked shortlist */
 } mrl_kernel_kind;
 
 typedef struct mrl_kernel_time {
@@ -259,7 +315,7 @@ typedef struct mrl_kernel_time {
   uint32_t reserved;
 } mrl_kernel_time;
 
-/* While enabled, every plan / scan-pass / threshold / select launch on the
+/* While enabled, every plan / scan-pass / threshold / select / rerank launch on the
  * context records its kernel start and end (events written by the dispatch). */
 int mrl_ctx_set_profiling(mrl_ctx *ctx, int enable);
 /* Waits for the stream, returns up to max recorded launches (oldest first),

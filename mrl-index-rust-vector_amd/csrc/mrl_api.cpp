@@ -171,6 +171,18 @@ struct mrl_results {
   mrl_scan_config last_cfg{};
   mrl_time_range last_time{};
   bool pending = false;
+  // rerank of the shortlists (allocated by the first mrl_results_rerank):
+  // scores/rows scratch, sorted rows/scores, status
+  void* d_rr = nullptr;
+};
+
+struct mrl_rerank_store {
+  mrl_ctx* ctx = nullptr;
+  int precision = 0;
+  uint64_t n_rows = 0;
+  uint32_t dims = 0;
+  void* d_data = nullptr;       // 768 dims: accumulator-major rows; else row-major f32
+  uint16_t* d_scales = nullptr; // int8: f16 scale bits per row
 };
 
 static void dev_free(void* p) {
@@ -623,6 +635,7 @@ static void results_free(mrl_results* r) {
   dev_free(r->d_err);
   dev_free(r->d_status);
   dev_free(r->d_stats);
+  dev_free(r->d_rr);
 }
 
 static const uint32_t kSegCap = 4096;  // kSegs * kSegCap = 65536 candidates per query and scan
@@ -843,11 +856,10 @@ static int dense_rerun(mrl_ctx* ctx, mrl_results* r, uint32_t q) {
                    : MRL_OK;
 }
 
-extern "C" int mrl_results_fetch(mrl_ctx* ctx, mrl_results* res, uint64_t* out_ids, float* out_scores,
-                                 uint32_t* out_counts, mrl_scan_stats* stats) {
-  if (!ctx || !res) return fail(MRL_ERR_INVALID_ARG, "null argument");
-  std::lock_guard<std::mutex> g(ctx->mu);
-  HIP_TRY(hipSetDevice(ctx->device));
+// Waits for the last scan on res; queries whose candidate lists overflowed are
+// re-run densely.  MRL_ERR_NAN if any query saw a NaN survivor.  Caller holds
+// the context lock.
+static int resolve_pending(mrl_ctx* ctx, mrl_results* res) {
   HIP_TRY(hipStreamSynchronize(ctx->stream));
   const uint32_t n_q = res->last_plans ? res->last_plans->n_q : 0;
   bool nan = false;
@@ -865,6 +877,17 @@ extern "C" int mrl_results_fetch(mrl_ctx* ctx, mrl_results* res, uint64_t* out_i
   }
   res->pending = false;
   if (nan) return fail(MRL_ERR_NAN, "NaN score among scan survivors (Shortlist::into_sorted would panic)");
+  return MRL_OK;
+}
+
+extern "C" int mrl_results_fetch(mrl_ctx* ctx, mrl_results* res, uint64_t* out_ids, float* out_scores,
+                                 uint32_t* out_counts, mrl_scan_stats* stats) {
+  if (!ctx || !res) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  int rc = resolve_pending(ctx, res);
+  if (rc) return rc;
+  const uint32_t n_q = res->last_plans ? res->last_plans->n_q : 0;
   const size_t K = res->k;
   if (out_ids && n_q) HIP_TRY(hipMemcpy(out_ids, res->d_ids, n_q * K * sizeof(uint64_t), hipMemcpyDeviceToHost));
   if (out_scores && n_q) HIP_TRY(hipMemcpy(out_scores, res->d_scores, n_q * K * sizeof(float), hipMemcpyDeviceToHost));
@@ -951,6 +974,249 @@ extern "C" int mrl_scan_fixed_tau(mrl_ctx* ctx, const mrl_index* index, const mr
   cleanup();
   if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("fixed-tau scan: ") + hipGetErrorString(e));
   return MRL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// post-scan rerank
+// ---------------------------------------------------------------------------
+static size_t store_row_bytes(int precision, uint32_t dims) {
+  return precision == MRL_RERANK_FP32 ? (size_t)dims * 4 : precision == MRL_RERANK_FP16 ? 768 * 2 : 768;
+}
+
+extern "C" int mrl_rerank_store_create(mrl_ctx* ctx, const float* rows, int rows_on_device, uint64_t n_rows,
+                                       uint32_t dims, int precision, mrl_rerank_store** out) {
+  if (!ctx || !out || (n_rows && !rows)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  *out = nullptr;
+  if (precision != MRL_RERANK_FP32 && precision != MRL_RERANK_FP16 && precision != MRL_RERANK_INT8)
+    return fail(MRL_ERR_INVALID_ARG, "unknown rerank precision");
+  if (dims == 0 || dims > MRL_MAX_DIMS) return fail(MRL_ERR_INVALID_ARG, "dims must be in [1, MRL_MAX_DIMS]");
+  if (precision != MRL_RERANK_FP32 && dims != 768)
+    return fail(MRL_ERR_INVALID_ARG, "fp16 / int8 rerank rows need 768 dims");  // lowprec.rs:50,73
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  std::unique_ptr<mrl_rerank_store> st(new mrl_rerank_store());
+  st->ctx = ctx;
+  st->precision = precision;
+  st->n_rows = n_rows;
+  st->dims = dims;
+  const size_t rb = store_row_bytes(precision, dims);
+  float* staging = nullptr;
+  auto cleanup = [&]() {
+    dev_free(st->d_data);
+    dev_free(st->d_scales);
+    dev_free(staging);
+  };
+  if (hipMalloc(&st->d_data, std::max<size_t>(n_rows * rb, 16)) != hipSuccess ||
+      (precision == MRL_RERANK_INT8 &&
+       hipMalloc(&st->d_scales, std::max<size_t>(n_rows * 2, 16)) != hipSuccess)) {
+    cleanup();
+    return fail(MRL_ERR_OUT_OF_MEMORY, "rerank store");
+  }
+  hipError_t e = hipSuccess;
+  if (dims != 768) {  // fp32 rows kept row-major
+    e = hipMemcpyAsync(st->d_data, rows, n_rows * rb, rows_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                       ctx->stream);
+  } else if (rows_on_device) {
+    e = launch_rerank_store(rows, n_rows, precision, st->d_data, st->d_scales, ctx->stream);
+  } else if (n_rows) {
+    // host rows go through a bounded device staging buffer
+    const uint64_t chunk = std::min<uint64_t>(n_rows, 1ull << 16);
+    if (hipMalloc(&staging, chunk * 768 * sizeof(float)) != hipSuccess) {
+      cleanup();
+      return fail(MRL_ERR_OUT_OF_MEMORY, "rerank store staging");
+    }
+    for (uint64_t r = 0; r < n_rows && e == hipSuccess; r += chunk) {
+      const uint64_t nr = std::min(chunk, n_rows - r);
+      e = hipMemcpyAsync(staging, rows + r * 768, nr * 768 * sizeof(float), hipMemcpyHostToDevice, ctx->stream);
+      if (e == hipSuccess)
+        e = launch_rerank_store(staging, nr, precision, static_cast<uint8_t*>(st->d_data) + r * rb,
+                                st->d_scales ? st->d_scales + r : nullptr, ctx->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);  // staging is reused
+    }
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  dev_free(staging);
+  staging = nullptr;
+  if (e != hipSuccess) {
+    cleanup();
+    return fail(MRL_ERR_HIP, std::string("rerank store: ") + hipGetErrorString(e));
+  }
+  *out = st.release();
+  return MRL_OK;
+}
+
+extern "C" void mrl_rerank_store_destroy(mrl_rerank_store* store) {
+  if (!store) return;
+  (void)hipSetDevice(store->ctx->device);
+  (void)hipStreamSynchronize(store->ctx->stream);
+  dev_free(store->d_data);
+  dev_free(store->d_scales);
+  delete store;
+}
+
+extern "C" int mrl_rerank_store_download(mrl_ctx* ctx, const mrl_rerank_store* store, void* out_rows,
+                                         uint16_t* out_scales) {
+  if (!ctx || !store || (store->n_rows && !out_rows)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (store->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "store belongs to another context");
+  if (store->precision == MRL_RERANK_INT8 && store->n_rows && !out_scales)
+    return fail(MRL_ERR_INVALID_ARG, "int8 store needs out_scales");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  const size_t rb = store_row_bytes(store->precision, store->dims);
+  if (store->dims != 768) {
+    HIP_TRY(hipMemcpy(out_rows, store->d_data, store->n_rows * rb, hipMemcpyDeviceToHost));
+    return MRL_OK;
+  }
+  // accumulator-major (element 8t + j at 96j + t) back to row-major
+  const size_t es = rb / 768;
+  const uint64_t chunk = 4096;
+  std::vector<uint8_t> buf(chunk * rb);
+  uint8_t* dst = static_cast<uint8_t*>(out_rows);
+  for (uint64_t r = 0; r < store->n_rows; r += chunk) {
+    const uint64_t nr = std::min(chunk, store->n_rows - r);
+    HIP_TRY(hipMemcpy(buf.data(), static_cast<const uint8_t*>(store->d_data) + r * rb, nr * rb,
+                      hipMemcpyDeviceToHost));
+    for (uint64_t k = 0; k < nr; ++k)
+      for (uint32_t i = 0; i < 768; ++i)
+        memcpy(dst + (r + k) * rb + i * es, buf.data() + k * rb + ((i & 7u) * 96u + (i >> 3)) * es, es);
+  }
+  if (store->precision == MRL_RERANK_INT8)
+    HIP_TRY(hipMemcpy(out_scales, store->d_scales, store->n_rows * 2, hipMemcpyDeviceToHost));
+  return MRL_OK;
+}
+
+// Sizes of the rerank buffers for n_q lists of `stride` entries, carved from
+// one allocation: score f32, row u64, out_rows u64, out_scores f32, status u32.
+struct RerankBuffers {
+  float* score;
+  uint64_t* row;
+  uint64_t* out_rows;
+  float* out_scores;
+  uint32_t* status;
+};
+static size_t rerank_bytes(uint32_t n_q, uint32_t stride) {
+  return (size_t)n_q * stride * 24 + (size_t)n_q * 4 + 64;
+}
+static RerankBuffers rerank_carve(void* base, uint32_t n_q, uint32_t stride) {
+  const size_t n = (size_t)n_q * stride;
+  uint8_t* p = static_cast<uint8_t*>(base);
+  RerankBuffers b;
+  b.row = reinterpret_cast<uint64_t*>(p);
+  b.out_rows = reinterpret_cast<uint64_t*>(p + n * 8);
+  b.score = reinterpret_cast<float*>(p + n * 16);
+  b.out_scores = reinterpret_cast<float*>(p + n * 20);
+  b.status = reinterpret_cast<uint32_t*>(p + n * 24);
+  return b;
+}
+
+static int status_error(const std::vector<uint32_t>& st) {
+  uint32_t all = 0;
+  for (uint32_t v : st) all |= v;
+  if (all & 2u) return fail(MRL_ERR_INVALID_ARG, "candidate row out of range of the rerank store");
+  if (all & 1u) return fail(MRL_ERR_NAN, "NaN rerank score (partial_cmp().unwrap() would panic)");
+  return MRL_OK;
+}
+
+// Enqueue score + sort.  Caller holds the lock.
+static int enqueue_rerank(mrl_ctx* ctx, const mrl_rerank_store* st, const float* d_queries, uint32_t n_q,
+                          const uint64_t* d_cand, int cand_ids, const uint32_t* d_counts, uint32_t stride,
+                          const RerankBuffers& b) {
+  RerankArgs a{};
+  a.data = st->d_data;
+  a.scales = st->d_scales;
+  a.n_rows = st->n_rows;
+  a.dims = st->dims;
+  a.precision = st->precision;
+  a.queries = d_queries;
+  a.cand = d_cand;
+  a.counts = d_counts;
+  a.stride = stride;
+  a.n_q = n_q;
+  a.cand_ids = cand_ids;
+  a.score = b.score;
+  a.row = b.row;
+  a.out_rows = b.out_rows;
+  a.out_scores = b.out_scores;
+  a.status = b.status;
+  ProfScope p1(ctx, MRL_KERNEL_RERANK, 0, 0, n_q);
+  ProfScope p2(ctx, MRL_KERNEL_RERANK_SORT, 0, 0, n_q);
+  HIP_TRY(launch_rerank(a, ctx->stream, p1.ev(), p2.ev()));
+  p1.commit(n_q != 0 && stride != 0);
+  p2.commit(n_q != 0 && stride != 0);
+  return MRL_OK;
+}
+
+extern "C" int mrl_rerank_rows(mrl_ctx* ctx, const mrl_rerank_store* store, const float* queries, uint32_t n_q,
+                               uint32_t dims, const uint64_t* cand_rows, const uint32_t* counts, uint32_t stride,
+                               uint64_t* out_rows, float* out_scores) {
+  if (!ctx || !store) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (store->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "store belongs to another context");
+  if (dims != store->dims) return fail(MRL_ERR_INVALID_ARG, "query dims differ from the store's");
+  if (stride > MRL_MAX_SHORTLIST) return fail(MRL_ERR_INVALID_ARG, "stride above MRL_MAX_SHORTLIST");
+  if (n_q == 0 || stride == 0) return MRL_OK;
+  if (!queries || !cand_rows || !counts || !out_rows || !out_scores) return fail(MRL_ERR_INVALID_ARG, "null buffer");
+  for (uint32_t q = 0; q < n_q; ++q) {
+    if (counts[q] > stride) return fail(MRL_ERR_INVALID_ARG, "count above stride");
+    for (uint32_t i = 0; i < counts[q]; ++i)
+      if (cand_rows[(size_t)q * stride + i] >= store->n_rows)
+        return fail(MRL_ERR_INVALID_ARG, "candidate row out of range of the rerank store");
+  }
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  const size_t nc = (size_t)n_q * stride;
+  const size_t qbytes = (size_t)n_q * dims * 4;
+  const size_t bytes = rerank_bytes(n_q, stride) + qbytes + nc * 8 + (size_t)n_q * 4 + 64;
+  uint8_t* base = nullptr;
+  if (hipMalloc(&base, bytes) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "rerank buffers");
+  const RerankBuffers b = rerank_carve(base, n_q, stride);
+  uint8_t* p = base + ((rerank_bytes(n_q, stride) + 15) & ~(size_t)15);
+  uint64_t* d_cand = reinterpret_cast<uint64_t*>(p);
+  float* d_q = reinterpret_cast<float*>(p + nc * 8);
+  uint32_t* d_counts = reinterpret_cast<uint32_t*>(p + nc * 8 + qbytes);
+  hipError_t e = hipMemcpyAsync(d_cand, cand_rows, nc * 8, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(d_q, queries, qbytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(d_counts, counts, (size_t)n_q * 4, hipMemcpyHostToDevice, ctx->stream);
+  int rc = MRL_OK;
+  if (e == hipSuccess) rc = enqueue_rerank(ctx, store, d_q, n_q, d_cand, 0, d_counts, stride, b);
+  std::vector<uint32_t> st(n_q);
+  if (e == hipSuccess && !rc) e = hipMemcpyAsync(out_rows, b.out_rows, nc * 8, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess && !rc) e = hipMemcpyAsync(out_scores, b.out_scores, nc * 4, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess && !rc) e = hipMemcpyAsync(st.data(), b.status, (size_t)n_q * 4, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  dev_free(base);
+  if (rc) return rc;
+  if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("rerank: ") + hipGetErrorString(e));
+  return status_error(st);
+}
+
+extern "C" int mrl_results_rerank(mrl_ctx* ctx, mrl_results* res, const mrl_rerank_store* store, uint64_t* out_rows,
+                                  float* out_scores, uint32_t* out_counts) {
+  if (!ctx || !res || !store) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (res->ctx != ctx || store->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "objects belong to another context");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  const mrl_plans* plans = res->last_plans;
+  if (!plans) return fail(MRL_ERR_INVALID_ARG, "no scan was enqueued on these results");
+  if (plans->dims != store->dims) return fail(MRL_ERR_INVALID_ARG, "query dims differ from the store's");
+  int rc = resolve_pending(ctx, res);
+  if (rc) return rc;
+  const uint32_t n_q = plans->n_q, K = res->k;
+  if (n_q == 0) return MRL_OK;
+  if (!res->d_rr && hipMalloc(&res->d_rr, rerank_bytes(res->n_q, K)) != hipSuccess) {
+    res->d_rr = nullptr;
+    return fail(MRL_ERR_OUT_OF_MEMORY, "rerank buffers");
+  }
+  const RerankBuffers b = rerank_carve(res->d_rr, res->n_q, K);
+  if ((rc = enqueue_rerank(ctx, store, plans->d_queries, n_q, res->d_ids, 1, res->d_counts, K, b))) return rc;
+  std::vector<uint32_t> st(n_q);
+  const size_t nc = (size_t)n_q * K;
+  HIP_TRY(hipMemcpyAsync(st.data(), b.status, (size_t)n_q * 4, hipMemcpyDeviceToHost, ctx->stream));
+  if (out_rows) HIP_TRY(hipMemcpyAsync(out_rows, b.out_rows, nc * 8, hipMemcpyDeviceToHost, ctx->stream));
+  if (out_scores) HIP_TRY(hipMemcpyAsync(out_scores, b.out_scores, nc * 4, hipMemcpyDeviceToHost, ctx->stream));
+  if (out_counts) HIP_TRY(hipMemcpyAsync(out_counts, res->d_counts, (size_t)n_q * 4, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return status_error(st);
 }
 
 // ---------------------------------------------------------------------------

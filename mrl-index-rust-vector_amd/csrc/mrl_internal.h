@@ -172,6 +172,27 @@ struct EncodeArgs {
 };
 hipError_t launch_encode(const EncodeArgs& a, hipStream_t s);
 
+// Post-scan rerank (mrl_rerank.hip).  At 768 dims the store rows are
+// accumulator-major: element i = 8t + j at position 96j + t.
+struct RerankArgs {
+  const void* data;         // store rows: f32 / f16 bits / int8 codes
+  const uint16_t* scales;   // int8: f16 scale bits per row
+  uint64_t n_rows;
+  uint32_t dims;
+  int32_t precision;        // mrl_rerank_precision
+  const float* queries;     // [n_q][dims]
+  const uint64_t* cand;     // [n_q][stride]: row ids, or VectorId::as_u64 ids when cand_ids
+  const uint32_t* counts;   // [n_q], each <= stride
+  uint32_t stride;          // <= MRL_MAX_SHORTLIST
+  uint32_t n_q;
+  int32_t cand_ids;
+  float* score;             // scratch [n_q][stride]
+  uint64_t* row;            // scratch [n_q][stride]
+  uint64_t* out_rows;       // [n_q][stride], sorted
+  float* out_scores;
+  uint32_t* status;         // [n_q]: bit 0 NaN score, bit 1 row out of range
+};
+
 // Launchers (mrl_kernels.hip).
 // Optional start/stop events written by the dispatch itself (kernel-only
 // duration, the same interval a kernel-trace profiler reports).
@@ -185,5 +206,11 @@ hipError_t launch_plan(const PlanArgs& a, hipStream_t s, const LaunchEvents& ev 
 hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_thresh(const ThreshArgs& a, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
+
+// mrl_rerank.hip: build a 768-dim store from f32 rows; score + sort.
+hipError_t launch_rerank_store(const float* rows, uint64_t n_rows, int precision, void* data, uint16_t* scales,
+                               hipStream_t s);
+hipError_t launch_rerank(const RerankArgs& a, hipStream_t s, const LaunchEvents& ev_score = {},
+                         const LaunchEvents& ev_sort = {});
 
 }  // namespace mrl

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "mrl_half.h"
 #include "mrl_internal.h"
 
 namespace mrl {
@@ -16,11 +17,6 @@ namespace mrl {
 // ---------------------------------------------------------------------------
 // small helpers
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float h2f(uint16_t h) {
-  _Float16 x = __builtin_bit_cast(_Float16, h);
-  return (float)x;
-}
-
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
 __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {

@@ -129,7 +129,7 @@ class KernelTimeC(C.Structure):
     ]
 
 
-KERNEL_PLAN, KERNEL_SCAN, KERNEL_SELECT, KERNEL_THRESH = 0, 1, 2, 3
+KERNEL_PLAN, KERNEL_SCAN, KERNEL_SELECT, KERNEL_THRESH, KERNEL_RERANK, KERNEL_RERANK_SORT = 0, 1, 2, 3, 4, 5
 
 
 class SynthSpecC(C.Structure):
@@ -194,6 +194,11 @@ SIGNATURES = {
     "mrl_device_free": (None, [_P, _P]),
     "mrl_copy_to_device": (C.c_int, [_P, _P, _P, C.c_size_t]),
     "mrl_copy_to_host": (C.c_int, [_P, _P, _P, C.c_size_t]),
+    "mrl_rerank_store_create": (C.c_int, [_P, _P, C.c_int, C.c_uint64, C.c_uint32, C.c_int, _PP]),
+    "mrl_rerank_store_destroy": (None, [_P]),
+    "mrl_rerank_store_download": (C.c_int, [_P, _P, _P, C.POINTER(C.c_uint16)]),
+    "mrl_rerank_rows": (C.c_int, [_P, _P, _F, C.c_uint32, C.c_uint32, _U64, _U32, C.c_uint32, _U64, _F]),
+    "mrl_results_rerank": (C.c_int, [_P, _P, _P, _U64, _F, _U32]),
     "mrl_synth_docs": (C.c_int, [C.POINTER(SynthSpecC), C.c_uint64, C.c_uint64, C.c_int, _F]),
     "mrl_synth_queries": (C.c_int, [C.POINTER(SynthSpecC), C.c_uint64, C.c_float, C.c_int, C.c_uint32, _F,
                                     _U64]),

@@ -11,6 +11,7 @@ import numpy as np
 from .block import VECTORS_PER_BLOCK, VectorId
 from .config import EngineConfig, MidCodec, PrefixCodec
 from .eden import EdenFit
+from .lowprec import RerankStore, rerank_rows
 from .scan import DeviceIndex, QueryPlan, ScanStats, ScoredHit, scan_blocks_stats
 
 
@@ -65,11 +66,23 @@ class QueryPipeline:
 
     @staticmethod
     def rerank_exact_rows(query, candidate_ids, corpus_row):
-        """pipeline.rs:157-169"""
-        q = np.asarray(query, dtype=np.float32)
-        ranked = [(i, float(np.dot(q, np.asarray(corpus_row(i), dtype=np.float32)))) for i in candidate_ids]
-        ranked.sort(key=lambda t: -t[1])
-        return ranked
+        """pipeline.rs:157-169 on the GPU: (row, dot(query, row)) for every
+        candidate, stably sorted by score, descending.  ``corpus_row`` is a
+        RerankStore (rows resident in HBM), or a callable row -> vector as in
+        the reference, whose rows are gathered into a transient fp32 store."""
+        ids = [int(i) for i in candidate_ids]
+        if isinstance(corpus_row, RerankStore):
+            return rerank_rows(query, ids, corpus_row)
+        if not ids:
+            return []
+        uniq = sorted(set(ids))
+        pos = {r: k for k, r in enumerate(uniq)}
+        store = RerankStore.create(np.stack([np.asarray(corpus_row(r), dtype=np.float32) for r in uniq]))
+        try:
+            ranked = rerank_rows(query, [pos[i] for i in ids], store)
+        finally:
+            store.close()
+        return [(uniq[r], s) for r, s in ranked]
 
 
 def scored_hits_to_row_ids(hits: List[ScoredHit]) -> List[int]:

@@ -326,6 +326,65 @@ def scan_blocks(blocks, plan: QueryPlan, cfg, time_lo=None, time_hi=None):
     return scan_blocks_stats(blocks, plan, cfg, time_lo, time_hi, None)
 
 
+class DeviceResults:
+    """Device-resident shortlists of an asynchronous scan (mrl_results): scan
+    now, then fetch the hits and / or rerank them on the GPU without the
+    shortlist leaving HBM."""
+
+    def __init__(self, n_queries: int, k: int, device: Optional[Device] = None):
+        self.device = device or default_device()
+        h = C.c_void_p()
+        _lib.check(_lib.lib.mrl_results_create(self.device.handle, n_queries, k, C.byref(h)))
+        self._h = h
+        self.n_queries = n_queries
+        self.k = k
+        self._plan = None
+        self._index = None
+
+    def scan(self, index: "DeviceIndex", plan: QueryPlan, cfg, time_lo=None, time_hi=None) -> None:
+        """Enqueue the scan of every plan row (mrl_scan_async); returns at once."""
+        c = _scan_cfg(cfg).to_c()
+        t = _time(time_lo, time_hi)
+        _lib.check(_lib.lib.mrl_scan_async(self.device.handle, index.handle, plan.handle, C.byref(c), C.byref(t),
+                                           self._h))
+        self._plan, self._index = plan, index  # the results refer to both until fetched
+        self._nq = plan.n_queries
+
+    def fetch(self) -> ScanResult:
+        nq, k = self._nq, self.k
+        ids = np.zeros((nq, k), dtype=np.uint64)
+        scores = np.zeros((nq, k), dtype=np.float32)
+        counts = np.zeros(nq, dtype=np.uint32)
+        st = _lib.ScanStatsC()
+        _lib.check(_lib.lib.mrl_results_fetch(self.device.handle, self._h, _lib.u64ptr(ids), _lib.fptr(scores),
+                                              _lib.u32ptr(counts), C.byref(st)))
+        stats = ScanStats(st.blocks, st.active_vecs, st.after_prefix, st.after_s1, st.after_s4_budget, st.pushed)
+        return ScanResult(ids, scores, counts, stats)
+
+    def rerank(self, store) -> "tuple[np.ndarray, np.ndarray, np.ndarray]":
+        """scored_hits_to_row_ids + rerank_exact_rows (pipeline.rs:157-180) of
+        every query's shortlist against ``store`` (a RerankStore): returns
+        (rows (n_q, K), scores (n_q, K), counts (n_q,))."""
+        nq, k = self._nq, self.k
+        rows = np.zeros((nq, k), dtype=np.uint64)
+        scores = np.zeros((nq, k), dtype=np.float32)
+        counts = np.zeros(nq, dtype=np.uint32)
+        _lib.check(_lib.lib.mrl_results_rerank(self.device.handle, self._h, store.handle, _lib.u64ptr(rows),
+                                               _lib.fptr(scores), _lib.u32ptr(counts)))
+        return rows, scores, counts
+
+    def close(self):
+        if self._h:
+            _lib.lib.mrl_results_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 @dataclass
 class StageTrace:
     """Per (query, block) output of the fixed-threshold diagnostic scan:

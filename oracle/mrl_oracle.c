@@ -1148,3 +1148,89 @@ void ora_exhaustive_scores(const uint8_t *blocks, uint64_t n_blocks, const ora_p
     }
   }
 }
+
+
+/* ========================================================================== */
+/* post-scan rerank                                                            */
+/* ========================================================================== */
+
+/* embed.rs:115-152 */
+float ora_dot(const float *a, const float *b, uint32_t n) {
+  if (n == 768) {
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t i = 0; i < 768; i += 8)
+      for (int j = 0; j < 8; ++j) acc[j] += a[i + j] * b[i + j];
+    return acc[0] + acc[1] + acc[2] + acc[3] + acc[4] + acc[5] + acc[6] + acc[7];
+  }
+  float s = -0.0f;
+  for (uint32_t i = 0; i < n; ++i) s += a[i] * b[i];
+  return s;
+}
+
+/* embed.rs:158-180, lowprec.rs:49-61 */
+float ora_dot_fp16_768(const float *q, const float *v) {
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t i = 0; i < 768; i += 8)
+    for (int j = 0; j < 8; ++j) acc[j] += q[i + j] * ora_f16_to_f32(ora_f32_to_f16(v[i + j]));
+  return acc[0] + acc[1] + acc[2] + acc[3] + acc[4] + acc[5] + acc[6] + acc[7];
+}
+
+/* lowprec.rs:72-94 */
+void ora_int8_quantize_768(const float *v, int8_t *codes, uint16_t *scale_f16) {
+  float max_abs = 0.0f;
+  for (int i = 0; i < 768; ++i) max_abs = rmax(max_abs, fabsf(v[i]));
+  const float scale = max_abs < 1e-12f ? 0.0f : max_abs / 127.0f;
+  const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+  for (int i = 0; i < 768; ++i) {
+    float q = roundf(v[i] * inv);
+    if (q < -127.0f) q = -127.0f; /* f32::clamp; NaN stays NaN */
+    if (q > 127.0f) q = 127.0f;
+    int32_t iq = (q == q) ? (int32_t)q : 0; /* `as i32`: NaN -> 0 */
+    codes[i] = (int8_t)iq;
+  }
+  *scale_f16 = ora_f32_to_f16(scale);
+}
+
+/* embed.rs:184-206 */
+float ora_dot_int8_768(const float *q, const int8_t *codes, uint16_t scale_f16) {
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t i = 0; i < 768; i += 8)
+    for (int j = 0; j < 8; ++j) acc[j] += q[i + j] * (float)codes[i + j];
+  return (acc[0] + acc[1] + acc[2] + acc[3] + acc[4] + acc[5] + acc[6] + acc[7]) * ora_f16_to_f32(scale_f16);
+}
+
+/* lowprec.rs:103-121 */
+float ora_rerank_dot(int precision, const float *q, const float *row, uint32_t n) {
+  if (precision == ORA_RERANK_FP16) return ora_dot_fp16_768(q, row);
+  if (precision == ORA_RERANK_INT8) {
+    int8_t codes[768];
+    uint16_t sc;
+    ora_int8_quantize_768(row, codes, &sc);
+    return ora_dot_int8_768(q, codes, sc);
+  }
+  return ora_dot(q, row, n);
+}
+
+/* pipeline.rs:157-169: map then stable sort_by(b.1.partial_cmp(&a.1).unwrap()) */
+int ora_rerank(int precision, const float *q, const float *rows, uint32_t n, const uint64_t *cand_rows,
+               uint32_t n_cand, uint64_t *out_rows, float *out_scores) {
+  for (uint32_t i = 0; i < n_cand; ++i) {
+    out_rows[i] = cand_rows[i];
+    out_scores[i] = ora_rerank_dot(precision, q, rows + cand_rows[i] * (uint64_t)n, n);
+    if (out_scores[i] != out_scores[i]) return -ORA_ERR_NAN;
+  }
+  /* stable insertion sort, descending */
+  for (uint32_t i = 1; i < n_cand; ++i) {
+    const float s = out_scores[i];
+    const uint64_t r = out_rows[i];
+    uint32_t j = i;
+    while (j > 0 && out_scores[j - 1] < s) {
+      out_scores[j] = out_scores[j - 1];
+      out_rows[j] = out_rows[j - 1];
+      --j;
+    }
+    out_scores[j] = s;
+    out_rows[j] = r;
+  }
+  return 0;
+}

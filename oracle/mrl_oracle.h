@@ -30,6 +30,9 @@
  *    N(0,1) Lloyd-Max centroid; the literal f32 bits are as read.
  *  - ora_scan_blocks with sharding on: which of several exactly tied scores
  *    survive at the K boundary (Rayon's merge order, scan.rs:846-865).
+ *  - ora_dot for n != 768: the sign of an exactly zero sum (Sum for f32
+ *    starts from -0.0 in the Rust releases that write Cargo.lock version 4,
+ *    the reference's; older releases start from +0.0).
  */
 #ifndef MRL_ORACLE_H
 #define MRL_ORACLE_H
@@ -217,6 +220,27 @@ int64_t ora_scan_blocks(const uint8_t *blocks, uint64_t n_blocks, const ora_plan
 void ora_exhaustive_scores(const uint8_t *blocks, uint64_t n_blocks, const ora_plan *plan,
                            const ora_scan_config *cfg, int has_lo, uint32_t lo, int has_hi,
                            uint32_t hi, float *out_scores, uint8_t *out_valid);
+
+/* ---- post-scan rerank (src/pipeline.rs:157-169, src/lowprec.rs:19-121,
+ *      src/embed.rs:115-206) ---- */
+enum { ORA_RERANK_FP32 = 0, ORA_RERANK_FP16 = 1, ORA_RERANK_INT8 = 2 };
+/* dot (embed.rs:115-124): dot_768 for n == 768 (eight accumulators over
+ * i mod 8, then acc0 + ... + acc7), otherwise the sequential sum of x*y
+ * starting from -0.0 (Sum for f32). */
+float ora_dot(const float *a, const float *b, uint32_t n);
+/* dot_f16_768 (embed.rs:158-180) of q with Fp16Vec768::from_f32(v) */
+float ora_dot_fp16_768(const float *q, const float *v);
+/* Int8Vec768::from_f32 (lowprec.rs:72-94): codes[768] and the f16 scale bits */
+void ora_int8_quantize_768(const float *v, int8_t *codes, uint16_t *scale_f16);
+/* dot_i8_768 (embed.rs:184-206) with the f16 scale read back as f32 */
+float ora_dot_int8_768(const float *q, const int8_t *codes, uint16_t scale_f16);
+/* rerank_dot (lowprec.rs:103-121): fp16 and int8 need n == 768 */
+float ora_rerank_dot(int precision, const float *q, const float *row, uint32_t n);
+/* rerank_exact_rows / the precision loop (retrieval_bench.rs:736-745): score
+ * every candidate row, stable sort by score descending.  rows: [n_rows][n].
+ * Returns 0, or -ORA_ERR_NAN when partial_cmp().unwrap() would panic. */
+int ora_rerank(int precision, const float *q, const float *rows, uint32_t n, const uint64_t *cand_rows,
+               uint32_t n_cand, uint64_t *out_rows, float *out_scores);
 
 #ifdef __cplusplus
 }

@@ -103,7 +103,15 @@ _SIGS = {
                                     C.c_uint32, C.c_int, C.c_uint32, _U64, _F, C.POINTER(ScanStatsC)]),
     "ora_exhaustive_scores": (None, [_U8, C.c_uint64, C.POINTER(PlanC), C.POINTER(ScanConfigC), C.c_int,
                                      C.c_uint32, C.c_int, C.c_uint32, _F, _U8]),
+    "ora_dot": (C.c_float, [_F, _F, C.c_uint32]),
+    "ora_dot_fp16_768": (C.c_float, [_F, _F]),
+    "ora_int8_quantize_768": (None, [_F, C.POINTER(C.c_int8), C.POINTER(C.c_uint16)]),
+    "ora_dot_int8_768": (C.c_float, [_F, C.POINTER(C.c_int8), C.c_uint16]),
+    "ora_rerank_dot": (C.c_float, [C.c_int, _F, _F, C.c_uint32]),
+    "ora_rerank": (C.c_int, [C.c_int, _F, _F, C.c_uint32, _U64, C.c_uint32, _U64, _F]),
 }
+
+RERANK_FP32, RERANK_FP16, RERANK_INT8 = 0, 1, 2
 
 
 def _load():
@@ -226,3 +234,52 @@ def exhaustive_topk(blocks, plan, cfg, k, lo=None, hi=None):
 def plan_to_dict(p):
     return {name: np.ctypeslib.as_array(getattr(p, name)).copy() if hasattr(getattr(p, name), "_length_")
             else getattr(p, name) for name, _ in PLAN_FIELDS}
+
+
+# ---- post-scan rerank (src/pipeline.rs:157-169, src/lowprec.rs, src/embed.rs:115-206) ----
+def dot(a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return lib.ora_dot(fp(a), fp(b), a.size)
+
+
+def dot_fp16_768(q, v):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    return lib.ora_dot_fp16_768(fp(q), fp(v))
+
+
+def int8_quantize_768(v):
+    """Int8Vec768::from_f32 -> (codes int8[768], scale f16 bits)."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    codes = np.zeros(768, dtype=np.int8)
+    sc = C.c_uint16(0)
+    lib.ora_int8_quantize_768(fp(v), codes.ctypes.data_as(C.POINTER(C.c_int8)), C.byref(sc))
+    return codes, sc.value
+
+
+def dot_int8_768(q, codes, scale_bits):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    return lib.ora_dot_int8_768(fp(q), codes.ctypes.data_as(C.POINTER(C.c_int8)), scale_bits)
+
+
+def rerank_dot(precision, q, row):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    row = np.ascontiguousarray(row, dtype=np.float32)
+    return lib.ora_rerank_dot(precision, fp(q), fp(row), q.size)
+
+
+def rerank(precision, q, rows, cand):
+    """rerank_exact_rows at a precision: (rows, scores) sorted; None where the
+    reference would panic on a NaN score."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    rows = np.ascontiguousarray(rows, dtype=np.float32)
+    cand = np.ascontiguousarray(cand, dtype=np.uint64)
+    n = cand.size
+    out_r = np.zeros(max(n, 1), dtype=np.uint64)
+    out_s = np.zeros(max(n, 1), dtype=np.float32)
+    rc = lib.ora_rerank(precision, fp(q), fp(rows), rows.shape[1], u64p(cand), n, u64p(out_r), fp(out_s))
+    if rc != 0:
+        return None
+    return out_r[:n], out_s[:n]
