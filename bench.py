@@ -42,6 +42,8 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-rerank", action="store_true", help="skip the post-scan rerank leg")
+    ap.add_argument("--rerank-reps", type=int, default=100)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (PMC byte-counter calibration) and exit")
     args = ap.parse_args()
@@ -177,11 +179,104 @@ def main():
     }
 
     out["host_boundary"] = host_boundary_rate(L, _lib, dev, ix, queries, fit, w, ccfg, tr)
+    if not args.no_rerank:
+        out["rerank"] = rerank_leg(L, _lib, m, dev, w, step, res, queries, args.rerank_reps, n_threads,
+                                   not args.no_cpu_baseline)
 
     if not args.no_cpu_baseline:
         out["cpu_baseline"], out["parity_query0"] = cpu_baseline(w, blocks, queries, fit, ids[0], scores[0],
                                                                  int(counts[0]), args.cpu_seconds, n_threads)
     print(json.dumps(out), flush=True)
+
+
+def rerank_leg(L, _lib, m, dev, w, step, res, queries, reps, n_threads, with_cpu):
+    """Post-scan rerank of every query's shortlist, kept in HBM, at fp32 / fp16 /
+    int8 (the reference's precision bench, retrieval_bench.rs:736-745).
+    us_per_batch: host wall time of one mrl_results_rerank call after a
+    finished scan (launches, sync and the copy of the reranked lists to the
+    host).  kernel_*: dispatch-recorded durations of the score and sort
+    kernels; the score kernel's algorithmic bytes are the shortlisted rows at
+    the store's precision plus the query and the candidate ids."""
+    import numpy as np
+    if w.n_docs > 2_000_000:
+        return {"skipped": f"corpus rows for {w.n_docs} vectors are not generated by the bench"}
+    log(f"rerank: generating {w.n_docs} x {w.dims} f32 rows")
+    rows = __import__("mrl_index_amd.synth", fromlist=["docs"]).docs(w, 0, w.n_docs, n_threads)
+    nq, K = w.n_queries, w.k
+    r_rows = np.zeros((nq, K), dtype=np.uint64)
+    r_scores = np.zeros((nq, K), dtype=np.float32)
+    r_counts = np.zeros(nq, dtype=np.uint32)
+    out = {"queries_per_batch": nq, "k_cand": K}
+    row_bytes = {m.RerankPrecision.FP32: 4 * w.dims, m.RerankPrecision.FP16: 2 * w.dims,
+                 m.RerankPrecision.INT8: w.dims + 2}
+    for prec in (m.RerankPrecision.FP32, m.RerankPrecision.FP16, m.RerankPrecision.INT8):
+        if prec != m.RerankPrecision.FP32 and w.dims != 768:
+            continue
+        t0 = time.perf_counter()
+        store = m.RerankStore.create(rows, prec, dev)
+        t_store = time.perf_counter() - t0
+
+        def rerank():
+            _lib.check(L.mrl_results_rerank(dev.handle, res, store.handle, _lib.u64ptr(r_rows), _lib.fptr(r_scores),
+                                            _lib.u32ptr(r_counts)))
+        step()
+        for _ in range(5):
+            rerank()
+        wall = []
+        for _ in range(reps):
+            step()
+            dev.synchronize()
+            t0 = time.perf_counter()
+            rerank()
+            wall.append(time.perf_counter() - t0)
+        _lib.check(L.mrl_ctx_set_profiling(dev.handle, 1))
+        for _ in range(reps):
+            step()
+            rerank()
+        _lib.check(L.mrl_ctx_set_profiling(dev.handle, 0))
+        cap = 64 * reps + 64
+        kt = (_lib.KernelTimeC * cap)()
+        nrec = C.c_uint32()
+        _lib.check(L.mrl_ctx_profile_collect(dev.handle, kt, cap, C.byref(nrec)))
+        sc = [kt[i].ms for i in range(min(nrec.value, cap)) if kt[i].kind == _lib.KERNEL_RERANK]
+        so = [kt[i].ms for i in range(min(nrec.value, cap)) if kt[i].kind == _lib.KERNEL_RERANK_SORT]
+        n_cand = float(r_counts.sum())
+        alg = n_cand * (row_bytes[prec] + 8) + nq * 4 * w.dims
+        k_ms = float(np.mean(sc))
+        rec = {"store_build_s": round(t_store, 3), "us_per_batch": round(float(np.median(wall)) * 1e6, 2),
+               "kernel_score_us": round(k_ms * 1000, 3), "kernel_sort_us": round(float(np.mean(so)) * 1000, 3),
+               "score_algorithmic_bytes": alg,
+               "score_achieved_gb_s": round(alg / (k_ms / 1000.0) / 1e9, 1)}
+        if with_cpu:
+            hit_ids = np.zeros((nq, K), dtype=np.uint64)
+            _lib.check(L.mrl_results_fetch(dev.handle, res, _lib.u64ptr(hit_ids), None, None, None))
+            c0 = int(r_counts[0])
+            cand = (hit_ids[0, :c0] >> np.uint64(16)) * np.uint64(64) + (hit_ids[0, :c0] & np.uint64(0xFFFF))
+            rec["cpu_us_per_query"], rec["parity_query0"] = cpu_rerank_us(
+                prec, queries[0], rows, cand, r_rows[0, :c0], r_scores[0, :c0])
+        out[prec.as_str()] = rec
+        store.close()
+    del rows
+    return out
+
+
+def cpu_rerank_us(prec, q, rows, cand, gpu_rows, gpu_scores, budget_s=2.0):
+    """The oracle's restatement of rerank_exact_rows (one host thread) on query
+    0's shortlist (cand: its scan hits as rows, in hit order), timed; and
+    whether the GPU's reranked rows and scores for that query are identical."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ora
+    cand = np.ascontiguousarray(cand, dtype=np.uint64)
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or n == 0:
+        ref = ora.rerank(int(prec), q, rows, cand)
+        n += 1
+    us = round((time.perf_counter() - t0) / n * 1e6, 2)
+    ok = ref is not None and np.array_equal(ref[0], gpu_rows) and \
+        np.array_equal(ref[1].view(np.uint32), np.asarray(gpu_scores, dtype=np.float32).view(np.uint32))
+    return us, "identical" if ok else "MISMATCH"
 
 
 def host_boundary_rate(L, _lib, dev, ix, queries, fit, w, ccfg, tr, reps=20):

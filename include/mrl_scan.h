@@ -293,6 +293,29 @@ int mrl_rerank_rows(mrl_ctx *ctx, const mrl_rerank_store *store, const float *qu
 int mrl_results_rerank(mrl_ctx *ctx, mrl_results *res, const mrl_rerank_store *store, uint64_t *out_rows,
                        float *out_scores, uint32_t *out_counts);
 
+/* RingBuffer::search_exact (src/ring.rs:109-119) for n_queries queries:
+ * every pending (unflushed) row, n_pending x dims f32 in host memory, is
+ * scored with dot (src/embed.rs:115-124) against each query, stably sorted by
+ * score descending and cut at top_k.  Row q of out_local / out_scores holds
+ * min(top_k, n_pending) entries (index into the pending rows, score); that
+ * count goes to out_counts[q].  n_pending <= MRL_MAX_SHORTLIST.
+ * MRL_ERR_NAN where partial_cmp().unwrap() would panic. */
+int mrl_ring_search(mrl_ctx *ctx, const float *pending, uint32_t n_pending, uint32_t dims,
+                    const float *queries, uint32_t n_queries, uint32_t top_k, uint64_t *out_local,
+                    float *out_scores, uint32_t *out_counts);
+
+/* The ring merge of IndexEngine::query_filtered (src/engine.rs:584-594) on
+ * the device-resident shortlists of the last scan on res: each query's ring
+ * hits (search_exact with top_k = K) are pushed into its shortlist with
+ * Shortlist::push semantics (src/scan.rs:351-369) and the list re-sorted, in
+ * place; a later mrl_results_fetch returns the merged lists and
+ * mrl_results_rerank skips the ring hits as scored_hits_to_row_ids does.
+ * Ring hits carry VectorId::new(u32::MAX, local index) ids.  Which of several
+ * entries of exactly equal score is kept or comes first can differ from the
+ * reference's heap order, as for the scan itself. */
+int mrl_results_merge_ring(mrl_ctx *ctx, mrl_results *res, const float *pending, uint32_t n_pending,
+                           uint32_t dims);
+
 /* ---------------------------------------------------------------- */
 /* kernel timing (no reference counterpart; the reference times     */
 /* scans with Instant, src/pipeline.rs:85-95)                       */

@@ -983,17 +983,10 @@ static size_t store_row_bytes(int precision, uint32_t dims) {
   return precision == MRL_RERANK_FP32 ? (size_t)dims * 4 : precision == MRL_RERANK_FP16 ? 768 * 2 : 768;
 }
 
-extern "C" int mrl_rerank_store_create(mrl_ctx* ctx, const float* rows, int rows_on_device, uint64_t n_rows,
-                                       uint32_t dims, int precision, mrl_rerank_store** out) {
-  if (!ctx || !out || (n_rows && !rows)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+// Builds a store; caller holds the context lock and has set the device.
+static int store_create_locked(mrl_ctx* ctx, const float* rows, int rows_on_device, uint64_t n_rows, uint32_t dims,
+                               int precision, mrl_rerank_store** out) {
   *out = nullptr;
-  if (precision != MRL_RERANK_FP32 && precision != MRL_RERANK_FP16 && precision != MRL_RERANK_INT8)
-    return fail(MRL_ERR_INVALID_ARG, "unknown rerank precision");
-  if (dims == 0 || dims > MRL_MAX_DIMS) return fail(MRL_ERR_INVALID_ARG, "dims must be in [1, MRL_MAX_DIMS]");
-  if (precision != MRL_RERANK_FP32 && dims != 768)
-    return fail(MRL_ERR_INVALID_ARG, "fp16 / int8 rerank rows need 768 dims");  // lowprec.rs:50,73
-  std::lock_guard<std::mutex> g(ctx->mu);
-  HIP_TRY(hipSetDevice(ctx->device));
   std::unique_ptr<mrl_rerank_store> st(new mrl_rerank_store());
   st->ctx = ctx;
   st->precision = precision;
@@ -1014,8 +1007,9 @@ extern "C" int mrl_rerank_store_create(mrl_ctx* ctx, const float* rows, int rows
   }
   hipError_t e = hipSuccess;
   if (dims != 768) {  // fp32 rows kept row-major
-    e = hipMemcpyAsync(st->d_data, rows, n_rows * rb, rows_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
-                       ctx->stream);
+    if (n_rows)
+      e = hipMemcpyAsync(st->d_data, rows, n_rows * rb,
+                         rows_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream);
   } else if (rows_on_device) {
     e = launch_rerank_store(rows, n_rows, precision, st->d_data, st->d_scales, ctx->stream);
   } else if (n_rows) {
@@ -1035,23 +1029,41 @@ extern "C" int mrl_rerank_store_create(mrl_ctx* ctx, const float* rows, int rows
     }
   }
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  dev_free(staging);
-  staging = nullptr;
   if (e != hipSuccess) {
     cleanup();
     return fail(MRL_ERR_HIP, std::string("rerank store: ") + hipGetErrorString(e));
   }
+  dev_free(staging);
   *out = st.release();
   return MRL_OK;
+}
+
+static void store_free(mrl_rerank_store* st) {
+  if (!st) return;
+  dev_free(st->d_data);
+  dev_free(st->d_scales);
+  delete st;
+}
+
+extern "C" int mrl_rerank_store_create(mrl_ctx* ctx, const float* rows, int rows_on_device, uint64_t n_rows,
+                                       uint32_t dims, int precision, mrl_rerank_store** out) {
+  if (!ctx || !out || (n_rows && !rows)) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  *out = nullptr;
+  if (precision != MRL_RERANK_FP32 && precision != MRL_RERANK_FP16 && precision != MRL_RERANK_INT8)
+    return fail(MRL_ERR_INVALID_ARG, "unknown rerank precision");
+  if (dims == 0 || dims > MRL_MAX_DIMS) return fail(MRL_ERR_INVALID_ARG, "dims must be in [1, MRL_MAX_DIMS]");
+  if (precision != MRL_RERANK_FP32 && dims != 768)
+    return fail(MRL_ERR_INVALID_ARG, "fp16 / int8 rerank rows need 768 dims");  // lowprec.rs:50,73
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  return store_create_locked(ctx, rows, rows_on_device, n_rows, dims, precision, out);
 }
 
 extern "C" void mrl_rerank_store_destroy(mrl_rerank_store* store) {
   if (!store) return;
   (void)hipSetDevice(store->ctx->device);
   (void)hipStreamSynchronize(store->ctx->stream);
-  dev_free(store->d_data);
-  dev_free(store->d_scales);
-  delete store;
+  store_free(store);
 }
 
 extern "C" int mrl_rerank_store_download(mrl_ctx* ctx, const mrl_rerank_store* store, void* out_rows,
@@ -1087,16 +1099,18 @@ extern "C" int mrl_rerank_store_download(mrl_ctx* ctx, const mrl_rerank_store* s
 }
 
 // Sizes of the rerank buffers for n_q lists of `stride` entries, carved from
-// one allocation: score f32, row u64, out_rows u64, out_scores f32, status u32.
+// one allocation: row u64, out_rows u64, score f32, out_scores f32, then
+// status u32 and counts u32 per query.
 struct RerankBuffers {
   float* score;
   uint64_t* row;
   uint64_t* out_rows;
   float* out_scores;
   uint32_t* status;
+  uint32_t* counts;
 };
 static size_t rerank_bytes(uint32_t n_q, uint32_t stride) {
-  return (size_t)n_q * stride * 24 + (size_t)n_q * 4 + 64;
+  return (size_t)n_q * stride * 24 + (size_t)n_q * 8 + 64;
 }
 static RerankBuffers rerank_carve(void* base, uint32_t n_q, uint32_t stride) {
   const size_t n = (size_t)n_q * stride;
@@ -1107,6 +1121,7 @@ static RerankBuffers rerank_carve(void* base, uint32_t n_q, uint32_t stride) {
   b.score = reinterpret_cast<float*>(p + n * 16);
   b.out_scores = reinterpret_cast<float*>(p + n * 20);
   b.status = reinterpret_cast<uint32_t*>(p + n * 24);
+  b.counts = b.status + n_q;
   return b;
 }
 
@@ -1139,6 +1154,7 @@ static int enqueue_rerank(mrl_ctx* ctx, const mrl_rerank_store* st, const float*
   a.out_rows = b.out_rows;
   a.out_scores = b.out_scores;
   a.status = b.status;
+  a.out_counts = b.counts;
   ProfScope p1(ctx, MRL_KERNEL_RERANK, 0, 0, n_q);
   ProfScope p2(ctx, MRL_KERNEL_RERANK_SORT, 0, 0, n_q);
   HIP_TRY(launch_rerank(a, ctx->stream, p1.ev(), p2.ev()));
@@ -1214,8 +1230,132 @@ extern "C" int mrl_results_rerank(mrl_ctx* ctx, mrl_results* res, const mrl_rera
   HIP_TRY(hipMemcpyAsync(st.data(), b.status, (size_t)n_q * 4, hipMemcpyDeviceToHost, ctx->stream));
   if (out_rows) HIP_TRY(hipMemcpyAsync(out_rows, b.out_rows, nc * 8, hipMemcpyDeviceToHost, ctx->stream));
   if (out_scores) HIP_TRY(hipMemcpyAsync(out_scores, b.out_scores, nc * 4, hipMemcpyDeviceToHost, ctx->stream));
-  if (out_counts) HIP_TRY(hipMemcpyAsync(out_counts, res->d_counts, (size_t)n_q * 4, hipMemcpyDeviceToHost, ctx->stream));
+  if (out_counts) HIP_TRY(hipMemcpyAsync(out_counts, b.counts, (size_t)n_q * 4, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return status_error(st);
+}
+
+// Ring search of n_q queries (device) over n_pending host rows: a transient
+// fp32 store, every row a candidate, rerank buffers carved from *scratch
+// (caller frees).  Caller holds the lock.
+static int ring_search_enqueue(mrl_ctx* ctx, const float* pending, uint32_t n_pending, uint32_t dims,
+                               const float* d_queries, uint32_t n_q, mrl_rerank_store** store, void** scratch,
+                               RerankBuffers* b) {
+  int rc = store_create_locked(ctx, pending, 0, n_pending, dims, MRL_RERANK_FP32, store);
+  if (rc) return rc;
+  if (hipMalloc(scratch, rerank_bytes(n_q, n_pending)) != hipSuccess) {
+    *scratch = nullptr;
+    return fail(MRL_ERR_OUT_OF_MEMORY, "ring search buffers");
+  }
+  *b = rerank_carve(*scratch, n_q, n_pending);
+  return enqueue_rerank(ctx, *store, d_queries, n_q, nullptr, 0, nullptr, n_pending, *b);
+}
+
+static int check_ring_args(const float* pending, uint32_t n_pending, uint32_t dims) {
+  if (n_pending && !pending) return fail(MRL_ERR_INVALID_ARG, "null pending rows");
+  if (n_pending > MRL_MAX_SHORTLIST) return fail(MRL_ERR_INVALID_ARG, "more than MRL_MAX_SHORTLIST pending rows");
+  if (dims == 0 || dims > MRL_MAX_DIMS) return fail(MRL_ERR_INVALID_ARG, "dims must be in [1, MRL_MAX_DIMS]");
+  return MRL_OK;
+}
+
+extern "C" int mrl_ring_search(mrl_ctx* ctx, const float* pending, uint32_t n_pending, uint32_t dims,
+                               const float* queries, uint32_t n_q, uint32_t top_k, uint64_t* out_local,
+                               float* out_scores, uint32_t* out_counts) {
+  if (!ctx) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  int rc = check_ring_args(pending, n_pending, dims);
+  if (rc) return rc;
+  if (n_q && (!queries || !out_counts || (top_k && (!out_local || !out_scores))))
+    return fail(MRL_ERR_INVALID_ARG, "null buffer");
+  const uint32_t keep = std::min(top_k, n_pending);
+  if (n_q == 0) return MRL_OK;
+  if (keep == 0) {
+    memset(out_counts, 0, (size_t)n_q * 4);
+    return MRL_OK;
+  }
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  float* d_q = nullptr;
+  mrl_rerank_store* store = nullptr;
+  void* scratch = nullptr;
+  RerankBuffers b{};
+  const size_t qbytes = (size_t)n_q * dims * 4;
+  if (hipMalloc(&d_q, qbytes) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "ring queries");
+  hipError_t e = hipMemcpyAsync(d_q, queries, qbytes, hipMemcpyHostToDevice, ctx->stream);
+  rc = e == hipSuccess ? ring_search_enqueue(ctx, pending, n_pending, dims, d_q, n_q, &store, &scratch, &b)
+                       : fail(MRL_ERR_HIP, "ring query copy");
+  std::vector<uint32_t> st(n_q);
+  if (!rc) {
+    // search_exact's truncate(top_k): the first `keep` of each sorted row
+    e = hipMemcpy2DAsync(out_local, keep * 8, b.out_rows, (size_t)n_pending * 8, keep * 8, n_q,
+                         hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess)
+      e = hipMemcpy2DAsync(out_scores, keep * 4, b.out_scores, (size_t)n_pending * 4, keep * 4, n_q,
+                           hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(st.data(), b.status, (size_t)n_q * 4, hipMemcpyDeviceToHost, ctx->stream);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  dev_free(d_q);
+  dev_free(scratch);
+  store_free(store);
+  if (rc) return rc;
+  if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("ring search: ") + hipGetErrorString(e));
+  for (uint32_t q = 0; q < n_q; ++q) out_counts[q] = keep;
+  return status_error(st);
+}
+
+extern "C" int mrl_results_merge_ring(mrl_ctx* ctx, mrl_results* res, const float* pending, uint32_t n_pending,
+                                      uint32_t dims) {
+  if (!ctx || !res) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (res->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "results belong to another context");
+  int rc = check_ring_args(pending, n_pending, dims);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  const mrl_plans* plans = res->last_plans;
+  if (!plans) return fail(MRL_ERR_INVALID_ARG, "no scan was enqueued on these results");
+  if (plans->dims != dims) return fail(MRL_ERR_INVALID_ARG, "pending rows have other dims than the queries");
+  if ((rc = resolve_pending(ctx, res))) return rc;
+  const uint32_t n_q = plans->n_q, K = res->k;
+  if (n_q == 0 || n_pending == 0) return MRL_OK;
+  mrl_rerank_store* store = nullptr;
+  void* scratch = nullptr;
+  uint8_t* merged = nullptr;
+  RerankBuffers b{};
+  const size_t nc = (size_t)n_q * K;
+  auto cleanup = [&]() {
+    dev_free(scratch);
+    dev_free(merged);
+    store_free(store);
+  };
+  if (hipMalloc(&merged, nc * 12 + (size_t)n_q * 4) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "ring merge");
+  rc = ring_search_enqueue(ctx, pending, n_pending, dims, plans->d_queries, n_q, &store, &scratch, &b);
+  if (rc) {
+    cleanup();
+    return rc;
+  }
+  RingMergeArgs ma{};
+  ma.ids = res->d_ids;
+  ma.scores = res->d_scores;
+  ma.counts = res->d_counts;
+  ma.ring_rows = b.out_rows;
+  ma.ring_scores = b.out_scores;
+  ma.ring_status = b.status;
+  ma.n_ring = n_pending;
+  ma.k = K;
+  ma.n_q = n_q;
+  ma.out_ids = reinterpret_cast<uint64_t*>(merged);
+  ma.out_scores = reinterpret_cast<float*>(merged + nc * 8);
+  ma.out_counts = reinterpret_cast<uint32_t*>(merged + nc * 12);
+  std::vector<uint32_t> st(n_q);
+  hipError_t e = launch_ring_merge(ma, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(res->d_ids, ma.out_ids, nc * 8, hipMemcpyDeviceToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(res->d_scores, ma.out_scores, nc * 4, hipMemcpyDeviceToDevice, ctx->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(res->d_counts, ma.out_counts, (size_t)n_q * 4, hipMemcpyDeviceToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(st.data(), b.status, (size_t)n_q * 4, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  cleanup();
+  if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("ring merge: ") + hipGetErrorString(e));
   return status_error(st);
 }
 

@@ -181,8 +181,9 @@ struct RerankArgs {
   uint32_t dims;
   int32_t precision;        // mrl_rerank_precision
   const float* queries;     // [n_q][dims]
-  const uint64_t* cand;     // [n_q][stride]: row ids, or VectorId::as_u64 ids when cand_ids
-  const uint32_t* counts;   // [n_q], each <= stride
+  const uint64_t* cand;     // [n_q][stride]: row ids, or VectorId::as_u64 ids when cand_ids;
+                            // null: candidate c is row c (every row of the store)
+  const uint32_t* counts;   // [n_q], each <= stride; null: stride for every query
   uint32_t stride;          // <= MRL_MAX_SHORTLIST
   uint32_t n_q;
   int32_t cand_ids;
@@ -191,6 +192,24 @@ struct RerankArgs {
   uint64_t* out_rows;       // [n_q][stride], sorted
   float* out_scores;
   uint32_t* status;         // [n_q]: bit 0 NaN score, bit 1 row out of range
+  uint32_t* out_counts;     // [n_q] or null: entries written per query (ring hits excluded)
+};
+
+// Ring merge (mrl_rerank.hip): push the sorted ring hits of each query into
+// its sorted scan shortlist with Shortlist::push semantics, then sort.
+struct RingMergeArgs {
+  const uint64_t* ids;        // [n_q][k] scan shortlist, sorted
+  const float* scores;
+  const uint32_t* counts;     // [n_q]
+  const uint64_t* ring_rows;  // [n_q][n_ring] ring hits (pending-row index), sorted
+  const float* ring_scores;
+  const uint32_t* ring_status;  // [n_q]: a query whose ring search failed is left as is
+  uint32_t n_ring;            // ring hits per query
+  uint32_t k;
+  uint32_t n_q;
+  uint64_t* out_ids;          // [n_q][k]
+  float* out_scores;
+  uint32_t* out_counts;       // [n_q]
 };
 
 // Launchers (mrl_kernels.hip).
@@ -212,5 +231,6 @@ hipError_t launch_rerank_store(const float* rows, uint64_t n_rows, int precision
                                hipStream_t s);
 hipError_t launch_rerank(const RerankArgs& a, hipStream_t s, const LaunchEvents& ev_score = {},
                          const LaunchEvents& ev_sort = {});
+hipError_t launch_ring_merge(const RingMergeArgs& a, hipStream_t s, const LaunchEvents& ev = {});
 
 }  // namespace mrl

@@ -132,12 +132,33 @@ __global__ __launch_bounds__(kStoreThreads) void k_store768(const float* __restr
 // ---------------------------------------------------------------------------
 // scoring
 // ---------------------------------------------------------------------------
+// Row markers in the scratch row array: a row outside the store, and a ring
+// hit that scored_hits_to_row_ids drops.
+constexpr uint64_t kRowBad = ~0ull;
+constexpr uint64_t kRowSkip = ~0ull - 1u;
+
+__device__ __forceinline__ uint32_t count_of(const RerankArgs& a, uint32_t q) {
+  return a.counts ? a.counts[q] : a.stride;
+}
+
+// Candidate c of query q -> store row.  *ok false: no row to score (*row says why).
 __device__ __forceinline__ void resolve_row(const RerankArgs& a, uint32_t q, uint32_t c, uint64_t* row, bool* ok) {
+  if (!a.cand) {
+    *row = c;
+    *ok = c < a.n_rows;
+    if (!*ok) *row = kRowBad;
+    return;
+  }
   const uint64_t id = a.cand[(uint64_t)q * a.stride + c];
+  if (a.cand_ids && (id >> 16) == 0xffffffffull) {  // ring sentinel (block == u32::MAX): skipped
+    *row = kRowSkip;
+    *ok = false;
+    return;
+  }
   // scored_hits_to_row_ids (src/pipeline.rs:175-180): block * 64 + slot
   const uint64_t r = a.cand_ids ? (id >> 16) * 64u + (id & 0xffffu) : id;
-  *row = r;
   *ok = r < a.n_rows;
+  *row = *ok ? r : kRowBad;
 }
 
 // Accumulator j of one candidate over its 96 stored elements.
@@ -199,7 +220,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_score768(RerankArgs a, uint32
   __shared__ __align__(16) float s_q[8 * kQStride];
   const uint32_t q = blockIdx.x / n_chunks;
   const uint32_t base = (blockIdx.x % n_chunks) * (kScoreThreads / 8);
-  const uint32_t cnt = a.counts[q];
+  const uint32_t cnt = count_of(a, q);
   if (base >= cnt) return;  // uniform over the workgroup
   // query element i = 8t + j at s_q[kQStride*j + t]
   const float* qv = a.queries + (uint64_t)q * 768u;
@@ -223,8 +244,8 @@ __global__ __launch_bounds__(kScoreThreads) void k_score768(RerankArgs a, uint32
     for (int k = 2; k < 8; ++k) s = s + part[k];
     if (P == MRL_RERANK_INT8 && ok) s = s * h2f(a.scales[row]);
     const uint64_t o = (uint64_t)q * a.stride + c;
-    a.score[o] = ok ? s : __uint_as_float(0x7fc00000u);
-    a.row[o] = ok ? row : ~0ull;
+    a.score[o] = ok ? s : 0.0f;
+    a.row[o] = row;
   }
 }
 
@@ -233,7 +254,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_score_seq(RerankArgs a, uint3
   __shared__ float s_q[MRL_MAX_DIMS];
   const uint32_t q = blockIdx.x / n_chunks;
   const uint32_t base = (blockIdx.x % n_chunks) * kScoreThreads;
-  const uint32_t cnt = a.counts[q];
+  const uint32_t cnt = count_of(a, q);
   if (base >= cnt) return;
   const uint32_t dims = a.dims;
   const float* qv = a.queries + (uint64_t)q * dims;
@@ -250,8 +271,8 @@ __global__ __launch_bounds__(kScoreThreads) void k_score_seq(RerankArgs a, uint3
     for (uint32_t i = 0; i < dims; ++i) s = s + s_q[i] * r[i];
   }
   const uint64_t o = (uint64_t)q * a.stride + c;
-  a.score[o] = ok ? s : __uint_as_float(0x7fc00000u);
-  a.row[o] = ok ? row : ~0ull;
+  a.score[o] = ok ? s : 0.0f;
+  a.row[o] = row;
 }
 
 // ---------------------------------------------------------------------------
@@ -276,23 +297,36 @@ __device__ void bitonic_desc(uint64_t* s, int n2) {
 }
 
 // Key = (score key, ~position): descending keys give score descending, then
-// input position ascending -- the order of a stable sort.  Keys are distinct.
+// input position ascending -- the order of a stable sort.  Keys are distinct;
+// skipped ring hits get a zero score key, below every scored entry (the
+// smallest score key, that of -inf, is 0x007fffff), and are not emitted.
 __global__ __launch_bounds__(kSortThreads) void k_rerank_sort(RerankArgs a) {
   __shared__ uint64_t s_key[kSortCap];
-  __shared__ uint32_t s_bad;
+  __shared__ uint32_t s_bad, s_skip;
   const uint32_t q = blockIdx.x, tid = threadIdx.x;
-  const uint32_t m = a.counts[q];
+  const uint32_t m = count_of(a, q);
   const uint64_t base = (uint64_t)q * a.stride;
-  if (tid == 0) s_bad = 0u;
+  if (tid == 0) {
+    s_bad = 0u;
+    s_skip = 0u;
+  }
   __syncthreads();
-  uint32_t bad = 0u;
+  uint32_t bad = 0u, skip = 0u;
   for (uint32_t i = tid; i < m; i += kSortThreads) {
     const float s = a.score[base + i];
-    if (!(s == s)) bad |= 1u;                 // partial_cmp(..).unwrap() panics
-    if (a.row[base + i] == ~0ull) bad |= 2u;  // row index out of range
-    s_key[i] = ((uint64_t)score_key(s) << 32) | (uint64_t)(~i);
+    const uint64_t r = a.row[base + i];
+    uint32_t key = score_key(s);
+    if (r == kRowSkip) {
+      key = 0u;
+      ++skip;
+    } else {
+      if (!(s == s)) bad |= 1u;     // partial_cmp(..).unwrap() panics
+      if (r == kRowBad) bad |= 2u;  // row index out of range
+    }
+    s_key[i] = ((uint64_t)key << 32) | (uint64_t)(~i);
   }
   if (bad) atomicOr(&s_bad, bad);
+  if (skip) atomicAdd(&s_skip, skip);
   __syncthreads();
   auto emit = [&](uint32_t r, uint64_t key) {
     const uint32_t i = ~(uint32_t)key;
@@ -314,7 +348,56 @@ __global__ __launch_bounds__(kSortThreads) void k_rerank_sort(RerankArgs a) {
     bitonic_desc(s_key, n2);
     for (uint32_t i = tid; i < m; i += kSortThreads) emit(i, s_key[i]);
   }
-  if (tid == 0) a.status[q] = s_bad;
+  if (tid == 0) {
+    a.status[q] = s_bad;
+    if (a.out_counts) a.out_counts[q] = m - s_skip;
+  }
+}
+
+// IndexEngine::query_filtered's ring merge (src/engine.rs:584-594): the ring
+// hits, sorted descending, are pushed one by one into the query's Shortlist
+// holding the scan hits (Shortlist::push, src/scan.rs:351-369), then
+// into_sorted.  Pushing a descending sequence keeps the K largest of both
+// lists where a ring hit never displaces an entry of equal score (push
+// replaces the minimum only if strictly greater; below capacity it appends).
+// So the result is the merge of the two sorted lists with the scan entry first
+// on equal scores, cut at K.  Entry positions come from binary searches:
+// scan entry i lands at i + #(ring > s_i), ring entry j at j + #(scan >= r_j).
+__device__ __forceinline__ uint32_t count_greater(const float* v, uint32_t n, float x, bool or_equal) {
+  uint32_t lo = 0, hi = n;  // v descending: first index whose value fails the test
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    const bool pass = or_equal ? (v[mid] >= x) : (v[mid] > x);
+    if (pass) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(kSortThreads) void k_ring_merge(RingMergeArgs a) {
+  const uint32_t q = blockIdx.x;
+  const uint64_t sb = (uint64_t)q * a.k, rb = (uint64_t)q * a.n_ring;
+  const uint32_t c = a.counts[q];
+  const bool ok = a.ring_status[q] == 0u;
+  const uint32_t r = ok ? (a.n_ring < a.k ? a.n_ring : a.k) : 0u;  // search_exact truncates to top_k
+  const float* ss = a.scores + sb;
+  const float* rs = a.ring_scores + rb;
+  for (uint32_t i = threadIdx.x; i < c; i += kSortThreads) {
+    const uint32_t pos = i + count_greater(rs, r, ss[i], false);
+    if (pos < a.k) {
+      a.out_ids[sb + pos] = a.ids[sb + i];
+      a.out_scores[sb + pos] = ss[i];
+    }
+  }
+  for (uint32_t j = threadIdx.x; j < r; j += kSortThreads) {
+    const uint32_t pos = j + count_greater(ss, c, rs[j], true);
+    if (pos < a.k) {
+      // VectorId::new(u32::MAX, local_i as u16)
+      a.out_ids[sb + pos] = (0xffffffffull << 16) | (a.ring_rows[rb + j] & 0xffffull);
+      a.out_scores[sb + pos] = rs[j];
+    }
+  }
+  if (threadIdx.x == 0) a.out_counts[q] = (c + r < a.k) ? c + r : a.k;
 }
 
 template <typename K, typename... Args>
@@ -337,6 +420,12 @@ hipError_t launch_rerank_store(const float* rows, uint64_t n_rows, int precision
     hipLaunchKernelGGL(k_store768<MRL_RERANK_FP16>, grid, dim3(kStoreThreads), 0, s, rows, d, scales, n_rows);
   else
     hipLaunchKernelGGL(k_store768<MRL_RERANK_INT8>, grid, dim3(kStoreThreads), 0, s, rows, d, scales, n_rows);
+  return hipGetLastError();
+}
+
+hipError_t launch_ring_merge(const RingMergeArgs& a, hipStream_t s, const LaunchEvents& ev) {
+  if (a.n_q == 0) return hipSuccess;
+  launch(k_ring_merge, dim3(a.n_q), dim3(kSortThreads), s, ev, a);
   return hipGetLastError();
 }
 

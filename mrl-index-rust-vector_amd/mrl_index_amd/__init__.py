@@ -8,6 +8,7 @@ from .block import (BLOCK_BYTES, MRL_PREFIX_DIMS, RABITQ_DIMS, TAIL_FOLD_DIMS, T
 from .config import EngineConfig, MidCodec, PrefixCodec, ScanConfig, StrataDepth
 from .eden import EdenFit
 from .lowprec import RerankPrecision, RerankStore, rerank_batch, rerank_rows
+from .ring import PendingVector, RingBuffer
 from .pipeline import QueryPipeline, ScanPhase, row_id_to_vector_id, scored_hits_to_row_ids
 from .quantize import encode_block, encode_corpus, encode_corpus_device
 from .scan import (Device, DeviceBuffer, DeviceIndex, DeviceResults, QueryPlan, ScanResult, ScanStats, ScoredHit, StageTrace, default_device,
@@ -21,5 +22,5 @@ __all__ = [
     "encode_block", "encode_corpus", "encode_corpus_device", "Device", "DeviceBuffer", "DeviceIndex", "QueryPlan", "ScanResult", "ScanStats", "ScoredHit",
     "StageTrace", "default_device", "scan_batch", "scan_blocks", "scan_blocks_stats", "scan_fixed_tau",
     "SegmentWriter", "read_segment", "DeviceResults", "RerankPrecision", "RerankStore", "rerank_batch",
-    "rerank_rows",
+    "rerank_rows", "PendingVector", "RingBuffer",
 ]

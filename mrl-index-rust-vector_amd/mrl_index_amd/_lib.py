@@ -199,6 +199,8 @@ SIGNATURES = {
     "mrl_rerank_store_download": (C.c_int, [_P, _P, _P, C.POINTER(C.c_uint16)]),
     "mrl_rerank_rows": (C.c_int, [_P, _P, _F, C.c_uint32, C.c_uint32, _U64, _U32, C.c_uint32, _U64, _F]),
     "mrl_results_rerank": (C.c_int, [_P, _P, _P, _U64, _F, _U32]),
+    "mrl_ring_search": (C.c_int, [_P, _F, C.c_uint32, C.c_uint32, _F, C.c_uint32, C.c_uint32, _U64, _F, _U32]),
+    "mrl_results_merge_ring": (C.c_int, [_P, _P, _F, C.c_uint32, C.c_uint32]),
     "mrl_synth_docs": (C.c_int, [C.POINTER(SynthSpecC), C.c_uint64, C.c_uint64, C.c_int, _F]),
     "mrl_synth_queries": (C.c_int, [C.POINTER(SynthSpecC), C.c_uint64, C.c_float, C.c_int, C.c_uint32, _F,
                                     _U64]),

@@ -1234,3 +1234,43 @@ int ora_rerank(int precision, const float *q, const float *rows, uint32_t n, con
   }
   return 0;
 }
+
+
+/* ring.rs:109-119 */
+int ora_ring_search_exact(const float *pending, uint32_t n_pending, uint32_t dims, const float *q,
+                          uint32_t top_k, uint64_t *out_local, float *out_scores) {
+  uint64_t *cand = (uint64_t *)calloc(n_pending ? n_pending : 1, sizeof(uint64_t));
+  uint64_t *rows = (uint64_t *)malloc(sizeof(uint64_t) * (n_pending ? n_pending : 1));
+  float *sc = (float *)malloc(sizeof(float) * (n_pending ? n_pending : 1));
+  for (uint32_t i = 0; i < n_pending; ++i) cand[i] = i;
+  int rc = ora_rerank(ORA_RERANK_FP32, q, pending, dims, cand, n_pending, rows, sc);
+  uint32_t keep = top_k < n_pending ? top_k : n_pending;
+  if (rc == 0)
+    for (uint32_t i = 0; i < keep; ++i) {
+      out_local[i] = rows[i];
+      out_scores[i] = sc[i];
+    }
+  free(cand);
+  free(rows);
+  free(sc);
+  return rc ? rc : (int)keep;
+}
+
+/* scan.rs:311-399 driven as engine.rs:584-594 drives it */
+int ora_shortlist_push_sorted(uint32_t capacity, const uint64_t *ids, const float *scores, uint32_t n,
+                              const uint64_t *push_ids, const float *push_scores, uint32_t n_push,
+                              uint64_t *out_ids, float *out_scores) {
+  shortlist s;
+  sl_init(&s, capacity, -INFINITY);
+  for (uint32_t i = 0; i < n; ++i) {
+    hit h = {ids[i], scores[i]};
+    sl_push(&s, h);
+  }
+  for (uint32_t i = 0; i < n_push; ++i) {
+    hit h = {push_ids[i], push_scores[i]};
+    sl_push(&s, h);
+  }
+  int rc = sl_into_sorted(&s, out_ids, out_scores);
+  sl_free(&s);
+  return rc;
+}

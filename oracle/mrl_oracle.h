@@ -242,6 +242,18 @@ float ora_rerank_dot(int precision, const float *q, const float *row, uint32_t n
 int ora_rerank(int precision, const float *q, const float *rows, uint32_t n, const uint64_t *cand_rows,
                uint32_t n_cand, uint64_t *out_rows, float *out_scores);
 
+/* RingBuffer::search_exact (src/ring.rs:109-119): dot of every pending row
+ * with q, stable sort descending, first top_k.  Returns the count or
+ * -ORA_ERR_NAN. */
+int ora_ring_search_exact(const float *pending, uint32_t n_pending, uint32_t dims, const float *q,
+                          uint32_t top_k, uint64_t *out_local, float *out_scores);
+/* Shortlist (src/scan.rs:311-399) of `capacity` holding n hits in the given
+ * internal order: push every push_* hit in order, then into_sorted.  Returns
+ * the count or -ORA_ERR_NAN.  The engine's ring merge (src/engine.rs:584-594). */
+int ora_shortlist_push_sorted(uint32_t capacity, const uint64_t *ids, const float *scores, uint32_t n,
+                              const uint64_t *push_ids, const float *push_scores, uint32_t n_push,
+                              uint64_t *out_ids, float *out_scores);
+
 #ifdef __cplusplus
 }
 #endif

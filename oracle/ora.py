@@ -109,6 +109,8 @@ _SIGS = {
     "ora_dot_int8_768": (C.c_float, [_F, C.POINTER(C.c_int8), C.c_uint16]),
     "ora_rerank_dot": (C.c_float, [C.c_int, _F, _F, C.c_uint32]),
     "ora_rerank": (C.c_int, [C.c_int, _F, _F, C.c_uint32, _U64, C.c_uint32, _U64, _F]),
+    "ora_ring_search_exact": (C.c_int, [_F, C.c_uint32, C.c_uint32, _F, C.c_uint32, _U64, _F]),
+    "ora_shortlist_push_sorted": (C.c_int, [C.c_uint32, _U64, _F, C.c_uint32, _U64, _F, C.c_uint32, _U64, _F]),
 }
 
 RERANK_FP32, RERANK_FP16, RERANK_INT8 = 0, 1, 2
@@ -283,3 +285,34 @@ def rerank(precision, q, rows, cand):
     if rc != 0:
         return None
     return out_r[:n], out_s[:n]
+
+
+def ring_search_exact(pending, q, top_k):
+    """(local indices, scores) of RingBuffer::search_exact; None on NaN."""
+    p = np.ascontiguousarray(pending, dtype=np.float32)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    n = p.shape[0]
+    out_l = np.zeros(max(n, 1), dtype=np.uint64)
+    out_s = np.zeros(max(n, 1), dtype=np.float32)
+    rc = lib.ora_ring_search_exact(fp(p), n, p.shape[1] if p.ndim == 2 else q.size, fp(q), top_k, u64p(out_l),
+                                   fp(out_s))
+    if rc < 0:
+        return None
+    return out_l[:rc], out_s[:rc]
+
+
+def shortlist_push_sorted(capacity, ids, scores, push_ids, push_scores):
+    """Shortlist holding (ids, scores) in that internal order, push the others
+    in order, into_sorted.  None on NaN."""
+    ids = np.ascontiguousarray(ids, dtype=np.uint64)
+    scores = np.ascontiguousarray(scores, dtype=np.float32)
+    pi = np.ascontiguousarray(push_ids, dtype=np.uint64)
+    ps = np.ascontiguousarray(push_scores, dtype=np.float32)
+    cap = max(capacity, 1)
+    out_i = np.zeros(cap, dtype=np.uint64)
+    out_s = np.zeros(cap, dtype=np.float32)
+    rc = lib.ora_shortlist_push_sorted(capacity, u64p(ids), fp(scores), ids.size, u64p(pi), fp(ps), pi.size,
+                                       u64p(out_i), fp(out_s))
+    if rc < 0:
+        return None
+    return out_i[:rc], out_s[:rc]

@@ -7,7 +7,7 @@ import pytest
 
 import mrl_index_amd as m
 import ora
-from helpers import normalized
+from helpers import assert_topk_equal, normalized
 
 pytestmark = pytest.mark.gpu
 
@@ -185,4 +185,101 @@ def test_scan_then_rerank_on_device(device, prec, prec_o):
     short = m.RerankStore.create(rows[:100], prec, device)
     with pytest.raises(m.MrlError):
         res.rerank(short)
+    res.close()
+
+
+@pytest.mark.parametrize("dims", [768, 384])
+@pytest.mark.parametrize("n_pending,top_k", [(1, 256), (17, 5), (63, 256), (300, 100), (1100, 1024)])
+def test_ring_search_matches_oracle(device, dims, n_pending, top_k):
+    rng = np.random.default_rng(n_pending + dims)
+    pending = normalized(rng, n_pending, dims)
+    if n_pending > 2:
+        pending[2] = pending[0]          # exact tie: the lower index first
+    queries = normalized(rng, 3, dims)
+    ring = m.RingBuffer(1024, device)
+    keep = min(top_k, n_pending)
+    loc = np.zeros((3, keep), dtype=np.uint64)
+    sc = np.zeros((3, keep), dtype=np.float32)
+    cnt = np.zeros(3, dtype=np.uint32)
+    from mrl_index_amd import _lib
+    _lib.check(_lib.lib.mrl_ring_search(device.handle, _lib.fptr(pending), n_pending, dims, _lib.fptr(queries), 3,
+                                        top_k, _lib.u64ptr(loc), _lib.fptr(sc), _lib.u32ptr(cnt)))
+    for q in range(3):
+        wl, ws = ora.ring_search_exact(pending, queries[q], top_k)
+        assert int(cnt[q]) == keep
+        assert np.array_equal(loc[q], wl) and np.array_equal(sc[q].view(np.uint32), ws.view(np.uint32))
+    # the RingBuffer mirror (pending < 64 after every push)
+    for i in range(min(n_pending, 63)):
+        assert ring.push(m.PendingVector(i, pending[i], i, 0)) is None
+    hits = ring.search_exact(queries[0], top_k)
+    wl, ws = ora.ring_search_exact(pending[:min(n_pending, 63)], queries[0], top_k)
+    assert [h[0] for h in hits] == wl.tolist()
+    assert np.array_equal(np.array([h[1] for h in hits], dtype=np.float32).view(np.uint32), ws.view(np.uint32))
+
+
+def test_ring_buffer_flushes_at_64(device):
+    rows = normalized(np.random.default_rng(30), 70, 384)
+    ring = m.RingBuffer(1024, device)
+    blocks = [ring.push(m.PendingVector(i, rows[i], 100 + i, 0)) for i in range(70)]
+    flushed = [b for b in blocks if b is not None]
+    assert len(flushed) == 1 and len(ring) == 6
+    assert np.array_equal(flushed[0], m.encode_block(rows[:64], 100 + np.arange(64), np.full(64, m.source.DOC), 384))
+    tail = ring.flush_partial()
+    assert np.array_equal(tail, m.encode_block(rows[64:], 164 + np.arange(6), np.full(6, m.source.DOC), 384))
+    assert ring.is_empty() and ring.search_exact(rows[0], 10) == []
+
+
+@pytest.mark.parametrize("n_pending", [5, 63, 600])
+def test_ring_merge_into_scan_shortlists(device, n_pending):
+    """engine.rs:584-594: ring hits pushed into each query's scan shortlist,
+    then the rerank of the merged list skips them (pipeline.rs:175-180)."""
+    n = 64 * 120
+    rng = np.random.default_rng(31 + n_pending)
+    rows = _rows(31, n)
+    queries = np.ascontiguousarray(rows[rng.integers(0, n, 4)] + np.float32(0.02) * normalized(rng, 4, 768),
+                                   dtype=np.float32)
+    # pending rows close to the queries so that ring hits interleave with scan hits
+    pending = np.ascontiguousarray(np.repeat(queries, (n_pending + 3) // 4, axis=0)[:n_pending]
+                                   + np.float32(0.05) * normalized(rng, n_pending, 768), dtype=np.float32)
+    index = m.DeviceIndex.upload(m.encode_corpus(rows, 8), device)
+    plan = m.QueryPlan.from_query(queries, 768, device)
+    k = 128
+    res = m.DeviceResults(4, k, device)
+    res.scan(index, plan, m.ScanConfig(shortlist_cand=k))
+    before = res.fetch()
+    from mrl_index_amd import _lib
+    _lib.check(_lib.lib.mrl_results_merge_ring(device.handle, res._h, _lib.fptr(pending), n_pending, 768))
+    after = res.fetch()
+    n_ring_hits = 0
+    for q in range(4):
+        c = int(before.counts[q])
+        rl, rs = ora.ring_search_exact(pending, queries[q], k)
+        ring_ids = (np.uint64(0xFFFFFFFF) << np.uint64(16)) | rl
+        wi, ws = ora.shortlist_push_sorted(k, before.ids[q, :c], before.scores[q, :c], ring_ids, rs)
+        ca = int(after.counts[q])
+        assert ca == wi.size
+        union = np.concatenate([before.scores[q, :c], rs])
+        if np.unique(union).size == union.size:  # no exact ties: identical lists
+            assert np.array_equal(after.ids[q, :ca], wi), f"q={q}: merged ids differ"
+            assert np.array_equal(after.scores[q, :ca].view(np.uint32), ws.view(np.uint32))
+        else:  # which tied entry is kept follows the reference's heap order
+            assert_topk_equal(after.ids[q, :ca], after.scores[q, :ca], wi, ws, k, f"q={q}")
+        n_ring_hits += int(np.sum((after.ids[q, :ca] >> np.uint64(16)) == np.uint64(0xFFFFFFFF)))
+    assert n_ring_hits > 0
+    store = m.RerankStore.create(rows, m.RerankPrecision.FP32, device)
+    rr, rsc, rc = res.rerank(store)
+    for q in range(4):
+        ids = after.ids[q, :int(after.counts[q])]
+        keep = ids[(ids >> np.uint64(16)) != np.uint64(0xFFFFFFFF)]
+        cand = (keep >> np.uint64(16)) * np.uint64(64) + (keep & np.uint64(0xFFFF))
+        assert int(rc[q]) == cand.size
+        wr, ws = ora.rerank(ora.RERANK_FP32, queries[q], rows, cand)
+        assert np.array_equal(rr[q, :cand.size], wr)
+        assert np.array_equal(rsc[q, :cand.size].view(np.uint32), ws.view(np.uint32))
+    bad = pending.copy()
+    bad[1, 4] = np.nan
+    res.scan(index, plan, m.ScanConfig(shortlist_cand=k))
+    with pytest.raises(m.MrlError) as e:
+        _lib.check(_lib.lib.mrl_results_merge_ring(device.handle, res._h, _lib.fptr(bad), n_pending, 768))
+    assert e.value.code == 3
     res.close()

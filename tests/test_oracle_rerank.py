@@ -184,3 +184,49 @@ def test_rerank_nan_is_an_error():
     assert ora.rerank(ora.RERANK_FP16, q, rows, np.array([2], dtype=np.uint64)) is None
     # int8 maps the NaN element to code 0: a finite score
     assert ora.rerank(ora.RERANK_INT8, q, rows, np.array([2], dtype=np.uint64)) is not None
+
+
+def test_ring_search_exact_sorts_and_truncates():
+    r = _rng(20)
+    pending = r.standard_normal((40, 768)).astype(np.float32)
+    pending[7] = pending[3]                       # tie: index 3 first
+    q = r.standard_normal(768).astype(np.float32)
+    loc, sc = ora.ring_search_exact(pending, q, 10)
+    scored = sorted([(i, ora.dot(pending[i], q)) for i in range(40)], key=lambda t: -t[1])[:10]
+    assert loc.tolist() == [i for i, _ in scored]
+    assert np.array_equal(sc, np.array([s for _, s in scored], dtype=np.float32))
+    loc, sc = ora.ring_search_exact(pending, q, 100)  # top_k above the pending count
+    assert loc.size == 40
+    pending[5, 0] = np.nan
+    assert ora.ring_search_exact(pending, q, 10) is None
+
+
+def test_shortlist_push_known_answers():
+    ids = np.array([1, 2, 3], dtype=np.uint64)
+    # full, equal to the minimum: rejected (push replaces only if strictly greater)
+    oi, os_ = ora.shortlist_push_sorted(3, ids, [5.0, 4.0, 3.0], [9], [3.0])
+    assert oi.tolist() == [1, 2, 3]
+    # below capacity: appended whatever the score
+    oi, os_ = ora.shortlist_push_sorted(3, ids[:1], [5.0], [9, 10, 11], [1.0, 0.5, 0.2])
+    assert oi.tolist() == [1, 9, 10] and os_.tolist() == [5.0, 1.0, 0.5]
+    # first minimum in internal order is replaced: [3a, 5, 3b] + 4 -> 3a goes
+    oi, os_ = ora.shortlist_push_sorted(3, ids, [3.0, 5.0, 3.0], [9], [4.0])
+    assert oi.tolist() == [2, 9, 3]
+    # into_sorted is stable: equal scores keep internal order
+    oi, _ = ora.shortlist_push_sorted(4, ids, [2.0, 2.0, 2.0], [9], [2.0])
+    assert oi.tolist() == [1, 2, 3, 9]
+
+
+def test_shortlist_push_keeps_the_top_k_of_the_union():
+    r = _rng(21)
+    for k, n, m in [(16, 16, 40), (16, 5, 8), (64, 64, 64), (8, 0, 20)]:
+        s = np.sort(r.standard_normal(n).astype(np.float32))[::-1]
+        p = np.sort(r.standard_normal(m).astype(np.float32))[::-1]
+        ids = np.arange(n, dtype=np.uint64)
+        pids = np.arange(1000, 1000 + m, dtype=np.uint64)
+        oi, os_ = ora.shortlist_push_sorted(k, ids, s, pids, p)
+        union = np.concatenate([s, p])
+        top = np.sort(union)[::-1][:k]
+        assert os_.size == min(k, n + m)
+        assert np.array_equal(os_, top)
+        assert np.all(np.diff(os_) <= 0)
