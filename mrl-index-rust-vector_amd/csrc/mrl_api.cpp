@@ -71,7 +71,27 @@ struct mrl_ctx {
   std::vector<hipEvent_t> event_pool; // reusable events
   uint32_t* d_crc = nullptr;          // encoder CRC tables: [256] byte table, then [64][32] carry map
   uint32_t crc_const = 0;
+  void* h_stage = nullptr;            // pinned host staging for result read-back
+  size_t h_stage_cap = 0;
+  mrl_results* spare = nullptr;       // result buffers kept between synchronous mrl_scan calls
 };
+
+// Pinned host buffer of at least `bytes` (grown on demand; every read-back
+// into it is waited for before the call returns).  Caller holds the lock.
+static uint8_t* host_stage(mrl_ctx* c, size_t bytes) {
+  if (bytes > c->h_stage_cap) {
+    if (c->h_stage) (void)hipHostFree(c->h_stage);
+    c->h_stage = nullptr;
+    c->h_stage_cap = 0;
+    const size_t cap = std::max<size_t>(bytes, (size_t)1 << 20);
+    if (hipHostMalloc(&c->h_stage, cap, hipHostMallocDefault) != hipSuccess) {
+      c->h_stage = nullptr;
+      return nullptr;
+    }
+    c->h_stage_cap = cap;
+  }
+  return static_cast<uint8_t*>(c->h_stage);
+}
 
 static hipEvent_t pool_event(mrl_ctx* c) {
   if (!c->event_pool.empty()) {
@@ -149,11 +169,17 @@ struct mrl_plans {
   uint64_t mid_seed = 0;
   float* d_queries = nullptr;  // owned copy, n_q * dims
   float* d_luts = nullptr;     // n_q * 1024 prefix LUT written by the plan kernel
+  uint8_t* d_block = nullptr;  // one allocation holding all of the above
 };
 
+// The per-query outputs sit in one device block, read back with one copy:
+// status u32[n_q], counts u32[n_q], stats u64[kStatCount], ids u64[n_q][k],
+// scores f32[n_q][k].
 struct mrl_results {
   mrl_ctx* ctx = nullptr;
   uint32_t n_q = 0, k = 0, seg_cap = 0;
+  uint8_t* d_out = nullptr;
+  size_t out_bytes = 0;
   uint64_t* d_ids = nullptr;
   float* d_scores = nullptr;
   uint32_t* d_counts = nullptr;
@@ -227,10 +253,13 @@ extern "C" int mrl_ctx_create(int device, mrl_ctx** out) {
   return MRL_OK;
 }
 
+static void results_release(mrl_results* r);
+
 extern "C" void mrl_ctx_destroy(mrl_ctx* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
+  results_release(ctx->spare);
   dev_free(ctx->d_flag_tabs);
   dev_free(ctx->d_crc);
   for (auto& r : ctx->prof) {
@@ -238,6 +267,7 @@ extern "C" void mrl_ctx_destroy(mrl_ctx* ctx) {
     (void)hipEventDestroy(r.stop);
   }
   for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
+  if (ctx->h_stage) (void)hipHostFree(ctx->h_stage);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -496,54 +526,57 @@ static int plans_build_impl(mrl_ctx* ctx, const float* queries, bool on_device, 
   p->dims = dims;
   p->prefix_codec = prefix_codec;
   p->mid_codec = mid_codec;
-  auto cleanup = [&]() {
-    dev_free(p->d_plans);
-    dev_free(p->d_luts);
-    dev_free(p->d_eden_mean);
-    dev_free(p->d_mid_mean);
-    dev_free(p->d_queries);
-  };
-  if (hipMalloc(&p->d_plans, sizeof(mrl_query_plan) * std::max<uint32_t>(n_q, 1)) != hipSuccess ||
-      hipMalloc(&p->d_luts, sizeof(float) * 1024 * std::max<uint32_t>(n_q, 1)) != hipSuccess) {
-    cleanup();
+  // One device block: plans, LUTs, then the inputs [eden mean 64][mid mean
+  // 128][queries], which arrive with one copy (host inputs staged in pinned
+  // memory).
+  const size_t nq = std::max<uint32_t>(n_q, 1);
+  const size_t plan_bytes = sizeof(mrl_query_plan) * nq, lut_bytes = sizeof(float) * 1024 * nq;
+  const size_t qbytes = (size_t)n_q * dims * sizeof(float);
+  const size_t in_bytes = (64 + 128) * sizeof(float) + qbytes;
+  if (hipMalloc(&p->d_block, plan_bytes + lut_bytes + in_bytes) != hipSuccess)
     return fail(MRL_ERR_OUT_OF_MEMORY, "plans");
-  }
+  p->d_plans = reinterpret_cast<mrl_query_plan*>(p->d_block);
+  p->d_luts = reinterpret_cast<float*>(p->d_block + plan_bytes);
+  float* d_in = reinterpret_cast<float*>(p->d_block + plan_bytes + lut_bytes);
   if (eden) {
     p->eden_seed = eden->seed;
-    if (hipMalloc(&p->d_eden_mean, 64 * sizeof(float)) != hipSuccess ||
-        hipMemcpy(p->d_eden_mean, eden->mean, 64 * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
-      cleanup();
-      return fail(MRL_ERR_HIP, "eden mean upload");
-    }
+    p->d_eden_mean = d_in;
   }
   if (eden_mid) {
     p->mid_seed = eden_mid->seed;
-    if (hipMalloc(&p->d_mid_mean, 128 * sizeof(float)) != hipSuccess ||
-        hipMemcpy(p->d_mid_mean, eden_mid->mean, 128 * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
-      cleanup();
-      return fail(MRL_ERR_HIP, "eden mid mean upload");
-    }
+    p->d_mid_mean = d_in + 64;
   }
-  if (n_q) {
-    const size_t qbytes = (size_t)n_q * dims * sizeof(float);
-    if (hipMalloc(&p->d_queries, qbytes) != hipSuccess) {
-      cleanup();
-      return fail(MRL_ERR_OUT_OF_MEMORY, "queries");
+  if (n_q) p->d_queries = d_in + 192;
+  hipError_t e = hipSuccess;
+  if (!on_device) {
+    uint8_t* h = host_stage(ctx, in_bytes);
+    if (!h) {
+      dev_free(p->d_block);
+      return fail(MRL_ERR_OUT_OF_MEMORY, "pinned staging buffer");
     }
-    if (hipMemcpyAsync(p->d_queries, queries, qbytes, on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
-                       ctx->stream) != hipSuccess) {
-      cleanup();
-      return fail(MRL_ERR_HIP, "query copy");
-    }
+    float* hf = reinterpret_cast<float*>(h);
+    if (eden) memcpy(hf, eden->mean, 64 * sizeof(float));
+    if (eden_mid) memcpy(hf + 64, eden_mid->mean, 128 * sizeof(float));
+    if (n_q) memcpy(hf + 192, queries, qbytes);
+    e = hipMemcpyAsync(d_in, h, in_bytes, hipMemcpyHostToDevice, ctx->stream);
+  } else {
+    float means[192] = {0};
+    if (eden) memcpy(means, eden->mean, 64 * sizeof(float));
+    if (eden_mid) memcpy(means + 64, eden_mid->mean, 128 * sizeof(float));
+    e = hipMemcpy(d_in, means, sizeof(means), hipMemcpyHostToDevice);
+    if (e == hipSuccess && n_q) e = hipMemcpyAsync(d_in + 192, queries, qbytes, hipMemcpyDeviceToDevice, ctx->stream);
+  }
+  if (e != hipSuccess) {
+    dev_free(p->d_block);
+    return fail(MRL_ERR_HIP, "plan inputs copy");
   }
   int rc2 = enqueue_plan(ctx, p.get());
+  // The pinned inputs are reused by the next call: wait for the copy (host path).
+  if (!rc2 && !on_device && hipStreamSynchronize(ctx->stream) != hipSuccess) rc2 = fail(MRL_ERR_HIP, "plan build");
   if (rc2) {
-    cleanup();
+    (void)hipStreamSynchronize(ctx->stream);
+    dev_free(p->d_block);
     return rc2;
-  }
-  if (!on_device && hipStreamSynchronize(ctx->stream) != hipSuccess) {  // host buffer may be released after return
-    cleanup();
-    return fail(MRL_ERR_HIP, "plan build");
   }
   *out = p.release();
   return MRL_OK;
@@ -590,11 +623,7 @@ extern "C" void mrl_plans_destroy(mrl_plans* plans) {
   if (!plans) return;
   (void)hipSetDevice(plans->ctx->device);
   (void)hipStreamSynchronize(plans->ctx->stream);
-  dev_free(plans->d_plans);
-  dev_free(plans->d_luts);
-  dev_free(plans->d_eden_mean);
-  dev_free(plans->d_mid_mean);
-  dev_free(plans->d_queries);
+  dev_free(plans->d_block);
   delete plans;
 }
 
@@ -625,18 +654,22 @@ static ScanParams make_params(const mrl_scan_config* cfg, const mrl_time_range* 
 }
 
 static void results_free(mrl_results* r) {
-  dev_free(r->d_ids);
-  dev_free(r->d_scores);
-  dev_free(r->d_counts);
+  dev_free(r->d_out);
   dev_free(r->d_cand_score);
   dev_free(r->d_cand_row);
   dev_free(r->d_seg_count);
   dev_free(r->d_tau);
   dev_free(r->d_err);
-  dev_free(r->d_status);
-  dev_free(r->d_stats);
   dev_free(r->d_rr);
 }
+
+static void results_release(mrl_results* r) {
+  if (!r) return;
+  results_free(r);
+  delete r;
+}
+
+static size_t results_head_bytes(uint32_t n_q) { return (size_t)n_q * 8 + kStatCount * 8; }
 
 static const uint32_t kSegCap = 4096;  // kSegs * kSegCap = 65536 candidates per query and scan
 
@@ -653,16 +686,21 @@ extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_re
   r->seg_cap = kSegCap;
   const size_t nq = std::max<uint32_t>(n_q, 1);
   const size_t cands = nq * kSegs * (size_t)kSegCap;
-  bool ok = hipMalloc(&r->d_ids, nq * k * sizeof(uint64_t)) == hipSuccess &&
-            hipMalloc(&r->d_scores, nq * k * sizeof(float)) == hipSuccess &&
-            hipMalloc(&r->d_counts, nq * sizeof(uint32_t)) == hipSuccess &&
-            hipMalloc(&r->d_cand_score, cands * sizeof(float)) == hipSuccess &&
+  const size_t head = results_head_bytes((uint32_t)nq);
+  r->out_bytes = head + nq * k * 12;
+  bool ok = hipMalloc(&r->d_out, r->out_bytes) == hipSuccess;
+  if (ok) {
+    r->d_status = reinterpret_cast<uint32_t*>(r->d_out);
+    r->d_counts = r->d_status + nq;
+    r->d_stats = reinterpret_cast<unsigned long long*>(r->d_out + nq * 8);
+    r->d_ids = reinterpret_cast<uint64_t*>(r->d_out + head);
+    r->d_scores = reinterpret_cast<float*>(r->d_out + head + nq * k * 8);
+  }
+  ok = ok && hipMalloc(&r->d_cand_score, cands * sizeof(float)) == hipSuccess &&
             hipMalloc(&r->d_cand_row, cands * sizeof(uint32_t)) == hipSuccess &&
             hipMalloc(&r->d_seg_count, nq * kSegs * sizeof(uint32_t)) == hipSuccess &&
             hipMalloc(&r->d_tau, nq * sizeof(float)) == hipSuccess &&
-            hipMalloc(&r->d_err, nq * sizeof(uint32_t)) == hipSuccess &&
-            hipMalloc(&r->d_status, nq * sizeof(uint32_t)) == hipSuccess &&
-            hipMalloc(&r->d_stats, kStatCount * sizeof(unsigned long long)) == hipSuccess;
+            hipMalloc(&r->d_err, nq * sizeof(uint32_t)) == hipSuccess;
   if (!ok) {
     results_free(r.get());
     return fail(MRL_ERR_OUT_OF_MEMORY, "results buffers");
@@ -670,9 +708,7 @@ extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_re
   // Pass state starts zeroed; each final selection leaves it zeroed again.
   ok = hipMemset(r->d_seg_count, 0, nq * kSegs * sizeof(uint32_t)) == hipSuccess &&
        hipMemset(r->d_err, 0, nq * sizeof(uint32_t)) == hipSuccess &&
-       hipMemset(r->d_status, 0, nq * sizeof(uint32_t)) == hipSuccess &&
-       hipMemset(r->d_counts, 0, nq * sizeof(uint32_t)) == hipSuccess &&
-       hipMemset(r->d_stats, 0, kStatCount * sizeof(unsigned long long)) == hipSuccess &&
+       hipMemset(r->d_out, 0, head) == hipSuccess &&
        hipDeviceSynchronize() == hipSuccess;
   if (!ok) {
     results_free(r.get());
@@ -880,20 +916,67 @@ static int resolve_pending(mrl_ctx* ctx, mrl_results* res) {
   return MRL_OK;
 }
 
+// One read-back of the results block into pinned memory: the head (status,
+// counts, stats) and the ids / scores rows of the first n_q queries.  Caller
+// holds the lock.
+static int read_back(mrl_ctx* ctx, mrl_results* res, uint32_t n_q, uint8_t** out) {
+  const size_t nq = std::max<uint32_t>(res->n_q, 1), K = res->k;
+  const size_t head = results_head_bytes((uint32_t)nq);
+  uint8_t* h = host_stage(ctx, res->out_bytes);
+  if (!h) return fail(MRL_ERR_OUT_OF_MEMORY, "pinned staging buffer");
+  if (n_q == nq) {
+    HIP_TRY(hipMemcpyAsync(h, res->d_out, res->out_bytes, hipMemcpyDeviceToHost, ctx->stream));
+  } else {
+    HIP_TRY(hipMemcpyAsync(h, res->d_out, head + n_q * K * 8, hipMemcpyDeviceToHost, ctx->stream));
+    if (n_q)
+      HIP_TRY(hipMemcpyAsync(h + head + nq * K * 8, res->d_out + head + nq * K * 8, n_q * K * 4,
+                             hipMemcpyDeviceToHost, ctx->stream));
+  }
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  *out = h;
+  return MRL_OK;
+}
+
+// Pending-scan statuses read back: dense re-run of overflowed queries; true
+// in *rerun if any ran.  Caller holds the lock.
+static int handle_scan_status(mrl_ctx* ctx, mrl_results* res, const uint32_t* status, uint32_t n_q, bool* rerun) {
+  *rerun = false;
+  bool nan = false;
+  if (res->pending && n_q && res->last_index && res->last_index->n_blocks) {
+    for (uint32_t q = 0; q < n_q; ++q) {
+      if (status[q] & 1u) nan = true;
+      if (status[q] & 2u) {
+        int rc = dense_rerun(ctx, res, q);
+        if (rc == MRL_ERR_NAN) nan = true;
+        else if (rc) return rc;
+        *rerun = true;
+      }
+    }
+  }
+  res->pending = false;
+  if (nan) return fail(MRL_ERR_NAN, "NaN score among scan survivors (Shortlist::into_sorted would panic)");
+  return MRL_OK;
+}
+
 extern "C" int mrl_results_fetch(mrl_ctx* ctx, mrl_results* res, uint64_t* out_ids, float* out_scores,
                                  uint32_t* out_counts, mrl_scan_stats* stats) {
   if (!ctx || !res) return fail(MRL_ERR_INVALID_ARG, "null argument");
   std::lock_guard<std::mutex> g(ctx->mu);
   HIP_TRY(hipSetDevice(ctx->device));
-  int rc = resolve_pending(ctx, res);
-  if (rc) return rc;
   const uint32_t n_q = res->last_plans ? res->last_plans->n_q : 0;
-  const size_t K = res->k;
-  if (out_ids && n_q) HIP_TRY(hipMemcpy(out_ids, res->d_ids, n_q * K * sizeof(uint64_t), hipMemcpyDeviceToHost));
-  if (out_scores && n_q) HIP_TRY(hipMemcpy(out_scores, res->d_scores, n_q * K * sizeof(float), hipMemcpyDeviceToHost));
-  if (out_counts && n_q) HIP_TRY(hipMemcpy(out_counts, res->d_counts, n_q * sizeof(uint32_t), hipMemcpyDeviceToHost));
-  unsigned long long st[kStatCount] = {0};
-  HIP_TRY(hipMemcpy(st, res->d_stats, sizeof(st), hipMemcpyDeviceToHost));
+  uint8_t* h = nullptr;
+  int rc = read_back(ctx, res, n_q, &h);
+  if (rc) return rc;
+  bool rerun = false;
+  if ((rc = handle_scan_status(ctx, res, reinterpret_cast<const uint32_t*>(h), n_q, &rerun))) return rc;
+  if (rerun && (rc = read_back(ctx, res, n_q, &h))) return rc;
+  const size_t nq = std::max<uint32_t>(res->n_q, 1), K = res->k;
+  const size_t head = results_head_bytes((uint32_t)nq);
+  if (out_ids && n_q) memcpy(out_ids, h + head, n_q * K * 8);
+  if (out_scores && n_q) memcpy(out_scores, h + head + nq * K * 8, n_q * K * 4);
+  if (out_counts && n_q) memcpy(out_counts, h + nq * 4, (size_t)n_q * 4);
+  unsigned long long st[kStatCount];
+  memcpy(st, h + nq * 8, sizeof(st));
   if (stats) {  // counters accumulated since the previous fetch
     stats->blocks = st[kStatBlocks] - res->stats_seen[kStatBlocks];
     stats->active_vecs = st[kStatActive] - res->stats_seen[kStatActive];
@@ -913,13 +996,34 @@ extern "C" int mrl_scan(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* p
   uint32_t K;
   int rc = check_cfg(cfg, &K);
   if (rc) return rc;
+  // Result buffers of the same K and at least n_q rows are reused from the
+  // previous call (every selection leaves the pass state zeroed again).
   mrl_results* res = nullptr;
-  if ((rc = mrl_results_create(ctx, plans->n_q, K, &res))) return rc;
+  {
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (ctx->spare && ctx->spare->k == K && ctx->spare->n_q >= plans->n_q) {
+      res = ctx->spare;
+      ctx->spare = nullptr;
+    }
+  }
+  if (!res && (rc = mrl_results_create(ctx, plans->n_q, K, &res))) return rc;
   rc = mrl_scan_async(ctx, index, plans, cfg, time, res);
   if (!rc) rc = mrl_results_fetch(ctx, res, out_ids, out_scores, out_counts, stats);
-  std::string msg = g_err;
-  mrl_results_destroy(res);
-  g_err = msg;
+  if (rc) {  // a failed scan may leave pass state behind: do not keep these buffers
+    std::string msg = g_err;
+    mrl_results_destroy(res);
+    g_err = msg;
+    return rc;
+  }
+  res->last_plans = nullptr;  // the caller may free the plans and index now
+  res->last_index = nullptr;
+  mrl_results* old = nullptr;
+  {
+    std::lock_guard<std::mutex> g(ctx->mu);
+    old = ctx->spare;
+    ctx->spare = res;
+  }
+  if (old) mrl_results_destroy(old);
   return rc;
 }
 
@@ -1098,9 +1202,10 @@ extern "C" int mrl_rerank_store_download(mrl_ctx* ctx, const mrl_rerank_store* s
   return MRL_OK;
 }
 
-// Sizes of the rerank buffers for n_q lists of `stride` entries, carved from
-// one allocation: row u64, out_rows u64, score f32, out_scores f32, then
-// status u32 and counts u32 per query.
+// Rerank buffers for n_q lists of `stride` entries, carved from one
+// allocation.  The outputs come first so one copy reads them back: status
+// u32[n_q], counts u32[n_q], out_rows u64[n], out_scores f32[n]; then the
+// scratch row u64[n] and score f32[n] (n = n_q * stride).
 struct RerankBuffers {
   float* score;
   uint64_t* row;
@@ -1109,25 +1214,29 @@ struct RerankBuffers {
   uint32_t* status;
   uint32_t* counts;
 };
+static size_t rerank_out_bytes(uint32_t n_q, uint32_t stride) {
+  return (size_t)n_q * 8 + (size_t)n_q * stride * 12;
+}
 static size_t rerank_bytes(uint32_t n_q, uint32_t stride) {
-  return (size_t)n_q * stride * 24 + (size_t)n_q * 8 + 64;
+  return ((rerank_out_bytes(n_q, stride) + 15) & ~(size_t)15) + (size_t)n_q * stride * 12 + 64;
 }
 static RerankBuffers rerank_carve(void* base, uint32_t n_q, uint32_t stride) {
   const size_t n = (size_t)n_q * stride;
   uint8_t* p = static_cast<uint8_t*>(base);
   RerankBuffers b;
-  b.row = reinterpret_cast<uint64_t*>(p);
-  b.out_rows = reinterpret_cast<uint64_t*>(p + n * 8);
-  b.score = reinterpret_cast<float*>(p + n * 16);
-  b.out_scores = reinterpret_cast<float*>(p + n * 20);
-  b.status = reinterpret_cast<uint32_t*>(p + n * 24);
+  b.status = reinterpret_cast<uint32_t*>(p);
   b.counts = b.status + n_q;
+  b.out_rows = reinterpret_cast<uint64_t*>(p + (size_t)n_q * 8);
+  b.out_scores = reinterpret_cast<float*>(p + (size_t)n_q * 8 + n * 8);
+  uint8_t* scratch = p + ((rerank_out_bytes(n_q, stride) + 15) & ~(size_t)15);
+  b.row = reinterpret_cast<uint64_t*>(scratch);
+  b.score = reinterpret_cast<float*>(scratch + n * 8);
   return b;
 }
 
-static int status_error(const std::vector<uint32_t>& st) {
+static int status_error(const uint32_t* st, uint32_t n) {
   uint32_t all = 0;
-  for (uint32_t v : st) all |= v;
+  for (uint32_t i = 0; i < n; ++i) all |= st[i] & 0xffu;
   if (all & 2u) return fail(MRL_ERR_INVALID_ARG, "candidate row out of range of the rerank store");
   if (all & 1u) return fail(MRL_ERR_NAN, "NaN rerank score (partial_cmp().unwrap() would panic)");
   return MRL_OK;
@@ -1136,7 +1245,7 @@ static int status_error(const std::vector<uint32_t>& st) {
 // Enqueue score + sort.  Caller holds the lock.
 static int enqueue_rerank(mrl_ctx* ctx, const mrl_rerank_store* st, const float* d_queries, uint32_t n_q,
                           const uint64_t* d_cand, int cand_ids, const uint32_t* d_counts, uint32_t stride,
-                          const RerankBuffers& b) {
+                          const RerankBuffers& b, const uint32_t* d_scan_status = nullptr) {
   RerankArgs a{};
   a.data = st->d_data;
   a.scales = st->d_scales;
@@ -1155,6 +1264,7 @@ static int enqueue_rerank(mrl_ctx* ctx, const mrl_rerank_store* st, const float*
   a.out_scores = b.out_scores;
   a.status = b.status;
   a.out_counts = b.counts;
+  a.scan_status = d_scan_status;
   ProfScope p1(ctx, MRL_KERNEL_RERANK, 0, 0, n_q);
   ProfScope p2(ctx, MRL_KERNEL_RERANK_SORT, 0, 0, n_q);
   HIP_TRY(launch_rerank(a, ctx->stream, p1.ev(), p2.ev()));
@@ -1203,7 +1313,7 @@ extern "C" int mrl_rerank_rows(mrl_ctx* ctx, const mrl_rerank_store* store, cons
   dev_free(base);
   if (rc) return rc;
   if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("rerank: ") + hipGetErrorString(e));
-  return status_error(st);
+  return status_error(st.data(), (uint32_t)st.size());
 }
 
 extern "C" int mrl_results_rerank(mrl_ctx* ctx, mrl_results* res, const mrl_rerank_store* store, uint64_t* out_rows,
@@ -1215,24 +1325,44 @@ extern "C" int mrl_results_rerank(mrl_ctx* ctx, mrl_results* res, const mrl_rera
   const mrl_plans* plans = res->last_plans;
   if (!plans) return fail(MRL_ERR_INVALID_ARG, "no scan was enqueued on these results");
   if (plans->dims != store->dims) return fail(MRL_ERR_INVALID_ARG, "query dims differ from the store's");
-  int rc = resolve_pending(ctx, res);
-  if (rc) return rc;
-  const uint32_t n_q = plans->n_q, K = res->k;
-  if (n_q == 0) return MRL_OK;
-  if (!res->d_rr && hipMalloc(&res->d_rr, rerank_bytes(res->n_q, K)) != hipSuccess) {
+  const uint32_t n_q = plans->n_q, K = res->k, nq = std::max<uint32_t>(res->n_q, 1);
+  if (n_q == 0) {
+    res->pending = false;
+    return MRL_OK;
+  }
+  if (!res->d_rr && hipMalloc(&res->d_rr, rerank_bytes(nq, K)) != hipSuccess) {
     res->d_rr = nullptr;
     return fail(MRL_ERR_OUT_OF_MEMORY, "rerank buffers");
   }
-  const RerankBuffers b = rerank_carve(res->d_rr, res->n_q, K);
-  if ((rc = enqueue_rerank(ctx, store, plans->d_queries, n_q, res->d_ids, 1, res->d_counts, K, b))) return rc;
-  std::vector<uint32_t> st(n_q);
-  const size_t nc = (size_t)n_q * K;
-  HIP_TRY(hipMemcpyAsync(st.data(), b.status, (size_t)n_q * 4, hipMemcpyDeviceToHost, ctx->stream));
-  if (out_rows) HIP_TRY(hipMemcpyAsync(out_rows, b.out_rows, nc * 8, hipMemcpyDeviceToHost, ctx->stream));
-  if (out_scores) HIP_TRY(hipMemcpyAsync(out_scores, b.out_scores, nc * 4, hipMemcpyDeviceToHost, ctx->stream));
-  if (out_counts) HIP_TRY(hipMemcpyAsync(out_counts, b.counts, (size_t)n_q * 4, hipMemcpyDeviceToHost, ctx->stream));
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
-  return status_error(st);
+  const RerankBuffers b = rerank_carve(res->d_rr, nq, K);
+  const size_t n = (size_t)nq * K;
+  uint8_t* h = host_stage(ctx, rerank_out_bytes(nq, K));
+  if (!h) return fail(MRL_ERR_OUT_OF_MEMORY, "pinned staging buffer");
+  // The rerank is enqueued right behind the scan; the scan's status rides
+  // along in bits 8.. of the rerank status, so one read-back serves both.
+  auto run = [&](const uint32_t* scan_status) -> int {
+    int rc = enqueue_rerank(ctx, store, plans->d_queries, n_q, res->d_ids, 1, res->d_counts, K, b, scan_status);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(h, b.status, (size_t)nq * 8 + (size_t)n_q * K * 8, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(h + (size_t)nq * 8 + n * 8, b.out_scores, (size_t)n_q * K * 4, hipMemcpyDeviceToHost,
+                           ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return MRL_OK;
+  };
+  const bool pend = res->pending && res->last_index && res->last_index->n_blocks;
+  int rc = run(pend ? res->d_status : nullptr);
+  if (rc) return rc;
+  const uint32_t* st = reinterpret_cast<const uint32_t*>(h);
+  std::vector<uint32_t> scan_st(n_q);
+  for (uint32_t q = 0; q < n_q; ++q) scan_st[q] = st[q] >> 8;
+  bool rerun = false;
+  if ((rc = handle_scan_status(ctx, res, scan_st.data(), n_q, &rerun))) return rc;
+  if (rerun && (rc = run(nullptr))) return rc;
+  if ((rc = status_error(st, n_q))) return rc;
+  if (out_rows) memcpy(out_rows, h + (size_t)nq * 8, (size_t)n_q * K * 8);
+  if (out_scores) memcpy(out_scores, h + (size_t)nq * 8 + n * 8, (size_t)n_q * K * 4);
+  if (out_counts) memcpy(out_counts, h + (size_t)nq * 4, (size_t)n_q * 4);
+  return MRL_OK;
 }
 
 // Ring search of n_q queries (device) over n_pending host rows: a transient
@@ -1300,7 +1430,7 @@ extern "C" int mrl_ring_search(mrl_ctx* ctx, const float* pending, uint32_t n_pe
   if (rc) return rc;
   if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("ring search: ") + hipGetErrorString(e));
   for (uint32_t q = 0; q < n_q; ++q) out_counts[q] = keep;
-  return status_error(st);
+  return status_error(st.data(), (uint32_t)st.size());
 }
 
 extern "C" int mrl_results_merge_ring(mrl_ctx* ctx, mrl_results* res, const float* pending, uint32_t n_pending,
@@ -1356,7 +1486,7 @@ extern "C" int mrl_results_merge_ring(mrl_ctx* ctx, mrl_results* res, const floa
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   cleanup();
   if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("ring merge: ") + hipGetErrorString(e));
-  return status_error(st);
+  return status_error(st.data(), (uint32_t)st.size());
 }
 
 // ---------------------------------------------------------------------------

@@ -193,6 +193,7 @@ struct RerankArgs {
   float* out_scores;
   uint32_t* status;         // [n_q]: bit 0 NaN score, bit 1 row out of range
   uint32_t* out_counts;     // [n_q] or null: entries written per query (ring hits excluded)
+  const uint32_t* scan_status;  // [n_q] or null: copied into status bits 8..9
 };
 
 // Ring merge (mrl_rerank.hip): push the sorted ring hits of each query into
