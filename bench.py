@@ -15,7 +15,9 @@ rocprofv3 FETCH_SIZE + WRITE_SIZE reading for the same workload.
 `cpu_baseline` times the C restatement of the reference's scan_blocks
 (oracle/, Rayon-equivalent sharding on host threads) on query 0 of the same
 index, which also cross-checks the GPU top-K for that query.  `host_boundary`
-is the PCIe-inclusive rate of the synchronous host-buffer calls.
+is the PCIe-inclusive rate of the synchronous host-buffer calls.  `rerank`
+reranks every query's device-resident shortlist at fp32 / fp16 / int8 after
+the scan; `encode` runs the GPU encoder over the workload's rows.
 """
 import argparse
 import ctypes as C
@@ -180,8 +182,8 @@ def main():
 
     out["host_boundary"] = host_boundary_rate(L, _lib, dev, ix, queries, fit, w, ccfg, tr)
     if not args.no_rerank:
-        out["rerank"] = rerank_leg(L, _lib, m, dev, w, step, res, queries, args.rerank_reps, n_threads,
-                                   not args.no_cpu_baseline)
+        out["rerank"], out["encode"] = rerank_leg(L, _lib, m, dev, w, step, res, queries, args.rerank_reps,
+                                                  n_threads, not args.no_cpu_baseline, fit, blocks)
 
     if not args.no_cpu_baseline:
         out["cpu_baseline"], out["parity_query0"] = cpu_baseline(w, blocks, queries, fit, ids[0], scores[0],
@@ -189,7 +191,38 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-def rerank_leg(L, _lib, m, dev, w, step, res, queries, reps, n_threads, with_cpu):
+def encode_leg(m, dev, w, rows, fit, blocks, n_threads, with_cpu, reps=5):
+    """GPU encoder (mrl_encode_corpus_device) over the workload's rows already
+    in HBM: median wall time of the synchronous call, algorithmic bytes = f32
+    rows in + records out, and whether its records equal the bench index's
+    (built by the host encoder).  cpu: the host C++ encoder on n_threads."""
+    import numpy as np
+    from mrl_index_amd import source
+    d_rows = m.DeviceBuffer.from_array(rows, dev)
+    d_out = m.DeviceBuffer(blocks.nbytes, dev)
+    n, dims = rows.shape
+    m.encode_corpus_device(d_rows.ptr, n, dims, d_out.ptr, dev, source.DOC, fit)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        m.encode_corpus_device(d_rows.ptr, n, dims, d_out.ptr, dev, source.DOC, fit)
+        ts.append(time.perf_counter() - t0)
+    same = bool(np.array_equal(d_out.to_array(np.uint8, blocks.shape), blocks))
+    d_rows.close()
+    d_out.close()
+    t = float(np.median(ts))
+    alg = n * dims * 4 + blocks.nbytes
+    rec = {"ms": round(t * 1000, 3), "rows_per_s": round(n / t, 1), "algorithmic_gb_s": round(alg / t / 1e9, 1),
+           "identical_to_host_encoder": same}
+    if with_cpu:
+        t0 = time.perf_counter()
+        m.encode_corpus(rows, source.DOC, fit, None, n_threads)
+        rec["cpu_ms"] = round((time.perf_counter() - t0) * 1000, 1)
+        rec["cpu_threads"] = n_threads
+    return rec
+
+
+def rerank_leg(L, _lib, m, dev, w, step, res, queries, reps, n_threads, with_cpu, fit, blocks):
     """Post-scan rerank of every query's shortlist, kept in HBM, at fp32 / fp16 /
     int8 (the reference's precision bench, retrieval_bench.rs:736-745).
     us_per_batch: host wall time of one mrl_results_rerank call after a
@@ -199,7 +232,8 @@ def rerank_leg(L, _lib, m, dev, w, step, res, queries, reps, n_threads, with_cpu
     the store's precision plus the query and the candidate ids."""
     import numpy as np
     if w.n_docs > 2_000_000:
-        return {"skipped": f"corpus rows for {w.n_docs} vectors are not generated by the bench"}
+        skip = {"skipped": f"corpus rows for {w.n_docs} vectors are not generated by the bench"}
+        return skip, skip
     log(f"rerank: generating {w.n_docs} x {w.dims} f32 rows")
     rows = __import__("mrl_index_amd.synth", fromlist=["docs"]).docs(w, 0, w.n_docs, n_threads)
     nq, K = w.n_queries, w.k
@@ -256,8 +290,10 @@ def rerank_leg(L, _lib, m, dev, w, step, res, queries, reps, n_threads, with_cpu
                 prec, queries[0], rows, cand, r_rows[0, :c0], r_scores[0, :c0])
         out[prec.as_str()] = rec
         store.close()
+    log("encode: GPU encoder over the same rows")
+    enc = encode_leg(m, dev, w, rows, fit, blocks, n_threads, with_cpu)
     del rows
-    return out
+    return out, enc
 
 
 def cpu_rerank_us(prec, q, rows, cand, gpu_rows, gpu_scores, budget_s=2.0):
