@@ -187,6 +187,8 @@ struct mrl_results {
   uint32_t* d_cand_row = nullptr;
   uint32_t* d_seg_count = nullptr; // [n_q][kSegs], zero between scans
   float* d_tau = nullptr;
+  float* d_tau_hi = nullptr;       // [n_q] floor of the final pass
+  uint32_t* d_hist = nullptr;      // [n_q][kHistBins] sampling-pass score counts, zero between scans
   uint32_t* d_err = nullptr;       // [n_q], zero between scans
   uint32_t* d_status = nullptr;    // [n_q]
   unsigned long long* d_stats = nullptr;
@@ -431,14 +433,11 @@ extern "C" void mrl_index_destroy(mrl_index* index) {
   delete index;
 }
 
-// Pass schedule for one K.  Pass 0 scores every S0-th block (S0 the
-// smallest power of two leaving at most 256 blocks) with no threshold; pass p
-// scores the multiples of S0 / r^p not scored before, pruning against the K-th
-// best score of all earlier passes (a lower bound of the final K-th score, so
-// pruning and filtering stay exact); the last pass has stride 1.  r is the
-// power of two nearest 16384/K - 1 (at least 2): each pass then grows the
-// scored set so that about 16K candidates per query pass the threshold.
-// Block ids are arithmetic, so a pass needs no index list.
+// Pass schedule (the same for every K).  When the index has more than 256
+// blocks, a sampling pass first scores every S0-th block (S0 the smallest
+// power of two leaving at most 256 blocks), with no threshold; the final pass
+// then scores every block.  Block ids are arithmetic, so a pass needs no
+// index list.
 static int get_levels(mrl_index* ix, uint32_t K, LevelPlan** out) {
   auto it = ix->levels.find(K);
   if (it != ix->levels.end()) {
@@ -449,22 +448,20 @@ static int get_levels(mrl_index* ix, uint32_t K, LevelPlan** out) {
   LevelPlan lp;
   uint32_t s0 = 0;
   while (((B + (1ull << s0) - 1) >> s0) > 256) ++s0;
-  const uint64_t want = std::max<uint64_t>(2, 16384 / std::max<uint32_t>(K, 1) - 1);
-  uint32_t lr = 1;
-  while ((1ull << (lr + 1)) <= want) ++lr;
-  if ((1ull << (lr + 1)) - want < want - (1ull << lr)) ++lr;  // nearest power of two
-  int32_t prev = -1;
-  for (int32_t sh = (int32_t)s0;; sh -= (int32_t)lr) {
-    if (sh < 0) sh = 0;
+  if (s0 > 0) {
     Pass p;
-    p.shift = (uint32_t)sh;
-    p.prev_shift = prev;
-    p.n_pos = (uint32_t)((B + (1ull << sh) - 1) >> sh);
-    p.n_new = p.n_pos - (prev < 0 ? 0u : (uint32_t)((B + (1ull << prev) - 1) >> prev));
+    p.shift = s0;
+    p.prev_shift = -1;
+    p.n_pos = (uint32_t)((B + (1ull << s0) - 1) >> s0);
+    p.n_new = p.n_pos;
     lp.passes.push_back(p);
-    prev = sh;
-    if (sh == 0) break;
   }
+  Pass f;
+  f.shift = 0;
+  f.prev_shift = -1;
+  f.n_pos = (uint32_t)B;
+  f.n_new = (uint32_t)B;
+  lp.passes.push_back(f);
   auto res = ix->levels.emplace(K, std::move(lp));
   *out = &res.first->second;
   return MRL_OK;
@@ -659,6 +656,8 @@ static void results_free(mrl_results* r) {
   dev_free(r->d_cand_row);
   dev_free(r->d_seg_count);
   dev_free(r->d_tau);
+  dev_free(r->d_tau_hi);
+  dev_free(r->d_hist);
   dev_free(r->d_err);
   dev_free(r->d_rr);
 }
@@ -700,6 +699,8 @@ extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_re
             hipMalloc(&r->d_cand_row, cands * sizeof(uint32_t)) == hipSuccess &&
             hipMalloc(&r->d_seg_count, nq * kSegs * sizeof(uint32_t)) == hipSuccess &&
             hipMalloc(&r->d_tau, nq * sizeof(float)) == hipSuccess &&
+            hipMalloc(&r->d_tau_hi, nq * sizeof(float)) == hipSuccess &&
+            hipMalloc(&r->d_hist, nq * kHistBins * sizeof(uint32_t)) == hipSuccess &&
             hipMalloc(&r->d_err, nq * sizeof(uint32_t)) == hipSuccess;
   if (!ok) {
     results_free(r.get());
@@ -709,6 +710,7 @@ extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_re
   ok = hipMemset(r->d_seg_count, 0, nq * kSegs * sizeof(uint32_t)) == hipSuccess &&
        hipMemset(r->d_err, 0, nq * sizeof(uint32_t)) == hipSuccess &&
        hipMemset(r->d_out, 0, head) == hipSuccess &&
+       hipMemset(r->d_hist, 0, nq * kHistBins * sizeof(uint32_t)) == hipSuccess &&
        hipDeviceSynchronize() == hipSuccess;
   if (!ok) {
     results_free(r.get());
@@ -735,21 +737,45 @@ struct PassBuffers {
   uint32_t seg_cap;
   uint32_t* err;
   float* tau;
+  float* tau_hi;
+  uint32_t* hist;
   uint32_t* status;
   uint64_t* out_ids;
   float* out_scores;
   uint32_t* out_counts;
 };
 
-// Enqueue all passes for n_q plans starting at plans_first.  Pass 0 runs
-// with no threshold; after every pass but the last, the histogram threshold
-// becomes the floor of the next; the final selection emits the top K.
-// Caller holds the context lock.
+// Floor rank for the final pass: the rank-th best score of a sample of n_s
+// of the index's n blocks.  The number of sampled vectors above the true
+// K-th score is about Poisson(lambda = K * n_s / n); the final floor is too
+// high only if at least `rank` of them are, and rank = lambda + 4 sqrt(lambda)
+// + 6 leaves a tail of ~1e-6 or less (then the query is re-run at the safe
+// floor) while the final pass keeps about rank * n / n_s candidates.  Never
+// above K (then the floor is the safe one).
+static uint32_t final_rank(uint32_t K, uint64_t n_s, uint64_t n) {
+  const double lambda = (double)K * (double)n_s / (double)std::max<uint64_t>(n, 1);
+  const double r = std::ceil(lambda + 4.0 * std::sqrt(lambda) + 6.0);
+  return (uint32_t)std::min<double>((double)K, std::max(1.0, r));
+}
+
+// Enqueue a scan of n_q plans starting at plans_first.  The sampling pass
+// (when the index has more than 256 blocks) scores a strided sample of
+// blocks with no candidate appends and counts the survivors' exact scores
+// per query.  The final pass scores every block; its workgroups take the
+// floor from those counts at rank final_rank, prune and append at it, and
+// k_select emits the top K (and flags a query whose floor left fewer than K
+// candidates).  rerun_safe: the final pass alone at the safe floor k_select
+// kept (rank K).  Caller holds the context lock.
 static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t plans_first, uint32_t n_q,
                         const ScanParams& sp, uint32_t K, const LevelPlan& lp, const PassBuffers& pb,
-                        unsigned long long* stats) {
+                        unsigned long long* stats, bool rerun_safe = false) {
   hipStream_t s = ctx->stream;
-  for (size_t pi = 0; pi < lp.passes.size(); ++pi) {
+  const size_t np = lp.passes.size();
+  const bool sampled = np > 1 && !rerun_safe;
+  const uint32_t rank = np > 1 ? final_rank(K, lp.passes[0].n_pos, ix->n_blocks) : K;
+  for (size_t pi = 0; pi < np; ++pi) {
+    const bool last = pi + 1 == np;
+    if (rerun_safe && !last) continue;
     ScanArgs a{};
     a.idx = ix->d_blocks;
     a.n_blocks = ix->n_blocks;
@@ -761,25 +787,20 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
     a.n_q = n_q;
     a.flag_tabs = ctx->d_flag_tabs;
     a.sp = sp;
-    a.tau = pi == 0 ? nullptr : pb.tau;
+    a.tau = (last && rerun_safe) ? pb.tau : nullptr;
+    a.hist = last ? nullptr : pb.hist;
+    a.floor_hist = (last && sampled) ? pb.hist : nullptr;
+    a.floor_rank = rank;
     a.cand_score = pb.cand_score;
     a.cand_row = pb.cand_row;
     a.seg_count = pb.seg_count;
     a.nseg = pb.nseg;
     a.seg_cap = pb.seg_cap;
-    a.stats = stats;
+    a.stats = last ? stats : nullptr;
     a.err = pb.err;
-    {
-      ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)pi, lp.passes[pi].n_new, n_q);
-      HIP_TRY(launch_scan(a, false, s, ps.ev()));
-      ps.commit(a.n_pos != 0 && n_q != 0);
-    }
-    if (pi + 1 < lp.passes.size()) {
-      ThreshArgs ta{pb.cand_score, pb.seg_count, pb.nseg, pb.seg_cap, pb.tau, K, n_q};
-      ProfScope ps(ctx, MRL_KERNEL_THRESH, (int)pi, lp.passes[pi].n_new, n_q);
-      HIP_TRY(launch_thresh(ta, s, ps.ev()));
-      ps.commit(n_q != 0);
-    }
+    ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)pi, lp.passes[pi].n_new, n_q);
+    HIP_TRY(launch_scan(a, false, s, ps.ev()));
+    ps.commit(a.n_pos != 0 && n_q != 0);
   }
   SelectArgs sa{};
   sa.cand_score = pb.cand_score;
@@ -793,7 +814,10 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
   sa.out_ids = pb.out_ids;
   sa.out_scores = pb.out_scores;
   sa.out_counts = pb.out_counts;
-  ProfScope ps(ctx, MRL_KERNEL_SELECT, (int)lp.passes.size() - 1, 0, n_q);
+  sa.hist = sampled ? pb.hist : nullptr;
+  sa.floor_rank = rank;
+  sa.tau_safe = pb.tau;
+  ProfScope ps(ctx, MRL_KERNEL_SELECT, (int)np - 1, 0, n_q);
   HIP_TRY(launch_select(sa, n_q, s, ps.ev()));
   ps.commit(n_q != 0);
   return MRL_OK;
@@ -808,6 +832,8 @@ static PassBuffers results_buffers(mrl_results* r) {
   pb.seg_cap = r->seg_cap;
   pb.err = r->d_err;
   pb.tau = r->d_tau;
+  pb.tau_hi = r->d_tau_hi;
+  pb.hist = r->d_hist;
   pb.status = r->d_status;
   pb.out_ids = r->d_ids;
   pb.out_scores = r->d_scores;
@@ -873,6 +899,8 @@ static int dense_rerun(mrl_ctx* ctx, mrl_results* r, uint32_t q) {
   pb.nseg = 1;
   pb.seg_cap = (uint32_t)n_vec;
   pb.tau = r->d_tau + q;
+  pb.tau_hi = r->d_tau_hi + q;
+  pb.hist = nullptr;
   pb.out_ids = r->d_ids + (size_t)q * r->k;
   pb.out_scores = r->d_scores + (size_t)q * r->k;
   pb.out_counts = r->d_counts + q;
@@ -892,6 +920,53 @@ static int dense_rerun(mrl_ctx* ctx, mrl_results* r, uint32_t q) {
                    : MRL_OK;
 }
 
+// The final pass alone, at the safe floor, for query q of the last scan (its
+// final floor left fewer than K candidates); rewrites the query's result row.
+// *st receives the new status.  Caller holds the lock.
+static int safe_rerun(mrl_ctx* ctx, mrl_results* r, uint32_t q, uint32_t* st) {
+  mrl_index* ix = const_cast<mrl_index*>(r->last_index);
+  LevelPlan* lp;
+  int rc = get_levels(ix, r->k, &lp);
+  if (rc) return rc;
+  PassBuffers pb = results_buffers(r);
+  const size_t cand = (size_t)q * kSegs * r->seg_cap;
+  pb.cand_score += cand;
+  pb.cand_row += cand;
+  pb.seg_count += (size_t)q * kSegs;
+  pb.err += q;
+  pb.tau += q;
+  pb.tau_hi += q;
+  pb.hist += (size_t)q * kHistBins;
+  pb.status += q;
+  pb.out_ids += (size_t)q * r->k;
+  pb.out_scores += (size_t)q * r->k;
+  pb.out_counts += q;
+  const ScanParams sp = make_params(&r->last_cfg, &r->last_time);
+  if ((rc = enqueue_scan(ctx, ix, r->last_plans, q, 1, sp, r->k, *lp, pb, nullptr, true))) return rc;
+  HIP_TRY(hipMemcpyAsync(st, pb.status, sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return MRL_OK;
+}
+
+// Acts on one query's scan status: bit 2 (final floor too high) re-runs the
+// final pass at the safe floor, bit 1 (a segment overflowed) re-runs densely,
+// bit 0 (NaN) sets *nan.  *rerun is set if anything ran.  Caller holds the lock.
+static int rerun_query(mrl_ctx* ctx, mrl_results* r, uint32_t q, uint32_t status, bool* nan, bool* rerun) {
+  int rc;
+  if (status & 4u) {
+    if ((rc = safe_rerun(ctx, r, q, &status))) return rc;
+    *rerun = true;
+  }
+  if (status & 1u) *nan = true;
+  if (status & 2u) {
+    rc = dense_rerun(ctx, r, q);
+    if (rc == MRL_ERR_NAN) *nan = true;
+    else if (rc) return rc;
+    *rerun = true;
+  }
+  return MRL_OK;
+}
+
 // Waits for the last scan on res; queries whose candidate lists overflowed are
 // re-run densely.  MRL_ERR_NAN if any query saw a NaN survivor.  Caller holds
 // the context lock.
@@ -902,13 +977,10 @@ static int resolve_pending(mrl_ctx* ctx, mrl_results* res) {
   if (res->pending && n_q && res->last_index && res->last_index->n_blocks) {
     std::vector<uint32_t> status(n_q);
     HIP_TRY(hipMemcpy(status.data(), res->d_status, n_q * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    bool rerun = false;
     for (uint32_t q = 0; q < n_q; ++q) {
-      if (status[q] & 1u) nan = true;
-      if (status[q] & 2u) {
-        int rc = dense_rerun(ctx, res, q);
-        if (rc == MRL_ERR_NAN) nan = true;
-        else if (rc) return rc;
-      }
+      int rc = rerun_query(ctx, res, q, status[q], &nan, &rerun);
+      if (rc) return rc;
     }
   }
   res->pending = false;
@@ -944,13 +1016,8 @@ static int handle_scan_status(mrl_ctx* ctx, mrl_results* res, const uint32_t* st
   bool nan = false;
   if (res->pending && n_q && res->last_index && res->last_index->n_blocks) {
     for (uint32_t q = 0; q < n_q; ++q) {
-      if (status[q] & 1u) nan = true;
-      if (status[q] & 2u) {
-        int rc = dense_rerun(ctx, res, q);
-        if (rc == MRL_ERR_NAN) nan = true;
-        else if (rc) return rc;
-        *rerun = true;
-      }
+      int rc = rerun_query(ctx, res, q, status[q], &nan, rerun);
+      if (rc) return rc;
     }
   }
   res->pending = false;

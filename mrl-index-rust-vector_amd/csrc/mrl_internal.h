@@ -96,9 +96,10 @@ struct PlanArgs {
 
 // Candidate lists: per query, kSegs segments with their own counters.  A
 // workgroup stages its appends in LDS and flushes them with one atomic on
-// its segment.  The threshold and select kernels histogram the appended
-// scores, bin = trunc(clamp((s + 2) * 512, 0, 2047)); the lower edge of the
-// bin holding the K-th best appended score is <= the final K-th score.
+// its segment.  Sampling passes append nothing: they count the exact scores
+// of their survivors in a per-query histogram, bin = trunc(clamp((s + 2) *
+// 512, 0, 2047)); the lower edge of the bin holding the K-th best counted
+// score is <= the final K-th score.
 constexpr int kSegs = 16;
 constexpr int kHistBins = 2048;
 
@@ -116,6 +117,9 @@ struct ScanArgs {
   const float* flag_tabs;      // [0,256) rho = f/255, [256,512) sqrt(max(1-rho^2,0))
   ScanParams sp;
   const float* tau;            // per query: pruning threshold and candidate floor (null: -inf)
+  uint32_t* hist;              // sampling pass: [n_q][kHistBins] score counts, no appends (null: final pass)
+  const uint32_t* floor_hist;  // final pass: floor = bin floor of the floor_rank-th best count
+  uint32_t floor_rank;         //   of this histogram (replaces tau when set)
   float* cand_score;           // [n_q][nseg][seg_cap]
   uint32_t* cand_row;
   uint32_t* seg_count;         // [n_q][nseg]
@@ -128,16 +132,6 @@ struct ScanArgs {
   float* d_score;              // [n_q][n_blocks][64]
 };
 
-struct ThreshArgs {
-  const float* cand_score;  // [n_q][nseg][seg_cap]
-  const uint32_t* seg_count;
-  uint32_t nseg;
-  uint32_t seg_cap;
-  float* tau;               // out [n_q]
-  uint32_t k;
-  uint32_t n_q;
-};
-
 struct SelectArgs {
   const float* cand_score;
   const uint32_t* cand_row;
@@ -146,7 +140,11 @@ struct SelectArgs {
   uint32_t seg_cap;
   uint32_t* err;          // consumed and zeroed
   uint32_t k;
-  uint32_t* status;       // out per query: bit 0 NaN seen, bit 1 a segment overflowed
+  uint32_t* status;       // out per query: bit 0 NaN seen, bit 1 a segment overflowed,
+                          // bit 2 fewer than k candidates above a floor tighter than the safe one
+  uint32_t* hist;         // sampling histogram [n_q][kHistBins] (null: none); zeroed for the next scan
+  uint32_t floor_rank;    // rank the final pass's floor was taken at
+  float* tau_safe;        // out [n_q]: the safe floor (rank k), for a re-run
   uint64_t* out_ids;      // [n_q][k]
   float* out_scores;
   uint32_t* out_counts;
@@ -193,7 +191,7 @@ struct RerankArgs {
   float* out_scores;
   uint32_t* status;         // [n_q]: bit 0 NaN score, bit 1 row out of range
   uint32_t* out_counts;     // [n_q] or null: entries written per query (ring hits excluded)
-  const uint32_t* scan_status;  // [n_q] or null: copied into status bits 8..9
+  const uint32_t* scan_status;  // [n_q] or null: copied into status bits 8..10
 };
 
 // Ring merge (mrl_rerank.hip): push the sorted ring hits of each query into
@@ -224,7 +222,6 @@ struct LaunchEvents {
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device, hipStream_t s);
 hipError_t launch_plan(const PlanArgs& a, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev = {});
-hipError_t launch_thresh(const ThreshArgs& a, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
 
 // mrl_rerank.hip: build a 768-dim store from f32 rows; score + sort.

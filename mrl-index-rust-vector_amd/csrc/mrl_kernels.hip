@@ -589,6 +589,49 @@ __device__ __forceinline__ float bin_floor(uint32_t b) {
   return f;
 }
 
+// One wave: the bin floor of the need-th best count of a histogram (-inf
+// when it holds fewer than need).  Lane l holds bins 32(63-l) .. +31, so the
+// lane order is descending in score.
+__device__ float wave_floor(const uint32_t* h, uint32_t need) {
+  const uint32_t lane = __lane_id();
+  const uint32_t seg = 63u - lane;
+  const uint4* p = reinterpret_cast<const uint4*>(h + seg * 32u);
+  uint32_t c[32];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint4 v = p[k];
+    c[4 * k] = v.x;
+    c[4 * k + 1] = v.y;
+    c[4 * k + 2] = v.z;
+    c[4 * k + 3] = v.w;
+  }
+  uint32_t part = 0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) part += c[i];
+  uint32_t incl = part;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = __shfl_up(incl, off);
+    if ((int)lane >= off) incl += o;
+  }
+  const uint32_t excl = incl - part;
+  const uint64_t hm = __ballot(excl < need && incl >= need);
+  if (hm == 0) return -INFINITY;
+  const uint32_t src = (uint32_t)__ffsll((long long)hm) - 1;
+  uint32_t bin = 0, before = excl;
+  bool found = false;
+#pragma unroll
+  for (int i = 31; i >= 0; --i) {
+    before += c[i];
+    if (!found && before >= need) {
+      bin = seg * 32u + (uint32_t)i;
+      found = true;
+    }
+  }
+  bin = __shfl(bin, (int)src);
+  return bin_floor(bin);
+}
+
 // Per-lane raw inputs of one block, loaded one block ahead.  Lane l < 4 of
 // `hdr` holds header dword {0, 1, 4, 5}[l]: min_ts, max_ts and the two halves
 // of the tombstone mask.  t14 holds this lane's 24 bytes of the S1/S4 planes;
@@ -708,6 +751,9 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   __shared__ float s_midf[256];
   __shared__ unsigned int s_stats[kStatCount];
   __shared__ Staging<DIAG ? 1 : QT> s_app;
+  constexpr bool kLdsHist = QT == 1 && !DIAG;  // sampling-pass counts gathered per workgroup
+  __shared__ uint32_t s_hist[kLdsHist ? kHistBins : 1];
+  __shared__ float s_floor[QT];
 
   const int tid = threadIdx.x;
   const uint32_t q0 = blockIdx.y * QT;
@@ -743,6 +789,17 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   }
   s_rho[tid] = a.flag_tabs[tid];
   s_midf[tid] = a.flag_tabs[256 + tid];
+  if (kLdsHist && a.hist)
+    for (int i = tid; i < kHistBins; i += 256) s_hist[i] = 0u;
+  // Per-query floor: from the sampling histogram (final pass), else tau.
+  if (a.floor_hist) {
+    for (int qi = wave; qi < nq; qi += 4) {
+      const float f = wave_floor(a.floor_hist + (uint64_t)(q0 + qi) * kHistBins, a.floor_rank);
+      if (lane == 0) s_floor[qi] = f;
+    }
+  } else if (tid < nq) {
+    s_floor[tid] = a.tau ? a.tau[q0 + tid] : -INFINITY;
+  }
   __syncthreads();
 
   const ScanParams sp = a.sp;
@@ -798,7 +855,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
       for (int qi = 0; qi < nq; ++qi) {
         const uint32_t q = q0 + qi;
         const CONST_AS mrl_query_plan* p = cview<mrl_query_plan>(a.plans + q);
-        const float tq = a.tau ? cview<float>(a.tau)[q] : -INFINITY;
+        const float tq = s_floor[qi];
         const float tau = sp.exhaustive ? -INFINITY : tq;
         uint64_t masks[5];
         masks[0] = active;
@@ -833,10 +890,18 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
             atomicAdd(&s_stats[kStatPushed], (unsigned)__popcll(surv));
           }
           const bool mine = (surv >> lane) & 1ull;
-          if (ballot(mine && score != score) != 0 && lane == 0) atomicOr(a.err + q, 1u);
-          // Append survivors whose score can still reach the top K.
-          const uint64_t pm = ballot(mine && score >= tq);
-          if (pm != 0) stage_append<QT>(s_app, a, qi, q, seg, pm, score, b * 64u + lane);
+          if (a.hist) {
+            // sampling pass: count the survivors' exact scores
+            if (mine) {
+              if constexpr (kLdsHist) atomicAdd(&s_hist[hist_bin(score)], 1u);
+              else atomicAdd(a.hist + (uint64_t)q * kHistBins + hist_bin(score), 1u);
+            }
+          } else {
+            if (ballot(mine && score != score) != 0 && lane == 0) atomicOr(a.err + q, 1u);
+            // Append survivors whose score can still reach the top K.
+            const uint64_t pm = ballot(mine && score >= tq);
+            if (pm != 0) stage_append<QT>(s_app, a, qi, q, seg, pm, score, b * 64u + lane);
+          }
         }
       }
     }
@@ -845,6 +910,13 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     b_cur = b_nxt;
   }
   flush_appends<QT, DIAG>(s_app, a, q0, nq, seg, s_stats);
+  if (kLdsHist && a.hist) {
+    __syncthreads();
+    for (int i = tid; i < kHistBins; i += 256) {
+      const uint32_t c = s_hist[i];
+      if (c) atomicAdd(a.hist + (uint64_t)q0 * kHistBins + i, c);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -946,6 +1018,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
   __shared__ __align__(16) float s_qc[QT * kQcCount];
   __shared__ unsigned int s_stats[kStatCount];
   __shared__ Staging<QT> s_app;
+  __shared__ float s_floor[QT];
 
   const int tid = threadIdx.x;
   const uint32_t q0 = blockIdx.y * QT;
@@ -980,6 +1053,15 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
     if (d < 128) s_w1[e] = w;
     else s_w4[e - 128 * QT] = w;
   }
+  if (a.floor_hist) {
+    for (int qi = wave; qi < nq; qi += 4) {
+      const float f = wave_floor(a.floor_hist + (uint64_t)(q0 + qi) * kHistBins, a.floor_rank);
+      if (lane == 0) s_floor[qi] = f;
+    }
+  } else if (tid < nq) {
+    s_floor[tid] = a.tau ? a.tau[q0 + tid] : -INFINITY;
+  }
+  __syncthreads();
   if (tid < QT) {
     const int qi = tid;
     float* c = s_qc + qi * kQcCount;
@@ -987,7 +1069,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
     c[kQcTauPrune] = __builtin_nanf("");  // absent query: no lane ever survives
     if (qi < nq) {
       const mrl_query_plan* pq = a.plans + q0 + qi;
-      const float tq = a.tau ? a.tau[q0 + qi] : -INFINITY;
+      const float tq = s_floor[qi];
       const bool b1 = pq->mid_codec == MRL_MID_EDEN_B1;
       c[kQcEden] = pq->prefix_codec == MRL_PREFIX_EDEN_PROD ? 1.0f : 0.0f;
       c[kQcMeanIp] = pq->eden_mean_ip;
@@ -1159,6 +1241,10 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
         const uint64_t pushed = ballot(mine);
         if (a.stats) c_s4b += (uint32_t)__popcll(pushed);
         if (pushed == 0) continue;
+        if (a.hist) {
+          if (mine) atomicAdd(a.hist + (uint64_t)q * kHistBins + hist_bin(score[qi]), 1u);
+          continue;
+        }
         const float tq = s_qc[qi * kQcCount + kQcTauPush];
         if (ballot(mine && score[qi] != score[qi]) != 0 && lane == 0) atomicOr(a.err + q, 1u);
         const uint64_t pm = ballot(mine && score[qi] >= tq);
@@ -1311,23 +1397,6 @@ __device__ void build_hist(uint32_t* hist, const CandView& v) {
   __syncthreads();
 }
 
-// Threshold after a pass: the lower edge of the bin holding the K-th best
-// score appended so far.  Those scores belong to real vectors, so the K-th
-// best of all vectors is at least this edge.  One workgroup per query.
-__global__ __launch_bounds__(1024) void k_thresh(ThreshArgs a) {
-  __shared__ uint32_t s_hist[kHistBins];
-  __shared__ uint32_t s_off[kSegs + 1];
-  __shared__ uint32_t s_coff[kSegs + 1];
-  __shared__ uint32_t s_out[2];
-  const uint32_t q = blockIdx.x;
-  seg_offsets(a.seg_count + (uint64_t)q * a.nseg, a.nseg, a.seg_cap, s_off, s_coff);
-  const CandView v{a.cand_score + (uint64_t)q * a.nseg * a.seg_cap, nullptr, a.seg_cap, a.nseg, s_off, s_coff};
-  build_hist(s_hist, v);
-  find_boundary(s_hist, kHistBins, a.k, true, &s_out[0], &s_out[1]);
-  __syncthreads();
-  if (threadIdx.x == 0) a.tau[q] = bin_floor(s_out[0]);
-}
-
 __device__ __forceinline__ uint64_t composite(uint32_t key, uint32_t row) {
   return ((uint64_t)key << 32) | (uint64_t)(~row);
 }
@@ -1364,10 +1433,18 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   __shared__ uint32_t s_off[kSegs + 1];
   __shared__ uint32_t s_coff[kSegs + 1];
 
+  __shared__ float s_fl[2];
+
   const uint32_t q = blockIdx.x;
   const int tid = threadIdx.x;
   const uint32_t K = a.k;
   const uint32_t* qcount = a.seg_count + (uint64_t)q * a.nseg;
+  // The sampling histogram's safe floor (rank K) and the final pass's floor
+  // (rank floor_rank), for the shortfall check below.
+  if (a.hist && tid < 128) {
+    const float f = wave_floor(a.hist + (uint64_t)q * kHistBins, tid < 64 ? K : a.floor_rank);
+    if ((tid & 63) == 0) s_fl[tid >> 6] = f;
+  }
   if (tid == 0) s_misc[7] = 0;
   __syncthreads();
   if (tid < (int)a.nseg && qcount[tid] > a.seg_cap) atomicOr(&s_misc[7], 2u);
@@ -1500,9 +1577,19 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   __syncthreads();
   // leave this query's pass state clean for the next scan
   if (tid < (int)a.nseg) a.seg_count[(uint64_t)q * a.nseg + tid] = 0u;
+  if (a.hist)
+    for (int i = tid; i < kHistBins; i += kSelThreads) a.hist[(uint64_t)q * kHistBins + i] = 0u;
   if (tid == 0) {
+    // Fewer than K candidates above a floor tighter than the safe one: the
+    // top K may lie below it, so the host re-runs the final pass at the safe
+    // floor, which is kept for that.
+    uint32_t short_k = 0u;
+    if (a.hist) {
+      a.tau_safe[q] = s_fl[0];
+      short_k = (keep < K && s_fl[1] > s_fl[0]) ? 4u : 0u;
+    }
     a.out_counts[q] = keep;
-    a.status[q] = (a.err[q] & 1u) | s_misc[7];
+    a.status[q] = (a.err[q] & 1u) | s_misc[7] | short_k;
     a.err[q] = 0u;
   }
 }
@@ -1583,12 +1670,6 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const Launch
       else launch(k_scan<1, false, false>, g, dim3(256), s, ev, a);
     }
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_thresh(const ThreshArgs& a, hipStream_t s, const LaunchEvents& ev) {
-  if (a.n_q == 0) return hipSuccess;
-  launch(k_thresh, dim3(a.n_q), dim3(1024), s, ev, a);
   return hipGetLastError();
 }
 

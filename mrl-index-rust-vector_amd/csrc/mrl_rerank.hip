@@ -349,7 +349,7 @@ __global__ __launch_bounds__(kSortThreads) void k_rerank_sort(RerankArgs a) {
     for (uint32_t i = tid; i < m; i += kSortThreads) emit(i, s_key[i]);
   }
   if (tid == 0) {
-    a.status[q] = s_bad | (a.scan_status ? (a.scan_status[q] & 3u) << 8 : 0u);
+    a.status[q] = s_bad | (a.scan_status ? (a.scan_status[q] & 7u) << 8 : 0u);
     if (a.out_counts) a.out_counts[q] = m - s_skip;
   }
 }

@@ -108,3 +108,26 @@ def test_nan_score_is_an_error(device):
     with pytest.raises(m.MrlError) as e:
         m.scan_batch(blocks, plan, m.ScanConfig(shortlist_cand=64))
     assert e.value.code == 3
+
+
+def test_final_floor_shortfall_reruns_at_the_safe_floor(device):
+    """The final pass prunes and appends at a floor taken from the sampling
+    pass (a higher rank than K).  Here the vectors near the query all sit in
+    sampled blocks (every 16th of 4096), so that floor lies above the true
+    K-th score and too few candidates remain: the query must be re-run at the
+    safe floor and still return the exact top K."""
+    rng = np.random.default_rng(15)
+    n_blocks, dims, k = 4096, 192, 64
+    rows = normalized(rng, n_blocks * 64, dims)
+    q = normalized(rng, 1, dims)[0]
+    near = (np.arange(40) // 8) * 16 * 64 + (np.arange(40) % 8)  # 8 slots in each of 5 sampled blocks
+    rows[near] = q[None, :] + np.float32(0.02) * normalized(rng, 40, dims)
+    rows[near] /= np.linalg.norm(rows[near], axis=1, keepdims=True).astype(np.float32)
+    blocks = m.encode_corpus(rows, 8)
+    plan = _minmax_plan(q, dims, device)
+    res = m.scan_batch(m.DeviceIndex.upload(blocks, device), plan, m.ScanConfig(shortlist_cand=k))
+    op = ora.plan_build(q, dims)
+    ref_ids, ref_sc = ora.scan_blocks(blocks, op, ora.scan_config(k))
+    n = int(res.counts[0])
+    assert n == len(ref_ids) == k
+    assert_topk_equal(res.ids[0, :n], res.scores[0, :n], ref_ids, ref_sc, k)
