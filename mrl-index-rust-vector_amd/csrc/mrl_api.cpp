@@ -791,6 +791,9 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
     a.hist = last ? nullptr : pb.hist;
     a.floor_hist = (last && sampled) ? pb.hist : nullptr;
     a.floor_rank = rank;
+    a.safe_rank = K;
+    a.floor_out = pb.tau_hi;
+    a.safe_out = pb.tau;
     a.cand_score = pb.cand_score;
     a.cand_row = pb.cand_row;
     a.seg_count = pb.seg_count;
@@ -815,7 +818,7 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
   sa.out_scores = pb.out_scores;
   sa.out_counts = pb.out_counts;
   sa.hist = sampled ? pb.hist : nullptr;
-  sa.floor_rank = rank;
+  sa.tau_final = pb.tau_hi;
   sa.tau_safe = pb.tau;
   ProfScope ps(ctx, MRL_KERNEL_SELECT, (int)np - 1, 0, n_q);
   HIP_TRY(launch_select(sa, n_q, s, ps.ev()));

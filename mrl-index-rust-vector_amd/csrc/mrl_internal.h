@@ -120,6 +120,9 @@ struct ScanArgs {
   uint32_t* hist;              // sampling pass: [n_q][kHistBins] score counts, no appends (null: final pass)
   const uint32_t* floor_hist;  // final pass: floor = bin floor of the floor_rank-th best count
   uint32_t floor_rank;         //   of this histogram (replaces tau when set)
+  uint32_t safe_rank;          // K: the safe floor, also taken from floor_hist
+  float* floor_out;            // [n_q] out: the final floor (written by one workgroup per query)
+  float* safe_out;             // [n_q] out: the safe floor
   float* cand_score;           // [n_q][nseg][seg_cap]
   uint32_t* cand_row;
   uint32_t* seg_count;         // [n_q][nseg]
@@ -143,8 +146,8 @@ struct SelectArgs {
   uint32_t* status;       // out per query: bit 0 NaN seen, bit 1 a segment overflowed,
                           // bit 2 fewer than k candidates above a floor tighter than the safe one
   uint32_t* hist;         // sampling histogram [n_q][kHistBins] (null: none); zeroed for the next scan
-  uint32_t floor_rank;    // rank the final pass's floor was taken at
-  float* tau_safe;        // out [n_q]: the safe floor (rank k), for a re-run
+  const float* tau_final; // [n_q] floor of the final pass (with hist)
+  const float* tau_safe;  // [n_q] safe floor (with hist)
   uint64_t* out_ids;      // [n_q][k]
   float* out_scores;
   uint32_t* out_counts;

@@ -668,6 +668,29 @@ __device__ __forceinline__ void retire_touch(const RawLane& r) {
   asm volatile("" ::"v"(r.t1.x), "v"(r.t1.y), "v"(r.t1.z), "v"(r.t1.w), "v"(r.t4.x), "v"(r.t4.y));
 }
 
+// Prologue of a scan workgroup: the floor of each of its queries.  In the
+// final pass it comes from the sampling histogram at floor_rank; the safe
+// floor (rank safe_rank) is taken too, and workgroup x = 0 of each query tile
+// writes both out for k_select.  Otherwise it is tau (or -inf).  Wave w
+// takes work items w, w + 4, ... (two per query).
+template <int QT>
+__device__ __forceinline__ void take_floors(const ScanArgs& a, uint32_t q0, int nq, int wave, uint32_t lane,
+                                            float* s_floor) {
+  if (a.floor_hist) {
+    for (int it = wave; it < 2 * nq; it += 4) {
+      const int qi = it >> 1;
+      const bool safe = it & 1;
+      const float f = wave_floor(a.floor_hist + (uint64_t)(q0 + qi) * kHistBins, safe ? a.safe_rank : a.floor_rank);
+      if (lane == 0) {
+        if (!safe) s_floor[qi] = f;
+        if (blockIdx.x == 0) (safe ? a.safe_out : a.floor_out)[q0 + qi] = f;
+      }
+    }
+  } else if ((int)threadIdx.x < nq) {
+    s_floor[threadIdx.x] = a.tau ? a.tau[q0 + threadIdx.x] : -INFINITY;
+  }
+}
+
 // Appends of one workgroup are staged here per query and flushed at the end.
 template <int QT>
 struct Staging {
@@ -792,14 +815,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   if (kLdsHist && a.hist)
     for (int i = tid; i < kHistBins; i += 256) s_hist[i] = 0u;
   // Per-query floor: from the sampling histogram (final pass), else tau.
-  if (a.floor_hist) {
-    for (int qi = wave; qi < nq; qi += 4) {
-      const float f = wave_floor(a.floor_hist + (uint64_t)(q0 + qi) * kHistBins, a.floor_rank);
-      if (lane == 0) s_floor[qi] = f;
-    }
-  } else if (tid < nq) {
-    s_floor[tid] = a.tau ? a.tau[q0 + tid] : -INFINITY;
-  }
+  take_floors<QT>(a, q0, nq, wave, lane, s_floor);
   __syncthreads();
 
   const ScanParams sp = a.sp;
@@ -1053,14 +1069,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
     if (d < 128) s_w1[e] = w;
     else s_w4[e - 128 * QT] = w;
   }
-  if (a.floor_hist) {
-    for (int qi = wave; qi < nq; qi += 4) {
-      const float f = wave_floor(a.floor_hist + (uint64_t)(q0 + qi) * kHistBins, a.floor_rank);
-      if (lane == 0) s_floor[qi] = f;
-    }
-  } else if (tid < nq) {
-    s_floor[tid] = a.tau ? a.tau[q0 + tid] : -INFINITY;
-  }
+  take_floors<QT>(a, q0, nq, wave, lane, s_floor);
   __syncthreads();
   if (tid < QT) {
     const int qi = tid;
@@ -1272,6 +1281,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
 // under it is unique and can be assembled from any superset).
 // ---------------------------------------------------------------------------
 constexpr int kSortCap = 8192;
+constexpr int kSelCap = 1024;   // entries at or above the K-th bin floor kept for the final sort
 constexpr int kSelThreads = 1024;
 constexpr int kRankMax = 512;  // up to this many gathered entries are rank-sorted
 
@@ -1363,6 +1373,40 @@ __device__ __forceinline__ void for_each_cand(const CandView& v, F&& fn) {
   }
 }
 
+// The same walk, loading each entry's score and row together; fn also gets
+// the entry's dense position (its index among all of the query's entries,
+// segments in order).
+template <typename F>
+__device__ __forceinline__ void for_each_pair(const CandView& v, F&& fn) {
+  constexpr int W = kWalk / 2;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  const uint32_t items = v.coff[v.nseg];
+  uint32_t s = 0;
+  for (uint32_t c = wave; c < items; c += nwaves) {
+    while (v.coff[s + 1] <= c) ++s;
+    const uint32_t base = (c - v.coff[s]) * kChunk;
+    const uint32_t cnt = v.off[s + 1] - v.off[s];
+    const uint32_t lim = cnt > base ? cnt - base : 0u;
+    for (int h = 0; h < kWalk / W; ++h) {
+      const uint32_t i0 = s * v.seg_cap + base + (uint32_t)h * 64u * W + lane;
+      const uint32_t d0 = v.off[s] + base + (uint32_t)h * 64u * W + lane;
+      const uint32_t lh = lim > (uint32_t)h * 64u * W ? lim - (uint32_t)h * 64u * W : 0u;
+      float sc[W];
+      uint32_t rw[W];
+#pragma unroll
+      for (int u = 0; u < W; ++u)
+        if (64u * u + lane < lh) {
+          sc[u] = v.sc[i0 + 64u * u];
+          rw[u] = v.rw[i0 + 64u * u];
+        }
+#pragma unroll
+      for (int u = 0; u < W; ++u)
+        if (64u * u + lane < lh) fn(sc[u], rw[u], d0 + 64u * u);
+    }
+  }
+}
+
 // Prefix offsets of the (capped) segment counts into off[0..nseg] and of
 // their item counts into coff[0..nseg]: the counters are loaded by nseg
 // threads at once, then summed in LDS.
@@ -1428,6 +1472,8 @@ __device__ void bitonic_desc(uint64_t* s, int n2) {
 // query's counters, histogram and error flag zeroed for the next scan.
 __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   __shared__ uint64_t s_buf[kSortCap];
+  __shared__ uint64_t s_sel[kSelCap + 16];
+  __shared__ uint32_t s_start[kHistBins];
   __shared__ uint32_t s_hist[2048];
   __shared__ uint32_t s_misc[8];
   __shared__ uint32_t s_off[kSegs + 1];
@@ -1439,11 +1485,10 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   const int tid = threadIdx.x;
   const uint32_t K = a.k;
   const uint32_t* qcount = a.seg_count + (uint64_t)q * a.nseg;
-  // The sampling histogram's safe floor (rank K) and the final pass's floor
-  // (rank floor_rank), for the shortfall check below.
-  if (a.hist && tid < 128) {
-    const float f = wave_floor(a.hist + (uint64_t)q * kHistBins, tid < 64 ? K : a.floor_rank);
-    if ((tid & 63) == 0) s_fl[tid >> 6] = f;
+  // The final pass's floor and the safe one, for the shortfall check below.
+  if (a.hist && tid == 0) {
+    s_fl[0] = a.tau_safe[q];
+    s_fl[1] = a.tau_final[q];
   }
   if (tid == 0) s_misc[7] = 0;
   __syncthreads();
@@ -1451,6 +1496,36 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   seg_offsets(qcount, a.nseg, a.seg_cap, s_off, s_coff);
   const CandView v{a.cand_score + (uint64_t)q * a.nseg * a.seg_cap, a.cand_row + (uint64_t)q * a.nseg * a.seg_cap,
                    a.seg_cap, a.nseg, s_off, s_coff};
+  const uint32_t total = s_off[a.nseg];
+  uint32_t m;
+  uint64_t* sb = s_buf;  // the entries the final sort reads
+  if (total <= (uint32_t)kSortCap) {
+    // Every entry fits in LDS: one walk loads (score, row) pairs and
+    // histograms them; the entries at or above the K-th bin's floor are then
+    // picked out of LDS.
+    for (int i = tid; i < kHistBins; i += kSelThreads) s_hist[i] = 0u;
+    __syncthreads();
+    for_each_pair(v, [&](float sc, uint32_t row, uint32_t dense) {
+      atomicAdd(&s_hist[hist_bin(sc)], 1u);
+      s_buf[dense] = composite(score_key(sc), row);
+    });
+    __syncthreads();
+    find_boundary(s_hist, kHistBins, K, true, &s_misc[0], &s_misc[1]);
+    if (tid == 0) s_misc[2] = 0;
+    __syncthreads();
+    const uint32_t fkey = score_key(bin_floor(s_misc[0]));
+    for (uint32_t i = tid; i < total; i += kSelThreads) {
+      const uint64_t c = s_buf[i];
+      if ((uint32_t)(c >> 32) >= fkey) {
+        const uint32_t slot = atomicAdd(&s_misc[2], 1u);
+        if (slot < (uint32_t)kSelCap) s_sel[slot] = c;
+      }
+    }
+    __syncthreads();
+    m = s_misc[2];
+    if (m <= (uint32_t)kSelCap) sb = s_sel;
+    else m = total;  // sort every entry
+  } else {
   build_hist(s_hist, v);
   find_boundary(s_hist, kHistBins, K, true, &s_misc[0], &s_misc[1]);
   __syncthreads();
@@ -1467,7 +1542,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     }
   });
   __syncthreads();
-  uint32_t m = s_misc[2];
+  m = s_misc[2];
   if (m <= (uint32_t)kSortCap) {
     for (uint32_t i = tid; i < m; i += kSelThreads) {
       const uint64_t c = s_buf[i];
@@ -1532,23 +1607,70 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     m = s_misc[2];  // == K
     if (m > (uint32_t)kSortCap) m = kSortCap;
   }
+  }
   const uint32_t keep = m < K ? m : K;
   auto emit = [&](uint32_t r, uint64_t c) {
     const uint32_t row = ~(uint32_t)c;
     a.out_ids[(uint64_t)q * K + r] = ((uint64_t)(row >> 6) << 16) | (uint64_t)(row & 63u);
     a.out_scores[(uint64_t)q * K + r] = key_score((uint32_t)(c >> 32));
   };
-  if (m <= (uint32_t)kRankMax) {
+  if (sb == s_sel) {
+    // Counting sort by histogram bin, descending: an entry's position is the
+    // number of selected entries in higher bins plus the number of larger
+    // keys in its own bin (keys are distinct).  s_hist counts per bin, then
+    // serves as the scatter cursor.
+    for (int i = tid; i < kHistBins; i += kSelThreads) s_hist[i] = 0u;
+    __syncthreads();
+    for (uint32_t i = tid; i < m; i += kSelThreads) atomicAdd(&s_hist[hist_bin(key_score((uint32_t)(sb[i] >> 32)))], 1u);
+    __syncthreads();
+    if (tid < 64) {  // start[b] = entries in bins above b; lane l owns bins 32(63-l) .. +31
+      const uint32_t lane = tid, seg = 63u - lane;
+      uint32_t c[32], part = 0;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        c[i] = s_hist[seg * 32u + i];
+        part += c[i];
+      }
+      uint32_t incl = part;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_up(incl, off);
+        if ((int)lane >= off) incl += o;
+      }
+      uint32_t run = incl - part;
+#pragma unroll
+      for (int i = 31; i >= 0; --i) {
+        s_start[seg * 32u + i] = run;
+        s_hist[seg * 32u + i] = 0u;
+        run += c[i];
+      }
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < m; i += kSelThreads) {
+      const uint64_t c = sb[i];
+      const uint32_t b = hist_bin(key_score((uint32_t)(c >> 32)));
+      s_buf[s_start[b] + atomicAdd(&s_hist[b], 1u)] = c;
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < m; i += kSelThreads) {
+      const uint64_t c = s_buf[i];
+      const uint32_t b = hist_bin(key_score((uint32_t)(c >> 32)));
+      const uint32_t lo = s_start[b], hi = lo + s_hist[b];
+      uint32_t r = lo;
+      for (uint32_t j = lo; j < hi; ++j) r += s_buf[j] > c ? 1u : 0u;
+      if (r < keep) emit(r, c);
+    }
+  } else if (m <= (uint32_t)kRankMax) {
     // Rank sort: the composite keys are distinct, so an entry's position in
     // the descending order is the number of larger keys.  Every lane of a
     // wave reads the same key j at the same time (an LDS broadcast).
     // pad to a multiple of 16 with keys below every composite key
-    for (uint32_t i = m + tid; i < ((m + 15u) & ~15u); i += kSelThreads) s_buf[i] = 0ull;
+    for (uint32_t i = m + tid; i < ((m + 15u) & ~15u); i += kSelThreads) sb[i] = 0ull;
     __syncthreads();
     const uint32_t m16 = (m + 15u) & ~15u;
-    const ulonglong2* b2 = reinterpret_cast<const ulonglong2*>(s_buf);
+    const ulonglong2* b2 = reinterpret_cast<const ulonglong2*>(sb);
     for (uint32_t i = tid; i < m; i += kSelThreads) {
-      const uint64_t key = s_buf[i];
+      const uint64_t key = sb[i];
       uint32_t r = 0;
       ulonglong2 nx[4];
 #pragma unroll
@@ -1569,10 +1691,10 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   } else {
     int n2 = 1;
     while ((uint32_t)n2 < m) n2 <<= 1;
-    for (int i = (int)m + tid; i < n2; i += kSelThreads) s_buf[i] = 0ull;
+    for (int i = (int)m + tid; i < n2; i += kSelThreads) sb[i] = 0ull;
     __syncthreads();
-    bitonic_desc(s_buf, n2);
-    for (uint32_t i = tid; i < keep; i += kSelThreads) emit(i, s_buf[i]);
+    bitonic_desc(sb, n2);
+    for (uint32_t i = tid; i < keep; i += kSelThreads) emit(i, sb[i]);
   }
   __syncthreads();
   // leave this query's pass state clean for the next scan
@@ -1582,12 +1704,8 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   if (tid == 0) {
     // Fewer than K candidates above a floor tighter than the safe one: the
     // top K may lie below it, so the host re-runs the final pass at the safe
-    // floor, which is kept for that.
-    uint32_t short_k = 0u;
-    if (a.hist) {
-      a.tau_safe[q] = s_fl[0];
-      short_k = (keep < K && s_fl[1] > s_fl[0]) ? 4u : 0u;
-    }
+    // floor.
+    const uint32_t short_k = (a.hist && keep < K && s_fl[1] > s_fl[0]) ? 4u : 0u;
     a.out_counts[q] = keep;
     a.status[q] = (a.err[q] & 1u) | s_misc[7] | short_k;
     a.err[q] = 0u;
