@@ -152,7 +152,10 @@ struct ProfScope {
 struct mrl_index {
   mrl_ctx* ctx = nullptr;
   uint8_t* d_blocks = nullptr;
+  uint8_t* d_rows = nullptr;  // each slot's S1 bits (uint4), then each slot's S4 bits (uint2)
   uint64_t n_blocks = 0;
+  uint4* rows1() const { return reinterpret_cast<uint4*>(d_rows); }
+  uint2* rows4() const { return reinterpret_cast<uint2*>(d_rows + n_blocks * 64 * 16); }
   std::map<uint32_t, LevelPlan> levels;
 };
 
@@ -168,7 +171,7 @@ struct mrl_plans {
   float* d_mid_mean = nullptr;
   uint64_t mid_seed = 0;
   float* d_queries = nullptr;  // owned copy, n_q * dims
-  float* d_luts = nullptr;     // n_q * 1024 prefix LUT written by the plan kernel
+  float* d_luts = nullptr;     // n_q * kQData scan constants written by the plan kernel
   uint8_t* d_block = nullptr;  // one allocation holding all of the above
 };
 
@@ -345,21 +348,29 @@ extern "C" int mrl_index_upload(mrl_ctx* ctx, const void* blocks, uint64_t n_blo
     const size_t bytes = (size_t)n_blocks * kBlockBytes;
     uint8_t* staging = nullptr;
     if (hipMalloc(&ix->d_blocks, bytes) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc index");
+    if (hipMalloc(&ix->d_rows, (size_t)n_blocks * 64 * 24) != hipSuccess) {
+      dev_free(ix->d_blocks);
+      return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc index rows");
+    }
     // stage in chunks of at most 256 MiB so the transient copy stays small
     const uint64_t chunk = std::min<uint64_t>(n_blocks, 65536);
     if (hipMalloc(&staging, chunk * kBlockBytes) != hipSuccess) {
       dev_free(ix->d_blocks);
+      dev_free(ix->d_rows);
       return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc staging");
     }
     for (uint64_t b = 0; b < n_blocks; b += chunk) {
       uint64_t nb = std::min(chunk, n_blocks - b);
       hipError_t e = hipMemcpyAsync(staging, src + b * kBlockBytes, nb * kBlockBytes, hipMemcpyHostToDevice,
                                     ctx->stream);
-      if (e == hipSuccess) e = launch_relayout(staging, ix->d_blocks + b * kBlockBytes, nb, true, ctx->stream);
+      if (e == hipSuccess)
+        e = launch_relayout(staging, ix->d_blocks + b * kBlockBytes, nb, true, ctx->stream, ix->rows1() + b * 64,
+                            ix->rows4() + b * 64);
       if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
       if (e != hipSuccess) {
         dev_free(staging);
         dev_free(ix->d_blocks);
+        dev_free(ix->d_rows);
         return fail(MRL_ERR_HIP, std::string("upload: ") + hipGetErrorString(e));
       }
     }
@@ -430,6 +441,7 @@ extern "C" void mrl_index_destroy(mrl_index* index) {
   (void)hipSetDevice(index->ctx->device);
   (void)hipStreamSynchronize(index->ctx->stream);
   dev_free(index->d_blocks);
+  dev_free(index->d_rows);
   delete index;
 }
 
@@ -527,7 +539,7 @@ static int plans_build_impl(mrl_ctx* ctx, const float* queries, bool on_device, 
   // 128][queries], which arrive with one copy (host inputs staged in pinned
   // memory).
   const size_t nq = std::max<uint32_t>(n_q, 1);
-  const size_t plan_bytes = sizeof(mrl_query_plan) * nq, lut_bytes = sizeof(float) * 1024 * nq;
+  const size_t plan_bytes = sizeof(mrl_query_plan) * nq, lut_bytes = sizeof(float) * kQData * nq;
   const size_t qbytes = (size_t)n_q * dims * sizeof(float);
   const size_t in_bytes = (64 + 128) * sizeof(float) + qbytes;
   if (hipMalloc(&p->d_block, plan_bytes + lut_bytes + in_bytes) != hipSuccess)
@@ -778,12 +790,14 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
     if (rerun_safe && !last) continue;
     ScanArgs a{};
     a.idx = ix->d_blocks;
+    a.rows1 = ix->rows1();
+    a.rows4 = ix->rows4();
     a.n_blocks = ix->n_blocks;
     a.n_pos = lp.passes[pi].n_pos;
     a.shift = lp.passes[pi].shift;
     a.prev_shift = lp.passes[pi].prev_shift;
     a.plans = plans->d_plans + plans_first;
-    a.luts = plans->d_luts + (size_t)plans_first * 1024;
+    a.luts = plans->d_luts + (size_t)plans_first * kQData;
     a.n_q = n_q;
     a.flag_tabs = ctx->d_flag_tabs;
     a.sp = sp;
@@ -1718,10 +1732,16 @@ extern "C" int mrl_index_from_device(mrl_ctx* ctx, const void* d_blocks, uint64_
   if (n_blocks) {
     if (hipMalloc(&ix->d_blocks, (size_t)n_blocks * kBlockBytes) != hipSuccess)
       return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc index");
-    hipError_t e = launch_relayout(static_cast<const uint8_t*>(d_blocks), ix->d_blocks, n_blocks, true, ctx->stream);
+    if (hipMalloc(&ix->d_rows, (size_t)n_blocks * 64 * 24) != hipSuccess) {
+      dev_free(ix->d_blocks);
+      return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc index rows");
+    }
+    hipError_t e = launch_relayout(static_cast<const uint8_t*>(d_blocks), ix->d_blocks, n_blocks, true, ctx->stream,
+                                   ix->rows1(), ix->rows4());
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
       dev_free(ix->d_blocks);
+      dev_free(ix->d_rows);
       return fail(MRL_ERR_HIP, std::string("index from device: ") + hipGetErrorString(e));
     }
   }

@@ -50,6 +50,17 @@ static_assert(kDevS4 + 64 * 8 == kBlockBytes, "device layout fills the block");
 
 static_assert(sizeof(mrl_query_plan) == 1664 * 4, "mrl_query_plan layout");
 
+// Scan constants of one query, written by the plan kernel next to its plan
+// (floats): the prefix LUT (codebook[level] * weight[d] at 16 d + level), the
+// S1 weights of the query's mid codec, the folded-tail weights, and the
+// upper ends of the S1 / S4 sums (base + positive weights).
+constexpr int kQdLut = 0;
+constexpr int kQdW1 = 1024;
+constexpr int kQdW4 = 1152;
+constexpr int kQdU1 = 1216;
+constexpr int kQdU4 = 1217;
+constexpr int kQData = 1280;
+
 // Scan-time parameters passed by value to the kernels.
 struct ScanParams {
   float alpha;        // cs_tolerance
@@ -91,7 +102,7 @@ struct PlanArgs {
   uint64_t mid_seed;
   PlanConsts c;
   mrl_query_plan* out;
-  float* luts;  // [n_q][1024] prefix LUT for the scan
+  float* luts;  // [n_q][kQData] scan constants
 };
 
 // Candidate lists: per query, kSegs segments with their own counters.  A
@@ -105,6 +116,8 @@ constexpr int kHistBins = 2048;
 
 struct ScanArgs {
   const uint8_t* idx;          // device-layout blocks
+  const uint4* rows1;          // [n_blocks * 64] each slot's S1 bits (dword k: dims 32k..32k+31)
+  const uint2* rows4;          // [n_blocks * 64] each slot's S4 bits
   uint64_t n_blocks;
   // Blocks of this pass: b = pos << shift for pos < n_pos, except those an
   // earlier pass covered (prev_shift >= 0 and b a multiple of 1 << prev_shift).
@@ -112,7 +125,7 @@ struct ScanArgs {
   uint32_t shift;
   int32_t prev_shift;
   const mrl_query_plan* plans;
-  const float* luts;           // [n_q][64][16] prefix LUT (codebook[level] * weight[d])
+  const float* luts;           // [n_q][kQData] scan constants (prefix LUT, stage weights, sum bounds)
   uint32_t n_q;
   const float* flag_tabs;      // [0,256) rho = f/255, [256,512) sqrt(max(1-rho^2,0))
   ScanParams sp;
@@ -222,7 +235,9 @@ struct LaunchEvents {
   hipEvent_t stop = nullptr;
 };
 
-hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device, hipStream_t s);
+// to_device also writes each slot's own S1 / S4 bits (rows1 / rows4, may be null).
+hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device, hipStream_t s,
+                           uint4* rows1 = nullptr, uint2* rows4 = nullptr);
 hipError_t launch_plan(const PlanArgs& a, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});

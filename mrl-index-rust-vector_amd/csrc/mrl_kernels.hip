@@ -137,7 +137,8 @@ __device__ __forceinline__ float masked_accumulate(float s, uint64_t m, const CO
 // one 64-lane workgroup per block; lane v owns slot v
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void k_relayout_to_device(const uint8_t* __restrict__ src,
-                                                          uint8_t* __restrict__ dst, uint64_t n_blocks) {
+                                                          uint8_t* __restrict__ dst, uint64_t n_blocks,
+                                                          uint4* __restrict__ rows1, uint2* __restrict__ rows4) {
   const uint32_t v = threadIdx.x;
   for (uint64_t b = blockIdx.x; b < n_blocks; b += gridDim.x) {
     const uint8_t* s = src + b * kBlockBytes;
@@ -169,6 +170,19 @@ __global__ __launch_bounds__(64) void k_relayout_to_device(const uint8_t* __rest
     d1[v] = s1[v];
     d1[v + 64] = s1[v + 64];
     d4[v] = s4[v];
+    if (rows1) {
+      // slot v's own S1 / S4 bits: dword k holds dims 32k..32k+31, bit i = dim 32k + i
+      uint32_t r[6];
+#pragma unroll
+      for (int k = 0; k < 6; ++k) {
+        const uint64_t* pl = k < 4 ? s1 + 32 * k : s4 + 32 * (k - 4);
+        uint32_t w = 0;
+        for (int i = 0; i < 32; ++i) w |= (uint32_t)((pl[i] >> v) & 1u) << i;
+        r[k] = w;
+      }
+      rows1[b * 64 + v] = make_uint4(r[0], r[1], r[2], r[3]);
+      rows4[b * 64 + v] = make_uint2(r[4], r[5]);
+    }
   }
 }
 
@@ -300,7 +314,9 @@ __global__ __launch_bounds__(128) void k_plan(PlanArgs a) {
     p->eden_q_rot[t] = s_eden[t];
     float tq = has_tail ? s_tail[t] : 0.0f;
     p->tail_fold_q[t] = tq;
-    p->tail_fold_weights2[t] = has_tail ? 2.0f * (tq * ts) : 0.0f;
+    const float w4 = has_tail ? 2.0f * (tq * ts) : 0.0f;
+    p->tail_fold_weights2[t] = w4;
+    a.luts[(uint64_t)q * kQData + kQdW4 + t] = w4;
     // scan.rs:457-461
     p->prefix_weight[t] = eden_codec ? s_eden[t] * a.c.inv_sqrt64 : v;
   }
@@ -313,7 +329,9 @@ __global__ __launch_bounds__(128) void k_plan(PlanArgs a) {
     float c0 = has_mid ? a.c.eden_mid_codebook[0] : 0.0f;
     float c1 = has_mid ? a.c.eden_mid_codebook[1] : 0.0f;
     float qq = s_emid[t] * a.c.inv_sqrt128;
-    p->eden_mid_deltas[t] = (c1 - c0) * qq;
+    const float dl = (c1 - c0) * qq;
+    p->eden_mid_deltas[t] = dl;
+    a.luts[(uint64_t)q * kQData + kQdW1 + t] = a.mid_codec == MRL_MID_EDEN_B1 ? dl : 2.0f * (rq * rs);
   }
   // rabitq_lut (scan.rs:188-201): 512 entries, 4 per thread
   for (int e = t; e < 512; e += 128) {
@@ -326,15 +344,16 @@ __global__ __launch_bounds__(128) void k_plan(PlanArgs a) {
     float v3 = (mask & 8) ? p3 : -p3;
     p->rabitq_lut[g][mask] = v0 + v1 + v2 + v3;
   }
-  // Prefix LUT for the scan: lut[d*16 + level] = codebook[level] * weight[d]
-  // (or level * weight[d]), the product scan.rs:476-484 forms per (d, level).
+  // Scan constants.  Prefix LUT: lut[d*16 + level] = codebook[level] *
+  // weight[d] (or level * weight[d]), the product scan.rs:476-484 forms per
+  // (d, level); then the stage weights as the plan holds them.
+  float* qd = a.luts + (uint64_t)q * kQData;
   {
-    float* lut = a.luts + (uint64_t)q * 1024;
     for (int e = t; e < 1024; e += 128) {
       const int d = e >> 4, l = e & 15;
       const float w = eden_codec ? s_eden[d] * a.c.inv_sqrt64 : s_q[d];
       const float cb = eden_codec ? a.c.eden_codebook[l] : (float)l;
-      lut[e] = cb * w;
+      qd[kQdLut + e] = cb * w;
     }
   }
   if (t < 16) p->eden_codebook[t] = has_eden ? a.c.eden_codebook[t] : 0.0f;
@@ -431,6 +450,22 @@ __global__ __launch_bounds__(128) void k_plan(PlanArgs a) {
     p->q_after_prefix = sqrtf(mid_sq + tail_sq);
     p->q_after_s1 = qt;
   }
+  if (t < 64) {
+    // upper ends of the S1 / S4 sums: base + positive weights (the qd writes
+    // above are this workgroup's own, visible after the barrier)
+    float p1 = fmaxf(qd[kQdW1 + t], 0.0f) + fmaxf(qd[kQdW1 + 64 + t], 0.0f);
+    float p4 = fmaxf(qd[kQdW4 + t], 0.0f);
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+      p1 += __shfl_xor(p1, h);
+      p4 += __shfl_xor(p4, h);
+    }
+    if (t == 0) {
+      qd[kQdU1] = s_sums[6] + p1;  // rabitq_base + positive rabitq_weights2
+      qd[kQdU4] = s_sums[7] + p4;  // tail_fold_base + positive tail weights
+    }
+  }
+  for (int e = kQdU4 + 1 + t; e < kQData; e += 128) qd[e] = 0.0f;
 }
 
 // ---------------------------------------------------------------------------
@@ -495,19 +530,48 @@ __device__ __forceinline__ uint32_t lut_off(uint32_t w2, uint32_t w3, uint32_t m
   return and_byte<I / 2>((I & 1) ? w3 : w2, m);
 }
 
-// One (block, query) evaluation: the stage functions of src/scan.rs:453-634
-// composed as run_default_scan_kernel (654-691).  Returns the pushed-survivor
-// mask; score/prefix_ip are this lane's values.
-__device__ __forceinline__ uint64_t eval_block(const CONST_AS uint8_t* blk, uint64_t active,
-                                              const LaneBlock& m, const float* __restrict__ lut,
-                                              const float* __restrict__ w_mid, const float* __restrict__ w_tail,
-                                              const CONST_AS mrl_query_plan* p, const ScanParams& sp,
-                                              float tau, float& prefix_ip_out, float& score_out,
-                                              uint64_t* masks) {
-  const float alpha = sp.alpha;
-  // Stage: 4-bit prefix IP (scan.rs:453-517).  lut[d*16 + level] holds the
-  // reference's product codebook[level] * weight (or level * weight), so the
-  // per-vector sum over d is the same sequence of f32 additions.
+// Tighter admissible bounds for the stage checks.  When the reference's own
+// bounds are admissible (alpha >= 1 and 2.4 * w_s4 <= alpha: every bound then
+// dominates the score still to come, so its top K is the exact top K by full
+// score), any bound on the full score gives the same top K.  The RaBitQ sum
+// s1 = base + (set weights) lies in [base + negative weights, base + positive
+// weights], and likewise the folded-tail sum, so with mid_n > 0 and hn > 0
+//   full score <= prefix_ip + U1 * mid_n + U4 * w_s4 * hn   (U = base + positive weights),
+// and after S1, score <= score + U4 * w_s4 * hn.  The float evaluation is
+// covered by a relative margin of 2^-8 on the remainder and 2^-20 * (|x| + 1)
+// on the sum (the sums run over at most 128 terms).  tight_coef() returns,
+// from the plan kernel's U1 and U4, A = U1 (1 + 2^-8) and B = U4 w_s4 (1 + 2^-8)
+// (B = 0 without a tail stage),
+// or A = NaN where the reference's checks are kept: EdenB1 mid-band, other
+// alpha / w_s4, or non-finite coefficients.
+constexpr float kTightMargin = 1.0f / 1048576.0f;
+
+__device__ __forceinline__ void tight_coef(float u1_raw, float u4_raw, bool eden_b1, bool has_tail, bool full,
+                                           const ScanParams& sp, float* A, float* B) {
+  const float u1 = u1_raw * (1.0f + 1.0f / 256.0f);
+  const float u4 = (full && has_tail) ? u4_raw * sp.w_s4 * (1.0f + 1.0f / 256.0f) : 0.0f;
+  const bool ok = !eden_b1 && sp.alpha >= 1.0f && sp.w_s4 >= 0.0f && 2.4f * sp.w_s4 <= sp.alpha &&
+                  sp.strata != MRL_STRATA_L0_ONLY && u1 - u1 == 0.0f && u4 - u4 == 0.0f;
+  *A = ok ? fmaxf(u1, 0.0f) : __builtin_nanf("");
+  *B = fmaxf(u4, 0.0f);
+}
+
+// Bound before the S1 stage: the tight one when A is a number, else the reference's.
+__device__ __forceinline__ float prefix_bound(float prefix_ip, float mid_n, float high_n, float A, float B,
+                                              float alpha, float q_mid, float q_tail) {
+  const float hn = fmaxf(high_n, 1e-6f);
+  return A == A ? prefix_ip + (A * mid_n + B * hn) + kTightMargin * (fabsf(prefix_ip) + 1.0f)
+                : prefix_ip + alpha * (q_mid * mid_n + q_tail * high_n);
+}
+__device__ __forceinline__ float s1_bound(float score, float high_n, float A, float B, float alpha, float q_after) {
+  const float hn = fmaxf(high_n, 1e-6f);
+  return A == A ? score + B * hn + kTightMargin * (fabsf(score) + 1.0f) : score + alpha * q_after * high_n;
+}
+
+// Stage: 4-bit prefix IP (scan.rs:453-517).  lut[d*16 + level] holds the
+// reference's product codebook[level] * weight (or level * weight), so the
+// per-vector sum over d is the same sequence of f32 additions.
+__device__ __forceinline__ float prefix_acc(const LaneBlock& m, const float* __restrict__ lut) {
   float acc = zero_acc();
   const char* lutb = reinterpret_cast<const char*>(lut);
   const uint32_t mask = 0x3Cu;
@@ -524,10 +588,24 @@ __device__ __forceinline__ uint64_t eval_block(const CONST_AS uint8_t* blk, uint
     acc = acc + ld(8 * j + 6, lut_off<6>(w2, w3, mask));
     acc = acc + ld(8 * j + 7, lut_off<7>(w2, w3, mask));
   }
+  return acc;
+}
+
+// One (block, query) evaluation: the stage functions of src/scan.rs:453-634
+// composed as run_default_scan_kernel (654-691).  Returns the pushed-survivor
+// mask; score/prefix_ip are this lane's values.
+__device__ __forceinline__ uint64_t eval_block(const CONST_AS uint8_t* blk, uint64_t active,
+                                              const LaneBlock& m, const float* __restrict__ lut,
+                                              const float* __restrict__ w_mid, const float* __restrict__ w_tail,
+                                              const CONST_AS mrl_query_plan* p, const ScanParams& sp,
+                                              float tau, float& prefix_ip_out, float& score_out,
+                                              uint64_t* masks, float tA, float tB) {
+  const float alpha = sp.alpha;
+  const float acc = prefix_acc(m, lut);
   const bool eden = p->prefix_codec == MRL_PREFIX_EDEN_PROD;
   float prefix_ip = eden ? p->eden_mean_ip + m.scale * acc : acc * m.scale + m.offset * p->prefix_sum;
   float score = prefix_ip;
-  float ub = prefix_ip + alpha * (p->q_mid_norm * m.mid_n + p->q_tail_norm * m.high_n);
+  float ub = prefix_bound(prefix_ip, m.mid_n, m.high_n, tA, tB, alpha, p->q_mid_norm, p->q_tail_norm);
   uint64_t surv = ballot(ub >= tau) & active;
   masks[1] = masks[2] = masks[3] = surv;
   prefix_ip_out = prefix_ip;
@@ -541,7 +619,7 @@ __device__ __forceinline__ uint64_t eval_block(const CONST_AS uint8_t* blk, uint
     float s1 = masked_accumulate<16>(b1 ? p->eden_mid_base : p->rabitq_base, surv, s1p, w_mid);
     score = b1 ? score + (p->eden_mid_mean_ip + m.offset * s1) : score + s1 * m.mid_n;
     // Stage: post-S1 CS (scan.rs:572-584)
-    float ub2 = score + alpha * p->q_after_s1 * m.high_n;
+    float ub2 = s1_bound(score, m.high_n, tA, tB, alpha, p->q_after_s1);
     surv &= ballot(ub2 >= tau);
     masks[2] = masks[3] = surv;
   }
@@ -592,18 +670,26 @@ __device__ __forceinline__ float bin_floor(uint32_t b) {
 // One wave: the bin floor of the need-th best count of a histogram (-inf
 // when it holds fewer than need).  Lane l holds bins 32(63-l) .. +31, so the
 // lane order is descending in score.
-__device__ float wave_floor(const uint32_t* h, uint32_t need) {
+struct HistRow {
+  uint4 v[8];
+};
+__device__ __forceinline__ HistRow hist_row(const uint32_t* h) {
+  const uint4* p = reinterpret_cast<const uint4*>(h + (63u - __lane_id()) * 32u);
+  HistRow r;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) r.v[k] = p[k];
+  return r;
+}
+__device__ float floor_of(const HistRow& r, uint32_t need) {
   const uint32_t lane = __lane_id();
   const uint32_t seg = 63u - lane;
-  const uint4* p = reinterpret_cast<const uint4*>(h + seg * 32u);
   uint32_t c[32];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    const uint4 v = p[k];
-    c[4 * k] = v.x;
-    c[4 * k + 1] = v.y;
-    c[4 * k + 2] = v.z;
-    c[4 * k + 3] = v.w;
+    c[4 * k] = r.v[k].x;
+    c[4 * k + 1] = r.v[k].y;
+    c[4 * k + 2] = r.v[k].z;
+    c[4 * k + 3] = r.v[k].w;
   }
   uint32_t part = 0;
 #pragma unroll
@@ -631,6 +717,7 @@ __device__ float wave_floor(const uint32_t* h, uint32_t need) {
   bin = __shfl(bin, (int)src);
   return bin_floor(bin);
 }
+__device__ float wave_floor(const uint32_t* h, uint32_t need) { return floor_of(hist_row(h), need); }
 
 // Per-lane raw inputs of one block, loaded one block ahead.  Lane l < 4 of
 // `hdr` holds header dword {0, 1, 4, 5}[l]: min_ts, max_ts and the two halves
@@ -646,6 +733,7 @@ struct RawLane {
   uint2 t4;
 };
 
+template <bool PLANES = true>
 __device__ __forceinline__ RawLane load_raw(const uint8_t* blk) {
   RawLane r;
   const uint32_t lane = __lane_id();
@@ -658,8 +746,13 @@ __device__ __forceinline__ RawLane load_raw(const uint8_t* blk) {
   for (int j = 0; j < 8; ++j) r.nib[j] = nibp[64 * j + lane];
   const uint32_t hw = lane < 2 ? lane : (lane < 4 ? lane + 2 : 0);
   r.hdr = reinterpret_cast<const uint32_t*>(blk)[hw];
-  r.t1 = reinterpret_cast<const uint4*>(blk + kDevS1)[lane];
-  r.t4 = reinterpret_cast<const uint2*>(blk + kDevS4)[lane];
+  if constexpr (PLANES) {
+    r.t1 = reinterpret_cast<const uint4*>(blk + kDevS1)[lane];
+    r.t4 = reinterpret_cast<const uint2*>(blk + kDevS4)[lane];
+  } else {
+    r.t1 = make_uint4(0u, 0u, 0u, 0u);
+    r.t4 = make_uint2(0u, 0u);
+  }
   return r;
 }
 
@@ -673,14 +766,23 @@ __device__ __forceinline__ void retire_touch(const RawLane& r) {
 // floor (rank safe_rank) is taken too, and workgroup x = 0 of each query tile
 // writes both out for k_select.  Otherwise it is tau (or -inf).  Wave w
 // takes work items w, w + 4, ... (two per query).
+// The histogram row of a wave's first item, loaded at the start of the prologue.
+__device__ __forceinline__ HistRow floor_prefetch(const ScanArgs& a, uint32_t q0, int nq, int wave) {
+  HistRow r{};
+  if (a.floor_hist && wave < 2 * nq) r = hist_row(a.floor_hist + (uint64_t)(q0 + (wave >> 1)) * kHistBins);
+  return r;
+}
+
 template <int QT>
 __device__ __forceinline__ void take_floors(const ScanArgs& a, uint32_t q0, int nq, int wave, uint32_t lane,
-                                            float* s_floor) {
+                                            float* s_floor, const HistRow& first) {
   if (a.floor_hist) {
     for (int it = wave; it < 2 * nq; it += 4) {
       const int qi = it >> 1;
       const bool safe = it & 1;
-      const float f = wave_floor(a.floor_hist + (uint64_t)(q0 + qi) * kHistBins, safe ? a.safe_rank : a.floor_rank);
+      const uint32_t need = safe ? a.safe_rank : a.floor_rank;
+      const float f = it == wave ? floor_of(first, need)
+                                 : wave_floor(a.floor_hist + (uint64_t)(q0 + qi) * kHistBins, need);
       if (lane == 0) {
         if (!safe) s_floor[qi] = f;
         if (blockIdx.x == 0) (safe ? a.safe_out : a.floor_out)[q0 + qi] = f;
@@ -762,14 +864,110 @@ __device__ __forceinline__ void flush_appends(Staging<DIAG ? 1 : QT>& st, const 
   }
 }
 
+// One-query scans defer the S1 / S4 stages: the prefix stage's survivors of
+// each block wait in a per-wave queue, and once 64 are queued they are
+// finished together with lane = survivor, from each slot's own S1 / S4 bits
+// (rows1 / rows4).  A survivor's stage sums are the same additions in the same
+// order as the exec-masked form (a clear bit adds -0.0, which leaves every
+// value unchanged, as skipping it does).
+struct DeferQ {
+  uint32_t row[64];
+  float score[64];  // prefix_ip
+  float mid_n[64];
+  float high_n[64];
+  float offset[64];
+};
+
+// w where bit k of word is set, else -0.0
+__device__ __forceinline__ float bit_weight(uint32_t word, int k, float w) {
+  const uint32_t m = (uint32_t)((int32_t)(word << (31 - k)) >> 31);
+  return __uint_as_float((__float_as_uint(w) & m) | (0x80000000u & ~m));
+}
+
+// s + the weights of the set bits of a row, in dim order (NW dwords = 32 NW dims)
+template <int NW>
+__device__ __forceinline__ float row_sum(float s, const uint32_t (&bits)[NW], const float* __restrict__ w) {
+#pragma unroll
+  for (int c = 0; c < NW * 8; ++c) {
+    const float4 w4 = reinterpret_cast<const float4*>(w)[c];
+    const uint32_t word = bits[c >> 3];
+    const int k0 = (c & 7) * 4;
+    s = s + bit_weight(word, k0, w4.x);
+    s = s + bit_weight(word, k0 + 1, w4.y);
+    s = s + bit_weight(word, k0 + 2, w4.z);
+    s = s + bit_weight(word, k0 + 3, w4.w);
+  }
+  return s;
+}
+
+// Finishes the qn queued survivors of this wave: S1, post-S1 check, S4
+// budget and S4 (scan.rs:520-634), then the push (or, in a sampling pass,
+// the score count).
+__device__ __forceinline__ void defer_flush(const DeferQ& dq, uint32_t qn, const ScanArgs& a,
+                                         const CONST_AS mrl_query_plan* p, const float* __restrict__ w1,
+                                         const float* __restrict__ w4, float tA, float tB, float tq, float tau,
+                                         Staging<1>& st, uint32_t q, uint32_t seg, uint32_t* s_hist,
+                                         unsigned int* s_stats) {
+  const uint32_t lane = __lane_id();
+  const ScanParams& sp = a.sp;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const bool have = lane < qn;
+  uint32_t row = 0;
+  float score = 0.0f, mid_n = 1e-6f, high_n = 0.0f, offset = 0.0f;
+  uint4 r1 = make_uint4(0u, 0u, 0u, 0u);
+  uint2 r4 = make_uint2(0u, 0u);
+  if (have) {
+    row = dq.row[lane];
+    score = dq.score[lane];
+    mid_n = dq.mid_n[lane];
+    high_n = dq.high_n[lane];
+    offset = dq.offset[lane];
+    r1 = a.rows1[row];
+    r4 = a.rows4[row];
+  }
+  const bool b1 = p->mid_codec == MRL_MID_EDEN_B1;
+  const uint32_t bits1[4] = {r1.x, r1.y, r1.z, r1.w};
+  const float s1 = row_sum<4>(b1 ? p->eden_mid_base : p->rabitq_base, bits1, w1);
+  score = b1 ? score + (p->eden_mid_mean_ip + offset * s1) : score + s1 * mid_n;
+  // Stage: post-S1 CS (scan.rs:572-584)
+  bool keep = have && s1_bound(score, high_n, tA, tB, sp.alpha, p->q_after_s1) >= tau;
+  const uint64_t k1 = ballot(keep);
+  uint64_t k3 = k1;
+  if (sp.strata == MRL_STRATA_FULL64B && k1 != 0) {
+    const float hn = fmaxf(high_n, 1e-6f);
+    // Stage: S4 abs-budget prune (scan.rs:587-607)
+    if (p->has_tail_fold && p->s4_abs_budget > 0.0f)
+      keep = keep && score + sp.alpha * hn * sp.w_s4 * p->s4_abs_budget >= tau;
+    k3 = ballot(keep);
+    // Stage: folded-tail 1-bit IP (scan.rs:610-634)
+    if (k3 != 0 && p->has_tail_fold) {
+      const uint32_t bits4[2] = {r4.x, r4.y};
+      const float s4 = row_sum<2>(p->tail_fold_base, bits4, w4);
+      score = keep ? score + s4 * hn * sp.w_s4 : score;
+    }
+  }
+  if (a.stats && lane == 0) {
+    atomicAdd(&s_stats[kStatS1], (unsigned)__popcll(k1));
+    atomicAdd(&s_stats[kStatS4Budget], (unsigned)__popcll(k3));
+    atomicAdd(&s_stats[kStatPushed], (unsigned)__popcll(k3));
+  }
+  if (a.hist) {
+    if (keep) atomicAdd(&s_hist[hist_bin(score)], 1u);
+  } else {
+    if (ballot(keep && score != score) != 0 && lane == 0) atomicOr(a.err + q, 1u);
+    const uint64_t pm = ballot(keep && score >= tq);
+    if (pm != 0) stage_append<1>(st, a, 0, q, seg, pm, score, row);
+  }
+}
+
 // One pass of the strata scan.  Workgroup = 4 waves; wave = one block at a
 // time (lane v = slot v), blocks pos = first + k * stride of the pass order.
 // QT queries share each block's loads.  L0 selects the L0Only stage set.
 template <int QT, bool DIAG, bool L0>
 __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
-  __shared__ __align__(16) float s_lut[L0 ? 1 : QT * 1024];
-  __shared__ __align__(16) float s_wmid[L0 ? 1 : QT * 128];  // S1 weights: rabitq_weights2 or eden_mid_deltas
-  __shared__ __align__(16) float s_wtail[L0 ? 1 : QT * 64];  // S4 weights: tail_fold_weights2
+  __shared__ __align__(16) float s_qd[L0 ? 1 : QT * kQData];  // scan constants of each query
   __shared__ float s_rho[256];
   __shared__ float s_midf[256];
   __shared__ unsigned int s_stats[kStatCount];
@@ -777,6 +975,9 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   constexpr bool kLdsHist = QT == 1 && !DIAG;  // sampling-pass counts gathered per workgroup
   __shared__ uint32_t s_hist[kLdsHist ? kHistBins : 1];
   __shared__ float s_floor[QT];
+  __shared__ float s_tight[QT][2];
+  constexpr bool DEFER = QT == 1 && !DIAG && !L0;  // S1 / S4 through the per-wave survivor queue
+  __shared__ DeferQ s_dq[DEFER ? 4 : 1];
 
   const int tid = threadIdx.x;
   const uint32_t q0 = blockIdx.y * QT;
@@ -795,31 +996,36 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   uint32_t b_cur = first << a.shift;
   RawLane cur;
   const uint32_t n_pos = first < stride ? a.n_pos : 0u;
-  if (first < n_pos) cur = load_raw(a.idx + (uint64_t)b_cur * kBlockBytes);
+  if (first < n_pos) cur = load_raw<!DEFER>(a.idx + (uint64_t)b_cur * kBlockBytes);
+  const HistRow fl = floor_prefetch(a, q0, nq, wave);
 
   if (tid < kStatCount) s_stats[tid] = 0u;
   if (tid < QT) s_app.n[tid] = 0u;
-  if (!L0) {
-    const float4* src = reinterpret_cast<const float4*>(a.luts + (uint64_t)q0 * 1024);
-    float4* dst = reinterpret_cast<float4*>(s_lut);
-    for (int e = tid; e < nq * 256; e += 256) dst[e] = src[e];
-    for (int e = tid; e < nq * 192; e += 256) {
-      const int qi = e / 192, d = e % 192;
-      const mrl_query_plan* pq = a.plans + q0 + qi;
-      if (d < 128) s_wmid[qi * 128 + d] = pq->mid_codec == MRL_MID_EDEN_B1 ? pq->eden_mid_deltas[d] : pq->rabitq_weights2[d];
-      else s_wtail[qi * 64 + d - 128] = pq->tail_fold_weights2[d - 128];
-    }
+  if (!L0) {  // one contiguous copy of each query's scan constants
+    const float4* src = reinterpret_cast<const float4*>(a.luts + (uint64_t)q0 * kQData);
+    float4* dst = reinterpret_cast<float4*>(s_qd);
+    for (int e = tid; e < nq * (kQData / 4); e += 256) dst[e] = src[e];
   }
   s_rho[tid] = a.flag_tabs[tid];
   s_midf[tid] = a.flag_tabs[256 + tid];
   if (kLdsHist && a.hist)
     for (int i = tid; i < kHistBins; i += 256) s_hist[i] = 0u;
+  if (!DIAG && !L0 && tid < nq) {  // diagnostic scans keep the reference's checks
+    const float* qd = a.luts + (uint64_t)(q0 + tid) * kQData;
+    const mrl_query_plan* pq = a.plans + q0 + tid;
+    float A, B;
+    tight_coef(qd[kQdU1], qd[kQdU4], pq->mid_codec == MRL_MID_EDEN_B1, pq->has_tail_fold != 0,
+               a.sp.strata == MRL_STRATA_FULL64B, a.sp, &A, &B);
+    s_tight[tid][0] = A;
+    s_tight[tid][1] = B;
+  }
   // Per-query floor: from the sampling histogram (final pass), else tau.
-  take_floors<QT>(a, q0, nq, wave, lane, s_floor);
+  take_floors<QT>(a, q0, nq, wave, lane, s_floor, fl);
   __syncthreads();
 
   const ScanParams sp = a.sp;
   const uint32_t seg = blockIdx.x % a.nseg;
+  uint32_t qn = 0;  // survivors in this wave's queue (DEFER)
 
   // Every wave reaches the flush barrier below, also one with no block.
   for (uint32_t pos = first; pos < n_pos; pos += stride) {
@@ -827,7 +1033,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     // is loaded again, so the loads are unconditional and the wait before
     // this block's compute covers only this block's own loads.
     const uint32_t b_nxt = pos + stride < n_pos ? (pos + stride) << a.shift : b_cur;
-    const RawLane nxt = load_raw(a.idx + (uint64_t)b_nxt * kBlockBytes);
+    const RawLane nxt = load_raw<!DEFER>(a.idx + (uint64_t)b_nxt * kBlockBytes);
 
     const uint32_t b = b_cur;
     const CONST_AS uint8_t* blk = cview<uint8_t>(a.idx + (uint64_t)b * kBlockBytes);
@@ -867,6 +1073,41 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
       for (int j = 0; j < 8; ++j) m.nib[j] = cur.nib[j];
 
       const uint32_t n_active = (uint32_t)__popcll(active);
+      if constexpr (DEFER) {
+        // prefix stage here; survivors join the queue for S1 / S4
+        const CONST_AS mrl_query_plan* p = cview<mrl_query_plan>(a.plans + q0);
+        const float tq = s_floor[0];
+        const float tau = sp.exhaustive ? -INFINITY : tq;
+        const float acc = prefix_acc(m, s_qd + kQdLut);
+        const bool eden = p->prefix_codec == MRL_PREFIX_EDEN_PROD;
+        const float prefix_ip = eden ? p->eden_mean_ip + m.scale * acc : acc * m.scale + m.offset * p->prefix_sum;
+        const float ub = prefix_bound(prefix_ip, m.mid_n, m.high_n, s_tight[0][0], s_tight[0][1], sp.alpha,
+                                      p->q_mid_norm, p->q_tail_norm);
+        const uint64_t surv = ballot(ub >= tau) & active;
+        if (a.stats && lane == 0) {
+          atomicAdd(&s_stats[kStatBlocks], 1u);
+          atomicAdd(&s_stats[kStatActive], n_active);
+          atomicAdd(&s_stats[kStatPrefix], (unsigned)__popcll(surv));
+        }
+        if (surv != 0) {
+          const uint32_t n = (uint32_t)__popcll(surv);
+          if (qn + n > 64u) {
+            defer_flush(s_dq[wave], qn, a, p, s_qd + kQdW1, s_qd + kQdW4, s_tight[0][0], s_tight[0][1], tq, tau,
+                        s_app, q0, seg, s_hist, s_stats);
+            qn = 0;
+          }
+          if ((surv >> lane) & 1ull) {
+            const uint32_t slot = qn + lanes_below(surv);
+            DeferQ& dq = s_dq[wave];
+            dq.row[slot] = b * 64u + lane;
+            dq.score[slot] = prefix_ip;
+            dq.mid_n[slot] = m.mid_n;
+            dq.high_n[slot] = m.high_n;
+            dq.offset[slot] = m.offset;
+          }
+          qn += n;
+        }
+      } else
 #pragma unroll 1
       for (int qi = 0; qi < nq; ++qi) {
         const uint32_t q = q0 + qi;
@@ -885,8 +1126,12 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
           uint64_t blk_bits = (uint64_t)blk;
           asm volatile("" : "+s"(blk_bits));
           const CONST_AS uint8_t* blk_q = (const CONST_AS uint8_t*)blk_bits;
-          surv = eval_block(blk_q, active, m, s_lut + qi * 1024, s_wmid + qi * 128, s_wtail + qi * 64, p, sp, tau,
-                            prefix_ip, score, masks);
+          // the diagnostic path keeps the reference's checks (its masks are compared)
+          const float tA = DIAG ? __builtin_nanf("") : s_tight[qi][0];
+          const float tB = DIAG ? 0.0f : s_tight[qi][1];
+          const float* qd = s_qd + qi * kQData;
+          surv = eval_block(blk_q, active, m, qd + kQdLut, qd + kQdW1, qd + kQdW4, p, sp, tau, prefix_ip, score, masks,
+                            tA, tB);
         }
         if constexpr (DIAG) {
           uint64_t o = ((uint64_t)q * a.n_blocks + b);
@@ -921,9 +1166,14 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
         }
       }
     }
-    retire_touch(cur);
+    if constexpr (!DEFER) retire_touch(cur);
     cur = nxt;
     b_cur = b_nxt;
+  }
+  if constexpr (DEFER) {
+    if (qn != 0)
+      defer_flush(s_dq[wave], qn, a, cview<mrl_query_plan>(a.plans + q0), s_qd + kQdW1, s_qd + kQdW4, s_tight[0][0],
+                  s_tight[0][1], s_floor[0], sp.exhaustive ? -INFINITY : s_floor[0], s_app, q0, seg, s_hist, s_stats);
   }
   flush_appends<QT, DIAG>(s_app, a, q0, nq, seg, s_stats);
   if (kLdsHist && a.hist) {
@@ -1020,6 +1270,8 @@ enum {
   kQcHasTail,       // has_tail_fold (1.0)
   kQcBudget,        // s4_abs_budget
   kQcTailBase,      // tail_fold_base
+  kQcTightA,        // tight bound coefficients (NaN: the reference's checks)
+  kQcTightB,
   kQcCount = 16
 };
 
@@ -1049,6 +1301,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
   uint32_t b_cur = first << a.shift;
   RawLane cur;
   if (first < n_pos) cur = load_raw(a.idx + (uint64_t)b_cur * kBlockBytes);
+  const HistRow fl = floor_prefetch(a, q0, nq, wave);
 
   const ScanParams sp = a.sp;
   if (tid < kStatCount) s_stats[tid] = 0u;
@@ -1056,25 +1309,23 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
   for (int e = tid; e < QT * 1024; e += 256) {
     const int j = e & 3, l = (e >> 2) & 15, d = (e >> 6) & 63, g = e >> 12;
     const int qi = 4 * g + j;
-    s_lut[e] = qi < nq ? a.luts[(uint64_t)(q0 + qi) * 1024 + d * 16 + l] : 0.0f;
+    s_lut[e] = qi < nq ? a.luts[(uint64_t)(q0 + qi) * kQData + kQdLut + d * 16 + l] : 0.0f;
   }
   for (int e = tid; e < 192 * QT; e += 256) {
     const int qi = e % QT, d = e / QT;
     float w = 0.0f;
-    if (qi < nq) {
-      const mrl_query_plan* pq = a.plans + q0 + qi;
-      if (d < 128) w = pq->mid_codec == MRL_MID_EDEN_B1 ? pq->eden_mid_deltas[d] : pq->rabitq_weights2[d];
-      else w = pq->tail_fold_weights2[d - 128];
-    }
+    if (qi < nq) w = a.luts[(uint64_t)(q0 + qi) * kQData + (d < 128 ? kQdW1 + d : kQdW4 + d - 128)];
     if (d < 128) s_w1[e] = w;
     else s_w4[e - 128 * QT] = w;
   }
-  take_floors<QT>(a, q0, nq, wave, lane, s_floor);
+  take_floors<QT>(a, q0, nq, wave, lane, s_floor, fl);
   __syncthreads();
   if (tid < QT) {
     const int qi = tid;
     float* c = s_qc + qi * kQcCount;
-    for (int i = 0; i < kQcCount; ++i) c[i] = 0.0f;
+    // the tight-bound slots of present queries are written by the loop below
+    for (int i = 0; i < kQcCount; ++i)
+      if (qi >= nq || (i != kQcTightA && i != kQcTightB)) c[i] = 0.0f;
     c[kQcTauPrune] = __builtin_nanf("");  // absent query: no lane ever survives
     if (qi < nq) {
       const mrl_query_plan* pq = a.plans + q0 + qi;
@@ -1095,6 +1346,14 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
       c[kQcBudget] = pq->s4_abs_budget;
       c[kQcTailBase] = pq->tail_fold_base;
     }
+  }
+  if (tid < nq) {
+    const float* qd = a.luts + (uint64_t)(q0 + tid) * kQData;
+    const mrl_query_plan* pq = a.plans + q0 + tid;
+    float A, B;
+    tight_coef(qd[kQdU1], qd[kQdU4], pq->mid_codec == MRL_MID_EDEN_B1, pq->has_tail_fold != 0, FULL, a.sp, &A, &B);
+    s_qc[tid * kQcCount + kQcTightA] = A;
+    s_qc[tid * kQcCount + kQcTightB] = B;
   }
   __syncthreads();
 
@@ -1178,7 +1437,8 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
         // c0 = {eden, mean_ip, prefix_sum, mid_norm}, c1 = {tail_norm, tau_prune, tau_push, b1}
         const float prefix_ip = c0.x != 0.0f ? c0.y + m_scale * acc[qi] : acc[qi] * m_scale + m_offset * c0.z;
         score[qi] = prefix_ip;
-        const float ub = prefix_ip + alpha * (c0.w * mid_n + c1.x * high_n);
+        const float4 c3 = qc4[qi * 4 + 3];
+        const float ub = prefix_bound(prefix_ip, mid_n, high_n, c3.z, c3.w, alpha, c0.w, c1.x);
         sv |= (act && ub >= c1.y) ? (1u << qi) : 0u;
       }
       if (a.stats) {
@@ -1206,7 +1466,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
           const float sc = c1.w != 0.0f ? score[qi] + (c2.y + m_offset * s1[qi]) : score[qi] + s1[qi] * mid_n;
           score[qi] = in ? sc : score[qi];
           // Stage: post-S1 CS (scan.rs:572-584)
-          const float ub2 = score[qi] + alpha * c2.z * high_n;
+          const float ub2 = s1_bound(score[qi], high_n, c3.z, c3.w, alpha, c2.z);
           bool keep = in && ub2 >= c1.y;
           if (a.stats) c_s1 += (uint32_t)__popcll(ballot(keep));
           if (FULL) {
@@ -1716,10 +1976,11 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
 // host launchers
 // ---------------------------------------------------------------------------
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device,
-                           hipStream_t s) {
+                           hipStream_t s, uint4* rows1, uint2* rows4) {
   if (n_blocks == 0) return hipSuccess;
   uint32_t grid = (uint32_t)(n_blocks < 65536 ? n_blocks : 65536);
-  if (to_device) hipLaunchKernelGGL(k_relayout_to_device, dim3(grid), dim3(64), 0, s, src, dst, n_blocks);
+  if (to_device)
+    hipLaunchKernelGGL(k_relayout_to_device, dim3(grid), dim3(64), 0, s, src, dst, n_blocks, rows1, rows4);
   else hipLaunchKernelGGL(k_relayout_to_host, dim3(grid), dim3(64), 0, s, src, dst, n_blocks);
   return hipGetLastError();
 }
