@@ -34,16 +34,17 @@ constexpr int kOrigS5 = 3584;  // bit 0
 // Device-resident layout of one block (same 4096 bytes, same information).
 // The header is kept verbatim.  Per-vector fields become structure-of-arrays
 // so lane v of a wave reads slot v with one coalesced load, and the four
-// prefix bitplanes become per-vector 4-bit levels: u32 word (j, v) at
-// kDevNibbles + 4*(64*j + v) holds the levels of dims 8j..8j+7 of slot v,
-// dim 8j+i in bits 4i..4i+3.  S1 and S4 stay bit-transposed (bit v of word d
+// prefix bitplanes become per-vector 4-bit levels: u32 word (v, j) at
+// kDevNibbles + 4*(8*v + j) holds the levels of dims 8j..8j+7 of slot v,
+// dim 8j+i in bits 4i..4i+3 (a slot's 32 bytes are contiguous, so a lane
+// takes its levels with two 16-byte loads).  S1 and S4 stay bit-transposed (bit v of word d
 // is slot v), which is exactly a wave64 lane mask.
 constexpr int kDevHeader = 0;
 constexpr int kDevScale = 64;     // u16[64]
 constexpr int kDevOffset = 192;   // u16[64]
 constexpr int kDevTail = 320;     // u16[64]
 constexpr int kDevFlags = 448;    // u8[64]
-constexpr int kDevNibbles = 512;  // u32[8][64]
+constexpr int kDevNibbles = 512;  // u32[64][8]
 constexpr int kDevS1 = 2560;      // u64[128]
 constexpr int kDevS4 = 3584;      // u64[64]
 static_assert(kDevS4 + 64 * 8 == kBlockBytes, "device layout fills the block");

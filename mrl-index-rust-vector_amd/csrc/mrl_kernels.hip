@@ -12,6 +12,13 @@
 #include "mrl_half.h"
 #include "mrl_internal.h"
 
+#ifndef MRL_SCAN_AHEAD
+#define MRL_SCAN_AHEAD 2  // blocks in flight per wave, one-query scan
+#endif
+#ifndef MRL_SCAN_GRID1
+#define MRL_SCAN_GRID1 512u  // workgroups of the one-query scan
+#endif
+
 namespace mrl {
 
 // ---------------------------------------------------------------------------
@@ -161,7 +168,7 @@ __global__ __launch_bounds__(64) void k_relayout_to_device(const uint8_t* __rest
                        ((uint32_t)((s2[dim] >> v) & 1u) << 2) | ((uint32_t)((s0[dim] >> v) & 1u) << 3);
         w |= lvl << (4 * i);
       }
-      reinterpret_cast<uint32_t*>(d + kDevNibbles)[64 * j + v] = w;
+      reinterpret_cast<uint32_t*>(d + kDevNibbles)[8 * v + j] = w;
     }
     const uint64_t* s1 = reinterpret_cast<const uint64_t*>(s + kOrigS1);
     const uint64_t* s4 = reinterpret_cast<const uint64_t*>(s + kOrigS4);
@@ -209,7 +216,7 @@ __global__ __launch_bounds__(64) void k_relayout_to_host(const uint8_t* __restri
     const int dim = (int)v;
     uint64_t w0 = 0, w2 = 0, w3 = 0, w5 = 0;
     for (int slot = 0; slot < 64; ++slot) {
-      uint32_t lvl = (nib[64 * (dim >> 3) + slot] >> (4 * (dim & 7))) & 15u;
+      uint32_t lvl = (nib[8 * slot + (dim >> 3)] >> (4 * (dim & 7))) & 15u;
       w5 |= (uint64_t)(lvl & 1u) << slot;
       w3 |= (uint64_t)((lvl >> 1) & 1u) << slot;
       w2 |= (uint64_t)((lvl >> 2) & 1u) << slot;
@@ -741,9 +748,16 @@ __device__ __forceinline__ RawLane load_raw(const uint8_t* blk) {
   r.offset = reinterpret_cast<const uint16_t*>(blk + kDevOffset)[lane];
   r.tail = reinterpret_cast<const uint16_t*>(blk + kDevTail)[lane];
   r.flags = blk[kDevFlags + lane];
-  const uint32_t* nibp = reinterpret_cast<const uint32_t*>(blk + kDevNibbles);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) r.nib[j] = nibp[64 * j + lane];
+  const uint4* nibq = reinterpret_cast<const uint4*>(blk + kDevNibbles) + 2 * lane;
+  const uint4 n0 = nibq[0], n1 = nibq[1];
+  r.nib[0] = n0.x;
+  r.nib[1] = n0.y;
+  r.nib[2] = n0.z;
+  r.nib[3] = n0.w;
+  r.nib[4] = n1.x;
+  r.nib[5] = n1.y;
+  r.nib[6] = n1.z;
+  r.nib[7] = n1.w;
   const uint32_t hw = lane < 2 ? lane : (lane < 4 ? lane + 2 : 0);
   r.hdr = reinterpret_cast<const uint32_t*>(blk)[hw];
   if constexpr (PLANES) {
@@ -997,25 +1011,58 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   RawLane cur;
   const uint32_t n_pos = first < stride ? a.n_pos : 0u;
   if (first < n_pos) cur = load_raw<!DEFER>(a.idx + (uint64_t)b_cur * kBlockBytes);
+  // DEFER keeps kAhead blocks in flight: the loads of the following ones go out now too
+  constexpr int kAhead = DEFER ? MRL_SCAN_AHEAD : 1;
+  uint32_t b_pf[kAhead > 1 ? kAhead - 1 : 1];
+  RawLane pf[kAhead > 1 ? kAhead - 1 : 1];
+#pragma unroll
+  for (int k = 0; k + 1 < kAhead; ++k) {
+    const uint32_t pk = first + (uint32_t)(k + 1) * stride;
+    b_pf[k] = pk < n_pos ? pk << a.shift : b_cur;
+    if (first < n_pos) pf[k] = load_raw<false>(a.idx + (uint64_t)b_pf[k] * kBlockBytes);
+  }
   const HistRow fl = floor_prefetch(a, q0, nq, wave);
+
+  // Every global read of the set-up goes out before any of it is used.
+  constexpr int kQdPer = L0 ? 1 : (QT * (kQData / 4) + 255) / 256;  // float4 per thread
+  float4 qdv[kQdPer];
+  if (!L0) {
+    const float4* src = reinterpret_cast<const float4*>(a.luts + (uint64_t)q0 * kQData);
+#pragma unroll
+    for (int k = 0; k < kQdPer; ++k) {
+      const int e = tid + 256 * k;
+      if (e < nq * (kQData / 4)) qdv[k] = src[e];
+    }
+  }
+  const float fr0 = a.flag_tabs[tid], fr1 = a.flag_tabs[256 + tid];
+  float tu1 = 0.0f, tu4 = 0.0f;
+  int t_b1 = 0, t_tail = 0;
+  if (!DIAG && !L0 && tid < nq) {
+    const float* qd = a.luts + (uint64_t)(q0 + tid) * kQData;
+    const mrl_query_plan* pq = a.plans + q0 + tid;
+    tu1 = qd[kQdU1];
+    tu4 = qd[kQdU4];
+    t_b1 = pq->mid_codec == MRL_MID_EDEN_B1;
+    t_tail = pq->has_tail_fold != 0;
+  }
 
   if (tid < kStatCount) s_stats[tid] = 0u;
   if (tid < QT) s_app.n[tid] = 0u;
   if (!L0) {  // one contiguous copy of each query's scan constants
-    const float4* src = reinterpret_cast<const float4*>(a.luts + (uint64_t)q0 * kQData);
     float4* dst = reinterpret_cast<float4*>(s_qd);
-    for (int e = tid; e < nq * (kQData / 4); e += 256) dst[e] = src[e];
+#pragma unroll
+    for (int k = 0; k < kQdPer; ++k) {
+      const int e = tid + 256 * k;
+      if (e < nq * (kQData / 4)) dst[e] = qdv[k];
+    }
   }
-  s_rho[tid] = a.flag_tabs[tid];
-  s_midf[tid] = a.flag_tabs[256 + tid];
+  s_rho[tid] = fr0;
+  s_midf[tid] = fr1;
   if (kLdsHist && a.hist)
     for (int i = tid; i < kHistBins; i += 256) s_hist[i] = 0u;
   if (!DIAG && !L0 && tid < nq) {  // diagnostic scans keep the reference's checks
-    const float* qd = a.luts + (uint64_t)(q0 + tid) * kQData;
-    const mrl_query_plan* pq = a.plans + q0 + tid;
     float A, B;
-    tight_coef(qd[kQdU1], qd[kQdU4], pq->mid_codec == MRL_MID_EDEN_B1, pq->has_tail_fold != 0,
-               a.sp.strata == MRL_STRATA_FULL64B, a.sp, &A, &B);
+    tight_coef(tu1, tu4, t_b1, t_tail, a.sp.strata == MRL_STRATA_FULL64B, a.sp, &A, &B);
     s_tight[tid][0] = A;
     s_tight[tid][1] = B;
   }
@@ -1032,7 +1079,8 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     // Prefetch the next block of this wave.  Past the end the current block
     // is loaded again, so the loads are unconditional and the wait before
     // this block's compute covers only this block's own loads.
-    const uint32_t b_nxt = pos + stride < n_pos ? (pos + stride) << a.shift : b_cur;
+    const uint32_t ahead = (uint32_t)kAhead * stride;
+    const uint32_t b_nxt = pos + ahead < n_pos ? (pos + ahead) << a.shift : b_cur;
     const RawLane nxt = load_raw<!DEFER>(a.idx + (uint64_t)b_nxt * kBlockBytes);
 
     const uint32_t b = b_cur;
@@ -1167,8 +1215,20 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
       }
     }
     if constexpr (!DEFER) retire_touch(cur);
-    cur = nxt;
-    b_cur = b_nxt;
+    if constexpr (kAhead > 1) {
+      cur = pf[0];
+      b_cur = b_pf[0];
+#pragma unroll
+      for (int k = 0; k + 2 < kAhead; ++k) {
+        pf[k] = pf[k + 1];
+        b_pf[k] = b_pf[k + 1];
+      }
+      pf[kAhead - 2] = nxt;
+      b_pf[kAhead - 2] = b_nxt;
+    } else {
+      cur = nxt;
+      b_cur = b_nxt;
+    }
   }
   if constexpr (DEFER) {
     if (qn != 0)
@@ -2026,6 +2086,7 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const Launch
   const uint32_t res = tile ? rest : (qt == 8 ? res8 : res1);
   uint32_t grid = (a.n_pos + 4) / 4;  // 4 * grid - 1 >= n_pos waves carry positions
   uint32_t max_grid = res / tiles;
+  if (!tile && qt == 1 && !diag && !l0 && max_grid > MRL_SCAN_GRID1) max_grid = MRL_SCAN_GRID1;
   if (max_grid < a.nseg) max_grid = a.nseg;
   if (grid > max_grid) grid = max_grid;
   dim3 g(grid, tiles);
