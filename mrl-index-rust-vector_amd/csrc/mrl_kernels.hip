@@ -238,207 +238,260 @@ __global__ __launch_bounds__(64) void k_relayout_to_host(const uint8_t* __restri
 
 // ---------------------------------------------------------------------------
 // batched query plan: QueryPlan::from_query_codec (src/scan.rs:105-266)
-// one 128-thread workgroup per query
+// one 192-thread workgroup per query
 // ---------------------------------------------------------------------------
 
-// In-place FWHT butterflies over an LDS array (fwht_inplace, rotate.rs:13-33,
-// without the final scale).  Each output of a stage is one add or subtract of
-// two outputs of the previous stage, so the parallel order is bit-identical.
-__device__ __forceinline__ void fwht_stage(float* a, int n, int h, int i) {
-  if (i < n / 2) {
-    int j = (i / h) * (2 * h) + (i % h);
-    float x = a[j];
-    float y = a[j + h];
-    a[j] = x + y;
-    a[j + h] = x - y;
-  }
+// One FWHT butterfly stage of stride h < 64 (fwht_inplace, rotate.rs:13-33)
+// over a vector held one element per lane: x + y at the lower index, x - y
+// at the upper, the same f32 operations as the in-place loop.
+__device__ __forceinline__ float fwht_lane(float v, int h, uint32_t lane) {
+  const float o = __shfl_xor(v, h);
+  return (lane & (uint32_t)h) ? o - v : v + o;
 }
 
-__global__ __launch_bounds__(128) void k_plan(PlanArgs a) {
+// acc + f(src[0]) + f(src[1]) + ... + f(src[n-1]), one f32 addition at a
+// time in index order.  Two 16-term buffers alternate: the LDS reads of one
+// go out before the additions of the other, so the chain runs at the adder's
+// pace.  src is 16-byte aligned.
+template <typename F>
+__device__ __forceinline__ void add16(float& acc, const float4 (&c)[4], F f) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) acc = (((acc + f(c[u].x)) + f(c[u].y)) + f(c[u].z)) + f(c[u].w);
+}
+template <typename F>
+__device__ __forceinline__ float chain_sum(float acc, const float* __restrict__ src, int n, F f) {
+  const float4* s4 = reinterpret_cast<const float4*>(src);
+  int i = 0;
+  if (n >= 16) {
+    float4 A[4], B[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) A[u] = s4[u];
+#pragma unroll 1
+    for (; i + 32 <= n; i += 32) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) B[u] = s4[((i + 16) >> 2) + u];
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the additions
+      add16(acc, A, f);
+      // the chunk after B, or chunk 0 again (unused) past the last full one
+      const int na = i + 48 <= n ? i + 32 : 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) A[u] = s4[(na >> 2) + u];
+      __builtin_amdgcn_sched_barrier(0);
+      add16(acc, B, f);
+    }
+    if (i + 16 <= n) {
+      add16(acc, A, f);
+      i += 16;
+    }
+  }
+  for (; i < n; ++i) acc = acc + f(src[i]);
+  return acc;
+}
+
+// Makes this wave's LDS writes visible to its own later reads.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Three waves per query, each on its own part after the query is in LDS
+// (rotations are FWHTs across lanes with shuffles):
+//  wave 0: the mid-band and folded-tail rotations, their fields and tables,
+//          the sums over them and the S1 / S4 scan constants;
+//  wave 1: q_tail_sq, the one long sum (dims - 192 terms);
+//  wave 2: the prefix rotation, the prefix fields and LUT, the sums over the
+//          raw query and the scalar fields.
+// Each sum is a chain of f32 additions in the reference's order (scan.rs:
+// 132-233, 528-531) whose terms are the reference's single rounded f32
+// operations; `x -= y` is accumulated as `x + (-y)`, the same IEEE operation.
+__global__ __launch_bounds__(192) void k_plan(PlanArgs a) {
   __shared__ __align__(16) float s_q[MRL_MAX_DIMS];
-  __shared__ float s_mid[128];
-  __shared__ float s_emid[128];
-  __shared__ float s_eden[64];
-  __shared__ float s_tail[64];
-  __shared__ __align__(16) float s_terms[10][128];
+  __shared__ __align__(16) float s_sq[MRL_MAX_DIMS - kTailStart];
+  __shared__ __align__(16) float s_mid[128];
+  __shared__ __align__(16) float s_eden[64];
+  __shared__ __align__(16) float s_terms[9][128];
   __shared__ float s_sums[10];
 
   const uint32_t q = blockIdx.x;
   const int t = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const uint32_t lane = (uint32_t)t & 63u;
   const uint32_t dims = a.dims;
   const float* x = a.queries + (uint64_t)q * dims;
   mrl_query_plan* p = a.out + q;
+  float* qd = a.luts + (uint64_t)q * kQData;
   const bool has_eden = a.eden_mean != nullptr;
   const bool has_mid = a.mid_mean != nullptr;
   const bool eden_codec = a.prefix_codec == MRL_PREFIX_EDEN_PROD;
-
-  for (uint32_t i = t; i < dims; i += 128) s_q[i] = x[i];
-  __syncthreads();
-
-  // rotate_query = diag(+-1) then FWHT (eden.rs:91-98, 275-281); fold_tail (rotate.rs:73-93)
-  s_mid[t] = s_q[64 + t];
-  s_emid[t] = has_mid ? s_q[64 + t] * mix_sign(a.mid_seed, (uint64_t)t) : 0.0f;
-  if (t < 64) {
-    s_eden[t] = has_eden ? s_q[t] * mix_sign(a.eden_seed, (uint64_t)t) : 0.0f;
-    float u = zero_acc();
-    if (dims > (uint32_t)kTailStart) {
-      int nb = (int)(dims - kTailStart) / 64;
-      if (nb > kTailFoldBlocks) nb = kTailFoldBlocks;
-      for (int b = 0; b < nb; ++b) u += mix_sign((uint64_t)b, (uint64_t)t) * s_q[kTailStart + 64 * b + t];
-    }
-    s_tail[t] = u;
-  }
-  __syncthreads();
-  for (int h = 1; h < 128; h *= 2) {
-    if (t < 64) fwht_stage(s_mid, 128, h, t);
-    else fwht_stage(s_emid, 128, h, t - 64);
-    if (h < 64) {
-      if (t < 32) fwht_stage(s_eden, 64, h, t);
-      else if (t < 64) fwht_stage(s_tail, 64, h, t - 32);
-    }
-    __syncthreads();
-  }
-  s_mid[t] *= a.c.inv_sqrt128;
-  s_emid[t] *= a.c.inv_sqrt128;
-  if (t < 64) {
-    s_eden[t] *= a.c.inv_sqrt64;
-    s_tail[t] *= a.c.inv_sqrt64;
-  }
-  __syncthreads();
-
   const bool has_tail = dims > (uint32_t)kTailStart;
+  const int tail_n = has_tail ? (int)dims - kTailStart : 0;
   const float rs = a.c.rabitq_scale;
   const float ts = a.c.tail_fold_scale;
+  const float c0 = has_mid ? a.c.eden_mid_codebook[0] : 0.0f;
+  const float c1 = has_mid ? a.c.eden_mid_codebook[1] : 0.0f;
 
-  // elementwise fields
-  if (t < 64) {
-    float v = s_q[t];
-    p->prefix[t] = v;
-    p->bit_weights[t][0] = v * 1.0f;
-    p->bit_weights[t][1] = v * 2.0f;
-    p->bit_weights[t][2] = v * 4.0f;
-    p->bit_weights[t][3] = v * 8.0f;
-    p->eden_q_rot[t] = s_eden[t];
-    float tq = has_tail ? s_tail[t] : 0.0f;
-    p->tail_fold_q[t] = tq;
+  for (uint32_t i = t; i < dims; i += 192) s_q[i] = x[i];
+  __syncthreads();
+
+  if (wave == 1) {
+    // q_tail_sq: the squares formed by every lane, then the chain on one
+    for (int i = (int)lane; i < tail_n; i += 64) s_sq[i] = s_q[kTailStart + i] * s_q[kTailStart + i];
+    wave_lds_sync();
+    if (lane == 0) s_sums[4] = chain_sum(zero_acc(), s_sq, tail_n, [](float v) { return v; });
+  } else if (wave == 2) {
+    // rotate_query of the prefix (eden.rs:91-98, 275-281)
+    const float v = s_q[lane];
+    float d = has_eden ? v * mix_sign(a.eden_seed, (uint64_t)lane) : 0.0f;
+#pragma unroll
+    for (int h = 1; h < 64; h *= 2) d = fwht_lane(d, h, lane);
+    d *= a.c.inv_sqrt64;
+    s_eden[lane] = d;
+    p->prefix[lane] = v;
+    p->bit_weights[lane][0] = v * 1.0f;
+    p->bit_weights[lane][1] = v * 2.0f;
+    p->bit_weights[lane][2] = v * 4.0f;
+    p->bit_weights[lane][3] = v * 8.0f;
+    p->eden_q_rot[lane] = d;
+    p->prefix_weight[lane] = eden_codec ? d * a.c.inv_sqrt64 : v;  // scan.rs:457-461
+    // terms of prefix_l1, prefix_sum, eden_mean_ip (64) and eden_mid_mean_ip, q_mid_sq (128)
+    const float em = has_eden ? a.eden_mean[lane] : 0.0f;
+    const float mm0 = has_mid ? a.mid_mean[lane] : 0.0f;
+    const float mm1 = has_mid ? a.mid_mean[64 + lane] : 0.0f;
+    const float mv0 = s_q[64 + lane], mv1 = s_q[128 + lane];
+    s_terms[0][lane] = fabsf(v);
+    s_terms[1][lane] = v;
+    s_terms[2][lane] = has_eden ? v * em : 0.0f;
+    s_terms[3][lane] = has_mid ? mv0 * mm0 : 0.0f;
+    s_terms[3][64 + lane] = has_mid ? mv1 * mm1 : 0.0f;
+    s_terms[4][lane] = mv0 * mv0;
+    s_terms[4][64 + lane] = mv1 * mv1;
+    if (lane < 16) p->eden_codebook[lane] = has_eden ? a.c.eden_codebook[lane] : 0.0f;
+    if (lane < 27) p->pad[lane] = 0.0f;
+    if (lane == 0) {
+      p->dims = dims;
+      p->prefix_codec = a.prefix_codec;
+      p->mid_codec = a.mid_codec;
+      p->has_tail_fold = has_tail ? 1u : 0u;
+      p->eden_inv_sqrt_d = a.c.inv_sqrt64;
+      p->eden_mid_inv_sqrt_d = a.c.inv_sqrt128;
+      p->eden_mid_codebook[0] = c0;
+      p->eden_mid_codebook[1] = c1;
+      p->rabitq_scale = rs;
+    }
+    for (int e = kQdU4 + 1 + (int)lane; e < kQData; e += 64) qd[e] = 0.0f;
+    wave_lds_sync();
+    // Prefix LUT: lut[d*16 + level] = codebook[level] * weight[d] (or
+    // level * weight[d]), the product scan.rs:476-484 forms per (d, level).
+    // Entry e = lane + 64 k has level lane & 15 for every k: one codebook
+    // read per lane (an indexed read of the kernel argument array).
+    const float cb = eden_codec ? a.c.eden_codebook[lane & 15u] : (float)(lane & 15u);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int dd = (int)(lane >> 4) + 4 * k;
+      const float w = eden_codec ? s_eden[dd] * a.c.inv_sqrt64 : s_q[dd];
+      qd[kQdLut + (int)lane + 64 * k] = cb * w;
+    }
+    if (lane < 5) {
+      const int n = lane < 3 ? 64 : 128;
+      const float sum = chain_sum(zero_acc(), s_terms[lane], n, [](float v) { return v; });
+      s_sums[lane < 4 ? lane : 5] = sum;  // q_mid_sq is sum 5
+    }
+  } else {
+    // rotate_query = diag(+-1) then FWHT (eden.rs:91-98, 275-281); fold_tail
+    // (rotate.rs:73-93).  Lane l holds elements l and l + 64 of the 128-dim
+    // rotations and element l of the folded tail.
+    float m0 = s_q[64 + lane], m1 = s_q[128 + lane];
+    float e0 = has_mid ? m0 * mix_sign(a.mid_seed, (uint64_t)lane) : 0.0f;
+    float e1 = has_mid ? m1 * mix_sign(a.mid_seed, (uint64_t)lane + 64u) : 0.0f;
+    float u = zero_acc();
+    if (has_tail) {
+      int nb = tail_n / 64;
+      if (nb > kTailFoldBlocks) nb = kTailFoldBlocks;
+      for (int b = 0; b < nb; ++b) u += mix_sign((uint64_t)b, (uint64_t)lane) * s_q[kTailStart + 64 * b + lane];
+    }
+#pragma unroll
+    for (int h = 1; h < 64; h *= 2) {
+      m0 = fwht_lane(m0, h, lane);
+      m1 = fwht_lane(m1, h, lane);
+      e0 = fwht_lane(e0, h, lane);
+      e1 = fwht_lane(e1, h, lane);
+      u = fwht_lane(u, h, lane);
+    }
+    {
+      const float a0 = m0, b0 = e0;
+      m0 = a0 + m1;
+      m1 = a0 - m1;
+      e0 = b0 + e1;
+      e1 = b0 - e1;
+    }
+    m0 *= a.c.inv_sqrt128;
+    m1 *= a.c.inv_sqrt128;
+    e0 *= a.c.inv_sqrt128;
+    e1 *= a.c.inv_sqrt128;
+    u *= a.c.inv_sqrt64;
+    s_mid[lane] = m0;
+    s_mid[64 + lane] = m1;
+
+    // elementwise fields
+    const float tq = has_tail ? u : 0.0f;
+    p->tail_fold_q[lane] = tq;
     const float w4 = has_tail ? 2.0f * (tq * ts) : 0.0f;
-    p->tail_fold_weights2[t] = w4;
-    a.luts[(uint64_t)q * kQData + kQdW4 + t] = w4;
-    // scan.rs:457-461
-    p->prefix_weight[t] = eden_codec ? s_eden[t] * a.c.inv_sqrt64 : v;
-  }
-  {
-    float rq = s_mid[t];
-    p->rabitq_q[t] = rq;
-    p->rabitq_weights2[t] = 2.0f * (rq * rs);
-    p->eden_mid_q_rot[t] = s_emid[t];
-    // scan.rs:528-532 (deltas) with eden_mid_inv_sqrt_d = 1/sqrt(128)
-    float c0 = has_mid ? a.c.eden_mid_codebook[0] : 0.0f;
-    float c1 = has_mid ? a.c.eden_mid_codebook[1] : 0.0f;
-    float qq = s_emid[t] * a.c.inv_sqrt128;
-    const float dl = (c1 - c0) * qq;
-    p->eden_mid_deltas[t] = dl;
-    a.luts[(uint64_t)q * kQData + kQdW1 + t] = a.mid_codec == MRL_MID_EDEN_B1 ? dl : 2.0f * (rq * rs);
-  }
-  // rabitq_lut (scan.rs:188-201): 512 entries, 4 per thread
-  for (int e = t; e < 512; e += 128) {
-    int g = e >> 4, mask = e & 15;
-    float p0 = s_mid[4 * g] * rs, p1 = s_mid[4 * g + 1] * rs;
-    float p2 = s_mid[4 * g + 2] * rs, p3 = s_mid[4 * g + 3] * rs;
-    float v0 = (mask & 1) ? p0 : -p0;
-    float v1 = (mask & 2) ? p1 : -p1;
-    float v2 = (mask & 4) ? p2 : -p2;
-    float v3 = (mask & 8) ? p3 : -p3;
-    p->rabitq_lut[g][mask] = v0 + v1 + v2 + v3;
-  }
-  // Scan constants.  Prefix LUT: lut[d*16 + level] = codebook[level] *
-  // weight[d] (or level * weight[d]), the product scan.rs:476-484 forms per
-  // (d, level); then the stage weights as the plan holds them.
-  float* qd = a.luts + (uint64_t)q * kQData;
-  {
-    for (int e = t; e < 1024; e += 128) {
-      const int d = e >> 4, l = e & 15;
-      const float w = eden_codec ? s_eden[d] * a.c.inv_sqrt64 : s_q[d];
-      const float cb = eden_codec ? a.c.eden_codebook[l] : (float)l;
-      qd[kQdLut + e] = cb * w;
-    }
-  }
-  if (t < 16) p->eden_codebook[t] = has_eden ? a.c.eden_codebook[t] : 0.0f;
-  if (t < 27) p->pad[t] = 0.0f;
-  if (t == 0) {
-    p->dims = dims;
-    p->prefix_codec = a.prefix_codec;
-    p->mid_codec = a.mid_codec;
-    p->has_tail_fold = has_tail ? 1u : 0u;
-    p->eden_inv_sqrt_d = a.c.inv_sqrt64;
-    p->eden_mid_inv_sqrt_d = a.c.inv_sqrt128;
-    p->eden_mid_codebook[0] = has_mid ? a.c.eden_mid_codebook[0] : 0.0f;
-    p->eden_mid_codebook[1] = has_mid ? a.c.eden_mid_codebook[1] : 0.0f;
-    p->rabitq_scale = rs;
-  }
-
-  // Sequential reductions (scan.rs:132-233, 528-531).  Each one is a chain of
-  // f32 additions in the reference's order; the terms (each a single rounded
-  // f32 operation of the reference, formed before its addition) are written
-  // to LDS in parallel, then lane c of wave 0 runs chain c (all in lockstep,
-  // 128 terms each) while wave 1 runs the long q_tail_sq chain.  `x -= y` is
-  // accumulated as `x + (-y)`, which IEEE-754 defines to be the same
-  // operation.  Past its length a chain adds +0.0, a no-op for a sum that
-  // starts at +0 (such a sum is never -0).
-  const int tail_n = has_tail ? (int)dims - kTailStart : 0;
-  {
-    const int i = t;  // 0..127
-    const float c0 = has_mid ? a.c.eden_mid_codebook[0] : 0.0f;
-    if (i < 64) {
-      const float v = s_q[i];
-      s_terms[0][i] = fabsf(v);                                         // prefix_l1
-      s_terms[1][i] = v;                                                // prefix_sum
-      s_terms[2][i] = has_eden ? v * a.eden_mean[i] : 0.0f;             // eden_mean_ip
-      const float pos = s_tail[i] * ts;
-      s_terms[7][i] = has_tail ? -pos : 0.0f;                           // tail_fold_base
-      s_terms[8][i] = has_tail ? fabsf(pos) : 0.0f;                     // s4_abs_budget
-    } else {
-      s_terms[0][i] = s_terms[1][i] = s_terms[2][i] = s_terms[7][i] = s_terms[8][i] = 0.0f;
-    }
-    const float mv = s_q[64 + i];
-    s_terms[3][i] = has_mid ? mv * a.mid_mean[i] : 0.0f;                // eden_mid_mean_ip
-    s_terms[5][i] = mv * mv;                                            // q_mid_sq
-    s_terms[6][i] = -(s_mid[i] * rs);                                   // rabitq_base
-    s_terms[9][i] = c0 * (s_emid[i] * a.c.inv_sqrt128);                 // eden_mid_base
-  }
-  __syncthreads();
-  // q_tail_sq terms, squared in place (s_q[192..] has no other reader now)
-  for (int i = t; i < tail_n; i += 128) s_q[kTailStart + i] = s_q[kTailStart + i] * s_q[kTailStart + i];
-  __syncthreads();
-  if (t < 10 && t != 4) {
-    // chains 0..9 except 4: 128 terms each (shorter chains are padded with +0)
-    const float4* src = reinterpret_cast<const float4*>(&s_terms[t][0]);
-    float acc = zero_acc();
-#pragma unroll 1
-    for (int i = 0; i < 32; i += 4) {
-      float4 v[4];
+    p->tail_fold_weights2[lane] = w4;
+    qd[kQdW4 + lane] = w4;
+    float w1[2];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = src[i + u];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc = ((((acc + v[u].x) + v[u].y) + v[u].z) + v[u].w);
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t i = lane + 64u * r;
+      const float rq = r ? m1 : m0, eq = r ? e1 : e0;
+      p->rabitq_q[i] = rq;
+      p->rabitq_weights2[i] = 2.0f * (rq * rs);
+      p->eden_mid_q_rot[i] = eq;
+      // scan.rs:528-532 (deltas) with eden_mid_inv_sqrt_d = 1/sqrt(128)
+      const float dl = (c1 - c0) * (eq * a.c.inv_sqrt128);
+      p->eden_mid_deltas[i] = dl;
+      w1[r] = a.mid_codec == MRL_MID_EDEN_B1 ? dl : 2.0f * (rq * rs);
+      qd[kQdW1 + i] = w1[r];
+      s_terms[5][i] = -(rq * rs);                          // rabitq_base
+      s_terms[8][i] = c0 * (eq * a.c.inv_sqrt128);         // eden_mid_base
     }
-    s_sums[t] = acc;
-  } else if (t == 64) {
-    // chain 4, q_tail_sq: dims - 192 terms, on a wave of its own
-    const float* src = s_q + kTailStart;
-    float acc = zero_acc();
-    int i = 0;
-#pragma unroll 1
-    for (; i + 16 <= tail_n; i += 16) {
-      const float4* s4 = reinterpret_cast<const float4*>(src + i);
-      float4 v[4];
+    const float pos = u * ts;
+    s_terms[6][lane] = has_tail ? -pos : 0.0f;             // tail_fold_base
+    s_terms[7][lane] = has_tail ? fabsf(pos) : 0.0f;       // s4_abs_budget
+    wave_lds_sync();
+    // rabitq_lut (scan.rs:188-201): 512 entries
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = s4[u];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc = ((((acc + v[u].x) + v[u].y) + v[u].z) + v[u].w);
+    for (int k = 0; k < 8; ++k) {
+      const int e = (int)lane + 64 * k;
+      const int g = e >> 4, mask = e & 15;
+      const float p0 = s_mid[4 * g] * rs, p1 = s_mid[4 * g + 1] * rs;
+      const float p2 = s_mid[4 * g + 2] * rs, p3 = s_mid[4 * g + 3] * rs;
+      const float v0 = (mask & 1) ? p0 : -p0;
+      const float v1 = (mask & 2) ? p1 : -p1;
+      const float v2 = (mask & 4) ? p2 : -p2;
+      const float v3 = (mask & 8) ? p3 : -p3;
+      p->rabitq_lut[g][mask] = v0 + v1 + v2 + v3;
     }
-    for (; i < tail_n; ++i) acc = acc + src[i];
-    s_sums[4] = acc;
+    // rabitq_base, tail_fold_base, s4_abs_budget, eden_mid_base on lanes 0..3
+    float sum = 0.0f;
+    if (lane < 4) {
+      const int row = 5 + (int)lane;
+      sum = chain_sum(zero_acc(), s_terms[row], lane == 1 || lane == 2 ? 64 : 128, [](float v) { return v; });
+      s_sums[6 + lane] = sum;
+    }
+    // upper ends of the S1 / S4 sums: base + positive weights
+    float pw1 = fmaxf(w1[0], 0.0f) + fmaxf(w1[1], 0.0f);
+    float pw4 = fmaxf(w4, 0.0f);
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+      pw1 += __shfl_xor(pw1, h);
+      pw4 += __shfl_xor(pw4, h);
+    }
+    const float base1 = __shfl(sum, 0), base4 = __shfl(sum, 1);
+    if (lane == 0) {
+      qd[kQdU1] = base1 + pw1;  // rabitq_base + positive rabitq_weights2
+      qd[kQdU4] = base4 + pw4;  // tail_fold_base + positive tail weights
+    }
   }
   __syncthreads();
   if (t == 0) {
@@ -457,22 +510,6 @@ __global__ __launch_bounds__(128) void k_plan(PlanArgs a) {
     p->q_after_prefix = sqrtf(mid_sq + tail_sq);
     p->q_after_s1 = qt;
   }
-  if (t < 64) {
-    // upper ends of the S1 / S4 sums: base + positive weights (the qd writes
-    // above are this workgroup's own, visible after the barrier)
-    float p1 = fmaxf(qd[kQdW1 + t], 0.0f) + fmaxf(qd[kQdW1 + 64 + t], 0.0f);
-    float p4 = fmaxf(qd[kQdW4 + t], 0.0f);
-#pragma unroll
-    for (int h = 1; h < 64; h <<= 1) {
-      p1 += __shfl_xor(p1, h);
-      p4 += __shfl_xor(p4, h);
-    }
-    if (t == 0) {
-      qd[kQdU1] = s_sums[6] + p1;  // rabitq_base + positive rabitq_weights2
-      qd[kQdU4] = s_sums[7] + p4;  // tail_fold_base + positive tail weights
-    }
-  }
-  for (int e = kQdU4 + 1 + t; e < kQData; e += 128) qd[e] = 0.0f;
 }
 
 // ---------------------------------------------------------------------------
@@ -578,23 +615,47 @@ __device__ __forceinline__ float s1_bound(float score, float high_n, float A, fl
 // Stage: 4-bit prefix IP (scan.rs:453-517).  lut[d*16 + level] holds the
 // reference's product codebook[level] * weight (or level * weight), so the
 // per-vector sum over d is the same sequence of f32 additions.
+template <bool READS_FIRST = false>
 __device__ __forceinline__ float prefix_acc(const LaneBlock& m, const float* __restrict__ lut) {
   float acc = zero_acc();
   const char* lutb = reinterpret_cast<const char*>(lut);
   const uint32_t mask = 0x3Cu;
   auto ld = [&](int d, uint32_t off) { return *reinterpret_cast<const float*>(lutb + d * 64 + off); };
+  if constexpr (!READS_FIRST) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t w2 = m.nib[j] << 2, w3 = m.nib[j] >> 2;
+      acc = acc + ld(8 * j + 0, lut_off<0>(w2, w3, mask));
+      acc = acc + ld(8 * j + 1, lut_off<1>(w2, w3, mask));
+      acc = acc + ld(8 * j + 2, lut_off<2>(w2, w3, mask));
+      acc = acc + ld(8 * j + 3, lut_off<3>(w2, w3, mask));
+      acc = acc + ld(8 * j + 4, lut_off<4>(w2, w3, mask));
+      acc = acc + ld(8 * j + 5, lut_off<5>(w2, w3, mask));
+      acc = acc + ld(8 * j + 6, lut_off<6>(w2, w3, mask));
+      acc = acc + ld(8 * j + 7, lut_off<7>(w2, w3, mask));
+    }
+    return acc;
+  }
+  // All 64 table reads are independent: issue them before the first
+  // addition so their LDS latency overlaps (the additions keep their order).
+  // Costs ~36 VGPRs, which only the one-query kernel (two waves per SIMD)
+  // can spare.
+  float v[64];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint32_t w2 = m.nib[j] << 2, w3 = m.nib[j] >> 2;
-    acc = acc + ld(8 * j + 0, lut_off<0>(w2, w3, mask));
-    acc = acc + ld(8 * j + 1, lut_off<1>(w2, w3, mask));
-    acc = acc + ld(8 * j + 2, lut_off<2>(w2, w3, mask));
-    acc = acc + ld(8 * j + 3, lut_off<3>(w2, w3, mask));
-    acc = acc + ld(8 * j + 4, lut_off<4>(w2, w3, mask));
-    acc = acc + ld(8 * j + 5, lut_off<5>(w2, w3, mask));
-    acc = acc + ld(8 * j + 6, lut_off<6>(w2, w3, mask));
-    acc = acc + ld(8 * j + 7, lut_off<7>(w2, w3, mask));
+    v[8 * j + 0] = ld(8 * j + 0, lut_off<0>(w2, w3, mask));
+    v[8 * j + 1] = ld(8 * j + 1, lut_off<1>(w2, w3, mask));
+    v[8 * j + 2] = ld(8 * j + 2, lut_off<2>(w2, w3, mask));
+    v[8 * j + 3] = ld(8 * j + 3, lut_off<3>(w2, w3, mask));
+    v[8 * j + 4] = ld(8 * j + 4, lut_off<4>(w2, w3, mask));
+    v[8 * j + 5] = ld(8 * j + 5, lut_off<5>(w2, w3, mask));
+    v[8 * j + 6] = ld(8 * j + 6, lut_off<6>(w2, w3, mask));
+    v[8 * j + 7] = ld(8 * j + 7, lut_off<7>(w2, w3, mask));
   }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int d = 0; d < 64; ++d) acc = acc + v[d];
   return acc;
 }
 
@@ -1126,7 +1187,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
         const CONST_AS mrl_query_plan* p = cview<mrl_query_plan>(a.plans + q0);
         const float tq = s_floor[0];
         const float tau = sp.exhaustive ? -INFINITY : tq;
-        const float acc = prefix_acc(m, s_qd + kQdLut);
+        const float acc = prefix_acc<true>(m, s_qd + kQdLut);
         const bool eden = p->prefix_codec == MRL_PREFIX_EDEN_PROD;
         const float prefix_ip = eden ? p->eden_mean_ip + m.scale * acc : acc * m.scale + m.offset * p->prefix_sum;
         const float ub = prefix_bound(prefix_ip, m.mid_n, m.high_n, s_tight[0][0], s_tight[0][1], sp.alpha,
@@ -2054,7 +2115,7 @@ static void launch(K kernel, dim3 grid, dim3 block, hipStream_t s, const LaunchE
 
 hipError_t launch_plan(const PlanArgs& a, hipStream_t s, const LaunchEvents& ev) {
   if (a.n_q == 0) return hipSuccess;
-  launch(k_plan, dim3(a.n_q), dim3(128), s, ev, a);
+  launch(k_plan, dim3(a.n_q), dim3(192), s, ev, a);
   return hipGetLastError();
 }
 
