@@ -176,8 +176,8 @@ struct mrl_plans {
 };
 
 // The per-query outputs sit in one device block, read back with one copy:
-// status u32[n_q], counts u32[n_q], stats u64[kStatCount], ids u64[n_q][k],
-// scores f32[n_q][k].
+// status u32[n_q], counts u32[n_q], stats u64[kStatCopies][kStatCount] (summed
+// over the copies when read), ids u64[n_q][k], scores f32[n_q][k].
 struct mrl_results {
   mrl_ctx* ctx = nullptr;
   uint32_t n_q = 0, k = 0, seg_cap = 0;
@@ -188,7 +188,7 @@ struct mrl_results {
   uint32_t* d_counts = nullptr;
   float* d_cand_score = nullptr;   // [n_q][kSegs][seg_cap]
   uint32_t* d_cand_row = nullptr;
-  uint32_t* d_seg_count = nullptr; // [n_q][kSegs], zero between scans
+  uint32_t* d_seg_count = nullptr; // [n_q][kMaxSegs] (a scan uses [n_q][nseg]), zero between scans
   float* d_tau = nullptr;
   float* d_tau_hi = nullptr;       // [n_q] floor of the final pass
   uint32_t* d_hist = nullptr;      // [n_q][kHistBins] sampling-pass score counts, zero between scans
@@ -680,7 +680,7 @@ static void results_release(mrl_results* r) {
   delete r;
 }
 
-static size_t results_head_bytes(uint32_t n_q) { return (size_t)n_q * 8 + kStatCount * 8; }
+static size_t results_head_bytes(uint32_t n_q) { return (size_t)n_q * 8 + kStatCopies * kStatCount * 8; }
 
 static const uint32_t kSegCap = 4096;  // kSegs * kSegCap = 65536 candidates per query and scan
 
@@ -709,7 +709,7 @@ extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_re
   }
   ok = ok && hipMalloc(&r->d_cand_score, cands * sizeof(float)) == hipSuccess &&
             hipMalloc(&r->d_cand_row, cands * sizeof(uint32_t)) == hipSuccess &&
-            hipMalloc(&r->d_seg_count, nq * kSegs * sizeof(uint32_t)) == hipSuccess &&
+            hipMalloc(&r->d_seg_count, nq * kMaxSegs * sizeof(uint32_t)) == hipSuccess &&
             hipMalloc(&r->d_tau, nq * sizeof(float)) == hipSuccess &&
             hipMalloc(&r->d_tau_hi, nq * sizeof(float)) == hipSuccess &&
             hipMalloc(&r->d_hist, nq * kHistBins * sizeof(uint32_t)) == hipSuccess &&
@@ -719,7 +719,7 @@ extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_re
     return fail(MRL_ERR_OUT_OF_MEMORY, "results buffers");
   }
   // Pass state starts zeroed; each final selection leaves it zeroed again.
-  ok = hipMemset(r->d_seg_count, 0, nq * kSegs * sizeof(uint32_t)) == hipSuccess &&
+  ok = hipMemset(r->d_seg_count, 0, nq * kMaxSegs * sizeof(uint32_t)) == hipSuccess &&
        hipMemset(r->d_err, 0, nq * sizeof(uint32_t)) == hipSuccess &&
        hipMemset(r->d_out, 0, head) == hipSuccess &&
        hipMemset(r->d_hist, 0, nq * kHistBins * sizeof(uint32_t)) == hipSuccess &&
@@ -770,6 +770,14 @@ static uint32_t final_rank(uint32_t K, uint64_t n_s, uint64_t n) {
   return (uint32_t)std::min<double>((double)K, std::max(1.0, r));
 }
 
+// The one-query kernel's final pass gives each workgroup a candidate segment
+// of its own (no atomic reservation) when the results hold kSegs segments per
+// query; an append count past the room flags the query for the dense re-run.
+static const uint32_t kExclCap = 1024;  // the kernel's per-workgroup staging room
+static bool excl_ok(const PassBuffers& pb, uint32_t n_q, const ScanParams& sp) {
+  return pb.nseg == (uint32_t)kSegs && scan_query_tile(n_q) == 1 && sp.strata != MRL_STRATA_L0_ONLY;
+}
+
 // Enqueue a scan of n_q plans starting at plans_first.  The sampling pass
 // (when the index has more than 256 blocks) scores a strided sample of
 // blocks with no candidate appends and counts the survivors' exact scores
@@ -784,6 +792,7 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
   hipStream_t s = ctx->stream;
   const size_t np = lp.passes.size();
   const bool sampled = np > 1 && !rerun_safe;
+  uint32_t nseg_final = pb.nseg, cap_final = pb.seg_cap;
   const uint32_t rank = np > 1 ? final_rank(K, lp.passes[0].n_pos, ix->n_blocks) : K;
   for (size_t pi = 0; pi < np; ++pi) {
     const bool last = pi + 1 == np;
@@ -813,6 +822,19 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
     a.seg_count = pb.seg_count;
     a.nseg = pb.nseg;
     a.seg_cap = pb.seg_cap;
+    if (last && excl_ok(pb, n_q, sp)) {
+      // one segment per workgroup of the final pass, the same candidate room per query
+      a.excl = 1;
+      const uint32_t g = scan_grid(a, false);
+      if (g >= 1 && g <= (uint32_t)kMaxSegs) {
+        a.nseg = g;
+        a.seg_cap = std::min<uint32_t>(pb.nseg * pb.seg_cap / g, kExclCap);
+        nseg_final = a.nseg;
+        cap_final = a.seg_cap;
+      } else {
+        a.excl = 0;
+      }
+    }
     a.stats = last ? stats : nullptr;
     a.err = pb.err;
     ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)pi, lp.passes[pi].n_new, n_q);
@@ -823,8 +845,8 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
   sa.cand_score = pb.cand_score;
   sa.cand_row = pb.cand_row;
   sa.seg_count = pb.seg_count;
-  sa.nseg = pb.nseg;
-  sa.seg_cap = pb.seg_cap;
+  sa.nseg = nseg_final;
+  sa.seg_cap = cap_final;
   sa.err = pb.err;
   sa.k = K;
   sa.status = pb.status;
@@ -949,7 +971,7 @@ static int safe_rerun(mrl_ctx* ctx, mrl_results* r, uint32_t q, uint32_t* st) {
   const size_t cand = (size_t)q * kSegs * r->seg_cap;
   pb.cand_score += cand;
   pb.cand_row += cand;
-  pb.seg_count += (size_t)q * kSegs;
+  pb.seg_count += (size_t)q * kMaxSegs;
   pb.err += q;
   pb.tau += q;
   pb.tau_hi += q;
@@ -1059,8 +1081,12 @@ extern "C" int mrl_results_fetch(mrl_ctx* ctx, mrl_results* res, uint64_t* out_i
   if (out_ids && n_q) memcpy(out_ids, h + head, n_q * K * 8);
   if (out_scores && n_q) memcpy(out_scores, h + head + nq * K * 8, n_q * K * 4);
   if (out_counts && n_q) memcpy(out_counts, h + nq * 4, (size_t)n_q * 4);
-  unsigned long long st[kStatCount];
-  memcpy(st, h + nq * 8, sizeof(st));
+  unsigned long long st[kStatCount] = {0};
+  for (int c = 0; c < kStatCopies; ++c) {
+    unsigned long long part[kStatCount];
+    memcpy(part, h + nq * 8 + (size_t)c * sizeof(part), sizeof(part));
+    for (int i = 0; i < kStatCount; ++i) st[i] += part[i];
+  }
   if (stats) {  // counters accumulated since the previous fetch
     stats->blocks = st[kStatBlocks] - res->stats_seen[kStatBlocks];
     stats->active_vecs = st[kStatActive] - res->stats_seen[kStatActive];

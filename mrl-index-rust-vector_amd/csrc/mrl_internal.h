@@ -89,6 +89,10 @@ struct PlanConsts {
 
 // Per-query statistic counters (ScanStats) accumulated on the device.
 enum { kStatBlocks = 0, kStatActive, kStatPrefix, kStatS1, kStatS4Budget, kStatPushed, kStatCount };
+// Workgroup w adds its counts into copy w % kStatCopies of the counters (one
+// address per counter would serialise the atomics of every workgroup); the
+// reader sums the copies.
+constexpr int kStatCopies = 64;
 
 // Kernel argument blocks (passed by value as kernarg segments).
 struct PlanArgs {
@@ -113,6 +117,10 @@ struct PlanArgs {
 // 512, 0, 2047)); the lower edge of the bin holding the K-th best counted
 // score is <= the final K-th score.
 constexpr int kSegs = 16;
+// A one-query final pass may instead give every workgroup a segment of its
+// own (ScanArgs::excl): then nseg = the grid (at most kMaxSegs), and a
+// workgroup writes its count with a plain store, no atomic.
+constexpr int kMaxSegs = 512;
 constexpr int kHistBins = 2048;
 
 struct ScanArgs {
@@ -142,7 +150,11 @@ struct ScanArgs {
   uint32_t* seg_count;         // [n_q][nseg]
   uint32_t nseg;
   uint32_t seg_cap;
-  unsigned long long* stats;   // kStatCount counters, or null
+  // nseg = gridDim.x and segment = workgroup: the workgroup stores its append
+  // count (which may exceed seg_cap: then the entries past it are dropped and
+  // k_select flags the overflow); one-query kernel only
+  uint32_t excl;
+  unsigned long long* stats;   // [kStatCopies][kStatCount] counters, or null
   uint32_t* err;               // [n_q] bit 0: NaN score among pushed survivors
   uint64_t* d_masks;           // diagnostic outputs, [n_q][n_blocks][5]
   float* d_prefix;             // [n_q][n_blocks][64]
@@ -240,6 +252,8 @@ struct LaunchEvents {
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device, hipStream_t s,
                            uint4* rows1 = nullptr, uint2* rows4 = nullptr);
 hipError_t launch_plan(const PlanArgs& a, hipStream_t s, const LaunchEvents& ev = {});
+int scan_query_tile(uint32_t n_q);  // queries per workgroup of the non-tile kernels
+uint32_t scan_grid(const ScanArgs& a, bool diag);
 hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
 

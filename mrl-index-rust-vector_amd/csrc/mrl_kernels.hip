@@ -896,7 +896,7 @@ __device__ __forceinline__ void stage_append(Staging<QT>& st, const ScanArgs& a,
     st.row[qi][slot] = row;
   }
   const uint64_t om = ballot(mine && slot >= (uint32_t)Staging<QT>::kCap);
-  if (om != 0) {
+  if (om != 0 && !a.excl) {  // an exclusive segment only counts them (its count then overflows)
     const uint64_t sq = (uint64_t)q * a.nseg + seg;
     const uint32_t olead = (uint32_t)__ffsll((long long)om) - 1;
     uint32_t g0 = 0;
@@ -920,9 +920,18 @@ __device__ __forceinline__ void flush_appends(Staging<DIAG ? 1 : QT>& st, const 
     __syncthreads();
     if (tid < nq) {
       const uint32_t n = min(st.n[tid], (uint32_t)Staging<QT>::kCap);
-      st.gbase[tid] = n ? atomicAdd(a.seg_count + (uint64_t)(q0 + tid) * a.nseg + seg, n) : 0u;
+      const uint64_t sq = (uint64_t)(q0 + tid) * a.nseg + seg;
+      if (a.excl) {  // this workgroup's own segment: every append counted, from 0
+        a.seg_count[sq] = st.n[tid];
+        st.gbase[tid] = 0u;
+      } else {
+        st.gbase[tid] = n ? atomicAdd(a.seg_count + sq, n) : 0u;
+      }
     }
-    if (a.stats && tid < kStatCount && s_stats[tid]) atomicAdd(a.stats + tid, (unsigned long long)s_stats[tid]);
+    if (a.stats && tid < kStatCount && s_stats[tid]) {
+      const uint32_t copy = (blockIdx.x + blockIdx.y * gridDim.x) % (uint32_t)kStatCopies;
+      atomicAdd(a.stats + copy * kStatCount + tid, (unsigned long long)s_stats[tid]);
+    }
     __syncthreads();
     for (int qi = 0; qi < nq; ++qi) {
       const uint32_t n = min(st.n[qi], (uint32_t)Staging<QT>::kCap);
@@ -1071,20 +1080,9 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   uint32_t b_cur = first << a.shift;
   RawLane cur;
   const uint32_t n_pos = first < stride ? a.n_pos : 0u;
-  if (first < n_pos) cur = load_raw<!DEFER>(a.idx + (uint64_t)b_cur * kBlockBytes);
-  // DEFER keeps kAhead blocks in flight: the loads of the following ones go out now too
-  constexpr int kAhead = DEFER ? MRL_SCAN_AHEAD : 1;
-  uint32_t b_pf[kAhead > 1 ? kAhead - 1 : 1];
-  RawLane pf[kAhead > 1 ? kAhead - 1 : 1];
-#pragma unroll
-  for (int k = 0; k + 1 < kAhead; ++k) {
-    const uint32_t pk = first + (uint32_t)(k + 1) * stride;
-    b_pf[k] = pk < n_pos ? pk << a.shift : b_cur;
-    if (first < n_pos) pf[k] = load_raw<false>(a.idx + (uint64_t)b_pf[k] * kBlockBytes);
-  }
+  // The set-up's reads go out first (memory returns loads in order, so the
+  // set-up below then waits for them alone), then the first blocks' loads.
   const HistRow fl = floor_prefetch(a, q0, nq, wave);
-
-  // Every global read of the set-up goes out before any of it is used.
   constexpr int kQdPer = L0 ? 1 : (QT * (kQData / 4) + 255) / 256;  // float4 per thread
   float4 qdv[kQdPer];
   if (!L0) {
@@ -1105,6 +1103,17 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     tu4 = qd[kQdU4];
     t_b1 = pq->mid_codec == MRL_MID_EDEN_B1;
     t_tail = pq->has_tail_fold != 0;
+  }
+  if (first < n_pos) cur = load_raw<!DEFER>(a.idx + (uint64_t)b_cur * kBlockBytes);
+  // DEFER keeps kAhead blocks in flight: the loads of the following ones go out now too
+  constexpr int kAhead = DEFER ? MRL_SCAN_AHEAD : 1;
+  uint32_t b_pf[kAhead > 1 ? kAhead - 1 : 1];
+  RawLane pf[kAhead > 1 ? kAhead - 1 : 1];
+#pragma unroll
+  for (int k = 0; k + 1 < kAhead; ++k) {
+    const uint32_t pk = first + (uint32_t)(k + 1) * stride;
+    b_pf[k] = pk < n_pos ? pk << a.shift : b_cur;
+    if (first < n_pos) pf[k] = load_raw<false>(a.idx + (uint64_t)b_pf[k] * kBlockBytes);
   }
 
   if (tid < kStatCount) s_stats[tid] = 0u;
@@ -1789,29 +1798,66 @@ __device__ __forceinline__ void for_each_pair(const CandView& v, F&& fn) {
 }
 
 // Prefix offsets of the (capped) segment counts into off[0..nseg] and of
-// their item counts into coff[0..nseg]: the counters are loaded by nseg
-// threads at once, then summed in LDS.
-__device__ void seg_offsets(const uint32_t* seg_count, uint32_t nseg, uint32_t seg_cap, uint32_t* off,
-                            uint32_t* coff) {
-  const uint32_t t = threadIdx.x;
-  if (t < nseg) {
-    const uint32_t c = seg_count[t];
-    off[t + 1] = c < seg_cap ? c : seg_cap;
-  }
-  __syncthreads();
-  if (t == 0) {
-    uint32_t acc = 0, cacc = 0;
-    off[0] = 0;
-    coff[0] = 0;
-    for (uint32_t s = 1; s <= nseg; ++s) {
-      const uint32_t c = off[s];
-      acc += c;
-      cacc += (c + kChunk - 1) / kChunk;
-      off[s] = acc;
-      coff[s] = cacc;
+// their item counts into coff[0..nseg] (nseg <= blockDim.x): thread t holds
+// counter t (`count`, 0 past nseg); wave scans, then a scan of the wave
+// totals (ws: 2 * 16 words).
+__device__ void seg_offsets(uint32_t count, uint32_t nseg, uint32_t seg_cap, uint32_t* off, uint32_t* coff,
+                            uint32_t* ws) {
+  const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+  const uint32_t c = count < seg_cap ? count : seg_cap;
+  uint32_t ic = c, ii = (c + kChunk - 1) / kChunk;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t x = __shfl_up(ic, o), y = __shfl_up(ii, o);
+    if ((int)lane >= o) {
+      ic += x;
+      ii += y;
     }
   }
+  if (lane == 63) {
+    ws[w] = ic;
+    ws[16 + w] = ii;
+  }
   __syncthreads();
+  uint32_t bc = 0, bi = 0;
+  for (uint32_t u = 0; u < w; ++u) {
+    bc += ws[u];
+    bi += ws[16 + u];
+  }
+  if (t < nseg) {
+    off[t + 1] = bc + ic;
+    coff[t + 1] = bi + ii;
+  }
+  if (t == 0) {
+    off[0] = 0;
+    coff[0] = 0;
+  }
+  __syncthreads();
+}
+
+// The walk of for_each_pair for many short segments (one per workgroup of
+// the final pass, nseg <= blockDim.x): thread t takes segment t and loads up
+// to kShortRound of its entries per round, all before any is used.
+constexpr int kShortRound = 16;
+template <typename F>
+__device__ __forceinline__ void for_each_pair_short(const CandView& v, F&& fn) {
+  const uint32_t t = threadIdx.x;
+  if (t >= v.nseg) return;
+  const uint32_t cnt = v.off[t + 1] - v.off[t];
+  const uint64_t base = (uint64_t)t * v.seg_cap;
+  for (uint32_t r = 0; r < cnt; r += kShortRound) {
+    float sc[kShortRound];
+    uint32_t rw[kShortRound];
+#pragma unroll
+    for (int u = 0; u < kShortRound; ++u)
+      if (r + u < cnt) {
+        sc[u] = v.sc[base + r + u];
+        rw[u] = v.rw[base + r + u];
+      }
+#pragma unroll
+    for (int u = 0; u < kShortRound; ++u)
+      if (r + u < cnt) fn(sc[u], rw[u], v.off[t] + r + u);
+  }
 }
 
 // LDS histogram of the appended scores of one query (all segments).
@@ -1857,8 +1903,9 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   __shared__ uint32_t s_start[kHistBins];
   __shared__ uint32_t s_hist[2048];
   __shared__ uint32_t s_misc[8];
-  __shared__ uint32_t s_off[kSegs + 1];
-  __shared__ uint32_t s_coff[kSegs + 1];
+  __shared__ uint32_t s_off[kMaxSegs + 1];
+  __shared__ uint32_t s_coff[kMaxSegs + 1];
+  __shared__ uint32_t s_ws[32];
 
   __shared__ float s_fl[2];
 
@@ -1866,17 +1913,25 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   const int tid = threadIdx.x;
   const uint32_t K = a.k;
   const uint32_t* qcount = a.seg_count + (uint64_t)q * a.nseg;
-  // The final pass's floor and the safe one, for the shortfall check below.
-  if (a.hist && tid == 0) {
-    s_fl[0] = a.tau_safe[q];
-    s_fl[1] = a.tau_final[q];
-  }
-  if (tid == 0) s_misc[7] = 0;
-  __syncthreads();
-  if (tid < (int)a.nseg && qcount[tid] > a.seg_cap) atomicOr(&s_misc[7], 2u);
-  seg_offsets(qcount, a.nseg, a.seg_cap, s_off, s_coff);
   const CandView v{a.cand_score + (uint64_t)q * a.nseg * a.seg_cap, a.cand_row + (uint64_t)q * a.nseg * a.seg_cap,
                    a.seg_cap, a.nseg, s_off, s_coff};
+  // The set-up's reads go out together: the final pass's floor and the safe
+  // one (for the shortfall check below) and this thread's segment count.
+  const bool short_segs = a.nseg > (uint32_t)kSegs;
+  float fl_safe = 0.0f, fl_final = 0.0f;
+  if (a.hist && tid == 0) {
+    fl_safe = a.tau_safe[q];
+    fl_final = a.tau_final[q];
+  }
+  const uint32_t c_own = tid < (int)a.nseg ? qcount[tid] : 0u;
+  if (tid == 0) {
+    s_misc[7] = 0;
+    s_fl[0] = fl_safe;
+    s_fl[1] = fl_final;
+  }
+  __syncthreads();
+  if (c_own > a.seg_cap) atomicOr(&s_misc[7], 2u);
+  seg_offsets(c_own, a.nseg, a.seg_cap, s_off, s_coff, s_ws);
   const uint32_t total = s_off[a.nseg];
   uint32_t m;
   uint64_t* sb = s_buf;  // the entries the final sort reads
@@ -1886,10 +1941,12 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     // picked out of LDS.
     for (int i = tid; i < kHistBins; i += kSelThreads) s_hist[i] = 0u;
     __syncthreads();
-    for_each_pair(v, [&](float sc, uint32_t row, uint32_t dense) {
+    auto take = [&](float sc, uint32_t row, uint32_t dense) {
       atomicAdd(&s_hist[hist_bin(sc)], 1u);
       s_buf[dense] = composite(score_key(sc), row);
-    });
+    };
+    if (short_segs) for_each_pair_short(v, take);
+    else for_each_pair(v, take);
     __syncthreads();
     find_boundary(s_hist, kHistBins, K, true, &s_misc[0], &s_misc[1]);
     if (tid == 0) s_misc[2] = 0;
@@ -2131,11 +2188,9 @@ static uint32_t resident_groups(K kernel) {
   return (uint32_t)(cus * per_cu);
 }
 
-hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev) {
-  if (a.n_pos == 0 || a.n_q == 0) return hipSuccess;
+// Workgroups along x of a scan launch (the same for every query tile).
+uint32_t scan_grid(const ScanArgs& a, bool diag) {
   const bool l0 = a.sp.strata == MRL_STRATA_L0_ONLY;
-  // batched: the tile kernel; otherwise one query per workgroup, or the
-  // 8-query workgroups of the diagnostic and L0Only paths
   const bool tile = a.n_q >= 8 && !diag && !l0;
   const int qt = tile ? kTileQ : scan_query_tile(a.n_q);
   const uint32_t tiles = (a.n_q + qt - 1) / qt;
@@ -2148,8 +2203,24 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const Launch
   uint32_t grid = (a.n_pos + 4) / 4;  // 4 * grid - 1 >= n_pos waves carry positions
   uint32_t max_grid = res / tiles;
   if (!tile && qt == 1 && !diag && !l0 && max_grid > MRL_SCAN_GRID1) max_grid = MRL_SCAN_GRID1;
-  if (max_grid < a.nseg) max_grid = a.nseg;
+  if (!a.excl && max_grid < a.nseg) max_grid = a.nseg;
   if (grid > max_grid) grid = max_grid;
+  return grid;
+}
+
+hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev) {
+  if (a.n_pos == 0 || a.n_q == 0) return hipSuccess;
+  const bool l0 = a.sp.strata == MRL_STRATA_L0_ONLY;
+  // batched: the tile kernel; otherwise one query per workgroup, or the
+  // 8-query workgroups of the diagnostic and L0Only paths
+  const bool tile = a.n_q >= 8 && !diag && !l0;
+  const int qt = tile ? kTileQ : scan_query_tile(a.n_q);
+  const uint32_t tiles = (a.n_q + qt - 1) / qt;
+  const uint32_t grid = scan_grid(a, diag);
+  // exclusive segments: the one-query kernel, one segment per workgroup
+  if (a.excl && (tile || qt != 1 || diag || l0 || grid != a.nseg || a.nseg > (uint32_t)kMaxSegs ||
+                 a.seg_cap > (uint32_t)Staging<1>::kCap))
+    return hipErrorInvalidValue;
   dim3 g(grid, tiles);
   if (tile) {
     if (a.sp.strata == MRL_STRATA_FULL64B) launch(k_scan_tile<kTileQ, true>, g, dim3(256), s, ev, a);
