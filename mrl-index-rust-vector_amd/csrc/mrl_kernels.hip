@@ -1675,48 +1675,52 @@ constexpr int kSelCap = 1024;   // entries at or above the K-th bin floor kept f
 constexpr int kSelThreads = 1024;
 constexpr int kRankMax = 512;  // up to this many gathered entries are rank-sorted
 
-// One wave: bin holding the need-th largest entry of a descending scan over
-// `hist` (nb = 64 * per bins).  Returns the bin and the count strictly above
-// it through LDS outputs; bin 0 when the histogram holds fewer than `need`.
+// Block-wide exclusive prefix sum of one value per thread; *total gets the
+// sum over the block.  ws: blockDim.x / 64 words of LDS, free until the
+// caller's next barrier.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* ws, uint32_t* total) {
+  const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6, nw = blockDim.x >> 6;
+  uint32_t incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t x = __shfl_up(incl, o);
+    if ((int)lane >= o) incl += x;
+  }
+  if (lane == 63) ws[w] = incl;
+  __syncthreads();
+  uint32_t base = 0, all = 0;
+  for (uint32_t u = 0; u < nw; ++u) {
+    const uint32_t x = ws[u];
+    base += u < w ? x : 0u;
+    all += x;
+  }
+  *total = all;
+  return base + incl - v;
+}
+
+// Block-wide: the bin holding the need-th largest entry of a scan of `hist`
+// (nb = blockDim.x or 2 * blockDim.x bins) from the top (desc) or the
+// bottom.  Writes the bin and the count strictly before it in the scan to
+// LDS outputs (read after the caller's barrier); bin 0 (desc) or nb - 1
+// when the histogram holds fewer than `need`.  Thread t takes scan
+// positions per*t .. per*t + per - 1, so neighbouring lanes read
+// neighbouring bins.
 __device__ void find_boundary(const uint32_t* hist, uint32_t nb, uint32_t need, bool desc,
-                              uint32_t* out_bin, uint32_t* out_before) {
-  if (threadIdx.x >= 64) return;
-  const uint32_t lane = threadIdx.x;
-  const uint32_t per = nb / 64;
-  uint32_t part = 0;
-  for (uint32_t i = 0; i < per; ++i) {
-    uint32_t bin = desc ? (nb - 1 - (lane * per + i)) : (lane * per + i);
-    part += hist[bin];
+                              uint32_t* out_bin, uint32_t* out_before, uint32_t* ws) {
+  const uint32_t t = threadIdx.x, per = nb / blockDim.x;
+  auto bin_at = [&](uint32_t pos) { return desc ? nb - 1 - pos : pos; };
+  const uint32_t c0 = hist[bin_at(per * t)];
+  const uint32_t c1 = per == 2 ? hist[bin_at(per * t + 1)] : 0u;
+  uint32_t total;
+  const uint32_t excl = block_excl_scan(c0 + c1, ws, &total);
+  if (excl < need && excl + c0 + c1 >= need) {
+    const bool first = excl + c0 >= need;
+    *out_bin = bin_at(per * t + (first ? 0u : 1u));
+    *out_before = first ? excl : excl + c0;
   }
-  uint32_t incl = part;
-  for (int off = 1; off < 64; off <<= 1) {
-    uint32_t o = __shfl_up(incl, off);
-    if ((int)lane >= off) incl += o;
-  }
-  const uint32_t excl = incl - part;
-  const bool hit = excl < need && incl >= need;
-  const uint64_t hm = __ballot(hit);
-  const uint32_t total = __shfl(incl, 63);
-  if (hm == 0) {  // fewer than need entries in total
-    if (lane == 0) {
-      *out_bin = desc ? 0u : nb - 1;
-      *out_before = total;
-    }
-    return;
-  }
-  const uint32_t src = (uint32_t)__ffsll((long long)hm) - 1;
-  if (lane == src) {
-    uint32_t before = excl;
-    for (uint32_t i = 0; i < per; ++i) {
-      uint32_t bin = desc ? (nb - 1 - (lane * per + i)) : (lane * per + i);
-      uint32_t c = hist[bin];
-      if (before + c >= need) {
-        *out_bin = bin;
-        *out_before = before;
-        break;
-      }
-      before += c;
-    }
+  if (t == 0 && (total < need || need == 0)) {  // no bin holds the need-th entry
+    *out_bin = desc ? 0u : nb - 1;
+    *out_before = total;
   }
 }
 
@@ -1948,7 +1952,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     if (short_segs) for_each_pair_short(v, take);
     else for_each_pair(v, take);
     __syncthreads();
-    find_boundary(s_hist, kHistBins, K, true, &s_misc[0], &s_misc[1]);
+    find_boundary(s_hist, kHistBins, K, true, &s_misc[0], &s_misc[1], s_ws);
     if (tid == 0) s_misc[2] = 0;
     __syncthreads();
     const uint32_t fkey = score_key(bin_floor(s_misc[0]));
@@ -1965,7 +1969,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     else m = total;  // sort every entry
   } else {
   build_hist(s_hist, v);
-  find_boundary(s_hist, kHistBins, K, true, &s_misc[0], &s_misc[1]);
+  find_boundary(s_hist, kHistBins, K, true, &s_misc[0], &s_misc[1], s_ws);
   __syncthreads();
   const float floor_t = bin_floor(s_misc[0]);
 
@@ -2004,7 +2008,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
         if (pass == 0 || (key >> (sh + wd)) == prefix) atomicAdd(&s_hist[(key >> sh) & (nb - 1)], 1u);
       });
       __syncthreads();
-      find_boundary(s_hist, nb, need, true, &s_misc[3], &s_misc[4]);
+      find_boundary(s_hist, nb, need, true, &s_misc[3], &s_misc[4], s_ws);
       __syncthreads();
       need -= s_misc[4];
       prefix = (prefix << wd) | s_misc[3];
@@ -2023,7 +2027,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
         if (pass == 0 || (r >> (sh + wd)) == rprefix) atomicAdd(&s_hist[(r >> sh) & (nb - 1)], 1u);
       });
       __syncthreads();
-      find_boundary(s_hist, nb, rneed, false, &s_misc[3], &s_misc[4]);
+      find_boundary(s_hist, nb, rneed, false, &s_misc[3], &s_misc[4], s_ws);
       __syncthreads();
       rneed -= s_misc[4];
       rprefix = (rprefix << wd) | s_misc[3];
@@ -2061,27 +2065,15 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     __syncthreads();
     for (uint32_t i = tid; i < m; i += kSelThreads) atomicAdd(&s_hist[hist_bin(key_score((uint32_t)(sb[i] >> 32)))], 1u);
     __syncthreads();
-    if (tid < 64) {  // start[b] = entries in bins above b; lane l owns bins 32(63-l) .. +31
-      const uint32_t lane = tid, seg = 63u - lane;
-      uint32_t c[32], part = 0;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        c[i] = s_hist[seg * 32u + i];
-        part += c[i];
-      }
-      uint32_t incl = part;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t o = __shfl_up(incl, off);
-        if ((int)lane >= off) incl += o;
-      }
-      uint32_t run = incl - part;
-#pragma unroll
-      for (int i = 31; i >= 0; --i) {
-        s_start[seg * 32u + i] = run;
-        s_hist[seg * 32u + i] = 0u;
-        run += c[i];
-      }
+    {  // start[b] = entries in bins above b; thread t owns bins 2047 - 2t and 2046 - 2t
+      const uint32_t b0 = kHistBins - 1 - 2u * (uint32_t)tid, b1 = b0 - 1;
+      const uint32_t c0 = s_hist[b0], c1 = s_hist[b1];
+      uint32_t total;
+      const uint32_t excl = block_excl_scan(c0 + c1, s_ws, &total);
+      s_start[b0] = excl;
+      s_start[b1] = excl + c0;
+      s_hist[b0] = 0u;
+      s_hist[b1] = 0u;
     }
     __syncthreads();
     for (uint32_t i = tid; i < m; i += kSelThreads) {
@@ -2094,8 +2086,12 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
       const uint64_t c = s_buf[i];
       const uint32_t b = hist_bin(key_score((uint32_t)(c >> 32)));
       const uint32_t lo = s_start[b], hi = lo + s_hist[b];
-      uint32_t r = lo;
-      for (uint32_t j = lo; j < hi; ++j) r += s_buf[j] > c ? 1u : 0u;
+      uint32_t r = lo, j = lo;
+      for (; j + 4 <= hi; j += 4) {  // four independent reads in flight
+        const uint64_t x0 = s_buf[j], x1 = s_buf[j + 1], x2 = s_buf[j + 2], x3 = s_buf[j + 3];
+        r += (x0 > c ? 1u : 0u) + (x1 > c ? 1u : 0u) + (x2 > c ? 1u : 0u) + (x3 > c ? 1u : 0u);
+      }
+      for (; j < hi; ++j) r += s_buf[j] > c ? 1u : 0u;
       if (r < keep) emit(r, c);
     }
   } else if (m <= (uint32_t)kRankMax) {
