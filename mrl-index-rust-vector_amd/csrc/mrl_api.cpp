@@ -188,6 +188,8 @@ struct mrl_results {
   uint32_t* d_counts = nullptr;
   float* d_cand_score = nullptr;   // [n_q][kSegs][seg_cap]
   uint32_t* d_cand_row = nullptr;
+  float* d_cand_lower = nullptr;   // [n_q][kSegs][seg_cap] lower bounds of the MFMA path's appends
+  uint8_t* d_mma = nullptr;        // MFMA path: query operands [n_q][kMmaSteps][2] uint4, then constants
   uint32_t* d_seg_count = nullptr; // [n_q][kMaxSegs] (a scan uses [n_q][nseg]), zero between scans
   float* d_tau = nullptr;
   float* d_tau_hi = nullptr;       // [n_q] floor of the final pass
@@ -300,7 +302,10 @@ extern "C" int mrl_ctx_profile_collect(mrl_ctx* ctx, mrl_kernel_time* out, uint3
   uint32_t i = 0;
   for (auto& r : ctx->prof) {
     float ms = 0.0f;
-    if (hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess) ms = -1.0f;
+    if (hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess) {
+      ms = -1.0f;
+      (void)hipGetLastError();  // do not leave the failure for the next launch check
+    }
     if (i < max) {
       out[i] = r.info;
       out[i].ms = ms;
@@ -666,6 +671,8 @@ static void results_free(mrl_results* r) {
   dev_free(r->d_out);
   dev_free(r->d_cand_score);
   dev_free(r->d_cand_row);
+  dev_free(r->d_cand_lower);
+  dev_free(r->d_mma);
   dev_free(r->d_seg_count);
   dev_free(r->d_tau);
   dev_free(r->d_tau_hi);
@@ -683,6 +690,9 @@ static void results_release(mrl_results* r) {
 static size_t results_head_bytes(uint32_t n_q) { return (size_t)n_q * 8 + kStatCopies * kStatCount * 8; }
 
 static const uint32_t kSegCap = 4096;  // kSegs * kSegCap = 65536 candidates per query and scan
+
+// MFMA path, per query: query operands, then kMcCount constants.
+static size_t mma_bytes_per_query() { return (size_t)2 * kMmaSteps * 16 + kMcCount * 4; }
 
 extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_results** out) {
   if (!ctx || !out) return fail(MRL_ERR_INVALID_ARG, "null argument");
@@ -709,6 +719,8 @@ extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_re
   }
   ok = ok && hipMalloc(&r->d_cand_score, cands * sizeof(float)) == hipSuccess &&
             hipMalloc(&r->d_cand_row, cands * sizeof(uint32_t)) == hipSuccess &&
+            hipMalloc(&r->d_cand_lower, cands * sizeof(float)) == hipSuccess &&
+            hipMalloc(&r->d_mma, nq * mma_bytes_per_query()) == hipSuccess &&
             hipMalloc(&r->d_seg_count, nq * kMaxSegs * sizeof(uint32_t)) == hipSuccess &&
             hipMalloc(&r->d_tau, nq * sizeof(float)) == hipSuccess &&
             hipMalloc(&r->d_tau_hi, nq * sizeof(float)) == hipSuccess &&
@@ -744,6 +756,9 @@ extern "C" void mrl_results_destroy(mrl_results* res) {
 struct PassBuffers {
   float* cand_score;
   uint32_t* cand_row;
+  float* cand_lower = nullptr;    // MFMA path (null: the exact kernels only)
+  uint4* mma_ops = nullptr;
+  float* mma_consts = nullptr;
   uint32_t* seg_count;
   uint32_t nseg;
   uint32_t seg_cap;
@@ -786,9 +801,128 @@ static bool excl_ok(const PassBuffers& pb, uint32_t n_q, const ScanParams& sp) {
 // k_select emits the top K (and flags a query whose floor left fewer than K
 // candidates).  rerun_safe: the final pass alone at the safe floor k_select
 // kept (rank K).  Caller holds the context lock.
+// The MFMA-bounded path serves batches under the settings where the
+// reference's top K is the top K by full score (the conditions tight_coef()
+// checks on the device) and the RaBitQ mid-band.
+static bool mma_ok(const mrl_plans* plans, uint32_t n_q, const ScanParams& sp, const PassBuffers& pb) {
+  return pb.cand_lower && n_q >= (uint32_t)kMmaMinQ && plans->mid_codec == MRL_MID_RABITQ &&
+         sp.strata != MRL_STRATA_L0_ONLY && sp.alpha >= 1.0f && sp.w_s4 >= 0.0f && 2.4f * sp.w_s4 <= sp.alpha;
+}
+
+// MFMA-bounded scan of n_q plans: operands (k_mma_prep); when the index has a
+// sampling pass, the lower bounds of the sampled blocks fill the histogram
+// and k_mma_floors takes the final floor (rank final_rank) and the safe one
+// (rank K) from it; the final pass appends (upper, lower, row) for the pairs
+// whose upper bound reaches the floor (every active pair without a sampling
+// pass); k_finish scores exactly the candidates whose upper bound reaches the
+// K-th best lower bound; k_select emits the top K.
+static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t plans_first, uint32_t n_q,
+                            const ScanParams& sp, uint32_t K, const LevelPlan& lp, const PassBuffers& pb,
+                            unsigned long long* stats, bool rerun_safe) {
+  hipStream_t s = ctx->stream;
+  const size_t np = lp.passes.size();
+  const bool sampled = np > 1 && !rerun_safe;
+  const uint32_t rank = np > 1 ? final_rank(K, lp.passes[0].n_pos, ix->n_blocks) : K;
+  {
+    MmaPrepArgs pa{};
+    pa.plans = plans->d_plans + plans_first;
+    pa.luts = plans->d_luts + (size_t)plans_first * kQData;
+    pa.n_q = n_q;
+    pa.sp = sp;
+    pa.ops = pb.mma_ops;
+    pa.consts = pb.mma_consts;
+    ProfScope ps(ctx, MRL_KERNEL_MMA_PREP, 0, 0, n_q);
+    HIP_TRY(launch_mma_prep(pa, s, ps.ev()));
+    ps.commit(n_q != 0);
+  }
+  for (size_t pi = 0; pi < np; ++pi) {
+    const bool last = pi + 1 == np;
+    if (rerun_safe && !last) continue;
+    ScanArgs a{};
+    a.idx = ix->d_blocks;
+    a.rows1 = ix->rows1();
+    a.rows4 = ix->rows4();
+    a.n_blocks = ix->n_blocks;
+    a.n_pos = lp.passes[pi].n_pos;
+    a.shift = lp.passes[pi].shift;
+    a.prev_shift = -1;
+    a.plans = plans->d_plans + plans_first;
+    a.luts = plans->d_luts + (size_t)plans_first * kQData;
+    a.n_q = n_q;
+    a.flag_tabs = ctx->d_flag_tabs;
+    a.sp = sp;
+    a.tau = last ? (rerun_safe ? pb.tau : (sampled ? pb.tau_hi : nullptr)) : nullptr;
+    a.hist = last ? nullptr : pb.hist;
+    a.cand_score = pb.cand_score;
+    a.cand_row = pb.cand_row;
+    a.cand_lower = pb.cand_lower;
+    a.seg_count = pb.seg_count;
+    a.nseg = pb.nseg;
+    a.seg_cap = pb.seg_cap;
+    a.stats = last ? stats : nullptr;
+    a.err = pb.err;
+    a.mma_ops = pb.mma_ops;
+    a.mma_consts = pb.mma_consts;
+    const int mode = !last ? 0 : ((sampled || rerun_safe) ? 1 : 2);
+    ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)pi, lp.passes[pi].n_new, n_q);
+    HIP_TRY(launch_scan_mma(a, mode, s, ps.ev()));
+    ps.commit(a.n_pos != 0 && n_q != 0);
+    if (!last) {
+      ProfScope pt(ctx, MRL_KERNEL_THRESH, (int)pi, 0, n_q);
+      HIP_TRY(launch_mma_floors(pb.hist, n_q, rank, K, pb.tau_hi, pb.tau, s, pt.ev()));
+      pt.commit(n_q != 0);
+    }
+  }
+  {
+    FinishArgs fa{};
+    fa.idx = ix->d_blocks;
+    fa.n_blocks = ix->n_blocks;
+    fa.rows1 = ix->rows1();
+    fa.rows4 = ix->rows4();
+    fa.plans = plans->d_plans + plans_first;
+    fa.luts = plans->d_luts + (size_t)plans_first * kQData;
+    fa.mma_consts = pb.mma_consts;
+    fa.sp = sp;
+    fa.k = K;
+    fa.cand_score = pb.cand_score;
+    fa.cand_lower = pb.cand_lower;
+    fa.cand_row = pb.cand_row;
+    fa.seg_count = pb.seg_count;
+    fa.nseg = pb.nseg;
+    fa.seg_cap = pb.seg_cap;
+    fa.tau_final = rerun_safe ? pb.tau : (sampled ? pb.tau_hi : nullptr);
+    fa.err = pb.err;
+    fa.stats = stats;
+    ProfScope ps(ctx, MRL_KERNEL_FINISH, (int)np - 1, 0, n_q);
+    HIP_TRY(launch_finish(fa, n_q, s, ps.ev()));
+    ps.commit(n_q != 0);
+  }
+  SelectArgs sa{};
+  sa.cand_score = pb.cand_score;
+  sa.cand_row = pb.cand_row;
+  sa.seg_count = pb.seg_count;
+  sa.nseg = pb.nseg;
+  sa.seg_cap = pb.seg_cap;
+  sa.err = pb.err;
+  sa.k = K;
+  sa.status = pb.status;
+  sa.out_ids = pb.out_ids;
+  sa.out_scores = pb.out_scores;
+  sa.out_counts = pb.out_counts;
+  sa.hist = sampled ? pb.hist : nullptr;
+  sa.tau_final = pb.tau_hi;
+  sa.tau_safe = pb.tau;
+  ProfScope ps(ctx, MRL_KERNEL_SELECT, (int)np - 1, 0, n_q);
+  HIP_TRY(launch_select(sa, n_q, s, ps.ev()));
+  ps.commit(n_q != 0);
+  return MRL_OK;
+}
+
 static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t plans_first, uint32_t n_q,
                         const ScanParams& sp, uint32_t K, const LevelPlan& lp, const PassBuffers& pb,
                         unsigned long long* stats, bool rerun_safe = false) {
+  if (mma_ok(plans, n_q, sp, pb))
+    return enqueue_scan_mma(ctx, ix, plans, plans_first, n_q, sp, K, lp, pb, stats, rerun_safe);
   hipStream_t s = ctx->stream;
   const size_t np = lp.passes.size();
   const bool sampled = np > 1 && !rerun_safe;
@@ -866,6 +1000,9 @@ static PassBuffers results_buffers(mrl_results* r) {
   PassBuffers pb;
   pb.cand_score = r->d_cand_score;
   pb.cand_row = r->d_cand_row;
+  pb.cand_lower = r->d_cand_lower;
+  pb.mma_ops = reinterpret_cast<uint4*>(r->d_mma);
+  pb.mma_consts = reinterpret_cast<float*>(r->d_mma + (size_t)std::max<uint32_t>(r->n_q, 1) * 2 * kMmaSteps * 16);
   pb.seg_count = r->d_seg_count;
   pb.nseg = kSegs;
   pb.seg_cap = r->seg_cap;
@@ -971,6 +1108,7 @@ static int safe_rerun(mrl_ctx* ctx, mrl_results* r, uint32_t q, uint32_t* st) {
   const size_t cand = (size_t)q * kSegs * r->seg_cap;
   pb.cand_score += cand;
   pb.cand_row += cand;
+  pb.cand_lower = nullptr;  // one query: the exact kernels
   pb.seg_count += (size_t)q * kMaxSegs;
   pb.err += q;
   pb.tau += q;

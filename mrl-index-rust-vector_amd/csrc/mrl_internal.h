@@ -123,6 +123,38 @@ constexpr int kSegs = 16;
 constexpr int kMaxSegs = 512;
 constexpr int kHistBins = 2048;
 
+// MFMA-bounded batched scan (k_mma_prep, k_scan_mma, k_mma_floors, k_finish).
+// Each (vector, query) pair gets an upper and a lower bound of the full score
+// from f16 32x32x16 MFMA tiles (queries x vectors, K = 16 per step); only the
+// pairs whose upper bound reaches the K-th best lower bound are scored exactly.
+constexpr int kMmaSteps = 17;   // K-steps of a tile: prefix 4, S1 8, S4 4, error columns 1
+constexpr int kMmaQ = 64;       // queries per workgroup (two 32-query tiles per wave)
+constexpr int kMmaMinQ = 8;     // batches of at least this many queries take the MFMA path
+// Per-query constants written by k_mma_prep (floats).
+enum {
+  kMcS = 0,   // power-of-two scale of the query operand
+  kMcInvS,    // its inverse
+  kMcMean,    // eden_mean_ip (EdenProd) or 0 (MinMax4)
+  kMcEP,      // error bound coefficients (score units): per |scale|,
+  kMcE1,      //   per mid_n,
+  kMcE4,      //   per max(high_n, 1e-6),
+  kMcEO,      //   per |offset|,
+  kMcE0,      //   and constant
+  kMcR,       // bound on |score| + error for vectors whose meta magnitudes are <= kMmaSafe
+  kMcOk,      // 1: operands finite; 0: the query is re-run by the exact kernels
+  kMcCount = 16
+};
+constexpr float kMmaSafe = 4096.0f;  // larger |scale|, mid_n, high_n or |offset|: always a candidate
+
+struct MmaPrepArgs {
+  const mrl_query_plan* plans;
+  const float* luts;   // [n_q][kQData]
+  uint32_t n_q;
+  ScanParams sp;
+  uint4* ops;          // [n_q][kMmaSteps][2]: 8 f16 query-operand values per (step, half of K)
+  float* consts;       // [n_q][kMcCount]
+};
+
 struct ScanArgs {
   const uint8_t* idx;          // device-layout blocks
   const uint4* rows1;          // [n_blocks * 64] each slot's S1 bits (dword k: dims 32k..32k+31)
@@ -159,6 +191,36 @@ struct ScanArgs {
   uint64_t* d_masks;           // diagnostic outputs, [n_q][n_blocks][5]
   float* d_prefix;             // [n_q][n_blocks][64]
   float* d_score;              // [n_q][n_blocks][64]
+  // MFMA path: query operands and constants from k_mma_prep; appends store
+  // the upper bound in cand_score and the lower bound in cand_lower
+  const uint4* mma_ops;
+  const float* mma_consts;
+  float* cand_lower;
+};
+
+// Exact finishing of the MFMA path, one workgroup per query: the K-th best
+// lower bound among the query's candidates, exact scores (the reference's f32
+// operations) of those whose upper bound reaches it, written back as the
+// query's candidate list for k_select.
+struct FinishArgs {
+  const uint8_t* idx;
+  uint64_t n_blocks;
+  const uint4* rows1;
+  const uint2* rows4;
+  const mrl_query_plan* plans;
+  const float* luts;
+  const float* mma_consts;
+  ScanParams sp;
+  uint32_t k;
+  float* cand_score;        // in: upper bounds; out: exact scores
+  float* cand_lower;
+  uint32_t* cand_row;
+  uint32_t* seg_count;
+  uint32_t nseg;
+  uint32_t seg_cap;
+  const float* tau_final;   // [n_q] floor of the final pass (null: none)
+  uint32_t* err;
+  unsigned long long* stats;  // or null: exact-scored and kept pairs go to kStatPushed
 };
 
 struct SelectArgs {
@@ -256,6 +318,14 @@ int scan_query_tile(uint32_t n_q);  // queries per workgroup of the non-tile ker
 uint32_t scan_grid(const ScanArgs& a, bool diag);
 hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
+// MFMA path: mode 0 samples (lower bounds into the histogram), 1 appends the
+// pairs whose upper bound reaches the floor in a.tau, 2 appends every active pair.
+hipError_t launch_mma_prep(const MmaPrepArgs& a, hipStream_t s, const LaunchEvents& ev = {});
+uint32_t mma_scan_grid(const ScanArgs& a);
+hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const LaunchEvents& ev = {});
+hipError_t launch_mma_floors(const uint32_t* hist, uint32_t n_q, uint32_t rank, uint32_t safe_rank, float* floor_out,
+                             float* safe_out, hipStream_t s, const LaunchEvents& ev = {});
+hipError_t launch_finish(const FinishArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
 
 // mrl_rerank.hip: build a 768-dim store from f32 rows; score + sort.
 hipError_t launch_rerank_store(const float* rows, uint64_t n_rows, int precision, void* data, uint16_t* scales,

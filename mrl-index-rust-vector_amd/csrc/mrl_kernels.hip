@@ -2147,6 +2147,703 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// MFMA-bounded batched scan
+// ---------------------------------------------------------------------------
+// In real arithmetic the reference's full score of a vector for a query
+// (scan.rs:453-634, every stage run; mid_n = max(mid_norm, 1e-6),
+// hn = max(high_n, 1e-6)) is
+//   P + mid_n * S1 + hn * w_s4 * S4,
+//   P  = mean_ip + scale * sum_d cb[l_d] w_d     (EdenProd; the LUT is cb * w)
+//      = scale * sum_d l_d q_d + offset * prefix_sum   (MinMax4),
+//   S1 = sum_d pos_d (2 b_d - 1)   (rabitq_base = -sum pos, weights2 = 2 pos),
+//   S4 = the same over the folded tail,
+// a dot product of a 261-value row per vector with a column per query.
+// k_scan_mma evaluates it for 32 queries x 32 vectors per f16 MFMA tile
+// (v_mfma_f32_32x32x16_f16, 17 K-steps): queries are the A operand, scaled
+// by a power of two s; vectors are the B operand, built from the block:
+// scale * cb[level] (a byte -> two-f16 LDS table, then a packed multiply),
+// +-mid_n / 2 and +-hn w_s4 / 2 from the sign of each S1 / S4 bit, and a last
+// step of error columns.  The accumulator starts at C = s (mean_ip - tau + e0).
+//   E(v, q) = |scale| eP + mid_n e1 + hn e4 + |offset| eO + e0
+// bounds |tile value / s - (reference's f32 score - tau)|: the f16 rounding of
+// both operands (2^-11 relative, 2^-25 absolute below the normal range), the
+// MFMA's f32 accumulation (measured below 2^-21 of the summed magnitudes) and
+// the reference's own f32 rounding (< 300 ulp of the summed magnitudes), each
+// covered two times or more.  With the error columns added the tile holds
+// s (U - tau), U = approximation + E >= score; the sampling pass subtracts
+// them and gets s L, L = approximation - E <= score.  Under the settings
+// tight_coef() accepts, the reference's top K is the top K by full score, so
+// dropping pairs with U < tau (tau <= the K-th best score) is exact, and so
+// is scoring exactly only the pairs whose U reaches the K-th best L
+// (k_finish).
+typedef _Float16 mma_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mma_h2 __attribute__((ext_vector_type(2)));
+typedef float mma_f16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ mma_h8 as_h8(uint4 u) { return __builtin_bit_cast(mma_h8, u); }
+
+// Dimension of the query weight behind element e (0..7) of K-half kh at
+// K-step st < 16.  Prefix step st: level word 4 kh + st, element e = nibble e.
+// S1 step 4 + t: dword 2 kh + t / 4 of the slot's S1 row, element 2 j + p =
+// bit 4 (t % 4) + j + 16 p.  S4 step 12 + t: dword kh of the S4 row, element
+// 2 j + p = bit 4 t + j + 16 p.  k_scan_mma builds the vector operand in the
+// same order.
+__device__ __forceinline__ int mma_dim(int st, int kh, int e) {
+  if (st < 4) return 8 * (4 * kh + st) + e;
+  const int j = e >> 1, p = e & 1;
+  if (st < 12) {
+    const int t = st - 4;
+    return 64 * kh + 32 * (t >> 2) + 4 * (t & 3) + j + 16 * p;
+  }
+  return 32 * kh + 4 * (st - 12) + j + 16 * p;
+}
+
+// f16 bits of x >= 0 with a magnitude no smaller than x.
+__device__ __forceinline__ uint32_t f16_up(float x) {
+  uint32_t h = f32_to_f16(x);
+  if (h2f((uint16_t)h) < x) h += 1u;
+  return h;
+}
+
+__device__ __forceinline__ uint32_t f16_bits(float x) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+// Query operands and error coefficients, one wave per query.
+__global__ __launch_bounds__(64) void k_mma_prep(MmaPrepArgs a) {
+  __shared__ float s_w[64], s_w1[128], s_w4[64], s_ex[8];
+  const uint32_t q = blockIdx.x, lane = threadIdx.x;
+  const mrl_query_plan* p = a.plans + q;
+  const float* qd = a.luts + (uint64_t)q * kQData;
+  const bool eden = p->prefix_codec == MRL_PREFIX_EDEN_PROD;
+  const bool s1on = a.sp.strata != MRL_STRATA_L0_ONLY;
+  const bool tail = a.sp.strata == MRL_STRATA_FULL64B && p->has_tail_fold != 0;
+  const float w = p->prefix_weight[lane];
+  const float w1a = s1on ? qd[kQdW1 + lane] : 0.0f, w1b = s1on ? qd[kQdW1 + 64 + lane] : 0.0f;
+  const float w4 = tail ? qd[kQdW4 + lane] : 0.0f;
+  s_w[lane] = w;
+  s_w1[lane] = w1a;
+  s_w1[64 + lane] = w1b;
+  s_w4[lane] = w4;
+  const float cbv = lane < 16 ? (eden ? fabsf(p->eden_codebook[lane]) : (float)lane) : 0.0f;
+  float l1w = fabsf(w), l1w2 = fabsf(w1a) + fabsf(w1b), l1w4 = fabsf(w4), cbm = cbv;
+  float mx = fmaxf(fmaxf(fabsf(w), fabsf(w4)), fmaxf(fabsf(w1a), fabsf(w1b)));
+  const bool fin_l = w - w == 0.0f && w1a - w1a == 0.0f && w1b - w1b == 0.0f && w4 - w4 == 0.0f && cbv - cbv == 0.0f;
+#pragma unroll
+  for (int h = 1; h < 64; h <<= 1) {
+    l1w += __shfl_xor(l1w, h);
+    l1w2 += __shfl_xor(l1w2, h);
+    l1w4 += __shfl_xor(l1w4, h);
+    mx = fmaxf(mx, __shfl_xor(mx, h));
+    cbm = fmaxf(cbm, __shfl_xor(cbm, h));
+  }
+  const float mean = eden ? p->eden_mean_ip : 0.0f;
+  const float psum = eden ? 0.0f : p->prefix_sum;
+  const float ws4 = tail ? a.sp.w_s4 : 0.0f;
+  // The f32 sums above run over at most 128 terms: relative error < 2^-17.
+  const float up = 1.0f + 1.0f / 1024.0f;
+  // s: every query-operand value times s stays below 2^14 in magnitude
+  const float bm = fmaxf(mx, fabsf(psum));
+  int ex = 0;
+  if (bm > 0.0f && bm - bm == 0.0f) (void)frexpf(bm, &ex);
+  ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
+  const float s = ldexpf(1.0f, 14 - ex), inv_s = ldexpf(1.0f, ex - 14);
+  const float t25 = 2.98023223876953125e-8f;  // 2^-25
+  const float eP = (cbm * l1w * (1.0f / 256.0f) + t25 * (64.0f * cbm + 1.0f) * inv_s) * up;
+  const float e1 = s1on ? (l1w2 * (1.0f / 512.0f) + t25 * 65.0f * inv_s) * up : 0.0f;
+  const float e4 = tail ? (ws4 * l1w4 * (1.0f / 512.0f) + t25 * (32.0f * ws4 + 1.0f) * inv_s) * up : 0.0f;
+  const float eO = eden ? 0.0f : (fabsf(psum) * (1.0f / 512.0f) + t25 * 2.0f * inv_s) * up;
+  const float e0 =
+      (fabsf(mean) * (1.0f / 16384.0f) + t25 * (l1w + l1w2 + l1w4 + fabsf(psum) + eP + e1 + e4 + eO)) * up +
+      1e-18f;
+  const float R = 2.0f * (fabsf(mean) +
+                          kMmaSafe * (cbm * l1w + l1w2 + ws4 * l1w4 + fabsf(psum) + eP + e1 + e4 + eO) + e0 + 1.0f);
+  const bool fin = ballot(!fin_l) == 0 && mean - mean == 0.0f && psum - psum == 0.0f && R - R == 0.0f;
+  if (lane == 0) {
+    s_ex[0] = eP;
+    s_ex[1] = e1;
+    s_ex[2] = e4;
+    s_ex[3] = eO;
+    float* mc = a.consts + (uint64_t)q * kMcCount;
+    mc[kMcS] = s;
+    mc[kMcInvS] = inv_s;
+    mc[kMcMean] = mean;
+    mc[kMcEP] = eP;
+    mc[kMcE1] = e1;
+    mc[kMcE4] = e4;
+    mc[kMcEO] = eO;
+    mc[kMcE0] = e0;
+    mc[kMcR] = R;
+    mc[kMcOk] = fin ? 1.0f : 0.0f;
+    for (int i = kMcOk + 1; i < kMcCount; ++i) mc[i] = 0.0f;
+  }
+  __syncthreads();
+  if (lane < 2 * kMmaSteps) {
+    const int st = (int)lane >> 1, kh = (int)lane & 1;
+    uint32_t hv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint32_t h = 0u;
+      if (st < 4) h = f32_to_f16(s * s_w[mma_dim(st, kh, e)]);
+      else if (st < 12) h = f32_to_f16(s * s_w1[mma_dim(st, kh, e)]);
+      else if (st < 16) h = f32_to_f16(s * s_w4[mma_dim(st, kh, e)]);
+      else if (kh == 0 && e < 4) h = f16_up(s * s_ex[e]);       // error columns
+      else if (kh == 0 && e == 4) h = f32_to_f16(s * psum);     // offset * prefix_sum
+      hv[e] = h;
+    }
+    a.ops[(uint64_t)q * (2 * kMmaSteps) + lane] =
+        make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
+  }
+}
+
+// Floors of the final pass from the sampling histogram: rank `rank` and the
+// safe rank K, one wave per query.
+__global__ __launch_bounds__(64) void k_mma_floors(const uint32_t* hist, uint32_t rank, uint32_t safe_rank,
+                                                   float* floor_out, float* safe_out) {
+  const uint32_t q = blockIdx.x;
+  const HistRow r = hist_row(hist + (uint64_t)q * kHistBins);
+  const float f = floor_of(r, rank);
+  const float sf = floor_of(r, safe_rank);
+  if (__lane_id() == 0) {
+    floor_out[q] = f;
+    safe_out[q] = sf;
+  }
+}
+
+// One block's per-lane inputs for both 32-vector tiles: lane l serves vector
+// 32 h + l % 32, half l / 32 of the K range.
+struct MmaRaw {
+  uint4 lev[2];      // level words 4 kh .. 4 kh + 3
+  uint2 r1[2];       // S1 row dwords 2 kh, 2 kh + 1
+  uint32_t r4[2];    // S4 row dword kh
+  uint32_t meta[2];  // scale | offset << 16 (f16 bits)
+  uint32_t tf[2];    // tail_norm | flags << 16
+  uint32_t hdr;      // lanes 0..3: header dwords 0, 1, 4, 5
+};
+
+__device__ __forceinline__ MmaRaw mma_load(const uint8_t* blk, const uint4* rows1, const uint2* rows4, uint64_t b) {
+  const uint32_t lane = __lane_id(), kh = lane >> 5, vl = lane & 31u;
+  const uint16_t* m16 = reinterpret_cast<const uint16_t*>(blk);
+  MmaRaw r;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t v = 32u * h + vl;
+    r.lev[h] = *reinterpret_cast<const uint4*>(blk + kDevNibbles + 32u * v + 16u * kh);
+    r.r1[h] = reinterpret_cast<const uint2*>(rows1 + b * 64u + v)[kh];
+    r.r4[h] = reinterpret_cast<const uint32_t*>(rows4 + b * 64u + v)[kh];
+    r.meta[h] = (uint32_t)m16[kDevScale / 2 + v] | ((uint32_t)m16[kDevOffset / 2 + v] << 16);
+    r.tf[h] = (uint32_t)m16[kDevTail / 2 + v] | ((uint32_t)blk[kDevFlags + v] << 16);
+  }
+  const uint32_t hw = lane < 2 ? lane : (lane < 4 ? lane + 2 : 0);
+  r.hdr = reinterpret_cast<const uint32_t*>(blk)[hw];
+  return r;
+}
+
+// Candidate appends of one workgroup, staged in LDS and flushed at its end
+// with one global atomic per (workgroup, query).  Each wave owns a region of
+// kMmaWaveCap entries and keeps its fill count in a scalar register, so an
+// append needs no atomic.
+constexpr int kMmaWaveCap = 1024;
+struct MmaStaging {
+  uint32_t n[4];
+  uint32_t cnt[kMmaQ];
+  uint32_t base[kMmaQ];
+  uint32_t row[4 * kMmaWaveCap];
+  float u[4 * kMmaWaveCap];
+  float l[4 * kMmaWaveCap];
+  uint8_t q[4 * kMmaWaveCap];
+};
+
+// Appends (u, l, row) of query q0 + qi (per lane) for the lanes in pm to this
+// wave's region at *fill (wave-uniform); past the region's room, straight
+// into the query's segment (one global atomic per lane).
+__device__ __forceinline__ void mma_append(MmaStaging& st, const ScanArgs& a, int wave, uint32_t* fill, uint32_t q0,
+                                           uint32_t qi, uint32_t seg, uint64_t pm, float u, float l, uint32_t row) {
+  const uint32_t lane = __lane_id();
+  const uint32_t base = *fill;
+  *fill = base + (uint32_t)__popcll(pm);
+  if (!((pm >> lane) & 1ull)) return;
+  const uint32_t slot = base + lanes_below(pm);
+  if (slot < (uint32_t)kMmaWaveCap) {
+    const uint32_t e = (uint32_t)wave * kMmaWaveCap + slot;
+    st.row[e] = row;
+    st.u[e] = u;
+    st.l[e] = l;
+    st.q[e] = (uint8_t)qi;
+  } else {
+    const uint64_t sq = (uint64_t)(q0 + qi) * a.nseg + seg;
+    const uint32_t g = atomicAdd(a.seg_count + sq, 1u);
+    if (g < a.seg_cap) {
+      const uint64_t i = sq * a.seg_cap + g;
+      a.cand_score[i] = u;
+      a.cand_lower[i] = l;
+      a.cand_row[i] = row;
+    }
+  }
+}
+
+// One pass of the MFMA-bounded scan.  Workgroup = 4 waves over the same 64
+// queries (blockIdx.y), wave = one block at a time, each block as two
+// 32-vector tiles; NQT 32-query tiles per wave, their operands held in
+// registers.  MODE 0: sampling pass, the lower bounds of every active pair
+// go into the query's histogram; 1: final pass, pairs with U >= the floor in
+// a.tau are appended; 2: single pass, every active pair is appended.
+template <int NQT, int MODE>
+__global__ __launch_bounds__(256) void k_scan_mma(ScanArgs a) {
+  __shared__ uint32_t s_tab[256];
+  __shared__ float s_flag[512];      // rho = f / 255, then sqrt(max(1 - rho^2, 0))
+  __shared__ __align__(16) float s_c[kMmaQ];
+  __shared__ __align__(16) float s_qk[kMmaQ][8];  // tau, 1/s, eP, e1, e4, eO, e0 (with the tau term), ok
+  __shared__ unsigned int s_stats[kStatCount];
+  __shared__ MmaStaging s_st;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t lane = lane_id(), kh = lane >> 5, vl = lane & 31u;
+  const uint32_t q0 = blockIdx.y * kMmaQ;
+  const int nq = (int)min((uint32_t)kMmaQ, a.n_q - q0);
+
+  const uint32_t stride = gridDim.x * 4 - 1;  // odd: see k_scan
+  const uint32_t first = blockIdx.x * 4 + wave;
+  const uint32_t n_pos = first < stride ? a.n_pos : 0u;
+  uint32_t b_cur = first << a.shift;
+  MmaRaw cur{};
+  if (first < n_pos) cur = mma_load(a.idx + (uint64_t)b_cur * kBlockBytes, a.rows1, a.rows4, b_cur);
+
+  {  // byte -> (f16 cb[low nibble], f16 cb[high nibble])
+    const mrl_query_plan* p0 = a.plans + q0;
+    const bool eden = p0->prefix_codec == MRL_PREFIX_EDEN_PROD;
+    const uint32_t lo = (uint32_t)tid & 15u, hi = (uint32_t)tid >> 4;
+    const float clo = eden ? p0->eden_codebook[lo] : (float)lo;
+    const float chi = eden ? p0->eden_codebook[hi] : (float)hi;
+    s_tab[tid] = f32_to_f16(clo) | (f32_to_f16(chi) << 16);
+  }
+  s_flag[tid] = a.flag_tabs[tid];
+  s_flag[256 + tid] = a.flag_tabs[256 + tid];
+  if (tid < kStatCount) s_stats[tid] = 0u;
+  if (tid < 4) s_st.n[tid] = 0u;
+  if (tid < kMmaQ) {
+    const int qi = tid;
+    s_st.cnt[qi] = 0u;
+    float C = -INFINITY, qk[8] = {0.0f, 1.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (qi < nq) {
+      const float* mc = a.mma_consts + (uint64_t)(q0 + qi) * kMcCount;
+      const float s = mc[kMcS], mean = mc[kMcMean], R = mc[kMcR];
+      const bool ok = mc[kMcOk] != 0.0f;
+      float tau = 0.0f;
+      if (MODE == 1) {
+        tau = a.tau ? a.tau[q0 + qi] : -INFINITY;
+        if (!(tau >= -R)) tau = -R;  // no floor: below every score of a vector with safe magnitudes
+      }
+      const float e0q = mc[kMcE0] + fabsf(tau) * (1.0f / 65536.0f);
+      if (ok) C = s * ((mean - tau) + (MODE == 0 ? -e0q : e0q));
+      qk[0] = tau;
+      qk[1] = mc[kMcInvS];
+      qk[2] = mc[kMcEP];
+      qk[3] = mc[kMcE1];
+      qk[4] = mc[kMcE4];
+      qk[5] = mc[kMcEO];
+      qk[6] = e0q;
+      qk[7] = ok ? 1.0f : 0.0f;
+    }
+    s_c[qi] = C;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s_qk[qi][i] = qk[i];
+  }
+  // query operands: tile t, lane -> query q0 + 32 t + l % 32, K-half l / 32
+  uint4 qa[NQT][kMmaSteps];
+#pragma unroll
+  for (int t = 0; t < NQT; ++t) {
+    const uint32_t qi = 32u * t + vl;
+    const bool have = (int)qi < nq;
+    const uint4* src = a.mma_ops + (uint64_t)(q0 + (have ? qi : 0u)) * (2 * kMmaSteps) + kh;
+#pragma unroll
+    for (int st = 0; st < kMmaSteps; ++st) qa[t][st] = have ? src[2 * st] : make_uint4(0u, 0u, 0u, 0u);
+    if (MODE == 0 && kh == 0) {  // the sampling pass subtracts the error columns
+      qa[t][kMmaSteps - 1].x ^= 0x80008000u;
+      qa[t][kMmaSteps - 1].y ^= 0x80008000u;
+    }
+  }
+  __syncthreads();
+
+  const float ws4 = a.sp.strata == MRL_STRATA_FULL64B ? a.sp.w_s4 : 0.0f;
+  const uint32_t seg = blockIdx.x % a.nseg;
+  uint32_t c_blocks = 0, c_active = 0, c_app = 0;
+  uint32_t fill = 0;  // entries of this wave's staging region (wave-uniform)
+  // bit 16 t + r: register r of tile t belongs to a query of the batch with usable operands
+  uint32_t okbits = 0;
+#pragma unroll
+  for (int t = 0; t < NQT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
+      if (qi < nq && s_qk[qi][7] != 0.0f) okbits |= 1u << (16 * t + r);
+    }
+
+  for (uint32_t pos = first; pos < n_pos; pos += stride) {
+    const uint32_t b_nxt = pos + stride < n_pos ? (pos + stride) << a.shift : b_cur;
+    const MmaRaw nxt = mma_load(a.idx + (uint64_t)b_nxt * kBlockBytes, a.rows1, a.rows4, b_nxt);
+    const uint32_t b = b_cur;
+    const uint32_t min_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 0);
+    const uint32_t max_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 1);
+    const uint64_t tomb = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(cur.hdr, 3) << 32) |
+                          (uint64_t)(uint32_t)__builtin_amdgcn_readlane(cur.hdr, 2);
+    bool skip = false;
+    if (a.sp.temporal) {  // scan.rs:719-730
+      if (a.sp.has_lo && max_ts < a.sp.lo) skip = true;
+      if (a.sp.has_hi && min_ts > a.sp.hi) skip = true;
+    }
+    const uint64_t active = ~tomb;
+    if (!skip && active != 0) {
+      c_blocks += (uint32_t)nq;
+      c_active += (uint32_t)nq * (uint32_t)__popcll(active);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t v = 32u * h + vl;
+        const bool act = (active >> v) & 1ull;
+        // meta (block.rs:61-99)
+        const uint32_t sc_b = cur.meta[h] & 0xffffu, of_b = cur.meta[h] >> 16;
+        const float m_scale = h2f((uint16_t)sc_b), m_offset = h2f((uint16_t)of_b);
+        // (flags / 255 and sqrt(max(1 - rho^2, 0)) from the context's tables)
+        const float tn = fmaxf(h2f((uint16_t)(cur.tf[h] & 0xffffu)), 0.0f);
+        const uint32_t fl = cur.tf[h] >> 16;
+        const float mid_n = fmaxf(s_flag[256 + fl] * tn, 1e-6f);
+        const float hn = fmaxf(fmaxf(s_flag[fl] * tn, 0.0f), 1e-6f);
+        const bool safe = fabsf(m_scale) <= kMmaSafe && mid_n <= kMmaSafe && hn <= kMmaSafe &&
+                          fabsf(m_offset) <= kMmaSafe;
+        mma_f16 acc[NQT];
+#pragma unroll
+        for (int t = 0; t < NQT; ++t) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const float4 c4 = *reinterpret_cast<const float4*>(&s_c[32 * t + 8 * g + 4 * (int)kh]);
+            acc[t][4 * g + 0] = c4.x;
+            acc[t][4 * g + 1] = c4.y;
+            acc[t][4 * g + 2] = c4.z;
+            acc[t][4 * g + 3] = c4.w;
+          }
+        }
+        // prefix: scale * cb[level], 8 dims per step
+        const mma_h2 sc2 = __builtin_bit_cast(mma_h2, sc_b | (sc_b << 16));
+        const uint32_t lw[4] = {cur.lev[h].x, cur.lev[h].y, cur.lev[h].z, cur.lev[h].w};
+        uint32_t tv[16];  // all 16 table reads go out before the first use
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tv[i] = s_tab[(lw[i >> 2] >> (8 * (i & 3))) & 255u];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          uint32_t d[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const mma_h2 c2 = __builtin_bit_cast(mma_h2, tv[4 * st + j]);
+            d[j] = __builtin_bit_cast(uint32_t, c2 * sc2);
+          }
+          const uint4 bo = make_uint4(d[0], d[1], d[2], d[3]);
+#pragma unroll
+          for (int t = 0; t < NQT; ++t)
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][st]), as_h8(bo), acc[t], 0, 0, 0);
+        }
+        // S1: +-mid_n / 2 by bit
+        const uint32_t hp1 = f16_bits(0.5f * mid_n) * 0x10001u;
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt) {
+          const uint32_t nx = ~(tt < 4 ? cur.r1[h].x : cur.r1[h].y);
+          const int jb = 4 * (tt & 3);
+          uint32_t d[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) d[j] = hp1 | ((nx << (15 - jb - j)) & 0x80008000u);
+          const uint4 bo = make_uint4(d[0], d[1], d[2], d[3]);
+#pragma unroll
+          for (int t = 0; t < NQT; ++t)
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][4 + tt]), as_h8(bo), acc[t], 0, 0, 0);
+        }
+        // S4: +-hn w_s4 / 2 by bit
+        if (ws4 != 0.0f) {
+          const uint32_t hp4 = f16_bits(0.5f * hn * ws4) * 0x10001u;
+          const uint32_t nx = ~cur.r4[h];
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) {
+            uint32_t d[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) d[j] = hp4 | ((nx << (15 - 4 * tt - j)) & 0x80008000u);
+            const uint4 bo = make_uint4(d[0], d[1], d[2], d[3]);
+#pragma unroll
+            for (int t = 0; t < NQT; ++t)
+              acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][12 + tt]), as_h8(bo), acc[t], 0, 0, 0);
+          }
+        }
+        {  // error columns and offset * prefix_sum
+          uint4 bo = make_uint4(0u, 0u, 0u, 0u);
+          if (kh == 0) {
+            bo.x = (sc_b & 0x7fffu) | (f16_bits(mid_n) << 16);
+            bo.y = f16_bits(hn) | ((of_b & 0x7fffu) << 16);
+            bo.z = of_b;
+          }
+#pragma unroll
+          for (int t = 0; t < NQT; ++t)
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][kMmaSteps - 1]), as_h8(bo), acc[t], 0, 0,
+                                                            0);
+        }
+        // Register r of tile t holds query 32 t + 8 (r / 4) + 4 kh + r % 4.
+        if constexpr (MODE == 0) {
+          if (act && safe) {
+#pragma unroll
+            for (int t = 0; t < NQT; ++t)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
+                if (qi < nq && s_qk[qi][7] != 0.0f) {
+                  const float L = acc[t][r] * s_qk[qi][1];
+                  atomicAdd(a.hist + (uint64_t)(q0 + qi) * kHistBins + hist_bin(L), 1u);
+                }
+              }
+          }
+        } else {
+          // Absent queries and those with unusable operands start at C = -inf,
+          // so acc >= 0 only holds for pairs of the batch.
+          const uint32_t row = b * 64u + v;
+          const float eb = fabsf(m_scale), eo = fabsf(m_offset);
+#pragma unroll
+          for (int t = 0; t < NQT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const bool forced = MODE == 2 || !safe;
+              const bool okq = (okbits >> (16 * t + r)) & 1u;
+              const uint64_t pm = ballot(act && (acc[t][r] >= 0.0f || (forced && okq)));
+              if (pm == 0) continue;
+              const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
+              float U = INFINITY, L = -INFINITY;
+              if (safe) {
+                const float4 k0 = *reinterpret_cast<const float4*>(&s_qk[qi][0]);
+                const float4 k1 = *reinterpret_cast<const float4*>(&s_qk[qi][4]);
+                // k0 = {tau, 1/s, eP, e1}, k1 = {e4, eO, e0, ok}
+                const float tau = k0.x;
+                const float u0 = tau + acc[t][r] * k0.y;
+                const float E = eb * k0.z + mid_n * k0.w + hn * k1.x + eo * k1.y + k1.z;
+                const float mg = (fabsf(u0) + fabsf(tau)) * (1.0f / 4194304.0f);
+                U = u0 + mg;
+                L = (u0 - 2.0f * E * (1.0f + 1.0f / 1048576.0f)) - mg;
+                if (!(U == U)) U = INFINITY;
+                if (!(L == L)) L = -INFINITY;
+              }
+              c_app += (uint32_t)__popcll(pm);
+              mma_append(s_st, a, wave, &fill, q0, (uint32_t)qi, seg, pm, U, L, row);
+            }
+        }
+      }
+    }
+    cur = nxt;
+    b_cur = b_nxt;
+  }
+  if (a.stats && lane == 0) {
+    atomicAdd(&s_stats[kStatBlocks], c_blocks);
+    atomicAdd(&s_stats[kStatActive], c_active);
+    atomicAdd(&s_stats[kStatPrefix], c_app);
+    atomicAdd(&s_stats[kStatS1], c_app);
+    atomicAdd(&s_stats[kStatS4Budget], c_app);
+  }
+  if constexpr (MODE != 0) {
+    if (lane == 0) s_st.n[wave] = min(fill, (uint32_t)kMmaWaveCap);
+    __syncthreads();
+    for (int w = 0; w < 4; ++w)
+      for (uint32_t i = tid; i < s_st.n[w]; i += 256) atomicAdd(&s_st.cnt[s_st.q[w * kMmaWaveCap + i]], 1u);
+    __syncthreads();
+    if (tid < nq) {
+      const uint32_t c = s_st.cnt[tid];
+      s_st.base[tid] = c ? atomicAdd(a.seg_count + (uint64_t)(q0 + tid) * a.nseg + seg, c) : 0u;
+      s_st.cnt[tid] = 0u;
+    }
+    if (a.stats && tid < kStatCount && s_stats[tid]) {
+      const uint32_t copy = (blockIdx.x + blockIdx.y * gridDim.x) % (uint32_t)kStatCopies;
+      atomicAdd(a.stats + copy * kStatCount + tid, (unsigned long long)s_stats[tid]);
+    }
+    __syncthreads();
+    for (int w = 0; w < 4; ++w)
+      for (uint32_t i0 = tid; i0 < s_st.n[w]; i0 += 256) {
+        const uint32_t i = (uint32_t)w * kMmaWaveCap + i0;
+        const uint32_t qi = s_st.q[i];
+        const uint32_t g = s_st.base[qi] + atomicAdd(&s_st.cnt[qi], 1u);
+        if (g < a.seg_cap) {
+          const uint64_t e = ((uint64_t)(q0 + qi) * a.nseg + seg) * a.seg_cap + g;
+          a.cand_score[e] = s_st.u[i];
+          a.cand_lower[e] = s_st.l[i];
+          a.cand_row[e] = s_st.row[i];
+        }
+      }
+  }
+}
+
+// The reference's full score of slot `row` for plan p (scan.rs:453-634, every
+// stage run, the f32 operations of eval_block in their order).  False when a
+// stage bound of the reference is NaN: NaN >= tau is false, so the reference
+// drops such a vector before it is pushed.
+__device__ bool exact_full(const FinishArgs& a, const mrl_query_plan* p, uint32_t row, const float* lut,
+                           const float* w1, const float* w4, float* out) {
+  const uint64_t b = row >> 6;
+  const uint32_t v = row & 63u;
+  const uint8_t* blk = a.idx + b * kBlockBytes;
+  const uint16_t* m16 = reinterpret_cast<const uint16_t*>(blk);
+  LaneBlock m;
+  m.scale = h2f(m16[kDevScale / 2 + v]);
+  m.offset = h2f(m16[kDevOffset / 2 + v]);
+  m.tail = h2f(m16[kDevTail / 2 + v]);
+  const uint32_t flags = blk[kDevFlags + v];
+  const uint4* nibq = reinterpret_cast<const uint4*>(blk + kDevNibbles) + 2u * v;
+  const uint4 n0 = nibq[0], n1 = nibq[1];
+  m.nib[0] = n0.x;
+  m.nib[1] = n0.y;
+  m.nib[2] = n0.z;
+  m.nib[3] = n0.w;
+  m.nib[4] = n1.x;
+  m.nib[5] = n1.y;
+  m.nib[6] = n1.z;
+  m.nib[7] = n1.w;
+  const float t = fmaxf(m.tail, 0.0f);
+  const float rho = (float)flags / 255.0f;
+  const float rc = rho > 1.0f ? 1.0f : rho;
+  const float mid_n = fmaxf(sqrtf(fmaxf(1.0f - rc * rc, 0.0f)) * t, 1e-6f);
+  const float high_n = fmaxf(rho * t, 0.0f);
+  const float acc = prefix_acc(m, lut);
+  const bool eden = p->prefix_codec == MRL_PREFIX_EDEN_PROD;
+  const float prefix_ip = eden ? p->eden_mean_ip + m.scale * acc : acc * m.scale + m.offset * p->prefix_sum;
+  const float alpha = a.sp.alpha;
+  const float ub1 = prefix_ip + alpha * (p->q_mid_norm * mid_n + p->q_tail_norm * high_n);  // scan.rs:499-505
+  if (ub1 != ub1) return false;
+  float score = prefix_ip;
+  // Stage: mid-band 1-bit IP (scan.rs:553-568)
+  const uint4 r1 = a.rows1[row];
+  const uint32_t bits1[4] = {r1.x, r1.y, r1.z, r1.w};
+  const float s1 = row_sum<4>(p->rabitq_base, bits1, w1);
+  score = score + s1 * mid_n;
+  const float ub2 = score + alpha * p->q_after_s1 * high_n;  // scan.rs:572-584
+  if (ub2 != ub2) return false;
+  if (a.sp.strata == MRL_STRATA_FULL64B) {
+    const float hn = fmaxf(high_n, 1e-6f);
+    if (p->has_tail_fold && p->s4_abs_budget > 0.0f) {  // scan.rs:587-607
+      const float ub3 = score + alpha * hn * a.sp.w_s4 * p->s4_abs_budget;
+      if (ub3 != ub3) return false;
+    }
+    if (p->has_tail_fold) {  // scan.rs:610-634
+      const uint2 r4 = a.rows4[row];
+      const uint32_t bits4[2] = {r4.x, r4.y};
+      const float s4 = row_sum<2>(p->tail_fold_base, bits4, w4);
+      score = score + s4 * hn * a.sp.w_s4;
+    }
+  }
+  *out = score;
+  return true;
+}
+
+constexpr int kFinThreads = 1024;
+constexpr int kFinCap = 8192;
+
+// One query: the K-th best lower bound among its candidates (exact radix
+// select on the order-preserving key), the candidates whose upper bound
+// reaches it, their exact scores, and those at or above the final floor
+// written back as the query's candidate list (segments in order) for
+// k_select.  A query whose candidate list overflowed, whose operands were
+// not finite, or with more than kFinCap such candidates gets a count past
+// the segment room, which k_select reports as an overflow (dense re-run).
+__global__ __launch_bounds__(kFinThreads) void k_finish(FinishArgs a) {
+  __shared__ __align__(16) float s_lut[1024];
+  __shared__ __align__(16) float s_w1[128];
+  __shared__ __align__(16) float s_w4[64];
+  __shared__ uint32_t s_frow[kFinCap];
+  __shared__ uint32_t s_hist[2048];
+  __shared__ uint32_t s_off[kSegs + 1];
+  __shared__ uint32_t s_coff[kSegs + 1];
+  __shared__ uint32_t s_ws[32];
+  __shared__ uint32_t s_misc[8];
+
+  const uint32_t q = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint32_t K = a.k;
+  uint32_t* qcount = a.seg_count + (uint64_t)q * a.nseg;
+  const uint32_t c_own = tid < (int)a.nseg ? qcount[tid] : 0u;
+  const bool ok = a.mma_consts[(uint64_t)q * kMcCount + kMcOk] != 0.0f;
+  const float floor_t = a.tau_final ? a.tau_final[q] : -INFINITY;
+  if (tid < 8) s_misc[tid] = 0u;
+  __syncthreads();
+  if (c_own > a.seg_cap || !ok) atomicOr(&s_misc[7], 1u);
+  seg_offsets(c_own, a.nseg, a.seg_cap, s_off, s_coff, s_ws);
+  if (s_misc[7]) {
+    if (tid == 0) qcount[0] = a.seg_cap + 1u;
+    return;
+  }
+  const uint32_t total = s_off[a.nseg];
+  const float* qd = a.luts + (uint64_t)q * kQData;
+  for (int i = tid; i < 1024; i += kFinThreads) s_lut[i] = qd[kQdLut + i];
+  if (tid < 128) s_w1[tid] = qd[kQdW1 + tid];
+  if (tid < 64) s_w4[tid] = qd[kQdW4 + tid];
+  const uint64_t qbase = (uint64_t)q * a.nseg * a.seg_cap;
+
+  // K-th largest lower-bound key (all candidates when there are at most K)
+  uint32_t tkey = 0u;
+  if (total > K) {
+    const CandView vl{a.cand_lower + qbase, a.cand_row + qbase, a.seg_cap, a.nseg, s_off, s_coff};
+    const int shifts[3] = {21, 10, 0};
+    const int widths[3] = {11, 11, 10};
+    uint32_t prefix = 0, need = K;
+    for (int pass = 0; pass < 3; ++pass) {
+      const int sh = shifts[pass], wd = widths[pass];
+      const uint32_t nb = 1u << wd;
+      for (int i = tid; i < 2048; i += kFinThreads) s_hist[i] = 0u;
+      __syncthreads();
+      for_each_cand<16>(vl, [&](float sc, uint32_t) {
+        const uint32_t key = score_key(sc);
+        if (pass == 0 || (key >> (sh + wd)) == prefix) atomicAdd(&s_hist[(key >> sh) & (nb - 1)], 1u);
+      });
+      __syncthreads();
+      find_boundary(s_hist, nb, need, true, &s_misc[3], &s_misc[4], s_ws);
+      __syncthreads();
+      need -= s_misc[4];
+      prefix = (prefix << wd) | s_misc[3];
+      __syncthreads();
+    }
+    tkey = prefix;
+  }
+  // candidates whose upper bound reaches it
+  const CandView vu{a.cand_score + qbase, a.cand_row + qbase, a.seg_cap, a.nseg, s_off, s_coff};
+  for_each_pair(vu, [&](float u, uint32_t row, uint32_t) {
+    if (score_key(u) >= tkey) {
+      const uint32_t slot = atomicAdd(&s_misc[2], 1u);
+      if (slot < (uint32_t)kFinCap) s_frow[slot] = row;
+    }
+  });
+  __syncthreads();
+  const uint32_t nf = s_misc[2];
+  if (nf > (uint32_t)kFinCap) {
+    if (tid == 0) qcount[0] = a.seg_cap + 1u;
+    return;
+  }
+  // exact scores; every read of the candidate lists is done, so they can be rewritten
+  const mrl_query_plan* p = a.plans + q;
+  for (uint32_t i = tid; i < nf; i += kFinThreads) {
+    const uint32_t row = s_frow[i];
+    float sc;
+    if ((uint64_t)(row >> 6) >= a.n_blocks) continue;  // rows come from this scan's appends
+    if (!exact_full(a, p, row, s_lut, s_w1, s_w4, &sc)) continue;
+    if (sc != sc) {
+      atomicOr(a.err + q, 1u);
+      continue;
+    }
+    if (!(sc >= floor_t)) continue;
+    const uint32_t slot = atomicAdd(&s_misc[5], 1u);
+    a.cand_score[qbase + slot] = sc;
+    a.cand_row[qbase + slot] = row;
+  }
+  __syncthreads();
+  const uint32_t n_out = s_misc[5];
+  if (tid < (int)a.nseg) {
+    const uint32_t lo = (uint32_t)tid * a.seg_cap;
+    qcount[tid] = n_out > lo ? min(n_out - lo, a.seg_cap) : 0u;
+  }
+  if (a.stats && tid == 0 && n_out) {
+    const uint32_t copy = q % (uint32_t)kStatCopies;
+    atomicAdd(a.stats + copy * kStatCount + kStatPushed, (unsigned long long)n_out);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device,
@@ -2244,6 +2941,54 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const Launch
 hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev) {
   if (n_q == 0) return hipSuccess;
   launch(k_select, dim3(n_q), dim3(kSelThreads), s, ev, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_mma_prep(const MmaPrepArgs& a, hipStream_t s, const LaunchEvents& ev) {
+  if (a.n_q == 0) return hipSuccess;
+  launch(k_mma_prep, dim3(a.n_q), dim3(64), s, ev, a);
+  return hipGetLastError();
+}
+
+// Workgroups along x of an MFMA scan launch: one round of resident
+// workgroups over the query chunks, at most one block per wave.
+uint32_t mma_scan_grid(const ScanArgs& a) {
+  const uint32_t chunks = (a.n_q + kMmaQ - 1) / kMmaQ;
+  static const uint32_t res = resident_groups(k_scan_mma<2, 1>);
+  uint32_t grid = (a.n_pos + 4) / 4;
+  uint32_t max_grid = res / chunks;
+  if (max_grid < 1) max_grid = 1;
+  if (grid > max_grid) grid = max_grid;
+  return grid;
+}
+
+hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const LaunchEvents& ev) {
+  if (a.n_pos == 0 || a.n_q == 0) return hipSuccess;
+  const dim3 g(mma_scan_grid(a), (a.n_q + kMmaQ - 1) / kMmaQ);
+  const bool two = a.n_q > 32;  // one 32-query tile per wave suffices up to 32 queries
+  if (mode == 0) {
+    if (two) launch(k_scan_mma<2, 0>, g, dim3(256), s, ev, a);
+    else launch(k_scan_mma<1, 0>, g, dim3(256), s, ev, a);
+  } else if (mode == 1) {
+    if (two) launch(k_scan_mma<2, 1>, g, dim3(256), s, ev, a);
+    else launch(k_scan_mma<1, 1>, g, dim3(256), s, ev, a);
+  } else {
+    if (two) launch(k_scan_mma<2, 2>, g, dim3(256), s, ev, a);
+    else launch(k_scan_mma<1, 2>, g, dim3(256), s, ev, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_mma_floors(const uint32_t* hist, uint32_t n_q, uint32_t rank, uint32_t safe_rank, float* floor_out,
+                             float* safe_out, hipStream_t s, const LaunchEvents& ev) {
+  if (n_q == 0) return hipSuccess;
+  launch(k_mma_floors, dim3(n_q), dim3(64), s, ev, hist, rank, safe_rank, floor_out, safe_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_finish(const FinishArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev) {
+  if (n_q == 0) return hipSuccess;
+  launch(k_finish, dim3(n_q), dim3(kFinThreads), s, ev, a);
   return hipGetLastError();
 }
 

@@ -129,7 +129,8 @@ class KernelTimeC(C.Structure):
     ]
 
 
-KERNEL_PLAN, KERNEL_SCAN, KERNEL_SELECT, KERNEL_THRESH, KERNEL_RERANK, KERNEL_RERANK_SORT = 0, 1, 2, 3, 4, 5
+(KERNEL_PLAN, KERNEL_SCAN, KERNEL_SELECT, KERNEL_THRESH, KERNEL_RERANK, KERNEL_RERANK_SORT, KERNEL_FINISH,
+ KERNEL_MMA_PREP) = 0, 1, 2, 3, 4, 5, 6, 7
 
 
 class SynthSpecC(C.Structure):
