@@ -2310,30 +2310,28 @@ __global__ __launch_bounds__(64) void k_mma_floors(const uint32_t* hist, uint32_
   }
 }
 
-// One block's per-lane inputs for both 32-vector tiles: lane l serves vector
-// 32 h + l % 32, half l / 32 of the K range.
+// One 32-vector tile's per-lane inputs: lane l serves vector 32 h + l % 32
+// of block b, half l / 32 of the K range.
 struct MmaRaw {
-  uint4 lev[2];      // level words 4 kh .. 4 kh + 3
-  uint2 r1[2];       // S1 row dwords 2 kh, 2 kh + 1
-  uint32_t r4[2];    // S4 row dword kh
-  uint32_t meta[2];  // scale | offset << 16 (f16 bits)
-  uint32_t tf[2];    // tail_norm | flags << 16
-  uint32_t hdr;      // lanes 0..3: header dwords 0, 1, 4, 5
+  uint4 lev;      // level words 4 kh .. 4 kh + 3
+  uint2 r1;       // S1 row dwords 2 kh, 2 kh + 1
+  uint32_t r4;    // S4 row dword kh
+  uint32_t meta;  // scale | offset << 16 (f16 bits)
+  uint32_t tf;    // tail_norm | flags << 16
+  uint32_t hdr;   // lanes 0..3: header dwords 0, 1, 4, 5
 };
 
-__device__ __forceinline__ MmaRaw mma_load(const uint8_t* blk, const uint4* rows1, const uint2* rows4, uint64_t b) {
-  const uint32_t lane = __lane_id(), kh = lane >> 5, vl = lane & 31u;
+__device__ __forceinline__ MmaRaw mma_load(const uint8_t* idx, const uint4* rows1, const uint2* rows4, uint64_t b,
+                                           uint32_t h) {
+  const uint32_t lane = __lane_id(), kh = lane >> 5, v = 32u * h + (lane & 31u);
+  const uint8_t* blk = idx + b * kBlockBytes;
   const uint16_t* m16 = reinterpret_cast<const uint16_t*>(blk);
   MmaRaw r;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint32_t v = 32u * h + vl;
-    r.lev[h] = *reinterpret_cast<const uint4*>(blk + kDevNibbles + 32u * v + 16u * kh);
-    r.r1[h] = reinterpret_cast<const uint2*>(rows1 + b * 64u + v)[kh];
-    r.r4[h] = reinterpret_cast<const uint32_t*>(rows4 + b * 64u + v)[kh];
-    r.meta[h] = (uint32_t)m16[kDevScale / 2 + v] | ((uint32_t)m16[kDevOffset / 2 + v] << 16);
-    r.tf[h] = (uint32_t)m16[kDevTail / 2 + v] | ((uint32_t)blk[kDevFlags + v] << 16);
-  }
+  r.lev = *reinterpret_cast<const uint4*>(blk + kDevNibbles + 32u * v + 16u * kh);
+  r.r1 = reinterpret_cast<const uint2*>(rows1 + b * 64u + v)[kh];
+  r.r4 = reinterpret_cast<const uint32_t*>(rows4 + b * 64u + v)[kh];
+  r.meta = (uint32_t)m16[kDevScale / 2 + v] | ((uint32_t)m16[kDevOffset / 2 + v] << 16);
+  r.tf = (uint32_t)m16[kDevTail / 2 + v] | ((uint32_t)blk[kDevFlags + v] << 16);
   const uint32_t hw = lane < 2 ? lane : (lane < 4 ? lane + 2 : 0);
   r.hdr = reinterpret_cast<const uint32_t*>(blk)[hw];
   return r;
@@ -2371,7 +2369,11 @@ __device__ __forceinline__ void mma_append(MmaStaging& st, const ScanArgs& a, in
     st.l[e] = l;
     st.q[e] = (uint8_t)qi;
   } else {
-    const uint64_t sq = (uint64_t)(q0 + qi) * a.nseg + seg;
+    // (the query index passes through an empty asm so the compiler cannot
+    // hoist this rare path's addresses out of the scan loop into registers)
+    uint32_t qq = q0 + qi;
+    asm volatile("" : "+v"(qq));
+    const uint64_t sq = (uint64_t)qq * a.nseg + seg;
     const uint32_t g = atomicAdd(a.seg_count + sq, 1u);
     if (g < a.seg_cap) {
       const uint64_t i = sq * a.seg_cap + g;
@@ -2383,13 +2385,14 @@ __device__ __forceinline__ void mma_append(MmaStaging& st, const ScanArgs& a, in
 }
 
 // One pass of the MFMA-bounded scan.  Workgroup = 4 waves over the same 64
-// queries (blockIdx.y), wave = one block at a time, each block as two
-// 32-vector tiles; NQT 32-query tiles per wave, their operands held in
-// registers.  MODE 0: sampling pass, the lower bounds of every active pair
-// go into the query's histogram; 1: final pass, pairs with U >= the floor in
-// a.tau are appended; 2: single pass, every active pair is appended.
+// queries (blockIdx.y); a wave takes one 32-vector tile (half a block) at a
+// time, items i = first + k * stride with block (i / 2) << shift and half
+// i % 2; NQT 32-query tiles per wave, their operands held in registers.
+// MODE 0: sampling pass, the lower bounds of every active pair go into the
+// query's histogram; 1: final pass, pairs with U >= the floor in a.tau are
+// appended; 2: single pass, every active pair is appended.
 template <int NQT, int MODE>
-__global__ __launch_bounds__(256) void k_scan_mma(ScanArgs a) {
+__global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
   __shared__ uint32_t s_tab[256];
   __shared__ float s_flag[512];      // rho = f / 255, then sqrt(max(1 - rho^2, 0))
   __shared__ __align__(16) float s_c[kMmaQ];
@@ -2403,12 +2406,13 @@ __global__ __launch_bounds__(256) void k_scan_mma(ScanArgs a) {
   const uint32_t q0 = blockIdx.y * kMmaQ;
   const int nq = (int)min((uint32_t)kMmaQ, a.n_q - q0);
 
+  const uint32_t n_items = 2u * a.n_pos;
   const uint32_t stride = gridDim.x * 4 - 1;  // odd: see k_scan
   const uint32_t first = blockIdx.x * 4 + wave;
-  const uint32_t n_pos = first < stride ? a.n_pos : 0u;
-  uint32_t b_cur = first << a.shift;
+  const uint32_t n_it = first < stride ? n_items : 0u;
+  uint32_t it_cur = first;
   MmaRaw cur{};
-  if (first < n_pos) cur = mma_load(a.idx + (uint64_t)b_cur * kBlockBytes, a.rows1, a.rows4, b_cur);
+  if (first < n_it) cur = mma_load(a.idx, a.rows1, a.rows4, (uint64_t)(first >> 1) << a.shift, first & 1u);
 
   {  // byte -> (f16 cb[low nibble], f16 cb[high nibble])
     const mrl_query_plan* p0 = a.plans + q0;
@@ -2428,7 +2432,7 @@ __global__ __launch_bounds__(256) void k_scan_mma(ScanArgs a) {
     float C = -INFINITY, qk[8] = {0.0f, 1.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     if (qi < nq) {
       const float* mc = a.mma_consts + (uint64_t)(q0 + qi) * kMcCount;
-      const float s = mc[kMcS], mean = mc[kMcMean], R = mc[kMcR];
+      const float sc = mc[kMcS], mean = mc[kMcMean], R = mc[kMcR];
       const bool ok = mc[kMcOk] != 0.0f;
       float tau = 0.0f;
       if (MODE == 1) {
@@ -2436,7 +2440,7 @@ __global__ __launch_bounds__(256) void k_scan_mma(ScanArgs a) {
         if (!(tau >= -R)) tau = -R;  // no floor: below every score of a vector with safe magnitudes
       }
       const float e0q = mc[kMcE0] + fabsf(tau) * (1.0f / 65536.0f);
-      if (ok) C = s * ((mean - tau) + (MODE == 0 ? -e0q : e0q));
+      if (ok) C = sc * ((mean - tau) + (MODE == 0 ? -e0q : e0q));
       qk[0] = tau;
       qk[1] = mc[kMcInvS];
       qk[2] = mc[kMcEP];
@@ -2470,20 +2474,11 @@ __global__ __launch_bounds__(256) void k_scan_mma(ScanArgs a) {
   const uint32_t seg = blockIdx.x % a.nseg;
   uint32_t c_blocks = 0, c_active = 0, c_app = 0;
   uint32_t fill = 0;  // entries of this wave's staging region (wave-uniform)
-  // bit 16 t + r: register r of tile t belongs to a query of the batch with usable operands
-  uint32_t okbits = 0;
-#pragma unroll
-  for (int t = 0; t < NQT; ++t)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
-      if (qi < nq && s_qk[qi][7] != 0.0f) okbits |= 1u << (16 * t + r);
-    }
 
-  for (uint32_t pos = first; pos < n_pos; pos += stride) {
-    const uint32_t b_nxt = pos + stride < n_pos ? (pos + stride) << a.shift : b_cur;
-    const MmaRaw nxt = mma_load(a.idx + (uint64_t)b_nxt * kBlockBytes, a.rows1, a.rows4, b_nxt);
-    const uint32_t b = b_cur;
+  for (uint32_t it = first; it < n_it; it += stride) {
+    const uint32_t it_nxt = it + stride < n_it ? it + stride : it_cur;
+    const MmaRaw nxt = mma_load(a.idx, a.rows1, a.rows4, (uint64_t)(it_nxt >> 1) << a.shift, it_nxt & 1u);
+    const uint32_t b = (it_cur >> 1) << a.shift, h = it_cur & 1u;
     const uint32_t min_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 0);
     const uint32_t max_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 1);
     const uint64_t tomb = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(cur.hdr, 3) << 32) |
@@ -2493,146 +2488,155 @@ __global__ __launch_bounds__(256) void k_scan_mma(ScanArgs a) {
       if (a.sp.has_lo && max_ts < a.sp.lo) skip = true;
       if (a.sp.has_hi && min_ts > a.sp.hi) skip = true;
     }
-    const uint64_t active = ~tomb;
+    const uint32_t active = (uint32_t)(~tomb >> (32u * h));  // this tile's slots
     if (!skip && active != 0) {
-      c_blocks += (uint32_t)nq;
-      c_active += (uint32_t)nq * (uint32_t)__popcll(active);
+      if (h == 0) {
+        c_blocks += (uint32_t)nq;
+        c_active += (uint32_t)nq * (uint32_t)__popcll(~tomb);
+      }
+      const uint32_t v = 32u * h + vl;
+      const bool act = (active >> vl) & 1u;
+      // meta (block.rs:61-99); flags / 255 and sqrt(max(1 - rho^2, 0)) from the context's tables
+      const uint32_t sc_b = cur.meta & 0xffffu, of_b = cur.meta >> 16;
+      const float m_scale = h2f((uint16_t)sc_b), m_offset = h2f((uint16_t)of_b);
+      const float tn = fmaxf(h2f((uint16_t)(cur.tf & 0xffffu)), 0.0f);
+      const uint32_t fl = cur.tf >> 16;
+      const float mid_n = fmaxf(s_flag[256 + fl] * tn, 1e-6f);
+      const float hn = fmaxf(fmaxf(s_flag[fl] * tn, 0.0f), 1e-6f);
+      const bool safe = fabsf(m_scale) <= kMmaSafe && mid_n <= kMmaSafe && hn <= kMmaSafe &&
+                        fabsf(m_offset) <= kMmaSafe;
+      mma_f16 acc[NQT];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint32_t v = 32u * h + vl;
-        const bool act = (active >> v) & 1ull;
-        // meta (block.rs:61-99)
-        const uint32_t sc_b = cur.meta[h] & 0xffffu, of_b = cur.meta[h] >> 16;
-        const float m_scale = h2f((uint16_t)sc_b), m_offset = h2f((uint16_t)of_b);
-        // (flags / 255 and sqrt(max(1 - rho^2, 0)) from the context's tables)
-        const float tn = fmaxf(h2f((uint16_t)(cur.tf[h] & 0xffffu)), 0.0f);
-        const uint32_t fl = cur.tf[h] >> 16;
-        const float mid_n = fmaxf(s_flag[256 + fl] * tn, 1e-6f);
-        const float hn = fmaxf(fmaxf(s_flag[fl] * tn, 0.0f), 1e-6f);
-        const bool safe = fabsf(m_scale) <= kMmaSafe && mid_n <= kMmaSafe && hn <= kMmaSafe &&
-                          fabsf(m_offset) <= kMmaSafe;
-        mma_f16 acc[NQT];
+      for (int t = 0; t < NQT; ++t) {
 #pragma unroll
-        for (int t = 0; t < NQT; ++t) {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const float4 c4 = *reinterpret_cast<const float4*>(&s_c[32 * t + 8 * g + 4 * (int)kh]);
-            acc[t][4 * g + 0] = c4.x;
-            acc[t][4 * g + 1] = c4.y;
-            acc[t][4 * g + 2] = c4.z;
-            acc[t][4 * g + 3] = c4.w;
-          }
+        for (int g = 0; g < 4; ++g) {
+          const float4 c4 = *reinterpret_cast<const float4*>(&s_c[32 * t + 8 * g + 4 * (int)kh]);
+          acc[t][4 * g + 0] = c4.x;
+          acc[t][4 * g + 1] = c4.y;
+          acc[t][4 * g + 2] = c4.z;
+          acc[t][4 * g + 3] = c4.w;
         }
-        // prefix: scale * cb[level], 8 dims per step
-        const mma_h2 sc2 = __builtin_bit_cast(mma_h2, sc_b | (sc_b << 16));
-        const uint32_t lw[4] = {cur.lev[h].x, cur.lev[h].y, cur.lev[h].z, cur.lev[h].w};
-        uint32_t tv[16];  // all 16 table reads go out before the first use
+      }
+      // prefix: scale * cb[level], 8 dims per step; all 16 table reads go out first
+      const mma_h2 sc2 = __builtin_bit_cast(mma_h2, sc_b | (sc_b << 16));
+      const uint32_t lw[4] = {cur.lev.x, cur.lev.y, cur.lev.z, cur.lev.w};
+      uint32_t tv[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) tv[i] = s_tab[(lw[i >> 2] >> (8 * (i & 3))) & 255u];
+      for (int i = 0; i < 16; ++i) tv[i] = s_tab[(lw[i >> 2] >> (8 * (i & 3))) & 255u];
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
+      for (int st = 0; st < 4; ++st) {
+        uint32_t d[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          d[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(mma_h2, tv[4 * st + j]) * sc2);
+        const uint4 bo = make_uint4(d[0], d[1], d[2], d[3]);
+#pragma unroll
+        for (int t = 0; t < NQT; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][st]), as_h8(bo), acc[t], 0, 0, 0);
+      }
+      // S1: +-mid_n / 2 by bit
+      const uint32_t hp1 = f16_bits(0.5f * mid_n) * 0x10001u;
+#pragma unroll
+      for (int tt = 0; tt < 8; ++tt) {
+        const uint32_t nx = ~(tt < 4 ? cur.r1.x : cur.r1.y);
+        const int jb = 4 * (tt & 3);
+        uint32_t d[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) d[j] = hp1 | ((nx << (15 - jb - j)) & 0x80008000u);
+        const uint4 bo = make_uint4(d[0], d[1], d[2], d[3]);
+#pragma unroll
+        for (int t = 0; t < NQT; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][4 + tt]), as_h8(bo), acc[t], 0, 0, 0);
+      }
+      // S4: +-hn w_s4 / 2 by bit
+      if (ws4 != 0.0f) {
+        const uint32_t hp4 = f16_bits(0.5f * hn * ws4) * 0x10001u;
+        const uint32_t nx = ~cur.r4;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
           uint32_t d[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const mma_h2 c2 = __builtin_bit_cast(mma_h2, tv[4 * st + j]);
-            d[j] = __builtin_bit_cast(uint32_t, c2 * sc2);
-          }
+          for (int j = 0; j < 4; ++j) d[j] = hp4 | ((nx << (15 - 4 * tt - j)) & 0x80008000u);
           const uint4 bo = make_uint4(d[0], d[1], d[2], d[3]);
 #pragma unroll
           for (int t = 0; t < NQT; ++t)
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][st]), as_h8(bo), acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][12 + tt]), as_h8(bo), acc[t], 0, 0, 0);
         }
-        // S1: +-mid_n / 2 by bit
-        const uint32_t hp1 = f16_bits(0.5f * mid_n) * 0x10001u;
-#pragma unroll
-        for (int tt = 0; tt < 8; ++tt) {
-          const uint32_t nx = ~(tt < 4 ? cur.r1[h].x : cur.r1[h].y);
-          const int jb = 4 * (tt & 3);
-          uint32_t d[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) d[j] = hp1 | ((nx << (15 - jb - j)) & 0x80008000u);
-          const uint4 bo = make_uint4(d[0], d[1], d[2], d[3]);
-#pragma unroll
-          for (int t = 0; t < NQT; ++t)
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][4 + tt]), as_h8(bo), acc[t], 0, 0, 0);
+      }
+      {  // error columns and offset * prefix_sum
+        uint4 bo = make_uint4(0u, 0u, 0u, 0u);
+        if (kh == 0) {
+          bo.x = (sc_b & 0x7fffu) | (f16_bits(mid_n) << 16);
+          bo.y = f16_bits(hn) | ((of_b & 0x7fffu) << 16);
+          bo.z = of_b;
         }
-        // S4: +-hn w_s4 / 2 by bit
-        if (ws4 != 0.0f) {
-          const uint32_t hp4 = f16_bits(0.5f * hn * ws4) * 0x10001u;
-          const uint32_t nx = ~cur.r4[h];
 #pragma unroll
-          for (int tt = 0; tt < 4; ++tt) {
-            uint32_t d[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) d[j] = hp4 | ((nx << (15 - 4 * tt - j)) & 0x80008000u);
-            const uint4 bo = make_uint4(d[0], d[1], d[2], d[3]);
-#pragma unroll
-            for (int t = 0; t < NQT; ++t)
-              acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][12 + tt]), as_h8(bo), acc[t], 0, 0, 0);
-          }
-        }
-        {  // error columns and offset * prefix_sum
-          uint4 bo = make_uint4(0u, 0u, 0u, 0u);
-          if (kh == 0) {
-            bo.x = (sc_b & 0x7fffu) | (f16_bits(mid_n) << 16);
-            bo.y = f16_bits(hn) | ((of_b & 0x7fffu) << 16);
-            bo.z = of_b;
-          }
-#pragma unroll
-          for (int t = 0; t < NQT; ++t)
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][kMmaSteps - 1]), as_h8(bo), acc[t], 0, 0,
-                                                            0);
-        }
-        // Register r of tile t holds query 32 t + 8 (r / 4) + 4 kh + r % 4.
-        if constexpr (MODE == 0) {
-          if (act && safe) {
-#pragma unroll
-            for (int t = 0; t < NQT; ++t)
-#pragma unroll
-              for (int r = 0; r < 16; ++r) {
-                const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
-                if (qi < nq && s_qk[qi][7] != 0.0f) {
-                  const float L = acc[t][r] * s_qk[qi][1];
-                  atomicAdd(a.hist + (uint64_t)(q0 + qi) * kHistBins + hist_bin(L), 1u);
-                }
-              }
-          }
-        } else {
-          // Absent queries and those with unusable operands start at C = -inf,
-          // so acc >= 0 only holds for pairs of the batch.
-          const uint32_t row = b * 64u + v;
-          const float eb = fabsf(m_scale), eo = fabsf(m_offset);
+        for (int t = 0; t < NQT; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][kMmaSteps - 1]), as_h8(bo), acc[t], 0, 0, 0);
+      }
+      // Register r of tile t holds query 32 t + 8 (r / 4) + 4 kh + r % 4.
+      if constexpr (MODE == 0) {
+        if (act && safe) {
 #pragma unroll
           for (int t = 0; t < NQT; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const bool forced = MODE == 2 || !safe;
-              const bool okq = (okbits >> (16 * t + r)) & 1u;
-              const uint64_t pm = ballot(act && (acc[t][r] >= 0.0f || (forced && okq)));
-              if (pm == 0) continue;
               const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
-              float U = INFINITY, L = -INFINITY;
-              if (safe) {
-                const float4 k0 = *reinterpret_cast<const float4*>(&s_qk[qi][0]);
-                const float4 k1 = *reinterpret_cast<const float4*>(&s_qk[qi][4]);
-                // k0 = {tau, 1/s, eP, e1}, k1 = {e4, eO, e0, ok}
-                const float tau = k0.x;
-                const float u0 = tau + acc[t][r] * k0.y;
-                const float E = eb * k0.z + mid_n * k0.w + hn * k1.x + eo * k1.y + k1.z;
-                const float mg = (fabsf(u0) + fabsf(tau)) * (1.0f / 4194304.0f);
-                U = u0 + mg;
-                L = (u0 - 2.0f * E * (1.0f + 1.0f / 1048576.0f)) - mg;
-                if (!(U == U)) U = INFINITY;
-                if (!(L == L)) L = -INFINITY;
+              if (qi < nq && s_qk[qi][7] != 0.0f) {
+                const float L = acc[t][r] * s_qk[qi][1];
+                uint32_t qq = q0 + qi;  // through an empty asm: no hoisted per-register addresses
+                asm volatile("" : "+v"(qq));
+                atomicAdd(a.hist + (uint64_t)qq * kHistBins + hist_bin(L), 1u);
               }
-              c_app += (uint32_t)__popcll(pm);
-              mma_append(s_st, a, wave, &fill, q0, (uint32_t)qi, seg, pm, U, L, row);
             }
         }
+      } else {
+        // Absent queries and those with unusable operands start at C = -inf,
+        // so acc >= 0 only holds for pairs of the batch.  A slot whose meta is
+        // beyond the operand range is a candidate of every query of the
+        // batch: its registers of present queries are raised to +inf (MODE 2
+        // takes every present query's register).
+        if (MODE == 2 || ballot(act && !safe) != 0) {
+#pragma unroll
+          for (int t = 0; t < NQT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
+              const bool okq = qi < nq && s_qk[qi][7] != 0.0f;
+              if (MODE == 2) acc[t][r] = okq ? fmaxf(acc[t][r], 0.0f) : -INFINITY;
+              else if (!safe && okq) acc[t][r] = INFINITY;
+            }
+        }
+        const uint32_t row = b * 64u + v;
+        const float eb = fabsf(m_scale), eo = fabsf(m_offset);
+#pragma unroll
+        for (int t = 0; t < NQT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const uint64_t pm = ballot(act && acc[t][r] >= 0.0f);
+            if (pm == 0) continue;
+            const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
+            float U = INFINITY, L = -INFINITY;
+            if (safe) {
+              const float4 k0 = *reinterpret_cast<const float4*>(&s_qk[qi][0]);
+              const float4 k1 = *reinterpret_cast<const float4*>(&s_qk[qi][4]);
+              // k0 = {tau, 1/s, eP, e1}, k1 = {e4, eO, e0, ok}
+              const float tau = k0.x;
+              const float u0 = tau + acc[t][r] * k0.y;
+              const float E = eb * k0.z + mid_n * k0.w + hn * k1.x + eo * k1.y + k1.z;
+              const float mg = (fabsf(u0) + fabsf(tau)) * (1.0f / 4194304.0f);
+              U = u0 + mg;
+              L = (u0 - 2.0f * E * (1.0f + 1.0f / 1048576.0f)) - mg;
+              if (!(U == U)) U = INFINITY;
+              if (!(L == L)) L = -INFINITY;
+            }
+            c_app += (uint32_t)__popcll(pm);
+            mma_append(s_st, a, wave, &fill, q0, (uint32_t)qi, seg, pm, U, L, row);
+          }
       }
     }
     cur = nxt;
-    b_cur = b_nxt;
+    it_cur = it_nxt;
   }
   if (a.stats && lane == 0) {
     atomicAdd(&s_stats[kStatBlocks], c_blocks);
@@ -2955,7 +2959,7 @@ hipError_t launch_mma_prep(const MmaPrepArgs& a, hipStream_t s, const LaunchEven
 uint32_t mma_scan_grid(const ScanArgs& a) {
   const uint32_t chunks = (a.n_q + kMmaQ - 1) / kMmaQ;
   static const uint32_t res = resident_groups(k_scan_mma<2, 1>);
-  uint32_t grid = (a.n_pos + 4) / 4;
+  uint32_t grid = (2u * a.n_pos + 4) / 4;  // items: two 32-vector tiles per block
   uint32_t max_grid = res / chunks;
   if (max_grid < 1) max_grid = 1;
   if (grid > max_grid) grid = max_grid;
