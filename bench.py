@@ -128,7 +128,7 @@ def main():
     groups = {}
     for i in range(min(nrec.value, cap)):
         r = kt[i]
-        key = ({0: "plan", 1: "scan", 2: "select", 3: "thresh", 6: "finish", 7: "mma_prep"}[r.kind], r.pass_)
+        key = ({0: "plan", 1: "scan", 2: "select", 3: "thresh", 6: "finish", 7: "mma_prep", 8: "exact"}[r.kind], r.pass_)
         g = groups.setdefault(key, {"ms": [], "blocks": []})
         g["ms"].append(r.ms)
         g["blocks"].append(r.n_blocks)

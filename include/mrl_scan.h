@@ -327,8 +327,9 @@ typedef enum mrl_kernel_kind {
   MRL_KERNEL_THRESH = 3, /* per-query threshold between passes */
   MRL_KERNEL_RERANK = 4, /* rerank scoring of shortlist rows */
   MRL_KERNEL_RERANK_SORT = 5, /* stable sort of the reranked shortlist */
-  MRL_KERNEL_FINISH = 6,      /* exact scores of the MFMA-bounded scan's candidates */
-  MRL_KERNEL_MMA_PREP = 7     /* query operands of the MFMA-bounded scan */
+  MRL_KERNEL_FINISH = 6,      /* candidates of the MFMA-bounded scan to score exactly */
+  MRL_KERNEL_MMA_PREP = 7,    /* query operands of the MFMA-bounded scan */
+  MRL_KERNEL_EXACT = 8        /* exact scores of those candidates */
 } mrl_kernel_kind;
 
 typedef struct mrl_kernel_time {

@@ -691,8 +691,10 @@ static size_t results_head_bytes(uint32_t n_q) { return (size_t)n_q * 8 + kStatC
 
 static const uint32_t kSegCap = 4096;  // kSegs * kSegCap = 65536 candidates per query and scan
 
-// MFMA path, per query: query operands, then kMcCount constants.
-static size_t mma_bytes_per_query() { return (size_t)2 * kMmaSteps * 16 + kMcCount * 4; }
+// MFMA path, per query: query operands, kMcCount constants and k_exact's
+// work items (kFinCap / kExactItem), plus 16 bytes for the work list's head.
+static size_t mma_bytes_per_query() { return (size_t)2 * kMmaSteps * 16 + kMcCount * 4 + kFinCap / kExactItem * 4; }
+static size_t mma_bytes(uint32_t n_q) { return (size_t)std::max<uint32_t>(n_q, 1) * mma_bytes_per_query() + 16; }
 
 extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_results** out) {
   if (!ctx || !out) return fail(MRL_ERR_INVALID_ARG, "null argument");
@@ -720,7 +722,7 @@ extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_re
   ok = ok && hipMalloc(&r->d_cand_score, cands * sizeof(float)) == hipSuccess &&
             hipMalloc(&r->d_cand_row, cands * sizeof(uint32_t)) == hipSuccess &&
             hipMalloc(&r->d_cand_lower, cands * sizeof(float)) == hipSuccess &&
-            hipMalloc(&r->d_mma, nq * mma_bytes_per_query()) == hipSuccess &&
+            hipMalloc(&r->d_mma, mma_bytes((uint32_t)nq)) == hipSuccess &&
             hipMalloc(&r->d_seg_count, nq * kMaxSegs * sizeof(uint32_t)) == hipSuccess &&
             hipMalloc(&r->d_tau, nq * sizeof(float)) == hipSuccess &&
             hipMalloc(&r->d_tau_hi, nq * sizeof(float)) == hipSuccess &&
@@ -759,6 +761,7 @@ struct PassBuffers {
   float* cand_lower = nullptr;    // MFMA path (null: the exact kernels only)
   uint4* mma_ops = nullptr;
   float* mma_consts = nullptr;
+  uint32_t* mma_work = nullptr;
   uint32_t* seg_count;
   uint32_t nseg;
   uint32_t seg_cap;
@@ -809,20 +812,39 @@ static bool mma_ok(const mrl_plans* plans, uint32_t n_q, const ScanParams& sp, c
          sp.strata != MRL_STRATA_L0_ONLY && sp.alpha >= 1.0f && sp.w_s4 >= 0.0f && 2.4f * sp.w_s4 <= sp.alpha;
 }
 
-// MFMA-bounded scan of n_q plans: operands (k_mma_prep); when the index has a
-// sampling pass, the lower bounds of the sampled blocks fill the histogram
-// and k_mma_floors takes the final floor (rank final_rank) and the safe one
-// (rank K) from it; the final pass appends (upper, lower, row) for the pairs
-// whose upper bound reaches the floor (every active pair without a sampling
-// pass); k_finish scores exactly the candidates whose upper bound reaches the
-// K-th best lower bound; k_select emits the top K.
+// Sampling stages of the MFMA path: blocks b = pos << shift, pos < n_pos.
+// Above 256 blocks a first stage scores at most 32 blocks; above 16 x that,
+// a second stage scores every 16th block but counts only lower bounds at or
+// above the first stage's floor, so its histogram stays small while its
+// floor (rank final_rank of a 16x larger sample) is much tighter.
+struct MmaStage {
+  uint32_t shift;
+  uint32_t n_pos;
+};
+static std::vector<MmaStage> mma_stages(uint64_t B) {
+  std::vector<MmaStage> st;
+  if (B <= 256) return st;
+  uint32_t s1 = 0;
+  while (((B + (1ull << s1) - 1) >> s1) > 32) ++s1;
+  st.push_back(MmaStage{s1, (uint32_t)((B + (1ull << s1) - 1) >> s1)});
+  if (s1 >= 5) st.push_back(MmaStage{4u, (uint32_t)((B + 15) >> 4)});  // >= 2x the first stage's blocks
+  return st;
+}
+
+// MFMA-bounded scan of n_q plans: operands (k_mma_prep); the sampling stages,
+// each followed by k_mma_floors (final floor at rank final_rank, safe floor
+// at rank K); the final pass, which appends (upper, lower, row) for the pairs
+// whose upper bound reaches the floor (every active pair when the index has
+// no sampling stage); k_finish lists the candidates whose upper bound reaches
+// the K-th best lower bound; k_exact scores them exactly; k_select emits the
+// top K.  rerun_safe: the final pass alone at the safe floor.
 static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t plans_first, uint32_t n_q,
-                            const ScanParams& sp, uint32_t K, const LevelPlan& lp, const PassBuffers& pb,
-                            unsigned long long* stats, bool rerun_safe) {
+                            const ScanParams& sp, uint32_t K, const PassBuffers& pb, unsigned long long* stats,
+                            bool rerun_safe) {
   hipStream_t s = ctx->stream;
-  const size_t np = lp.passes.size();
-  const bool sampled = np > 1 && !rerun_safe;
-  const uint32_t rank = np > 1 ? final_rank(K, lp.passes[0].n_pos, ix->n_blocks) : K;
+  const uint64_t B = ix->n_blocks;
+  const std::vector<MmaStage> stages = rerun_safe ? std::vector<MmaStage>() : mma_stages(B);
+  const bool sampled = !stages.empty();
   {
     MmaPrepArgs pa{};
     pa.plans = plans->d_plans + plans_first;
@@ -831,70 +853,86 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
     pa.sp = sp;
     pa.ops = pb.mma_ops;
     pa.consts = pb.mma_consts;
+    pa.work = pb.mma_work;
     ProfScope ps(ctx, MRL_KERNEL_MMA_PREP, 0, 0, n_q);
     HIP_TRY(launch_mma_prep(pa, s, ps.ev()));
     ps.commit(n_q != 0);
   }
-  for (size_t pi = 0; pi < np; ++pi) {
-    const bool last = pi + 1 == np;
-    if (rerun_safe && !last) continue;
-    ScanArgs a{};
-    a.idx = ix->d_blocks;
-    a.rows1 = ix->rows1();
-    a.rows4 = ix->rows4();
-    a.n_blocks = ix->n_blocks;
-    a.n_pos = lp.passes[pi].n_pos;
-    a.shift = lp.passes[pi].shift;
-    a.prev_shift = -1;
-    a.plans = plans->d_plans + plans_first;
-    a.luts = plans->d_luts + (size_t)plans_first * kQData;
-    a.n_q = n_q;
-    a.flag_tabs = ctx->d_flag_tabs;
-    a.sp = sp;
-    a.tau = last ? (rerun_safe ? pb.tau : (sampled ? pb.tau_hi : nullptr)) : nullptr;
-    a.hist = last ? nullptr : pb.hist;
-    a.cand_score = pb.cand_score;
-    a.cand_row = pb.cand_row;
-    a.cand_lower = pb.cand_lower;
-    a.seg_count = pb.seg_count;
-    a.nseg = pb.nseg;
-    a.seg_cap = pb.seg_cap;
-    a.stats = last ? stats : nullptr;
-    a.err = pb.err;
-    a.mma_ops = pb.mma_ops;
-    a.mma_consts = pb.mma_consts;
-    const int mode = !last ? 0 : ((sampled || rerun_safe) ? 1 : 2);
-    ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)pi, lp.passes[pi].n_new, n_q);
-    HIP_TRY(launch_scan_mma(a, mode, s, ps.ev()));
+  ScanArgs a{};
+  a.idx = ix->d_blocks;
+  a.rows1 = ix->rows1();
+  a.rows4 = ix->rows4();
+  a.n_blocks = B;
+  a.prev_shift = -1;
+  a.plans = plans->d_plans + plans_first;
+  a.luts = plans->d_luts + (size_t)plans_first * kQData;
+  a.n_q = n_q;
+  a.flag_tabs = ctx->d_flag_tabs;
+  a.sp = sp;
+  a.cand_score = pb.cand_score;
+  a.cand_row = pb.cand_row;
+  a.cand_lower = pb.cand_lower;
+  a.seg_count = pb.seg_count;
+  a.nseg = pb.nseg;
+  a.seg_cap = pb.seg_cap;
+  a.err = pb.err;
+  a.mma_ops = pb.mma_ops;
+  a.mma_consts = pb.mma_consts;
+  for (size_t si = 0; si < stages.size(); ++si) {
+    a.n_pos = stages[si].n_pos;
+    a.shift = stages[si].shift;
+    a.tau = si ? pb.tau_hi : nullptr;  // count only lower bounds at or above the previous floor
+    a.hist = pb.hist;
+    a.stats = nullptr;
+    ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)si, stages[si].n_pos, n_q);
+    HIP_TRY(launch_scan_mma(a, 0, s, ps.ev()));
     ps.commit(a.n_pos != 0 && n_q != 0);
-    if (!last) {
-      ProfScope pt(ctx, MRL_KERNEL_THRESH, (int)pi, 0, n_q);
-      HIP_TRY(launch_mma_floors(pb.hist, n_q, rank, K, pb.tau_hi, pb.tau, s, pt.ev()));
-      pt.commit(n_q != 0);
-    }
+    ProfScope pt(ctx, MRL_KERNEL_THRESH, (int)si, 0, n_q);
+    HIP_TRY(launch_mma_floors(pb.hist, n_q, final_rank(K, stages[si].n_pos, B), K, pb.tau_hi, pb.tau, si != 0, s,
+                              pt.ev()));
+    pt.commit(n_q != 0);
+  }
+  const int final_pass = (int)stages.size();
+  const float* floor = rerun_safe ? pb.tau : (sampled ? pb.tau_hi : nullptr);
+  a.n_pos = (uint32_t)B;
+  a.shift = 0;
+  a.tau = floor;
+  a.hist = nullptr;
+  a.stats = stats;
+  {
+    ProfScope ps(ctx, MRL_KERNEL_SCAN, final_pass, (uint32_t)B, n_q);
+    HIP_TRY(launch_scan_mma(a, floor ? 1 : 2, s, ps.ev()));
+    ps.commit(a.n_pos != 0 && n_q != 0);
+  }
+  FinishArgs fa{};
+  fa.idx = ix->d_blocks;
+  fa.n_blocks = B;
+  fa.rows1 = ix->rows1();
+  fa.rows4 = ix->rows4();
+  fa.plans = plans->d_plans + plans_first;
+  fa.luts = plans->d_luts + (size_t)plans_first * kQData;
+  fa.mma_consts = pb.mma_consts;
+  fa.sp = sp;
+  fa.k = K;
+  fa.cand_score = pb.cand_score;
+  fa.cand_lower = pb.cand_lower;
+  fa.cand_row = pb.cand_row;
+  fa.seg_count = pb.seg_count;
+  fa.nseg = pb.nseg;
+  fa.seg_cap = pb.seg_cap;
+  fa.tau_final = floor;
+  fa.err = pb.err;
+  fa.stats = stats;
+  fa.n_q = n_q;
+  fa.work = pb.mma_work;
+  {
+    ProfScope ps(ctx, MRL_KERNEL_FINISH, final_pass, 0, n_q);
+    HIP_TRY(launch_finish(fa, n_q, s, ps.ev()));
+    ps.commit(n_q != 0);
   }
   {
-    FinishArgs fa{};
-    fa.idx = ix->d_blocks;
-    fa.n_blocks = ix->n_blocks;
-    fa.rows1 = ix->rows1();
-    fa.rows4 = ix->rows4();
-    fa.plans = plans->d_plans + plans_first;
-    fa.luts = plans->d_luts + (size_t)plans_first * kQData;
-    fa.mma_consts = pb.mma_consts;
-    fa.sp = sp;
-    fa.k = K;
-    fa.cand_score = pb.cand_score;
-    fa.cand_lower = pb.cand_lower;
-    fa.cand_row = pb.cand_row;
-    fa.seg_count = pb.seg_count;
-    fa.nseg = pb.nseg;
-    fa.seg_cap = pb.seg_cap;
-    fa.tau_final = rerun_safe ? pb.tau : (sampled ? pb.tau_hi : nullptr);
-    fa.err = pb.err;
-    fa.stats = stats;
-    ProfScope ps(ctx, MRL_KERNEL_FINISH, (int)np - 1, 0, n_q);
-    HIP_TRY(launch_finish(fa, n_q, s, ps.ev()));
+    ProfScope ps(ctx, MRL_KERNEL_EXACT, final_pass, 0, n_q);
+    HIP_TRY(launch_exact(fa, n_q, s, ps.ev()));
     ps.commit(n_q != 0);
   }
   SelectArgs sa{};
@@ -912,7 +950,7 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
   sa.hist = sampled ? pb.hist : nullptr;
   sa.tau_final = pb.tau_hi;
   sa.tau_safe = pb.tau;
-  ProfScope ps(ctx, MRL_KERNEL_SELECT, (int)np - 1, 0, n_q);
+  ProfScope ps(ctx, MRL_KERNEL_SELECT, final_pass, 0, n_q);
   HIP_TRY(launch_select(sa, n_q, s, ps.ev()));
   ps.commit(n_q != 0);
   return MRL_OK;
@@ -921,8 +959,7 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
 static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t plans_first, uint32_t n_q,
                         const ScanParams& sp, uint32_t K, const LevelPlan& lp, const PassBuffers& pb,
                         unsigned long long* stats, bool rerun_safe = false) {
-  if (mma_ok(plans, n_q, sp, pb))
-    return enqueue_scan_mma(ctx, ix, plans, plans_first, n_q, sp, K, lp, pb, stats, rerun_safe);
+  if (mma_ok(plans, n_q, sp, pb)) return enqueue_scan_mma(ctx, ix, plans, plans_first, n_q, sp, K, pb, stats, rerun_safe);
   hipStream_t s = ctx->stream;
   const size_t np = lp.passes.size();
   const bool sampled = np > 1 && !rerun_safe;
@@ -1002,7 +1039,9 @@ static PassBuffers results_buffers(mrl_results* r) {
   pb.cand_row = r->d_cand_row;
   pb.cand_lower = r->d_cand_lower;
   pb.mma_ops = reinterpret_cast<uint4*>(r->d_mma);
-  pb.mma_consts = reinterpret_cast<float*>(r->d_mma + (size_t)std::max<uint32_t>(r->n_q, 1) * 2 * kMmaSteps * 16);
+  const size_t nq = std::max<uint32_t>(r->n_q, 1);
+  pb.mma_consts = reinterpret_cast<float*>(r->d_mma + nq * 2 * kMmaSteps * 16);
+  pb.mma_work = reinterpret_cast<uint32_t*>(r->d_mma + nq * (2 * kMmaSteps * 16 + kMcCount * 4));
   pb.seg_count = r->d_seg_count;
   pb.nseg = kSegs;
   pb.seg_cap = r->seg_cap;

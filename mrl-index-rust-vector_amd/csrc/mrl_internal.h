@@ -153,6 +153,7 @@ struct MmaPrepArgs {
   ScanParams sp;
   uint4* ops;          // [n_q][kMmaSteps][2]: 8 f16 query-operand values per (step, half of K)
   float* consts;       // [n_q][kMcCount]
+  uint32_t* work;      // k_exact's work list; its count is cleared here
 };
 
 struct ScanArgs {
@@ -198,10 +199,15 @@ struct ScanArgs {
   float* cand_lower;
 };
 
-// Exact finishing of the MFMA path, one workgroup per query: the K-th best
-// lower bound among the query's candidates, exact scores (the reference's f32
-// operations) of those whose upper bound reaches it, written back as the
-// query's candidate list for k_select.
+// Exact finishing of the MFMA path.  k_finish, one workgroup per query: a
+// key at or below the K-th best lower bound among the query's candidates, and
+// the list of candidates whose upper bound reaches it (written over the
+// query's lower-bound area: count, then rows); the query's segment counts are
+// cleared.  k_exact, over the whole GPU: the reference's f32 score of every
+// listed candidate, appended to the query's segments (at or above the final
+// floor) for k_select.
+constexpr int kFinCap = 8192;     // exact-scoring list room per query
+constexpr int kExactItem = 256;   // list entries per k_exact work item (one per thread)
 struct FinishArgs {
   const uint8_t* idx;
   uint64_t n_blocks;
@@ -220,7 +226,9 @@ struct FinishArgs {
   uint32_t seg_cap;
   const float* tau_final;   // [n_q] floor of the final pass (null: none)
   uint32_t* err;
-  unsigned long long* stats;  // or null: exact-scored and kept pairs go to kStatPushed
+  unsigned long long* stats;  // or null: listed pairs go to kStatS1 / kStatS4Budget, kept ones to kStatPushed
+  uint32_t n_q;
+  uint32_t* work;           // [0] item count, [2..] items (q << 8 | chunk): n_q * kFinCap / kExactItem + 2 words
 };
 
 struct SelectArgs {
@@ -323,9 +331,13 @@ hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const
 hipError_t launch_mma_prep(const MmaPrepArgs& a, hipStream_t s, const LaunchEvents& ev = {});
 uint32_t mma_scan_grid(const ScanArgs& a);
 hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const LaunchEvents& ev = {});
-hipError_t launch_mma_floors(const uint32_t* hist, uint32_t n_q, uint32_t rank, uint32_t safe_rank, float* floor_out,
-                             float* safe_out, hipStream_t s, const LaunchEvents& ev = {});
+// Floors of a sampling stage from its histogram (which is then cleared): rank
+// `rank` into floor_out and rank safe_rank into safe_out, each raised to the
+// previous stage's value when `prev` is set (those arrays hold it on entry).
+hipError_t launch_mma_floors(uint32_t* hist, uint32_t n_q, uint32_t rank, uint32_t safe_rank, float* floor_out,
+                             float* safe_out, bool prev, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_finish(const FinishArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
+hipError_t launch_exact(const FinishArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
 
 // mrl_rerank.hip: build a 768-dim store from f32 rows; score + sort.
 hipError_t launch_rerank_store(const float* rows, uint64_t n_rows, int precision, void* data, uint16_t* scales,

@@ -1671,7 +1671,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
 // under it is unique and can be assembled from any superset).
 // ---------------------------------------------------------------------------
 constexpr int kSortCap = 8192;
-constexpr int kSelCap = 1024;   // entries at or above the K-th bin floor kept for the final sort
+constexpr int kSelCap = 2048;   // entries at or above the K-th bin floor kept for the final sort
 constexpr int kSelThreads = 1024;
 constexpr int kRankMax = 512;  // up to this many gathered entries are rank-sorted
 
@@ -2259,6 +2259,7 @@ __global__ __launch_bounds__(64) void k_mma_prep(MmaPrepArgs a) {
   const float R = 2.0f * (fabsf(mean) +
                           kMmaSafe * (cbm * l1w + l1w2 + ws4 * l1w4 + fabsf(psum) + eP + e1 + e4 + eO) + e0 + 1.0f);
   const bool fin = ballot(!fin_l) == 0 && mean - mean == 0.0f && psum - psum == 0.0f && R - R == 0.0f;
+  if (q == 0 && lane == 0) a.work[0] = 0u;  // k_exact's item count, filled by k_finish
   if (lane == 0) {
     s_ex[0] = eP;
     s_ex[1] = e1;
@@ -2296,15 +2297,26 @@ __global__ __launch_bounds__(64) void k_mma_prep(MmaPrepArgs a) {
   }
 }
 
-// Floors of the final pass from the sampling histogram: rank `rank` and the
-// safe rank K, one wave per query.
-__global__ __launch_bounds__(64) void k_mma_floors(const uint32_t* hist, uint32_t rank, uint32_t safe_rank,
-                                                   float* floor_out, float* safe_out) {
-  const uint32_t q = blockIdx.x;
-  const HistRow r = hist_row(hist + (uint64_t)q * kHistBins);
-  const float f = floor_of(r, rank);
-  const float sf = floor_of(r, safe_rank);
-  if (__lane_id() == 0) {
+// Floors of a sampling stage from its histogram, one wave per query: rank
+// `rank` and the safe rank K, raised to the previous stage's floors when
+// `prev` (a later stage counts only lower bounds at or above the previous
+// floor, so its own floor is -inf when too few were counted).  The histogram
+// is left zeroed for the next stage.
+__global__ __launch_bounds__(64) void k_mma_floors(uint32_t* hist, uint32_t rank, uint32_t safe_rank,
+                                                   float* floor_out, float* safe_out, int prev) {
+  const uint32_t q = blockIdx.x, lane = __lane_id();
+  uint32_t* h = hist + (uint64_t)q * kHistBins;
+  const HistRow r = hist_row(h);
+  float f = floor_of(r, rank);
+  float sf = floor_of(r, safe_rank);
+  uint4* mine = reinterpret_cast<uint4*>(h + (63u - lane) * 32u);  // the bins hist_row gave this lane
+#pragma unroll
+  for (int k = 0; k < 8; ++k) mine[k] = make_uint4(0u, 0u, 0u, 0u);
+  if (lane == 0) {
+    if (prev) {
+      f = fmaxf(f, floor_out[q]);
+      sf = fmaxf(sf, safe_out[q]);
+    }
     floor_out[q] = f;
     safe_out[q] = sf;
   }
@@ -2441,7 +2453,8 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
       }
       const float e0q = mc[kMcE0] + fabsf(tau) * (1.0f / 65536.0f);
       if (ok) C = sc * ((mean - tau) + (MODE == 0 ? -e0q : e0q));
-      qk[0] = tau;
+      // sampling: only lower bounds at or above the previous stage's floor are counted
+      qk[0] = MODE == 0 ? (a.tau ? a.tau[q0 + qi] : -INFINITY) : tau;
       qk[1] = mc[kMcInvS];
       qk[2] = mc[kMcEP];
       qk[3] = mc[kMcE1];
@@ -2474,6 +2487,19 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
   const uint32_t seg = blockIdx.x % a.nseg;
   uint32_t c_blocks = 0, c_active = 0, c_app = 0;
   uint32_t fill = 0;  // entries of this wave's staging region (wave-uniform)
+  // bit 16 t + r: register r of tile t belongs to a query of the batch with
+  // usable operands (read only on the rare paths that force candidates)
+  uint32_t okbits = 0u;
+  if constexpr (MODE != 0) {
+#pragma unroll
+    for (int t = 0; t < NQT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
+        if (qi < nq && s_qk[qi][7] != 0.0f) okbits |= 1u << (16 * t + r);
+      }
+    asm volatile("" : "+v"(okbits));  // one register, not 32 hoisted masks
+  }
 
   for (uint32_t it = first; it < n_it; it += stride) {
     const uint32_t it_nxt = it + stride < n_it ? it + stride : it_cur;
@@ -2584,28 +2610,27 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
               const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
               if (qi < nq && s_qk[qi][7] != 0.0f) {
                 const float L = acc[t][r] * s_qk[qi][1];
-                uint32_t qq = q0 + qi;  // through an empty asm: no hoisted per-register addresses
-                asm volatile("" : "+v"(qq));
-                atomicAdd(a.hist + (uint64_t)qq * kHistBins + hist_bin(L), 1u);
+                if (L >= s_qk[qi][0]) {
+                  uint32_t qq = q0 + qi;  // through an empty asm: no hoisted per-register addresses
+                  asm volatile("" : "+v"(qq));
+                  atomicAdd(a.hist + (uint64_t)qq * kHistBins + hist_bin(L), 1u);
+                }
               }
             }
         }
       } else {
         // Absent queries and those with unusable operands start at C = -inf,
         // so acc >= 0 only holds for pairs of the batch.  A slot whose meta is
-        // beyond the operand range is a candidate of every query of the
-        // batch: its registers of present queries are raised to +inf (MODE 2
-        // takes every present query's register).
-        if (MODE == 2 || ballot(act && !safe) != 0) {
+        // beyond the operand range is a candidate of every present query: its
+        // registers are raised to +inf (its bounds are then taken as +-inf);
+        // MODE 2 takes every present query's register as it is.
+        const uint64_t actm = ballot(act);
+        if (MODE == 1 && ballot(act && !safe) != 0) {
 #pragma unroll
           for (int t = 0; t < NQT; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
-              const bool okq = qi < nq && s_qk[qi][7] != 0.0f;
-              if (MODE == 2) acc[t][r] = okq ? fmaxf(acc[t][r], 0.0f) : -INFINITY;
-              else if (!safe && okq) acc[t][r] = INFINITY;
-            }
+            for (int r = 0; r < 16; ++r)
+              if (!safe && ((okbits >> (16 * t + r)) & 1u)) acc[t][r] = INFINITY;
         }
         const uint32_t row = b * 64u + v;
         const float eb = fabsf(m_scale), eo = fabsf(m_offset);
@@ -2613,7 +2638,7 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
         for (int t = 0; t < NQT; ++t)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const uint64_t pm = ballot(act && acc[t][r] >= 0.0f);
+            const uint64_t pm = (MODE == 2 ? ballot((okbits >> (16 * t + r)) & 1u) : ballot(acc[t][r] >= 0.0f)) & actm;
             if (pm == 0) continue;
             const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
             float U = INFINITY, L = -INFINITY;
@@ -2642,8 +2667,6 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
     atomicAdd(&s_stats[kStatBlocks], c_blocks);
     atomicAdd(&s_stats[kStatActive], c_active);
     atomicAdd(&s_stats[kStatPrefix], c_app);
-    atomicAdd(&s_stats[kStatS1], c_app);
-    atomicAdd(&s_stats[kStatS4Budget], c_app);
   }
   if constexpr (MODE != 0) {
     if (lane == 0) s_st.n[wave] = min(fill, (uint32_t)kMmaWaveCap);
@@ -2738,7 +2761,21 @@ __device__ bool exact_full(const FinishArgs& a, const mrl_query_plan* p, uint32_
 }
 
 constexpr int kFinThreads = 1024;
-constexpr int kFinCap = 8192;
+
+// Log-scale bin of a key distance d: d itself below 64, else 64 bins per
+// octave (the leading bit's position and the 6 bits after it); monotone in d,
+// bins 0..1727.
+__device__ __forceinline__ uint32_t dist_bin(uint32_t d) {
+  if (d < 64u) return d;
+  const uint32_t e = 31u - (uint32_t)__clz((int)d);
+  return ((e - 5u) << 6) | ((d >> (e - 6u)) & 63u);
+}
+// The largest distance in bin b.
+__device__ __forceinline__ uint64_t dist_bin_top(uint32_t b) {
+  if (b < 64u) return b;
+  const uint32_t e = (b >> 6) + 5u, m = b & 63u;
+  return ((uint64_t)(65u + m) << (e - 6u)) - 1u;
+}
 
 // One query: the K-th best lower bound among its candidates (exact radix
 // select on the order-preserving key), the candidates whose upper bound
@@ -2748,9 +2785,6 @@ constexpr int kFinCap = 8192;
 // not finite, or with more than kFinCap such candidates gets a count past
 // the segment room, which k_select reports as an overflow (dense re-run).
 __global__ __launch_bounds__(kFinThreads) void k_finish(FinishArgs a) {
-  __shared__ __align__(16) float s_lut[1024];
-  __shared__ __align__(16) float s_w1[128];
-  __shared__ __align__(16) float s_w4[64];
   __shared__ uint32_t s_frow[kFinCap];
   __shared__ uint32_t s_hist[2048];
   __shared__ uint32_t s_off[kSegs + 1];
@@ -2764,48 +2798,45 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(FinishArgs a) {
   uint32_t* qcount = a.seg_count + (uint64_t)q * a.nseg;
   const uint32_t c_own = tid < (int)a.nseg ? qcount[tid] : 0u;
   const bool ok = a.mma_consts[(uint64_t)q * kMcCount + kMcOk] != 0.0f;
-  const float floor_t = a.tau_final ? a.tau_final[q] : -INFINITY;
+  const uint64_t qbase = (uint64_t)q * a.nseg * a.seg_cap;
+  uint32_t* list = reinterpret_cast<uint32_t*>(a.cand_lower + qbase);  // written once the walks are done
   if (tid < 8) s_misc[tid] = 0u;
   __syncthreads();
   if (c_own > a.seg_cap || !ok) atomicOr(&s_misc[7], 1u);
   seg_offsets(c_own, a.nseg, a.seg_cap, s_off, s_coff, s_ws);
   if (s_misc[7]) {
-    if (tid == 0) qcount[0] = a.seg_cap + 1u;
+    if (tid == 0) {
+      qcount[0] = a.seg_cap + 1u;
+      list[0] = 0u;
+    }
     return;
   }
   const uint32_t total = s_off[a.nseg];
-  const float* qd = a.luts + (uint64_t)q * kQData;
-  for (int i = tid; i < 1024; i += kFinThreads) s_lut[i] = qd[kQdLut + i];
-  if (tid < 128) s_w1[tid] = qd[kQdW1 + tid];
-  if (tid < 64) s_w4[tid] = qd[kQdW4 + tid];
-  const uint64_t qbase = (uint64_t)q * a.nseg * a.seg_cap;
 
-  // K-th largest lower-bound key (all candidates when there are at most K)
+  // A key at or below the K-th largest lower-bound key (all candidates when
+  // there are at most K): the largest key, then a histogram of each key's
+  // distance below it on a log scale, so candidates crowded just under the
+  // top spread over many bins.
   uint32_t tkey = 0u;
   if (total > K) {
     const CandView vl{a.cand_lower + qbase, a.cand_row + qbase, a.seg_cap, a.nseg, s_off, s_coff};
-    const int shifts[3] = {21, 10, 0};
-    const int widths[3] = {11, 11, 10};
-    uint32_t prefix = 0, need = K;
-    for (int pass = 0; pass < 3; ++pass) {
-      const int sh = shifts[pass], wd = widths[pass];
-      const uint32_t nb = 1u << wd;
-      for (int i = tid; i < 2048; i += kFinThreads) s_hist[i] = 0u;
-      __syncthreads();
-      for_each_cand<16>(vl, [&](float sc, uint32_t) {
-        const uint32_t key = score_key(sc);
-        if (pass == 0 || (key >> (sh + wd)) == prefix) atomicAdd(&s_hist[(key >> sh) & (nb - 1)], 1u);
-      });
-      __syncthreads();
-      find_boundary(s_hist, nb, need, true, &s_misc[3], &s_misc[4], s_ws);
-      __syncthreads();
-      need -= s_misc[4];
-      prefix = (prefix << wd) | s_misc[3];
-      __syncthreads();
-    }
-    tkey = prefix;
+    uint32_t mk = 0u;
+    for_each_cand<16>(vl, [&](float sc, uint32_t) { mk = max(mk, score_key(sc)); });
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mk = max(mk, (uint32_t)__shfl_xor((int)mk, o));
+    for (int i = tid; i < 2048; i += kFinThreads) s_hist[i] = 0u;
+    if ((tid & 63) == 0) atomicMax(&s_misc[6], mk);
+    __syncthreads();
+    const uint32_t kmax = s_misc[6];
+    for_each_cand<16>(vl, [&](float sc, uint32_t) { atomicAdd(&s_hist[dist_bin(kmax - score_key(sc))], 1u); });
+    __syncthreads();
+    find_boundary(s_hist, 2048, K, false, &s_misc[3], &s_misc[4], s_ws);
+    __syncthreads();
+    const uint64_t dhi = dist_bin_top(s_misc[3]);
+    tkey = dhi < (uint64_t)kmax ? kmax - (uint32_t)dhi : 0u;
   }
-  // candidates whose upper bound reaches it
+  // candidates whose upper bound reaches it, listed over the lower-bound area
+  // (every read of it is done)
   const CandView vu{a.cand_score + qbase, a.cand_row + qbase, a.seg_cap, a.nseg, s_off, s_coff};
   for_each_pair(vu, [&](float u, uint32_t row, uint32_t) {
     if (score_key(u) >= tkey) {
@@ -2816,34 +2847,85 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(FinishArgs a) {
   __syncthreads();
   const uint32_t nf = s_misc[2];
   if (nf > (uint32_t)kFinCap) {
-    if (tid == 0) qcount[0] = a.seg_cap + 1u;
+    if (tid == 0) {
+      qcount[0] = a.seg_cap + 1u;
+      list[0] = 0u;
+    }
     return;
   }
-  // exact scores; every read of the candidate lists is done, so they can be rewritten
-  const mrl_query_plan* p = a.plans + q;
-  for (uint32_t i = tid; i < nf; i += kFinThreads) {
-    const uint32_t row = s_frow[i];
-    float sc;
-    if ((uint64_t)(row >> 6) >= a.n_blocks) continue;  // rows come from this scan's appends
-    if (!exact_full(a, p, row, s_lut, s_w1, s_w4, &sc)) continue;
-    if (sc != sc) {
-      atomicOr(a.err + q, 1u);
-      continue;
-    }
-    if (!(sc >= floor_t)) continue;
-    const uint32_t slot = atomicAdd(&s_misc[5], 1u);
-    a.cand_score[qbase + slot] = sc;
-    a.cand_row[qbase + slot] = row;
+  for (uint32_t i = tid; i < nf; i += kFinThreads) list[1 + i] = s_frow[i];
+  if (tid == 0) {
+    list[0] = nf;
+    // k_exact's work items of this query: (q, chunk) for every kExactItem entries
+    const uint32_t items = (nf + kExactItem - 1) / kExactItem;
+    s_misc[6] = items ? atomicAdd(a.work, items) : 0u;
   }
   __syncthreads();
-  const uint32_t n_out = s_misc[5];
-  if (tid < (int)a.nseg) {
-    const uint32_t lo = (uint32_t)tid * a.seg_cap;
-    qcount[tid] = n_out > lo ? min(n_out - lo, a.seg_cap) : 0u;
-  }
-  if (a.stats && tid == 0 && n_out) {
+  if ((uint32_t)tid < (nf + kExactItem - 1) / kExactItem) a.work[2 + s_misc[6] + tid] = (q << 8) | (uint32_t)tid;
+  if (tid < (int)a.nseg) qcount[tid] = 0u;  // k_exact appends from zero
+  if (a.stats && tid == 0 && nf) {
     const uint32_t copy = q % (uint32_t)kStatCopies;
-    atomicAdd(a.stats + copy * kStatCount + kStatPushed, (unsigned long long)n_out);
+    atomicAdd(a.stats + copy * kStatCount + kStatS1, (unsigned long long)nf);
+    atomicAdd(a.stats + copy * kStatCount + kStatS4Budget, (unsigned long long)nf);
+  }
+}
+
+// Exact scores of the listed candidates.  Work item = kExactItem entries of
+// one query's list, one per thread; workgroups loop over the item list
+// k_finish published (work[0] items at work[2..]).  Scores at or above
+// the final floor are appended (one atomic per wave) to segment item % nseg
+// of the query; a NaN score sets the query's error flag, as a NaN survivor
+// does on the exact path.
+__global__ __launch_bounds__(kExactItem) void k_exact(FinishArgs a) {
+  __shared__ __align__(16) float s_lut[1024];
+  __shared__ __align__(16) float s_w1[128];
+  __shared__ __align__(16) float s_w4[64];
+  const uint32_t n_items = a.work[0];
+  const int tid = threadIdx.x;
+  const uint32_t lane = __lane_id();
+  for (uint32_t item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const uint32_t wi = a.work[2 + item];
+    const uint32_t q = wi >> 8, c = wi & 255u;
+    if (q >= a.n_q) continue;
+    const uint64_t qbase = (uint64_t)q * a.nseg * a.seg_cap;
+    const uint32_t* list = reinterpret_cast<const uint32_t*>(a.cand_lower + qbase);
+    const uint32_t nf = min(list[0], (uint32_t)kFinCap);
+    if (c * (uint32_t)kExactItem >= nf) continue;
+    __syncthreads();  // the previous item's table reads are done
+    const float* qd = a.luts + (uint64_t)q * kQData;
+    for (int i = tid; i < 1024; i += kExactItem) s_lut[i] = qd[kQdLut + i];
+    if (tid < 128) s_w1[tid] = qd[kQdW1 + tid];
+    if (tid < 64) s_w4[tid] = qd[kQdW4 + tid];
+    __syncthreads();
+    const uint32_t i = c * (uint32_t)kExactItem + (uint32_t)tid;
+    const float floor_t = a.tau_final ? a.tau_final[q] : -INFINITY;
+    bool keep = false;
+    float sc = 0.0f;
+    uint32_t row = 0u;
+    if (i < nf) {
+      row = list[1 + i];
+      if ((uint64_t)(row >> 6) < a.n_blocks && exact_full(a, a.plans + q, row, s_lut, s_w1, s_w4, &sc)) {
+        if (sc != sc) atomicOr(a.err + q, 1u);
+        else keep = sc >= floor_t;
+      }
+    }
+    const uint64_t pm = ballot(keep);
+    if (pm == 0) continue;
+    const uint32_t seg = c % a.nseg;
+    const uint64_t sq = (uint64_t)q * a.nseg + seg;
+    const uint32_t lead = (uint32_t)__ffsll((long long)pm) - 1;
+    uint32_t base = 0;
+    if (lane == lead) {
+      base = atomicAdd(a.seg_count + sq, (uint32_t)__popcll(pm));
+      if (a.stats)
+        atomicAdd(a.stats + (q % (uint32_t)kStatCopies) * kStatCount + kStatPushed, (unsigned long long)__popcll(pm));
+    }
+    base = __shfl(base, (int)lead);
+    const uint32_t slot = base + lanes_below(pm);
+    if (keep && slot < a.seg_cap) {
+      a.cand_score[sq * a.seg_cap + slot] = sc;
+      a.cand_row[sq * a.seg_cap + slot] = row;
+    }
   }
 }
 
@@ -2875,14 +2957,19 @@ hipError_t launch_plan(const PlanArgs& a, hipStream_t s, const LaunchEvents& ev)
 
 int scan_query_tile(uint32_t n_q) { return n_q >= 8 ? 8 : 1; }
 
-// Workgroups of `kernel` resident at once on the current device.
+// Workgroups of `kernel` (of `threads` threads) resident at once on the current device.
 template <typename K>
-static uint32_t resident_groups(K kernel) {
+static uint32_t resident_groups_n(K kernel, int threads) {
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 1024;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 1024;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu < 1) per_cu = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu < 1)
+    per_cu = 1;
   return (uint32_t)(cus * per_cu);
+}
+template <typename K>
+static uint32_t resident_groups(K kernel) {
+  return resident_groups_n(kernel, 256);
 }
 
 // Workgroups along x of a scan launch (the same for every query tile).
@@ -2983,16 +3070,24 @@ hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const Lau
   return hipGetLastError();
 }
 
-hipError_t launch_mma_floors(const uint32_t* hist, uint32_t n_q, uint32_t rank, uint32_t safe_rank, float* floor_out,
-                             float* safe_out, hipStream_t s, const LaunchEvents& ev) {
+hipError_t launch_mma_floors(uint32_t* hist, uint32_t n_q, uint32_t rank, uint32_t safe_rank, float* floor_out,
+                             float* safe_out, bool prev, hipStream_t s, const LaunchEvents& ev) {
   if (n_q == 0) return hipSuccess;
-  launch(k_mma_floors, dim3(n_q), dim3(64), s, ev, hist, rank, safe_rank, floor_out, safe_out);
+  launch(k_mma_floors, dim3(n_q), dim3(64), s, ev, hist, rank, safe_rank, floor_out, safe_out, prev ? 1 : 0);
   return hipGetLastError();
 }
 
 hipError_t launch_finish(const FinishArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev) {
   if (n_q == 0) return hipSuccess;
   launch(k_finish, dim3(n_q), dim3(kFinThreads), s, ev, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_exact(const FinishArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev) {
+  if (n_q == 0) return hipSuccess;
+  static const uint32_t res = resident_groups_n(k_exact, kExactItem);
+  const uint32_t items = n_q * (uint32_t)(kFinCap / kExactItem);  // at most
+  launch(k_exact, dim3(items < res ? items : res), dim3(kExactItem), s, ev, a);
   return hipGetLastError();
 }
 
