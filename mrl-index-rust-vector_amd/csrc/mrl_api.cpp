@@ -813,7 +813,8 @@ static bool mma_ok(const mrl_plans* plans, uint32_t n_q, const ScanParams& sp, c
 }
 
 // Sampling stages of the MFMA path: blocks b = pos << shift, pos < n_pos.
-// Above 256 blocks a first stage scores at most 32 blocks; above 16 x that,
+// Above 256 blocks a first stage scores 16..128 blocks (fewer for larger
+// batches); when that is at most 1/32 of the index,
 // a second stage scores every 16th block but counts only lower bounds at or
 // above the first stage's floor, so its histogram stays small while its
 // floor (rank final_rank of a 16x larger sample) is much tighter.
@@ -821,11 +822,13 @@ struct MmaStage {
   uint32_t shift;
   uint32_t n_pos;
 };
-static std::vector<MmaStage> mma_stages(uint64_t B) {
+static std::vector<MmaStage> mma_stages(uint64_t B, uint32_t n_q) {
   std::vector<MmaStage> st;
   if (B <= 256) return st;
+  // the first stage counts every pair: keep it near 4096 x 64 block-queries
+  const uint64_t cap = std::min<uint64_t>(128, std::max<uint64_t>(16, 4096 / std::max<uint32_t>(n_q, 1)));
   uint32_t s1 = 0;
-  while (((B + (1ull << s1) - 1) >> s1) > 32) ++s1;
+  while (((B + (1ull << s1) - 1) >> s1) > cap) ++s1;
   st.push_back(MmaStage{s1, (uint32_t)((B + (1ull << s1) - 1) >> s1)});
   if (s1 >= 5) st.push_back(MmaStage{4u, (uint32_t)((B + 15) >> 4)});  // >= 2x the first stage's blocks
   return st;
@@ -843,7 +846,7 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
                             bool rerun_safe) {
   hipStream_t s = ctx->stream;
   const uint64_t B = ix->n_blocks;
-  const std::vector<MmaStage> stages = rerun_safe ? std::vector<MmaStage>() : mma_stages(B);
+  const std::vector<MmaStage> stages = rerun_safe ? std::vector<MmaStage>() : mma_stages(B, n_q);
   const bool sampled = !stages.empty();
   {
     MmaPrepArgs pa{};

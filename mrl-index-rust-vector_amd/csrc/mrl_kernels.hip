@@ -2410,6 +2410,7 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
   __shared__ __align__(16) float s_c[kMmaQ];
   __shared__ __align__(16) float s_qk[kMmaQ][8];  // tau, 1/s, eP, e1, e4, eO, e0 (with the tau term), ok
   __shared__ unsigned int s_stats[kStatCount];
+  __shared__ uint32_t s_anyall;  // sampling: some query counts every lower bound
   __shared__ MmaStaging s_st;
 
   const int tid = threadIdx.x;
@@ -2417,6 +2418,8 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
   const uint32_t lane = lane_id(), kh = lane >> 5, vl = lane & 31u;
   const uint32_t q0 = blockIdx.y * kMmaQ;
   const int nq = (int)min((uint32_t)kMmaQ, a.n_q - q0);
+  if (tid == 0) s_anyall = 0u;
+  __syncthreads();
 
   const uint32_t n_items = 2u * a.n_pos;
   const uint32_t stride = gridDim.x * 4 - 1;  // odd: see k_scan
@@ -2446,15 +2449,21 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
       const float* mc = a.mma_consts + (uint64_t)(q0 + qi) * kMcCount;
       const float sc = mc[kMcS], mean = mc[kMcMean], R = mc[kMcR];
       const bool ok = mc[kMcOk] != 0.0f;
+      // MODE 1: tau = the floor.  MODE 0: tau = the previous stage's floor;
+      // only lower bounds at or above it are counted (all of them without one).
       float tau = 0.0f;
-      if (MODE == 1) {
+      bool all = false;
+      if (MODE != 2) {
         tau = a.tau ? a.tau[q0 + qi] : -INFINITY;
-        if (!(tau >= -R)) tau = -R;  // no floor: below every score of a vector with safe magnitudes
+        if (!(tau >= -R)) {
+          all = MODE == 0;
+          tau = MODE == 0 ? 0.0f : -R;  // MODE 1 without a floor: below every score of a vector with safe magnitudes
+        }
       }
+      if (all) atomicOr(&s_anyall, 1u);
       const float e0q = mc[kMcE0] + fabsf(tau) * (1.0f / 65536.0f);
       if (ok) C = sc * ((mean - tau) + (MODE == 0 ? -e0q : e0q));
-      // sampling: only lower bounds at or above the previous stage's floor are counted
-      qk[0] = MODE == 0 ? (a.tau ? a.tau[q0 + qi] : -INFINITY) : tau;
+      qk[0] = tau;
       qk[1] = mc[kMcInvS];
       qk[2] = mc[kMcEP];
       qk[3] = mc[kMcE1];
@@ -2602,22 +2611,28 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
       }
       // Register r of tile t holds query 32 t + 8 (r / 4) + 4 kh + r % 4.
       if constexpr (MODE == 0) {
-        if (act && safe) {
+        // Tile value = s (L - tau): the pairs at or above the previous floor
+        // pass a compare; without one (some query counts all) every pair of
+        // a present query is counted.  L = tau + value / s, less a margin
+        // for that addition's rounding.
+        const uint64_t cm = ballot(act && safe);
+        const bool all = s_anyall != 0u;
 #pragma unroll
-          for (int t = 0; t < NQT; ++t)
+        for (int t = 0; t < NQT; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
-              if (qi < nq && s_qk[qi][7] != 0.0f) {
-                const float L = acc[t][r] * s_qk[qi][1];
-                if (L >= s_qk[qi][0]) {
-                  uint32_t qq = q0 + qi;  // through an empty asm: no hoisted per-register addresses
-                  asm volatile("" : "+v"(qq));
-                  atomicAdd(a.hist + (uint64_t)qq * kHistBins + hist_bin(L), 1u);
-                }
-              }
-            }
-        }
+          for (int r = 0; r < 16; ++r) {
+            const uint64_t pm = (all ? ~0ull : ballot(acc[t][r] >= 0.0f)) & cm;
+            if (pm == 0 || !((pm >> lane) & 1ull)) continue;
+            const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
+            if (qi >= nq) continue;
+            const float2 k = *reinterpret_cast<const float2*>(&s_qk[qi][0]);  // tau, 1/s
+            if (s_qk[qi][7] == 0.0f) continue;
+            float L = k.x + acc[t][r] * k.y;
+            L = L - (fabsf(L) + fabsf(k.x)) * (1.0f / 4194304.0f);
+            uint32_t qq = q0 + qi;  // through an empty asm: no hoisted per-register addresses
+            asm volatile("" : "+v"(qq));
+            atomicAdd(a.hist + (uint64_t)qq * kHistBins + hist_bin(L), 1u);
+          }
       } else {
         // Absent queries and those with unusable operands start at C = -inf,
         // so acc >= 0 only holds for pairs of the batch.  A slot whose meta is
