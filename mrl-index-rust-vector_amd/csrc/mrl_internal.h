@@ -129,6 +129,7 @@ constexpr int kHistBins = 2048;
 // pairs whose upper bound reaches the K-th best lower bound are scored exactly.
 constexpr int kMmaSteps = 17;   // K-steps of a tile: prefix 4, S1 8, S4 4, error columns 1
 constexpr int kMmaQ = 64;       // queries per workgroup (two 32-query tiles per wave)
+constexpr int kMmaWaves = 8;    // waves per MFMA scan workgroup (four waves per SIMD)
 constexpr int kMmaMinQ = 8;     // batches of at least this many queries take the MFMA path
 // Per-query constants written by k_mma_prep (floats).
 enum {

@@ -2353,29 +2353,32 @@ __device__ __forceinline__ MmaRaw mma_load(const uint8_t* idx, const uint4* rows
 // with one global atomic per (workgroup, query).  Each wave owns a region of
 // kMmaWaveCap entries and keeps its fill count in a scalar register, so an
 // append needs no atomic.
-constexpr int kMmaWaveCap = 1024;
+template <int W, int CAP>
 struct MmaStaging {
-  uint32_t n[4];
+  static constexpr int kWaves = W;
+  static constexpr int kCap = CAP;  // entries per wave
+  uint32_t n[W];
   uint32_t cnt[kMmaQ];
   uint32_t base[kMmaQ];
-  uint32_t row[4 * kMmaWaveCap];
-  float u[4 * kMmaWaveCap];
-  float l[4 * kMmaWaveCap];
-  uint8_t q[4 * kMmaWaveCap];
+  uint32_t row[W * CAP];
+  float u[W * CAP];
+  float l[W * CAP];
+  uint8_t q[W * CAP];
 };
 
 // Appends (u, l, row) of query q0 + qi (per lane) for the lanes in pm to this
 // wave's region at *fill (wave-uniform); past the region's room, straight
 // into the query's segment (one global atomic per lane).
-__device__ __forceinline__ void mma_append(MmaStaging& st, const ScanArgs& a, int wave, uint32_t* fill, uint32_t q0,
+template <typename ST>
+__device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, int wave, uint32_t* fill, uint32_t q0,
                                            uint32_t qi, uint32_t seg, uint64_t pm, float u, float l, uint32_t row) {
   const uint32_t lane = __lane_id();
   const uint32_t base = *fill;
   *fill = base + (uint32_t)__popcll(pm);
   if (!((pm >> lane) & 1ull)) return;
   const uint32_t slot = base + lanes_below(pm);
-  if (slot < (uint32_t)kMmaWaveCap) {
-    const uint32_t e = (uint32_t)wave * kMmaWaveCap + slot;
+  if (slot < (uint32_t)ST::kCap) {
+    const uint32_t e = (uint32_t)wave * ST::kCap + slot;
     st.row[e] = row;
     st.u[e] = u;
     st.l[e] = l;
@@ -2396,22 +2399,27 @@ __device__ __forceinline__ void mma_append(MmaStaging& st, const ScanArgs& a, in
   }
 }
 
-// One pass of the MFMA-bounded scan.  Workgroup = 4 waves over the same 64
+// One pass of the MFMA-bounded scan.  Workgroup = 8 waves over the same 64
 // queries (blockIdx.y); a wave takes one 32-vector tile (half a block) at a
 // time, items i = first + k * stride with block (i / 2) << shift and half
-// i % 2; NQT 32-query tiles per wave, their operands held in registers.
+// i % 2; NQT 32-query tiles per wave.  The query operands sit in LDS and are
+// read one K-step ahead of the MFMAs that use them, which keeps the register
+// file small enough for four waves per SIMD.
 // MODE 0: sampling pass, the lower bounds of every active pair go into the
 // query's histogram; 1: final pass, pairs with U >= the floor in a.tau are
 // appended; 2: single pass, every active pair is appended.
 template <int NQT, int MODE>
-__global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
+__global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
+  constexpr int WPG = kMmaWaves;  // waves per workgroup
+  using Staging = MmaStaging<WPG, 256>;
+  __shared__ __align__(16) uint4 s_qa[NQT][kMmaSteps][64];
   __shared__ uint32_t s_tab[256];
   __shared__ float s_flag[512];      // rho = f / 255, then sqrt(max(1 - rho^2, 0))
   __shared__ __align__(16) float s_c[kMmaQ];
   __shared__ __align__(16) float s_qk[kMmaQ][8];  // tau, 1/s, eP, e1, e4, eO, e0 (with the tau term), ok
   __shared__ unsigned int s_stats[kStatCount];
   __shared__ uint32_t s_anyall;  // sampling: some query counts every lower bound
-  __shared__ MmaStaging s_st;
+  __shared__ Staging s_st;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2422,14 +2430,14 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
   __syncthreads();
 
   const uint32_t n_items = 2u * a.n_pos;
-  const uint32_t stride = gridDim.x * 4 - 1;  // odd: see k_scan
-  const uint32_t first = blockIdx.x * 4 + wave;
+  const uint32_t stride = gridDim.x * WPG - 1;  // odd: see k_scan
+  const uint32_t first = blockIdx.x * WPG + wave;
   const uint32_t n_it = first < stride ? n_items : 0u;
   uint32_t it_cur = first;
   MmaRaw cur{};
   if (first < n_it) cur = mma_load(a.idx, a.rows1, a.rows4, (uint64_t)(first >> 1) << a.shift, first & 1u);
 
-  {  // byte -> (f16 cb[low nibble], f16 cb[high nibble])
+  if (tid < 256) {  // byte -> (f16 cb[low nibble], f16 cb[high nibble])
     const mrl_query_plan* p0 = a.plans + q0;
     const bool eden = p0->prefix_codec == MRL_PREFIX_EDEN_PROD;
     const uint32_t lo = (uint32_t)tid & 15u, hi = (uint32_t)tid >> 4;
@@ -2437,10 +2445,12 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
     const float chi = eden ? p0->eden_codebook[hi] : (float)hi;
     s_tab[tid] = f32_to_f16(clo) | (f32_to_f16(chi) << 16);
   }
-  s_flag[tid] = a.flag_tabs[tid];
-  s_flag[256 + tid] = a.flag_tabs[256 + tid];
+  if (tid < 256) {
+    s_flag[tid] = a.flag_tabs[tid];
+    s_flag[256 + tid] = a.flag_tabs[256 + tid];
+  }
   if (tid < kStatCount) s_stats[tid] = 0u;
-  if (tid < 4) s_st.n[tid] = 0u;
+  if (tid < WPG) s_st.n[tid] = 0u;
   if (tid < kMmaQ) {
     const int qi = tid;
     s_st.cnt[qi] = 0u;
@@ -2477,19 +2487,22 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
     for (int i = 0; i < 8; ++i) s_qk[qi][i] = qk[i];
   }
   // query operands: tile t, lane -> query q0 + 32 t + l % 32, K-half l / 32
-  uint4 qa[NQT][kMmaSteps];
-#pragma unroll
-  for (int t = 0; t < NQT; ++t) {
-    const uint32_t qi = 32u * t + vl;
-    const bool have = (int)qi < nq;
-    const uint4* src = a.mma_ops + (uint64_t)(q0 + (have ? qi : 0u)) * (2 * kMmaSteps) + kh;
-#pragma unroll
-    for (int st = 0; st < kMmaSteps; ++st) qa[t][st] = have ? src[2 * st] : make_uint4(0u, 0u, 0u, 0u);
-    if (MODE == 0 && kh == 0) {  // the sampling pass subtracts the error columns
-      qa[t][kMmaSteps - 1].x ^= 0x80008000u;
-      qa[t][kMmaSteps - 1].y ^= 0x80008000u;
+  // (the sampling pass subtracts the error columns)
+  auto qa_load = [&](int t, int st, uint32_t ln) -> uint4 {
+    const uint32_t qi = 32u * t + (ln & 31u), h = ln >> 5;
+    if ((int)qi >= nq) return make_uint4(0u, 0u, 0u, 0u);
+    uint4 v = a.mma_ops[(uint64_t)(q0 + qi) * (2 * kMmaSteps) + 2 * st + h];
+    if (MODE == 0 && h == 0 && st == kMmaSteps - 1) {
+      v.x ^= 0x80008000u;
+      v.y ^= 0x80008000u;
     }
+    return v;
+  };
+  for (int e = tid; e < NQT * kMmaSteps * 64; e += 64 * WPG) {
+    const int t = e / (kMmaSteps * 64), st = (e / 64) % kMmaSteps, ln = e & 63;
+    s_qa[t][st][ln] = qa_load(t, st, (uint32_t)ln);
   }
+  auto qa_raw = [&](int t, int st) -> uint4 { return s_qa[t][st][lane]; };
   __syncthreads();
 
   const float ws4 = a.sp.strata == MRL_STRATA_FULL64B ? a.sp.w_s4 : 0.0f;
@@ -2552,62 +2565,62 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
           acc[t][4 * g + 3] = c4.w;
         }
       }
-      // prefix: scale * cb[level], 8 dims per step; all 16 table reads go out first
+      // The vector operand of K-step st: prefix scale * cb[level] (8 dims per
+      // step, the 16 table reads issued together), S1 +-mid_n / 2 and S4
+      // +-hn w_s4 / 2 by bit (zero without a tail stage), then the error
+      // columns and offset * prefix_sum.
       const mma_h2 sc2 = __builtin_bit_cast(mma_h2, sc_b | (sc_b << 16));
       const uint32_t lw[4] = {cur.lev.x, cur.lev.y, cur.lev.z, cur.lev.w};
       uint32_t tv[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) tv[i] = s_tab[(lw[i >> 2] >> (8 * (i & 3))) & 255u];
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        uint32_t d[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          d[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(mma_h2, tv[4 * st + j]) * sc2);
-        const uint4 bo = make_uint4(d[0], d[1], d[2], d[3]);
-#pragma unroll
-        for (int t = 0; t < NQT; ++t)
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][st]), as_h8(bo), acc[t], 0, 0, 0);
-      }
-      // S1: +-mid_n / 2 by bit
       const uint32_t hp1 = f16_bits(0.5f * mid_n) * 0x10001u;
-#pragma unroll
-      for (int tt = 0; tt < 8; ++tt) {
-        const uint32_t nx = ~(tt < 4 ? cur.r1.x : cur.r1.y);
-        const int jb = 4 * (tt & 3);
+      const uint32_t hp4 = f16_bits(0.5f * hn * ws4) * 0x10001u;
+      auto vec_op = [&](int st) -> uint4 {
         uint32_t d[4];
+        if (st < 4) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) d[j] = hp1 | ((nx << (15 - jb - j)) & 0x80008000u);
-        const uint4 bo = make_uint4(d[0], d[1], d[2], d[3]);
+          for (int j = 0; j < 4; ++j)
+            d[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(mma_h2, tv[4 * st + j]) * sc2);
+        } else if (st < 12) {
+          const int tt = st - 4;
+          const uint32_t nx = ~(tt < 4 ? cur.r1.x : cur.r1.y);
+          const int jb = 4 * (tt & 3);
 #pragma unroll
-        for (int t = 0; t < NQT; ++t)
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][4 + tt]), as_h8(bo), acc[t], 0, 0, 0);
-      }
-      // S4: +-hn w_s4 / 2 by bit
-      if (ws4 != 0.0f) {
-        const uint32_t hp4 = f16_bits(0.5f * hn * ws4) * 0x10001u;
-        const uint32_t nx = ~cur.r4;
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-          uint32_t d[4];
+          for (int j = 0; j < 4; ++j) d[j] = hp1 | ((nx << (15 - jb - j)) & 0x80008000u);
+        } else if (st < 16) {
+          const int tt = st - 12;
+          const uint32_t nx = ~cur.r4;
 #pragma unroll
           for (int j = 0; j < 4; ++j) d[j] = hp4 | ((nx << (15 - 4 * tt - j)) & 0x80008000u);
-          const uint4 bo = make_uint4(d[0], d[1], d[2], d[3]);
+        } else {
+          d[0] = d[1] = d[2] = d[3] = 0u;
+          if (kh == 0) {
+            d[0] = (sc_b & 0x7fffu) | (f16_bits(mid_n) << 16);
+            d[1] = f16_bits(hn) | ((of_b & 0x7fffu) << 16);
+            d[2] = of_b;
+          }
+        }
+        return make_uint4(d[0], d[1], d[2], d[3]);
+      };
+      // The query operands of step st + 1 are requested before step st's
+      // MFMAs, so their LDS latency overlaps the matrix work.
+      uint4 an[NQT];
 #pragma unroll
-          for (int t = 0; t < NQT; ++t)
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][12 + tt]), as_h8(bo), acc[t], 0, 0, 0);
+      for (int t = 0; t < NQT; ++t) an[t] = qa_raw(t, 0);
+#pragma unroll
+      for (int st = 0; st < kMmaSteps; ++st) {
+        uint4 ac[NQT];
+#pragma unroll
+        for (int t = 0; t < NQT; ++t) ac[t] = an[t];
+        if (st + 1 < kMmaSteps) {
+#pragma unroll
+          for (int t = 0; t < NQT; ++t) an[t] = qa_raw(t, st + 1);
         }
-      }
-      {  // error columns and offset * prefix_sum
-        uint4 bo = make_uint4(0u, 0u, 0u, 0u);
-        if (kh == 0) {
-          bo.x = (sc_b & 0x7fffu) | (f16_bits(mid_n) << 16);
-          bo.y = f16_bits(hn) | ((of_b & 0x7fffu) << 16);
-          bo.z = of_b;
-        }
+        const uint4 bo = vec_op(st);
 #pragma unroll
         for (int t = 0; t < NQT; ++t)
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(qa[t][kMmaSteps - 1]), as_h8(bo), acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ac[t]), as_h8(bo), acc[t], 0, 0, 0);
       }
       // Register r of tile t holds query 32 t + 8 (r / 4) + 4 kh + r % 4.
       if constexpr (MODE == 0) {
@@ -2684,10 +2697,10 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
     atomicAdd(&s_stats[kStatPrefix], c_app);
   }
   if constexpr (MODE != 0) {
-    if (lane == 0) s_st.n[wave] = min(fill, (uint32_t)kMmaWaveCap);
+    if (lane == 0) s_st.n[wave] = min(fill, (uint32_t)Staging::kCap);
     __syncthreads();
-    for (int w = 0; w < 4; ++w)
-      for (uint32_t i = tid; i < s_st.n[w]; i += 256) atomicAdd(&s_st.cnt[s_st.q[w * kMmaWaveCap + i]], 1u);
+    for (int w = 0; w < WPG; ++w)
+      for (uint32_t i = tid; i < s_st.n[w]; i += 64 * WPG) atomicAdd(&s_st.cnt[s_st.q[w * Staging::kCap + i]], 1u);
     __syncthreads();
     if (tid < nq) {
       const uint32_t c = s_st.cnt[tid];
@@ -2699,9 +2712,9 @@ __global__ __launch_bounds__(256, 2) void k_scan_mma(ScanArgs a) {
       atomicAdd(a.stats + copy * kStatCount + tid, (unsigned long long)s_stats[tid]);
     }
     __syncthreads();
-    for (int w = 0; w < 4; ++w)
-      for (uint32_t i0 = tid; i0 < s_st.n[w]; i0 += 256) {
-        const uint32_t i = (uint32_t)w * kMmaWaveCap + i0;
+    for (int w = 0; w < WPG; ++w)
+      for (uint32_t i0 = tid; i0 < s_st.n[w]; i0 += 64 * WPG) {
+        const uint32_t i = (uint32_t)w * Staging::kCap + i0;
         const uint32_t qi = s_st.q[i];
         const uint32_t g = s_st.base[qi] + atomicAdd(&s_st.cnt[qi], 1u);
         if (g < a.seg_cap) {
@@ -3060,8 +3073,9 @@ hipError_t launch_mma_prep(const MmaPrepArgs& a, hipStream_t s, const LaunchEven
 // workgroups over the query chunks, at most one block per wave.
 uint32_t mma_scan_grid(const ScanArgs& a) {
   const uint32_t chunks = (a.n_q + kMmaQ - 1) / kMmaQ;
-  static const uint32_t res = resident_groups(k_scan_mma<2, 1>);
-  uint32_t grid = (2u * a.n_pos + 4) / 4;  // items: two 32-vector tiles per block
+  static const uint32_t res = resident_groups_n(k_scan_mma<2, 1>, kMmaWaves * 64);
+  const uint32_t wpg = kMmaWaves;
+  uint32_t grid = (2u * a.n_pos + wpg) / wpg;  // items: two 32-vector tiles per block
   uint32_t max_grid = res / chunks;
   if (max_grid < 1) max_grid = 1;
   if (grid > max_grid) grid = max_grid;
@@ -3070,17 +3084,17 @@ uint32_t mma_scan_grid(const ScanArgs& a) {
 
 hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const LaunchEvents& ev) {
   if (a.n_pos == 0 || a.n_q == 0) return hipSuccess;
-  const dim3 g(mma_scan_grid(a), (a.n_q + kMmaQ - 1) / kMmaQ);
+  const dim3 g(mma_scan_grid(a), (a.n_q + kMmaQ - 1) / kMmaQ), b(kMmaWaves * 64);
   const bool two = a.n_q > 32;  // one 32-query tile per wave suffices up to 32 queries
   if (mode == 0) {
-    if (two) launch(k_scan_mma<2, 0>, g, dim3(256), s, ev, a);
-    else launch(k_scan_mma<1, 0>, g, dim3(256), s, ev, a);
+    if (two) launch(k_scan_mma<2, 0>, g, b, s, ev, a);
+    else launch(k_scan_mma<1, 0>, g, b, s, ev, a);
   } else if (mode == 1) {
-    if (two) launch(k_scan_mma<2, 1>, g, dim3(256), s, ev, a);
-    else launch(k_scan_mma<1, 1>, g, dim3(256), s, ev, a);
+    if (two) launch(k_scan_mma<2, 1>, g, b, s, ev, a);
+    else launch(k_scan_mma<1, 1>, g, b, s, ev, a);
   } else {
-    if (two) launch(k_scan_mma<2, 2>, g, dim3(256), s, ev, a);
-    else launch(k_scan_mma<1, 2>, g, dim3(256), s, ev, a);
+    if (two) launch(k_scan_mma<2, 2>, g, b, s, ev, a);
+    else launch(k_scan_mma<1, 2>, g, b, s, ev, a);
   }
   return hipGetLastError();
 }
