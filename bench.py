@@ -7,11 +7,15 @@ selection, all enqueued on the library's stream with the index already in
 HBM.  Default workload: BASELINE configs[1] (1M x 768, EDEN-prod prefix,
 batch 1, K_cand 256).  --config 1..5 selects another BASELINE workload.
 
-`roofline` uses the dominant kernel's (k_scan) durations from HIP events that
-each dispatch records at its own start and end (hipExtLaunchKernelGGL), from
-a second run of the same steps after the timed one (events stay out of the
-timed region), on the library's stream; `traffic` is the committed
-rocprofv3 FETCH_SIZE + WRITE_SIZE reading for the same workload.
+`roofline` uses the dominant kernel's durations from HIP events that each
+dispatch records at its own start and end (hipExtLaunchKernelGGL), from a
+second run of the same steps after the timed one (events stay out of the
+timed region), on the library's stream; `traffic` is the committed rocprofv3
+FETCH_SIZE + WRITE_SIZE reading for the same workload.  Batch 1 (and batches
+under 8) run the one-query k_scan, HBM-bound: 4096 B per block scanned.
+Batches of 8+ run the MFMA-bounded scan, whose final pass (k_scan_mma over
+every block) dominates: 2 x 261 f16 MACs per (query, vector) pair against
+the dense f16 MFMA peak, with that launch's HBM rate beside it.
 `cpu_baseline` times the C restatement of the reference's scan_blocks
 (oracle/, Rayon-equivalent sharding on host threads) on query 0 of the same
 index, which also cross-checks the GPU top-K for that query.  `host_boundary`
@@ -30,6 +34,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "mrl-index-rust-vector_amd"))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFS = 2500.0  # dense f16 MFMA, MI355X
+# MACs per (query, vector) pair of the MFMA bound: 64 prefix dims, 128 S1
+# bits, 64 S4 bits and the 5 meta / error columns of the last K-step
+MMA_MACS_PER_PAIR = 64 + 128 + 64 + 5
 
 
 def log(msg):
@@ -136,20 +144,42 @@ def main():
     for (kind, p), g in sorted(groups.items()):
         kernels[f"{kind}[{p}]"] = {"avg_ms": float(np.mean(g["ms"])), "launches": len(g["ms"]),
                                    "avg_blocks": float(np.mean(g["blocks"])), "total_ms": float(np.sum(g["ms"]))}
-    # The dominant kernel is k_scan (every pass launches it); its roofline is
-    # taken over all of its launches, as rocprofv3's per-kernel average is:
-    # algorithmic bytes per launch = 4096 B x blocks scanned by that launch.
-    scan_ms = [ms for (kind, _), g in groups.items() if kind == "scan" for ms in g["ms"]]
-    scan_blk = [b for (kind, _), g in groups.items() if kind == "scan" for b in g["blocks"]]
-    avg_ms = float(np.mean(scan_ms))
-    bytes_per_launch = 4096.0 * float(np.mean(scan_blk))
-    achieved = bytes_per_launch / (avg_ms / 1000.0) / 1e9
-    traffic = committed_traffic(w.name)
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": traffic["bytes_per_launch"] if traffic else None,
-                "kernel": "k_scan", "launches_per_step": len(scan_ms) / prof_steps,
-                "kernel_avg_ms": round(avg_ms, 5), "algorithmic_bytes_per_launch": bytes_per_launch}
+    mma = any(kind == "mma_prep" for kind, _ in groups)
+    if not mma:
+        # One-query path: the dominant kernel is k_scan (every pass launches
+        # it); its roofline is taken over all of its launches, as rocprofv3's
+        # per-kernel average is: algorithmic bytes per launch = 4096 B x
+        # blocks scanned by that launch.
+        scan_ms = [ms for (kind, _), g in groups.items() if kind == "scan" for ms in g["ms"]]
+        scan_blk = [b for (kind, _), g in groups.items() if kind == "scan" for b in g["blocks"]]
+        avg_ms = float(np.mean(scan_ms))
+        bytes_per_launch = 4096.0 * float(np.mean(scan_blk))
+        achieved = bytes_per_launch / (avg_ms / 1000.0) / 1e9
+        traffic = committed_traffic("k_scan", w.name)
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": traffic["bytes_per_launch"] if traffic else None,
+                    "kernel": "k_scan", "launches_per_step": len(scan_ms) / prof_steps,
+                    "kernel_avg_ms": round(avg_ms, 5), "algorithmic_bytes_per_launch": bytes_per_launch}
+    else:
+        # MFMA path: the final pass (the highest pass index) scans every
+        # block once for every query of the batch.
+        final = max(p for kind, p in groups if kind == "scan")
+        g = groups[("scan", final)]
+        avg_ms = float(np.mean(g["ms"]))
+        pairs = 64.0 * float(np.mean(g["blocks"])) * nq
+        flops = 2.0 * MMA_MACS_PER_PAIR * pairs
+        achieved = flops / (avg_ms / 1000.0) / 1e12
+        bytes_per_launch = 4096.0 * float(np.mean(g["blocks"]))
+        hbm = bytes_per_launch / (avg_ms / 1000.0) / 1e9
+        traffic = committed_traffic("k_scan_mma", w.name)
+        roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
+                    "frac": round(achieved / MFMA_F16_PEAK_TFS, 4),
+                    "traffic": traffic["bytes_per_launch"] if traffic else None,
+                    "kernel": "k_scan_mma (final pass)", "launches_per_step": len(g["ms"]) / prof_steps,
+                    "kernel_avg_ms": round(avg_ms, 5), "algorithmic_flops_per_launch": flops,
+                    "algorithmic_bytes_per_launch": bytes_per_launch, "hbm_achieved_gb_s": round(hbm, 1),
+                    "hbm_frac": round(hbm / HBM_PEAK_GBS, 4)}
     if traffic:
         roofline["traffic_source"] = traffic["source"]
 
@@ -356,17 +386,18 @@ def copy_calibration(mib):
     print(json.dumps({"copy_bytes_per_dispatch": n, "dispatches": 5}), flush=True)
 
 
-def committed_traffic(workload):
-    """HBM bytes per k_scan launch for this workload, from the committed
+def committed_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` for this workload, from the committed
     rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the same
     counters' reading on a copy of known size); None when not measured."""
-    path = os.path.join(ROOT, "profiles", "k_scan_traffic.txt")
+    name = f"{kernel}_traffic.txt"
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     for line in open(path):
         f = line.split()
         if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == workload:
-            return {"bytes_per_launch": float(f[2]), "source": "profiles/k_scan_traffic.txt"}
+            return {"bytes_per_launch": float(f[2]), "source": f"profiles/{name}"}
     return None
 
 
