@@ -96,7 +96,11 @@ typedef struct mrl_time_range {
 /* ScanStats (src/scan.rs:270-278), summed over all queries of a call.  The
  * GPU prunes against its own running threshold, so prune counts are
  * reported, not compared; the per-stage masks of mrl_scan_fixed_tau are the
- * tau-independent comparison. */
+ * tau-independent comparison.  Calls of 8 or more queries on the
+ * MFMA-bounded path (RaBitQ mid-band, admissible weights) count
+ * after_prefix = pairs whose f16 bound reached the floor, after_s1 =
+ * after_s4_budget = pairs scored exactly, pushed = exactly scored pairs
+ * kept as candidates. */
 typedef struct mrl_scan_stats {
   uint64_t blocks;
   uint64_t active_vecs;
