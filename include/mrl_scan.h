@@ -243,6 +243,18 @@ int mrl_scan_fixed_tau(mrl_ctx *ctx, const mrl_index *index, const mrl_plans *pl
                        const mrl_scan_config *cfg, const mrl_time_range *time, const float *tau,
                        uint64_t *out_masks, float *out_prefix_ip, float *out_scores);
 
+/* Diagnostic of the batched path's MFMA bounds (no counterpart in the
+ * reference; it exposes the intermediate that batched mrl_scan calls prune
+ * on): for every (query, slot) pair, upper and lower bounds of the full
+ * score of src/scan.rs:453-634 with every stage run, from the f16 MFMA
+ * tiles.  Outputs are [query][block * 64 + slot]; inactive slots (tombstoned,
+ * time-filtered, past the corpus end) and queries with non-finite operands
+ * read NaN; slots beyond the operand range read +inf / -inf.  Requires the
+ * RaBitQ mid-band and a depth other than L0Only; at most 2^24 slots. */
+int mrl_scan_mma_bounds(mrl_ctx *ctx, const mrl_index *index, const mrl_plans *plans,
+                        const mrl_scan_config *cfg, const mrl_time_range *time, float *out_upper,
+                        float *out_lower);
+
 /* ---------------------------------------------------------------- */
 /* post-scan rerank (src/pipeline.rs:157-180, src/lowprec.rs:18-121) */
 /* ---------------------------------------------------------------- */

@@ -9,6 +9,7 @@
 #include <atomic>
 #include <map>
 #include <memory>
+#include <limits>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -1367,6 +1368,103 @@ extern "C" int mrl_scan_fixed_tau(mrl_ctx* ctx, const mrl_index* index, const mr
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   cleanup();
   if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("fixed-tau scan: ") + hipGetErrorString(e));
+  return MRL_OK;
+}
+
+// Every (query, slot) pair's MFMA bounds: k_mma_prep, then the single-pass
+// k_scan_mma (every active pair appended with its upper and lower bound) into
+// one segment per query with room for every slot; the host scatters the
+// appended pairs to out[q][row].  Pairs not appended (inactive slots, queries
+// with unusable operands) read NaN.
+extern "C" int mrl_scan_mma_bounds(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* plans,
+                                   const mrl_scan_config* cfg, const mrl_time_range* time, float* out_upper,
+                                   float* out_lower) {
+  if (!ctx || !index || !plans) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  uint32_t K;
+  int rc = check_cfg(cfg, &K);
+  if (rc) return rc;
+  const ScanParams sp = make_params(cfg, time);
+  if (plans->mid_codec != MRL_MID_RABITQ || sp.strata == MRL_STRATA_L0_ONLY)
+    return fail(MRL_ERR_INVALID_ARG, "MFMA bounds need the RaBitQ mid-band and an S1 stage");
+  const uint64_t nq = plans->n_q, B = index->n_blocks, N = B * 64;
+  if (!nq || !B) return MRL_OK;
+  if (!out_upper || !out_lower) return fail(MRL_ERR_INVALID_ARG, "null output");
+  if (N > (1ull << 24)) return fail(MRL_ERR_INVALID_ARG, "MFMA bounds dump is limited to 2^24 slots");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  float *d_u = nullptr, *d_l = nullptr, *d_consts = nullptr;
+  uint32_t *d_row = nullptr, *d_cnt = nullptr, *d_work = nullptr;
+  uint4* d_ops = nullptr;
+  auto cleanup = [&]() {
+    dev_free(d_u);
+    dev_free(d_l);
+    dev_free(d_row);
+    dev_free(d_cnt);
+    dev_free(d_ops);
+    dev_free(d_consts);
+    dev_free(d_work);
+  };
+  if (hipMalloc(&d_u, nq * N * 4) != hipSuccess || hipMalloc(&d_l, nq * N * 4) != hipSuccess ||
+      hipMalloc(&d_row, nq * N * 4) != hipSuccess || hipMalloc(&d_cnt, nq * 4) != hipSuccess ||
+      hipMalloc(&d_ops, nq * 2 * kMmaSteps * 16) != hipSuccess ||
+      hipMalloc(&d_consts, nq * kMcCount * 4) != hipSuccess || hipMalloc(&d_work, 16) != hipSuccess) {
+    cleanup();
+    return fail(MRL_ERR_OUT_OF_MEMORY, "bounds buffers");
+  }
+  MmaPrepArgs pa{};
+  pa.plans = plans->d_plans;
+  pa.luts = plans->d_luts;
+  pa.n_q = (uint32_t)nq;
+  pa.sp = sp;
+  pa.ops = d_ops;
+  pa.consts = d_consts;
+  pa.work = d_work;
+  ScanArgs a{};
+  a.idx = index->d_blocks;
+  a.rows1 = index->rows1();
+  a.rows4 = index->rows4();
+  a.n_blocks = B;
+  a.n_pos = (uint32_t)B;
+  a.shift = 0;
+  a.prev_shift = -1;
+  a.plans = plans->d_plans;
+  a.luts = plans->d_luts;
+  a.n_q = (uint32_t)nq;
+  a.flag_tabs = ctx->d_flag_tabs;
+  a.sp = sp;
+  a.cand_score = d_u;
+  a.cand_lower = d_l;
+  a.cand_row = d_row;
+  a.seg_count = d_cnt;
+  a.nseg = 1;
+  a.seg_cap = (uint32_t)N;
+  a.mma_ops = d_ops;
+  a.mma_consts = d_consts;
+  std::vector<uint32_t> cnt(nq);
+  std::vector<float> u(nq * N), l(nq * N);
+  std::vector<uint32_t> row(nq * N);
+  hipError_t e = hipMemsetAsync(d_cnt, 0, nq * 4, ctx->stream);
+  if (e == hipSuccess) e = launch_mma_prep(pa, ctx->stream);
+  if (e == hipSuccess) e = launch_scan_mma(a, 2, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(cnt.data(), d_cnt, nq * 4, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(u.data(), d_u, nq * N * 4, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(l.data(), d_l, nq * N * 4, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(row.data(), d_row, nq * N * 4, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  cleanup();
+  if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("MFMA bounds: ") + hipGetErrorString(e));
+  const float nan = std::numeric_limits<float>::quiet_NaN();
+  std::fill(out_upper, out_upper + nq * N, nan);
+  std::fill(out_lower, out_lower + nq * N, nan);
+  for (uint64_t q = 0; q < nq; ++q) {
+    if (cnt[q] > N) return fail(MRL_ERR_HIP, "MFMA bounds: more appends than slots");
+    for (uint64_t i = 0; i < cnt[q]; ++i) {
+      const uint32_t r = row[q * N + i];
+      if (r >= N) return fail(MRL_ERR_HIP, "MFMA bounds: row out of range");
+      out_upper[q * N + r] = u[q * N + i];
+      out_lower[q * N + r] = l[q * N + i];
+    }
+  }
   return MRL_OK;
 }
 

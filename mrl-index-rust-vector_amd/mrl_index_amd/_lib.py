@@ -181,6 +181,7 @@ SIGNATURES = {
     "mrl_results_fetch": (C.c_int, [_P, _P, _U64, _F, _U32, C.POINTER(ScanStatsC)]),
     "mrl_scan_fixed_tau": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), C.POINTER(TimeRangeC), _F, _U64,
                                      _F, _F]),
+    "mrl_scan_mma_bounds": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), C.POINTER(TimeRangeC), _F, _F]),
     "mrl_ctx_set_profiling": (C.c_int, [_P, C.c_int]),
     "mrl_ctx_profile_collect": (C.c_int, [_P, C.POINTER(KernelTimeC), C.c_uint32, _U32]),
     "mrl_encode_block": (C.c_int, [_F, C.c_uint32, C.c_uint32, _U32, _U32, C.POINTER(EdenFitC),

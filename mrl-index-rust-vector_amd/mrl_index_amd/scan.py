@@ -412,3 +412,23 @@ def scan_fixed_tau(blocks, plan: QueryPlan, cfg, tau, time_lo=None, time_hi=None
     finally:
         if owned:
             idx.close()
+
+
+def scan_mma_bounds(blocks, plan: QueryPlan, cfg, time_lo=None, time_hi=None):
+    """Upper and lower bounds of every (query, slot) pair's full score from
+    the batched path's f16 MFMA tiles (mrl_scan_mma_bounds): two float32
+    arrays [query, block * 64 + slot], NaN where a slot is inactive."""
+    sc = _scan_cfg(cfg)
+    idx, owned = _as_index(blocks, plan.device)
+    try:
+        nq, n = plan.n_queries, idx.block_count() * 64
+        up = np.zeros((nq, n), dtype=np.float32)
+        lo = np.zeros((nq, n), dtype=np.float32)
+        c = sc.to_c()
+        t = _time(time_lo, time_hi)
+        _lib.check(_lib.lib.mrl_scan_mma_bounds(plan.device.handle, idx.handle, plan.handle, C.byref(c), C.byref(t),
+                                                _lib.fptr(up), _lib.fptr(lo)))
+        return up, lo
+    finally:
+        if owned:
+            idx.close()
