@@ -1086,11 +1086,14 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   constexpr int kQdPer = L0 ? 1 : (QT * (kQData / 4) + 255) / 256;  // float4 per thread
   float4 qdv[kQdPer];
   if (!L0) {
+    // unconditional loads (the index clamped to the last element): the
+    // values stay in registers and no wait lands before the block loads
     const float4* src = reinterpret_cast<const float4*>(a.luts + (uint64_t)q0 * kQData);
+    const int lim = nq * (kQData / 4);
 #pragma unroll
     for (int k = 0; k < kQdPer; ++k) {
       const int e = tid + 256 * k;
-      if (e < nq * (kQData / 4)) qdv[k] = src[e];
+      qdv[k] = src[e < lim ? e : lim - 1];
     }
   }
   const float fr0 = a.flag_tabs[tid], fr1 = a.flag_tabs[256 + tid];
@@ -1705,7 +1708,7 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* ws, ui
 // when the histogram holds fewer than `need`.  Thread t takes scan
 // positions per*t .. per*t + per - 1, so neighbouring lanes read
 // neighbouring bins.
-__device__ void find_boundary(const uint32_t* hist, uint32_t nb, uint32_t need, bool desc,
+__device__ __forceinline__ void find_boundary(const uint32_t* hist, uint32_t nb, uint32_t need, bool desc,
                               uint32_t* out_bin, uint32_t* out_before, uint32_t* ws) {
   const uint32_t t = threadIdx.x, per = nb / blockDim.x;
   auto bin_at = [&](uint32_t pos) { return desc ? nb - 1 - pos : pos; };
@@ -1805,7 +1808,7 @@ __device__ __forceinline__ void for_each_pair(const CandView& v, F&& fn) {
 // their item counts into coff[0..nseg] (nseg <= blockDim.x): thread t holds
 // counter t (`count`, 0 past nseg); wave scans, then a scan of the wave
 // totals (ws: 2 * 16 words).
-__device__ void seg_offsets(uint32_t count, uint32_t nseg, uint32_t seg_cap, uint32_t* off, uint32_t* coff,
+__device__ __forceinline__ void seg_offsets(uint32_t count, uint32_t nseg, uint32_t seg_cap, uint32_t* off, uint32_t* coff,
                             uint32_t* ws) {
   const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
   const uint32_t c = count < seg_cap ? count : seg_cap;
@@ -1865,7 +1868,7 @@ __device__ __forceinline__ void for_each_pair_short(const CandView& v, F&& fn) {
 }
 
 // LDS histogram of the appended scores of one query (all segments).
-__device__ void build_hist(uint32_t* hist, const CandView& v) {
+__device__ __forceinline__ void build_hist(uint32_t* hist, const CandView& v) {
   for (int i = threadIdx.x; i < kHistBins; i += blockDim.x) hist[i] = 0u;
   __syncthreads();
   for_each_cand(v, [&](float sc, uint32_t) { atomicAdd(&hist[hist_bin(sc)], 1u); });
@@ -1877,7 +1880,7 @@ __device__ __forceinline__ uint64_t composite(uint32_t key, uint32_t row) {
 }
 
 // Descending bitonic sort of s[0..n2) (n2 a power of two).
-__device__ void bitonic_desc(uint64_t* s, int n2) {
+__device__ __forceinline__ void bitonic_desc(uint64_t* s, int n2) {
   for (int size = 2; size <= n2; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
       for (int i = threadIdx.x; i < n2 / 2; i += blockDim.x) {
