@@ -153,10 +153,9 @@ struct ProfScope {
 struct mrl_index {
   mrl_ctx* ctx = nullptr;
   uint8_t* d_blocks = nullptr;
-  uint8_t* d_rows = nullptr;  // each slot's S1 bits (uint4), then each slot's S4 bits (uint2)
+  uint4* d_recs = nullptr;  // each slot's 64-byte record (kRecWords uint4, slot-major)
   uint64_t n_blocks = 0;
-  uint4* rows1() const { return reinterpret_cast<uint4*>(d_rows); }
-  uint2* rows4() const { return reinterpret_cast<uint2*>(d_rows + n_blocks * 64 * 16); }
+  const uint4* recs() const { return d_recs; }
   std::map<uint32_t, LevelPlan> levels;
 };
 
@@ -354,15 +353,15 @@ extern "C" int mrl_index_upload(mrl_ctx* ctx, const void* blocks, uint64_t n_blo
     const size_t bytes = (size_t)n_blocks * kBlockBytes;
     uint8_t* staging = nullptr;
     if (hipMalloc(&ix->d_blocks, bytes) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc index");
-    if (hipMalloc(&ix->d_rows, (size_t)n_blocks * 64 * 24) != hipSuccess) {
+    if (hipMalloc(&ix->d_recs, (size_t)n_blocks * 64 * kRecWords * 16) != hipSuccess) {
       dev_free(ix->d_blocks);
-      return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc index rows");
+      return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc index records");
     }
     // stage in chunks of at most 256 MiB so the transient copy stays small
     const uint64_t chunk = std::min<uint64_t>(n_blocks, 65536);
     if (hipMalloc(&staging, chunk * kBlockBytes) != hipSuccess) {
       dev_free(ix->d_blocks);
-      dev_free(ix->d_rows);
+      dev_free(ix->d_recs);
       return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc staging");
     }
     for (uint64_t b = 0; b < n_blocks; b += chunk) {
@@ -370,13 +369,13 @@ extern "C" int mrl_index_upload(mrl_ctx* ctx, const void* blocks, uint64_t n_blo
       hipError_t e = hipMemcpyAsync(staging, src + b * kBlockBytes, nb * kBlockBytes, hipMemcpyHostToDevice,
                                     ctx->stream);
       if (e == hipSuccess)
-        e = launch_relayout(staging, ix->d_blocks + b * kBlockBytes, nb, true, ctx->stream, ix->rows1() + b * 64,
-                            ix->rows4() + b * 64);
+        e = launch_relayout(staging, ix->d_blocks + b * kBlockBytes, nb, true, ctx->stream,
+                            ix->d_recs + b * 64 * kRecWords);
       if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
       if (e != hipSuccess) {
         dev_free(staging);
         dev_free(ix->d_blocks);
-        dev_free(ix->d_rows);
+        dev_free(ix->d_recs);
         return fail(MRL_ERR_HIP, std::string("upload: ") + hipGetErrorString(e));
       }
     }
@@ -447,7 +446,7 @@ extern "C" void mrl_index_destroy(mrl_index* index) {
   (void)hipSetDevice(index->ctx->device);
   (void)hipStreamSynchronize(index->ctx->stream);
   dev_free(index->d_blocks);
-  dev_free(index->d_rows);
+  dev_free(index->d_recs);
   delete index;
 }
 
@@ -864,8 +863,7 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
   }
   ScanArgs a{};
   a.idx = ix->d_blocks;
-  a.rows1 = ix->rows1();
-  a.rows4 = ix->rows4();
+  a.recs = ix->recs();
   a.n_blocks = B;
   a.prev_shift = -1;
   a.plans = plans->d_plans + plans_first;
@@ -911,8 +909,7 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
   FinishArgs fa{};
   fa.idx = ix->d_blocks;
   fa.n_blocks = B;
-  fa.rows1 = ix->rows1();
-  fa.rows4 = ix->rows4();
+  fa.recs = ix->recs();
   fa.plans = plans->d_plans + plans_first;
   fa.luts = plans->d_luts + (size_t)plans_first * kQData;
   fa.mma_consts = pb.mma_consts;
@@ -974,8 +971,7 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
     if (rerun_safe && !last) continue;
     ScanArgs a{};
     a.idx = ix->d_blocks;
-    a.rows1 = ix->rows1();
-    a.rows4 = ix->rows4();
+    a.recs = ix->recs();
     a.n_blocks = ix->n_blocks;
     a.n_pos = lp.passes[pi].n_pos;
     a.shift = lp.passes[pi].shift;
@@ -1421,8 +1417,7 @@ extern "C" int mrl_scan_mma_bounds(mrl_ctx* ctx, const mrl_index* index, const m
   pa.work = d_work;
   ScanArgs a{};
   a.idx = index->d_blocks;
-  a.rows1 = index->rows1();
-  a.rows4 = index->rows4();
+  a.recs = index->recs();
   a.n_blocks = B;
   a.n_pos = (uint32_t)B;
   a.shift = 0;
@@ -2036,16 +2031,16 @@ extern "C" int mrl_index_from_device(mrl_ctx* ctx, const void* d_blocks, uint64_
   if (n_blocks) {
     if (hipMalloc(&ix->d_blocks, (size_t)n_blocks * kBlockBytes) != hipSuccess)
       return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc index");
-    if (hipMalloc(&ix->d_rows, (size_t)n_blocks * 64 * 24) != hipSuccess) {
+    if (hipMalloc(&ix->d_recs, (size_t)n_blocks * 64 * kRecWords * 16) != hipSuccess) {
       dev_free(ix->d_blocks);
-      return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc index rows");
+      return fail(MRL_ERR_OUT_OF_MEMORY, "hipMalloc index records");
     }
     hipError_t e = launch_relayout(static_cast<const uint8_t*>(d_blocks), ix->d_blocks, n_blocks, true, ctx->stream,
-                                   ix->rows1(), ix->rows4());
+                                   ix->d_recs);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
       dev_free(ix->d_blocks);
-      dev_free(ix->d_rows);
+      dev_free(ix->d_recs);
       return fail(MRL_ERR_HIP, std::string("index from device: ") + hipGetErrorString(e));
     }
   }

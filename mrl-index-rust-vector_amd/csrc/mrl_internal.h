@@ -122,6 +122,13 @@ constexpr int kSegs = 16;
 // workgroup writes its count with a plain store, no atomic.
 constexpr int kMaxSegs = 512;
 constexpr int kHistBins = 2048;
+// Per-slot records beside the blocks (64 B = 4 uint4 per slot, slot-major):
+// everything one slot's stages read, in one line.  kRecLev0 / kRecLev1: the
+// slot's level words 0..3 / 4..7 (nibble i of word j = dim 8j + i); kRecS1:
+// its S1 bits (dword k = dims 32k..32k+31); kRecS4Meta: {S4 dword 0, S4
+// dword 1, scale | offset << 16, tail_norm | flags << 16} (f16 bits).
+constexpr int kRecWords = 4;
+constexpr int kRecLev0 = 0, kRecLev1 = 1, kRecS1 = 2, kRecS4Meta = 3;
 
 // MFMA-bounded batched scan (k_mma_prep, k_scan_mma, k_mma_floors, k_finish).
 // Each (vector, query) pair gets an upper and a lower bound of the full score
@@ -159,8 +166,7 @@ struct MmaPrepArgs {
 
 struct ScanArgs {
   const uint8_t* idx;          // device-layout blocks
-  const uint4* rows1;          // [n_blocks * 64] each slot's S1 bits (dword k: dims 32k..32k+31)
-  const uint2* rows4;          // [n_blocks * 64] each slot's S4 bits
+  const uint4* recs;           // [n_blocks * 64 * kRecWords] each slot's record (kRecLev0 ..)
   uint64_t n_blocks;
   // Blocks of this pass: b = pos << shift for pos < n_pos, except those an
   // earlier pass covered (prev_shift >= 0 and b a multiple of 1 << prev_shift).
@@ -212,8 +218,7 @@ constexpr int kExactItem = 256;   // list entries per k_exact work item (one per
 struct FinishArgs {
   const uint8_t* idx;
   uint64_t n_blocks;
-  const uint4* rows1;
-  const uint2* rows4;
+  const uint4* recs;
   const mrl_query_plan* plans;
   const float* luts;
   const float* mma_consts;
@@ -319,9 +324,9 @@ struct LaunchEvents {
   hipEvent_t stop = nullptr;
 };
 
-// to_device also writes each slot's own S1 / S4 bits (rows1 / rows4, may be null).
+// to_device also writes each slot's record (recs, may be null).
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device, hipStream_t s,
-                           uint4* rows1 = nullptr, uint2* rows4 = nullptr);
+                           uint4* recs = nullptr);
 hipError_t launch_plan(const PlanArgs& a, hipStream_t s, const LaunchEvents& ev = {});
 int scan_query_tile(uint32_t n_q);  // queries per workgroup of the non-tile kernels
 uint32_t scan_grid(const ScanArgs& a, bool diag);

@@ -145,7 +145,7 @@ __device__ __forceinline__ float masked_accumulate(float s, uint64_t m, const CO
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void k_relayout_to_device(const uint8_t* __restrict__ src,
                                                           uint8_t* __restrict__ dst, uint64_t n_blocks,
-                                                          uint4* __restrict__ rows1, uint2* __restrict__ rows4) {
+                                                          uint4* __restrict__ recs) {
   const uint32_t v = threadIdx.x;
   for (uint64_t b = blockIdx.x; b < n_blocks; b += gridDim.x) {
     const uint8_t* s = src + b * kBlockBytes;
@@ -160,6 +160,7 @@ __global__ __launch_bounds__(64) void k_relayout_to_device(const uint8_t* __rest
     const uint64_t* s2 = reinterpret_cast<const uint64_t*>(s + kOrigS2);
     const uint64_t* s3 = reinterpret_cast<const uint64_t*>(s + kOrigS3);
     const uint64_t* s5 = reinterpret_cast<const uint64_t*>(s + kOrigS5);
+    uint32_t lw[8];
     for (int j = 0; j < 8; ++j) {
       uint32_t w = 0;
       for (int i = 0; i < 8; ++i) {
@@ -168,6 +169,7 @@ __global__ __launch_bounds__(64) void k_relayout_to_device(const uint8_t* __rest
                        ((uint32_t)((s2[dim] >> v) & 1u) << 2) | ((uint32_t)((s0[dim] >> v) & 1u) << 3);
         w |= lvl << (4 * i);
       }
+      lw[j] = w;
       reinterpret_cast<uint32_t*>(d + kDevNibbles)[8 * v + j] = w;
     }
     const uint64_t* s1 = reinterpret_cast<const uint64_t*>(s + kOrigS1);
@@ -177,8 +179,9 @@ __global__ __launch_bounds__(64) void k_relayout_to_device(const uint8_t* __rest
     d1[v] = s1[v];
     d1[v + 64] = s1[v + 64];
     d4[v] = s4[v];
-    if (rows1) {
-      // slot v's own S1 / S4 bits: dword k holds dims 32k..32k+31, bit i = dim 32k + i
+    if (recs) {
+      // slot v's record: its level words, then its own S1 / S4 bits (dword k
+      // holds dims 32k..32k+31, bit i = dim 32k + i), then its meta
       uint32_t r[6];
 #pragma unroll
       for (int k = 0; k < 6; ++k) {
@@ -187,8 +190,12 @@ __global__ __launch_bounds__(64) void k_relayout_to_device(const uint8_t* __rest
         for (int i = 0; i < 32; ++i) w |= (uint32_t)((pl[i] >> v) & 1u) << i;
         r[k] = w;
       }
-      rows1[b * 64 + v] = make_uint4(r[0], r[1], r[2], r[3]);
-      rows4[b * 64 + v] = make_uint2(r[4], r[5]);
+      uint4* rec = recs + (b * 64 + v) * kRecWords;
+      rec[kRecLev0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+      rec[kRecLev1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+      rec[kRecS1] = make_uint4(r[0], r[1], r[2], r[3]);
+      rec[kRecS4Meta] = make_uint4(r[4], r[5], (uint32_t)(m[0] | (m[1] << 8)) | ((uint32_t)(m[2] | (m[3] << 8)) << 16),
+                                   (uint32_t)(m[4] | (m[5] << 8)) | ((uint32_t)m[6] << 16));
     }
   }
 }
@@ -951,7 +958,7 @@ __device__ __forceinline__ void flush_appends(Staging<DIAG ? 1 : QT>& st, const 
 // One-query scans defer the S1 / S4 stages: the prefix stage's survivors of
 // each block wait in a per-wave queue, and once 64 are queued they are
 // finished together with lane = survivor, from each slot's own S1 / S4 bits
-// (rows1 / rows4).  A survivor's stage sums are the same additions in the same
+// (its record).  A survivor's stage sums are the same additions in the same
 // order as the exec-masked form (a clear bit adds -0.0, which leaves every
 // value unchanged, as skipping it does).
 struct DeferQ {
@@ -1008,8 +1015,10 @@ __device__ __forceinline__ void defer_flush(const DeferQ& dq, uint32_t qn, const
     mid_n = dq.mid_n[lane];
     high_n = dq.high_n[lane];
     offset = dq.offset[lane];
-    r1 = a.rows1[row];
-    r4 = a.rows4[row];
+    const uint4* rec = a.recs + (uint64_t)row * kRecWords;
+    r1 = rec[kRecS1];
+    const uint4 x = rec[kRecS4Meta];
+    r4 = make_uint2(x.x, x.y);
   }
   const bool b1 = p->mid_codec == MRL_MID_EDEN_B1;
   const uint32_t bits1[4] = {r1.x, r1.y, r1.z, r1.w};
@@ -2336,17 +2345,17 @@ struct MmaRaw {
   uint32_t hdr;   // lanes 0..3: header dwords 0, 1, 4, 5
 };
 
-__device__ __forceinline__ MmaRaw mma_load(const uint8_t* idx, const uint4* rows1, const uint2* rows4, uint64_t b,
-                                           uint32_t h) {
+__device__ __forceinline__ MmaRaw mma_load(const uint8_t* idx, const uint4* recs, uint64_t b, uint32_t h) {
   const uint32_t lane = __lane_id(), kh = lane >> 5, v = 32u * h + (lane & 31u);
   const uint8_t* blk = idx + b * kBlockBytes;
-  const uint16_t* m16 = reinterpret_cast<const uint16_t*>(blk);
+  const uint4* rec = recs + (b * 64u + v) * kRecWords;
   MmaRaw r;
-  r.lev = *reinterpret_cast<const uint4*>(blk + kDevNibbles + 32u * v + 16u * kh);
-  r.r1 = reinterpret_cast<const uint2*>(rows1 + b * 64u + v)[kh];
-  r.r4 = reinterpret_cast<const uint32_t*>(rows4 + b * 64u + v)[kh];
-  r.meta = (uint32_t)m16[kDevScale / 2 + v] | ((uint32_t)m16[kDevOffset / 2 + v] << 16);
-  r.tf = (uint32_t)m16[kDevTail / 2 + v] | ((uint32_t)blk[kDevFlags + v] << 16);
+  r.lev = rec[kRecLev0 + kh];
+  r.r1 = reinterpret_cast<const uint2*>(rec + kRecS1)[kh];
+  const uint4 x = rec[kRecS4Meta];
+  r.r4 = kh ? x.y : x.x;
+  r.meta = x.z;
+  r.tf = x.w;
   const uint32_t hw = lane < 2 ? lane : (lane < 4 ? lane + 2 : 0);
   r.hdr = reinterpret_cast<const uint32_t*>(blk)[hw];
   return r;
@@ -2438,7 +2447,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   const uint32_t n_it = first < stride ? n_items : 0u;
   uint32_t it_cur = first;
   MmaRaw cur{};
-  if (first < n_it) cur = mma_load(a.idx, a.rows1, a.rows4, (uint64_t)(first >> 1) << a.shift, first & 1u);
+  if (first < n_it) cur = mma_load(a.idx, a.recs, (uint64_t)(first >> 1) << a.shift, first & 1u);
 
   if (tid < 256) {  // byte -> (f16 cb[low nibble], f16 cb[high nibble])
     const mrl_query_plan* p0 = a.plans + q0;
@@ -2528,7 +2537,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
 
   for (uint32_t it = first; it < n_it; it += stride) {
     const uint32_t it_nxt = it + stride < n_it ? it + stride : it_cur;
-    const MmaRaw nxt = mma_load(a.idx, a.rows1, a.rows4, (uint64_t)(it_nxt >> 1) << a.shift, it_nxt & 1u);
+    const MmaRaw nxt = mma_load(a.idx, a.recs, (uint64_t)(it_nxt >> 1) << a.shift, it_nxt & 1u);
     const uint32_t b = (it_cur >> 1) << a.shift, h = it_cur & 1u;
     const uint32_t min_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 0);
     const uint32_t max_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 1);
@@ -2736,17 +2745,14 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
 // drops such a vector before it is pushed.
 __device__ bool exact_full(const FinishArgs& a, const mrl_query_plan* p, uint32_t row, const float* lut,
                            const float* w1, const float* w4, float* out) {
-  const uint64_t b = row >> 6;
-  const uint32_t v = row & 63u;
-  const uint8_t* blk = a.idx + b * kBlockBytes;
-  const uint16_t* m16 = reinterpret_cast<const uint16_t*>(blk);
+  // the slot's record: one 64-byte line holds every value the stages read
+  const uint4* rec = a.recs + (uint64_t)row * kRecWords;
+  const uint4 n0 = rec[kRecLev0], n1 = rec[kRecLev1], r1 = rec[kRecS1], x = rec[kRecS4Meta];
   LaneBlock m;
-  m.scale = h2f(m16[kDevScale / 2 + v]);
-  m.offset = h2f(m16[kDevOffset / 2 + v]);
-  m.tail = h2f(m16[kDevTail / 2 + v]);
-  const uint32_t flags = blk[kDevFlags + v];
-  const uint4* nibq = reinterpret_cast<const uint4*>(blk + kDevNibbles) + 2u * v;
-  const uint4 n0 = nibq[0], n1 = nibq[1];
+  m.scale = h2f((uint16_t)(x.z & 0xFFFFu));
+  m.offset = h2f((uint16_t)(x.z >> 16));
+  m.tail = h2f((uint16_t)(x.w & 0xFFFFu));
+  const uint32_t flags = (x.w >> 16) & 0xFFu;
   m.nib[0] = n0.x;
   m.nib[1] = n0.y;
   m.nib[2] = n0.z;
@@ -2768,7 +2774,6 @@ __device__ bool exact_full(const FinishArgs& a, const mrl_query_plan* p, uint32_
   if (ub1 != ub1) return false;
   float score = prefix_ip;
   // Stage: mid-band 1-bit IP (scan.rs:553-568)
-  const uint4 r1 = a.rows1[row];
   const uint32_t bits1[4] = {r1.x, r1.y, r1.z, r1.w};
   const float s1 = row_sum<4>(p->rabitq_base, bits1, w1);
   score = score + s1 * mid_n;
@@ -2781,8 +2786,7 @@ __device__ bool exact_full(const FinishArgs& a, const mrl_query_plan* p, uint32_
       if (ub3 != ub3) return false;
     }
     if (p->has_tail_fold) {  // scan.rs:610-634
-      const uint2 r4 = a.rows4[row];
-      const uint32_t bits4[2] = {r4.x, r4.y};
+      const uint32_t bits4[2] = {x.x, x.y};
       const float s4 = row_sum<2>(p->tail_fold_base, bits4, w4);
       score = score + s4 * hn * a.sp.w_s4;
     }
@@ -2908,34 +2912,53 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(FinishArgs a) {
 // of the query; a NaN score sets the query's error flag, as a NaN survivor
 // does on the exact path.
 __global__ __launch_bounds__(kExactItem) void k_exact(FinishArgs a) {
-  __shared__ __align__(16) float s_lut[1024];
-  __shared__ __align__(16) float s_w1[128];
-  __shared__ __align__(16) float s_w4[64];
+  // the query's LUT (1024 floats), then its S1 (128) and S4 (64) weights:
+  // the first 1216 floats of its scan data, 304 float4
+  __shared__ __align__(16) float4 s_qd4[(kQdW4 + 64) / 4];
+  static_assert(kQdLut == 0 && kQdW1 == 1024 && kQdW4 == 1152, "scan data layout");
+  const float* s_lut = reinterpret_cast<const float*>(s_qd4);
   const uint32_t n_items = a.work[0];
   const int tid = threadIdx.x;
   const uint32_t lane = __lane_id();
-  for (uint32_t item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const uint32_t wi = a.work[2 + item];
+  // A contiguous run of items per workgroup: the items of one query are
+  // published together, so the query's tables are loaded once per run.
+  const uint32_t per = (n_items + gridDim.x - 1) / gridDim.x;
+  const uint32_t i0 = blockIdx.x * per, i1 = min(i0 + per, n_items);
+  uint32_t q_have = ~0u;
+  uint32_t wi = i0 < i1 ? a.work[2 + i0] : 0u;
+  for (uint32_t item = i0; item < i1; ++item) {
     const uint32_t q = wi >> 8, c = wi & 255u;
+    // next item's descriptor, in flight during this one
+    wi = item + 1 < i1 ? a.work[2 + item + 1] : 0u;
     if (q >= a.n_q) continue;
     const uint64_t qbase = (uint64_t)q * a.nseg * a.seg_cap;
     const uint32_t* list = reinterpret_cast<const uint32_t*>(a.cand_lower + qbase);
-    const uint32_t nf = min(list[0], (uint32_t)kFinCap);
-    if (c * (uint32_t)kExactItem >= nf) continue;
-    __syncthreads();  // the previous item's table reads are done
-    const float* qd = a.luts + (uint64_t)q * kQData;
-    for (int i = tid; i < 1024; i += kExactItem) s_lut[i] = qd[kQdLut + i];
-    if (tid < 128) s_w1[tid] = qd[kQdW1 + tid];
-    if (tid < 64) s_w4[tid] = qd[kQdW4 + tid];
-    __syncthreads();
+    // the count, this thread's row (read whether or not it is below the
+    // count: the list area holds 1 + kFinCap entries), the floor and the
+    // tables all go out together
     const uint32_t i = c * (uint32_t)kExactItem + (uint32_t)tid;
+    const uint32_t nf_raw = list[0];
+    const uint32_t row_raw = list[1 + min(i, (uint32_t)kFinCap - 1u)];
     const float floor_t = a.tau_final ? a.tau_final[q] : -INFINITY;
+    if (q != q_have) {
+      const float4* qd4 = reinterpret_cast<const float4*>(a.luts + (uint64_t)q * kQData);
+      const float4 v0 = qd4[tid];
+      const float4 v1 = qd4[kExactItem + (tid < 48 ? tid : 0)];
+      __syncthreads();  // the previous query's table reads are done
+      s_qd4[tid] = v0;
+      if (tid < 48) s_qd4[kExactItem + tid] = v1;
+      __syncthreads();
+      q_have = q;
+    }
+    const uint32_t nf = min(nf_raw, (uint32_t)kFinCap);
+    if (c * (uint32_t)kExactItem >= nf) continue;
     bool keep = false;
     float sc = 0.0f;
     uint32_t row = 0u;
     if (i < nf) {
-      row = list[1 + i];
-      if ((uint64_t)(row >> 6) < a.n_blocks && exact_full(a, a.plans + q, row, s_lut, s_w1, s_w4, &sc)) {
+      row = row_raw;
+      if ((uint64_t)(row >> 6) < a.n_blocks &&
+          exact_full(a, a.plans + q, row, s_lut, s_lut + kQdW1, s_lut + kQdW4, &sc)) {
         if (sc != sc) atomicOr(a.err + q, 1u);
         else keep = sc >= floor_t;
       }
@@ -2964,11 +2987,11 @@ __global__ __launch_bounds__(kExactItem) void k_exact(FinishArgs a) {
 // host launchers
 // ---------------------------------------------------------------------------
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device,
-                           hipStream_t s, uint4* rows1, uint2* rows4) {
+                           hipStream_t s, uint4* recs) {
   if (n_blocks == 0) return hipSuccess;
   uint32_t grid = (uint32_t)(n_blocks < 65536 ? n_blocks : 65536);
   if (to_device)
-    hipLaunchKernelGGL(k_relayout_to_device, dim3(grid), dim3(64), 0, s, src, dst, n_blocks, rows1, rows4);
+    hipLaunchKernelGGL(k_relayout_to_device, dim3(grid), dim3(64), 0, s, src, dst, n_blocks, recs);
   else hipLaunchKernelGGL(k_relayout_to_host, dim3(grid), dim3(64), 0, s, src, dst, n_blocks);
   return hipGetLastError();
 }
