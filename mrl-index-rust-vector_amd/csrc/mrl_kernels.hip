@@ -2370,20 +2370,54 @@ struct MmaStaging {
   static constexpr int kWaves = W;
   static constexpr int kCap = CAP;  // entries per wave
   uint32_t n[W];
-  uint32_t cnt[kMmaQ];
+  uint32_t cnt[kMmaQ];      // final flush: entries per query of the workgroup
   uint32_t base[kMmaQ];
+  uint32_t wcnt[W][kMmaQ];  // a wave's own flush: entries per query
+  uint32_t wbase[W][kMmaQ];
   uint32_t row[W * CAP];
-  float u[W * CAP];
-  float l[W * CAP];
+  float acc[W * CAP];       // tile value; the bounds are formed when the entry is written out
   uint8_t q[W * CAP];
 };
 
 // Appends (u, l, row) of query q0 + qi (per lane) for the lanes in pm to this
 // wave's region at *fill (wave-uniform); past the region's room, straight
 // into the query's segment (one global atomic per lane).
+// Bounds (U, L) of a staged pair from its tile value acc = s (U' - tau): the
+// query's constants qk = {tau, 1/s, eP, e1, e4, eO, e0, ok} and the slot's
+// meta from its record.  A slot beyond the operand range gets (+inf, -inf).
+__device__ __forceinline__ void mma_bounds(float acc, const uint4* recs, uint32_t row, const float* qk,
+                                           const float* s_flag, float* U, float* L) {
+  const uint4 x = recs[(uint64_t)row * kRecWords + kRecS4Meta];
+  const float m_scale = h2f((uint16_t)(x.z & 0xffffu)), m_offset = h2f((uint16_t)(x.z >> 16));
+  const float tn = fmaxf(h2f((uint16_t)(x.w & 0xffffu)), 0.0f);
+  const uint32_t fl = (x.w >> 16) & 0xffu;
+  const float mid_n = fmaxf(s_flag[256 + fl] * tn, 1e-6f);
+  const float hn = fmaxf(fmaxf(s_flag[fl] * tn, 0.0f), 1e-6f);
+  const bool safe = fabsf(m_scale) <= kMmaSafe && mid_n <= kMmaSafe && hn <= kMmaSafe && fabsf(m_offset) <= kMmaSafe;
+  float u = INFINITY, l = -INFINITY;
+  if (safe) {
+    const float4 k0 = *reinterpret_cast<const float4*>(qk);      // tau, 1/s, eP, e1
+    const float4 k1 = *reinterpret_cast<const float4*>(qk + 4);  // e4, eO, e0, ok
+    const float tau = k0.x;
+    const float u0 = tau + acc * k0.y;
+    const float E = fabsf(m_scale) * k0.z + mid_n * k0.w + hn * k1.x + fabsf(m_offset) * k1.y + k1.z;
+    const float mg = (fabsf(u0) + fabsf(tau)) * (1.0f / 4194304.0f);
+    u = u0 + mg;
+    l = (u0 - 2.0f * E * (1.0f + 1.0f / 1048576.0f)) - mg;
+    if (!(u == u)) u = INFINITY;
+    if (!(l == l)) l = -INFINITY;
+  }
+  *U = u;
+  *L = l;
+}
+
+// Stages the pairs of pm (one query per lane: qi) as (row, tile value, query)
+// in this wave's region; past its end they go straight to the query's
+// segment, bounds formed here.
 template <typename ST>
-__device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, int wave, uint32_t* fill, uint32_t q0,
-                                           uint32_t qi, uint32_t seg, uint64_t pm, float u, float l, uint32_t row) {
+__device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, const float (*s_qk)[8], const float* s_flag,
+                                           int wave, uint32_t* fill, uint32_t q0, uint32_t qi, uint32_t seg,
+                                           uint64_t pm, float acc, uint32_t row) {
   const uint32_t lane = __lane_id();
   const uint32_t base = *fill;
   *fill = base + (uint32_t)__popcll(pm);
@@ -2392,8 +2426,7 @@ __device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, int wave, 
   if (slot < (uint32_t)ST::kCap) {
     const uint32_t e = (uint32_t)wave * ST::kCap + slot;
     st.row[e] = row;
-    st.u[e] = u;
-    st.l[e] = l;
+    st.acc[e] = acc;
     st.q[e] = (uint8_t)qi;
   } else {
     // (the query index passes through an empty asm so the compiler cannot
@@ -2403,12 +2436,57 @@ __device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, int wave, 
     const uint64_t sq = (uint64_t)qq * a.nseg + seg;
     const uint32_t g = atomicAdd(a.seg_count + sq, 1u);
     if (g < a.seg_cap) {
+      float u, l;
+      mma_bounds(acc, a.recs, row, s_qk[qq - q0], s_flag, &u, &l);
       const uint64_t i = sq * a.seg_cap + g;
       a.cand_score[i] = u;
       a.cand_lower[i] = l;
       a.cand_row[i] = row;
     }
   }
+}
+
+// Writes out the n entries of this wave's region: a count per query in LDS,
+// one global reservation per query with entries, then each entry's bounds.
+template <typename ST>
+__device__ __forceinline__ void mma_wave_flush(ST& st, const ScanArgs& a, const float (*s_qk)[8],
+                                               const float* s_flag, int wave, uint32_t n, uint32_t q0,
+                                               uint32_t seg) {
+  constexpr int kPer = ST::kCap / 64;
+  const uint32_t lane = __lane_id();
+  uint32_t* cnt = st.wcnt[wave];
+  uint32_t* base = st.wbase[wave];
+  cnt[lane] = 0u;
+  wave_lds_sync();
+  uint32_t rk[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t e = lane + 64u * (uint32_t)k;
+    rk[k] = e < n ? atomicAdd(&cnt[st.q[(uint32_t)wave * ST::kCap + e]], 1u) : 0u;
+  }
+  wave_lds_sync();
+  const uint32_t c = cnt[lane];
+  base[lane] = c ? atomicAdd(a.seg_count + (uint64_t)(q0 + lane) * a.nseg + seg, c) : 0u;
+  wave_lds_sync();
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t e = lane + 64u * (uint32_t)k;
+    if (e < n) {
+      const uint32_t i = (uint32_t)wave * ST::kCap + e;
+      const uint32_t qi = st.q[i];
+      const uint32_t g = base[qi] + rk[k];
+      if (g < a.seg_cap) {
+        const uint32_t row = st.row[i];
+        float u, l;
+        mma_bounds(st.acc[i], a.recs, row, s_qk[qi], s_flag, &u, &l);
+        const uint64_t o = ((uint64_t)(q0 + qi) * a.nseg + seg) * a.seg_cap + g;
+        a.cand_score[o] = u;
+        a.cand_lower[o] = l;
+        a.cand_row[o] = row;
+      }
+    }
+  }
+  wave_lds_sync();  // the region is read before it is refilled
 }
 
 // One pass of the MFMA-bounded scan.  Workgroup = 8 waves over the same 64
@@ -2664,6 +2742,11 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
         // beyond the operand range is a candidate of every present query: its
         // registers are raised to +inf (its bounds are then taken as +-inf);
         // MODE 2 takes every present query's register as it is.
+        // a region that may not hold this tile's pairs is written out first
+        if (fill > (uint32_t)Staging::kCap - 128u) {
+          mma_wave_flush(s_st, a, s_qk, s_flag, wave, min(fill, (uint32_t)Staging::kCap), q0, seg);
+          fill = 0u;
+        }
         const uint64_t actm = ballot(act);
         if (MODE == 1 && ballot(act && !safe) != 0) {
 #pragma unroll
@@ -2673,7 +2756,6 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
               if (!safe && ((okbits >> (16 * t + r)) & 1u)) acc[t][r] = INFINITY;
         }
         const uint32_t row = b * 64u + v;
-        const float eb = fabsf(m_scale), eo = fabsf(m_offset);
 #pragma unroll
         for (int t = 0; t < NQT; ++t)
 #pragma unroll
@@ -2681,22 +2763,8 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
             const uint64_t pm = (MODE == 2 ? ballot((okbits >> (16 * t + r)) & 1u) : ballot(acc[t][r] >= 0.0f)) & actm;
             if (pm == 0) continue;
             const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
-            float U = INFINITY, L = -INFINITY;
-            if (safe) {
-              const float4 k0 = *reinterpret_cast<const float4*>(&s_qk[qi][0]);
-              const float4 k1 = *reinterpret_cast<const float4*>(&s_qk[qi][4]);
-              // k0 = {tau, 1/s, eP, e1}, k1 = {e4, eO, e0, ok}
-              const float tau = k0.x;
-              const float u0 = tau + acc[t][r] * k0.y;
-              const float E = eb * k0.z + mid_n * k0.w + hn * k1.x + eo * k1.y + k1.z;
-              const float mg = (fabsf(u0) + fabsf(tau)) * (1.0f / 4194304.0f);
-              U = u0 + mg;
-              L = (u0 - 2.0f * E * (1.0f + 1.0f / 1048576.0f)) - mg;
-              if (!(U == U)) U = INFINITY;
-              if (!(L == L)) L = -INFINITY;
-            }
             c_app += (uint32_t)__popcll(pm);
-            mma_append(s_st, a, wave, &fill, q0, (uint32_t)qi, seg, pm, U, L, row);
+            mma_append(s_st, a, s_qk, s_flag, wave, &fill, q0, (uint32_t)qi, seg, pm, acc[t][r], row);
           }
       }
     }
@@ -2731,9 +2799,12 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
         const uint32_t g = s_st.base[qi] + atomicAdd(&s_st.cnt[qi], 1u);
         if (g < a.seg_cap) {
           const uint64_t e = ((uint64_t)(q0 + qi) * a.nseg + seg) * a.seg_cap + g;
-          a.cand_score[e] = s_st.u[i];
-          a.cand_lower[e] = s_st.l[i];
-          a.cand_row[e] = s_st.row[i];
+          const uint32_t row = s_st.row[i];
+          float u, l;
+          mma_bounds(s_st.acc[i], a.recs, row, s_qk[qi], s_flag, &u, &l);
+          a.cand_score[e] = u;
+          a.cand_lower[e] = l;
+          a.cand_row[e] = row;
         }
       }
   }
