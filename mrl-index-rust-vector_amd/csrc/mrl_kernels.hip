@@ -1855,13 +1855,25 @@ __device__ __forceinline__ void seg_offsets(uint32_t count, uint32_t nseg, uint3
 // the final pass, nseg <= blockDim.x): thread t takes segment t and loads up
 // to kShortRound of its entries per round, all before any is used.
 constexpr int kShortRound = 16;
+// With a segment per workgroup of the final pass, a thread of k_select reads
+// the first kShortPre entries of its segment together with the segment's
+// count (segments hold at least that many), before the offsets are known.
+constexpr int kShortPre = 8;
+struct ShortPre {
+  float sc[kShortPre];
+  uint32_t rw[kShortPre];
+};
 template <typename F>
-__device__ __forceinline__ void for_each_pair_short(const CandView& v, F&& fn) {
+__device__ __forceinline__ void for_each_pair_short(const CandView& v, const ShortPre& pre, F&& fn) {
   const uint32_t t = threadIdx.x;
   if (t >= v.nseg) return;
   const uint32_t cnt = v.off[t + 1] - v.off[t];
   const uint64_t base = (uint64_t)t * v.seg_cap;
-  for (uint32_t r = 0; r < cnt; r += kShortRound) {
+  // the first kShortPre entries were read with the segment's count
+#pragma unroll
+  for (int u = 0; u < kShortPre; ++u)
+    if ((uint32_t)u < cnt) fn(pre.sc[u], pre.rw[u], v.off[t] + (uint32_t)u);
+  for (uint32_t r = kShortPre; r < cnt; r += kShortRound) {
     float sc[kShortRound];
     uint32_t rw[kShortRound];
 #pragma unroll
@@ -1940,6 +1952,15 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     fl_final = a.tau_final[q];
   }
   const uint32_t c_own = tid < (int)a.nseg ? qcount[tid] : 0u;
+  ShortPre pre;
+  if (short_segs && tid < (int)a.nseg && a.seg_cap >= (uint32_t)kShortPre) {
+    const uint64_t base = (uint64_t)tid * a.seg_cap;
+#pragma unroll
+    for (int u = 0; u < kShortPre; ++u) {
+      pre.sc[u] = v.sc[base + u];
+      pre.rw[u] = v.rw[base + u];
+    }
+  }
   if (tid == 0) {
     s_misc[7] = 0;
     s_fl[0] = fl_safe;
@@ -1961,7 +1982,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
       atomicAdd(&s_hist[hist_bin(sc)], 1u);
       s_buf[dense] = composite(score_key(sc), row);
     };
-    if (short_segs) for_each_pair_short(v, take);
+    if (short_segs && a.seg_cap >= (uint32_t)kShortPre) for_each_pair_short(v, pre, take);
     else for_each_pair(v, take);
     __syncthreads();
     find_boundary(s_hist, kHistBins, K, true, &s_misc[0], &s_misc[1], s_ws);
