@@ -2597,21 +2597,30 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) s_qk[qi][i] = qk[i];
   }
-  // query operands: tile t, lane -> query q0 + 32 t + l % 32, K-half l / 32
-  // (the sampling pass subtracts the error columns)
-  auto qa_load = [&](int t, int st, uint32_t ln) -> uint4 {
-    const uint32_t qi = 32u * t + (ln & 31u), h = ln >> 5;
-    if ((int)qi >= nq) return make_uint4(0u, 0u, 0u, 0u);
-    uint4 v = a.mma_ops[(uint64_t)(q0 + qi) * (2 * kMmaSteps) + 2 * st + h];
-    if (MODE == 0 && h == 0 && st == kMmaSteps - 1) {
-      v.x ^= 0x80008000u;
-      v.y ^= 0x80008000u;
-    }
-    return v;
-  };
-  for (int e = tid; e < NQT * kMmaSteps * 64; e += 64 * WPG) {
+  // Query operands, element e: tile t, K-step st, lane ln -> query
+  // q0 + 32 t + ln % 32, K-half ln / 32.  Every thread's loads go out first (from a clamped query
+  // index), then the stores, zeroed past the batch.
+  constexpr int kQaN = NQT * kMmaSteps * 64, kQaPer = (kQaN + 64 * WPG - 1) / (64 * WPG);
+  uint4 qav[kQaPer];
+#pragma unroll
+  for (int k = 0; k < kQaPer; ++k) {
+    const int e = min(tid + 64 * WPG * k, kQaN - 1);
     const int t = e / (kMmaSteps * 64), st = (e / 64) % kMmaSteps, ln = e & 63;
-    s_qa[t][st][ln] = qa_load(t, st, (uint32_t)ln);
+    const int qi = 32 * t + (ln & 31), qc = qi < nq ? qi : nq - 1;
+    qav[k] = a.mma_ops[(uint64_t)(q0 + qc) * (2 * kMmaSteps) + 2 * st + (ln >> 5)];
+  }
+#pragma unroll
+  for (int k = 0; k < kQaPer; ++k) {
+    const int e = tid + 64 * WPG * k;
+    if (e < kQaN) {
+      const int t = e / (kMmaSteps * 64), st = (e / 64) % kMmaSteps, ln = e & 63;
+      uint4 v = 32 * t + (ln & 31) < nq ? qav[k] : make_uint4(0u, 0u, 0u, 0u);
+      if (MODE == 0 && (ln >> 5) == 0 && st == kMmaSteps - 1) {  // the sampling pass subtracts the error columns
+        v.x ^= 0x80008000u;
+        v.y ^= 0x80008000u;
+      }
+      s_qa[t][st][ln] = v;
+    }
   }
   auto qa_raw = [&](int t, int st) -> uint4 { return s_qa[t][st][lane]; };
   __syncthreads();
