@@ -814,10 +814,12 @@ static bool mma_ok(const mrl_plans* plans, uint32_t n_q, const ScanParams& sp, c
 
 // Sampling stages of the MFMA path: blocks b = pos << shift, pos < n_pos.
 // Above 256 blocks a first stage scores 16..128 blocks (fewer for larger
-// batches); when that is at most 1/32 of the index,
-// a second stage scores every 16th block but counts only lower bounds at or
-// above the first stage's floor, so its histogram stays small while its
-// floor (rank final_rank of a 16x larger sample) is much tighter.
+// batches); when that is at most 1/64 of the index, a second stage scores
+// every 32nd block but counts only lower bounds at or above the first
+// stage's floor, so its histogram stays small while its floor (rank
+// final_rank of a much larger sample) is much tighter.  (Every 16th block
+// gave a slightly tighter floor, but that stage cost more than the final
+// pass saved on the 1M..8.8M-vector benchmark indexes.)
 struct MmaStage {
   uint32_t shift;
   uint32_t n_pos;
@@ -830,7 +832,7 @@ static std::vector<MmaStage> mma_stages(uint64_t B, uint32_t n_q) {
   uint32_t s1 = 0;
   while (((B + (1ull << s1) - 1) >> s1) > cap) ++s1;
   st.push_back(MmaStage{s1, (uint32_t)((B + (1ull << s1) - 1) >> s1)});
-  if (s1 >= 5) st.push_back(MmaStage{4u, (uint32_t)((B + 15) >> 4)});  // >= 2x the first stage's blocks
+  if (s1 >= 6) st.push_back(MmaStage{5u, (uint32_t)((B + 31) >> 5)});  // >= 2x the first stage's blocks
   return st;
 }
 
