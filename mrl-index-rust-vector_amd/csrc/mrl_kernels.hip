@@ -2920,7 +2920,7 @@ __device__ __forceinline__ uint64_t dist_bin_top(uint32_t b) {
 // k_select.  A query whose candidate list overflowed, whose operands were
 // not finite, or with more than kFinCap such candidates gets a count past
 // the segment room, which k_select reports as an overflow (dense re-run).
-__global__ __launch_bounds__(kFinThreads) void k_finish(FinishArgs a) {
+__global__ __launch_bounds__(kFinThreads, 8) void k_finish(FinishArgs a) {
   __shared__ uint32_t s_frow[kFinCap];
   __shared__ uint32_t s_hist[2048];
   __shared__ uint32_t s_off[kSegs + 1];
