@@ -338,7 +338,23 @@ __global__ __launch_bounds__(192) void k_plan(PlanArgs a) {
   const float c0 = has_mid ? a.c.eden_mid_codebook[0] : 0.0f;
   const float c1 = has_mid ? a.c.eden_mid_codebook[1] : 0.0f;
 
-  for (uint32_t i = t; i < dims; i += 192) s_q[i] = x[i];
+  // four loads in flight per thread (index clamped), then the stores
+  for (uint32_t i0 = t; i0 < dims; i0 += 4u * 192u) {
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t i = i0 + 192u * (uint32_t)k;
+      v[k] = x[i < dims ? i : dims - 1u];
+    }
+    // (the empty asm keeps the compiler from sinking a load into its store's branch)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) asm volatile("" : "+v"(v[k]));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t i = i0 + 192u * (uint32_t)k;
+      if (i < dims) s_q[i] = v[k];
+    }
+  }
   __syncthreads();
 
   if (wave == 1) {
