@@ -1171,6 +1171,23 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   const ScanParams sp = a.sp;
   const uint32_t seg = blockIdx.x % a.nseg;
   uint32_t qn = 0;  // survivors in this wave's queue (DEFER)
+  // The one-query prefix stage's constants, read once before the block loop
+  // (the loop's stores would otherwise make the compiler reload them per block).
+  bool d_eden = false;
+  float d_mean = 0.0f, d_psum = 0.0f, d_qmid = 0.0f, d_qtail = 0.0f, d_tq = 0.0f, d_tA = 0.0f, d_tB = 0.0f;
+  if constexpr (DEFER) {
+    const CONST_AS mrl_query_plan* p = cview<mrl_query_plan>(a.plans + q0);
+    d_eden = p->prefix_codec == MRL_PREFIX_EDEN_PROD;
+    d_mean = p->eden_mean_ip;
+    d_psum = p->prefix_sum;
+    d_qmid = p->q_mid_norm;
+    d_qtail = p->q_tail_norm;
+    d_tq = s_floor[0];
+    d_tA = s_tight[0][0];
+    d_tB = s_tight[0][1];
+    // (through an empty asm: held in registers, not re-read from the plan)
+    asm volatile("" : "+s"(d_mean), "+s"(d_psum), "+s"(d_qmid), "+s"(d_qtail));
+  }
 
   // Every wave reaches the flush barrier below, also one with no block.
   for (uint32_t pos = first; pos < n_pos; pos += stride) {
@@ -1222,13 +1239,11 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
       if constexpr (DEFER) {
         // prefix stage here; survivors join the queue for S1 / S4
         const CONST_AS mrl_query_plan* p = cview<mrl_query_plan>(a.plans + q0);
-        const float tq = s_floor[0];
+        const float tq = d_tq;
         const float tau = sp.exhaustive ? -INFINITY : tq;
         const float acc = prefix_acc<true>(m, s_qd + kQdLut);
-        const bool eden = p->prefix_codec == MRL_PREFIX_EDEN_PROD;
-        const float prefix_ip = eden ? p->eden_mean_ip + m.scale * acc : acc * m.scale + m.offset * p->prefix_sum;
-        const float ub = prefix_bound(prefix_ip, m.mid_n, m.high_n, s_tight[0][0], s_tight[0][1], sp.alpha,
-                                      p->q_mid_norm, p->q_tail_norm);
+        const float prefix_ip = d_eden ? d_mean + m.scale * acc : acc * m.scale + m.offset * d_psum;
+        const float ub = prefix_bound(prefix_ip, m.mid_n, m.high_n, d_tA, d_tB, sp.alpha, d_qmid, d_qtail);
         const uint64_t surv = ballot(ub >= tau) & active;
         if (a.stats && lane == 0) {
           atomicAdd(&s_stats[kStatBlocks], 1u);
@@ -1238,8 +1253,8 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
         if (surv != 0) {
           const uint32_t n = (uint32_t)__popcll(surv);
           if (qn + n > 64u) {
-            defer_flush(s_dq[wave], qn, a, p, s_qd + kQdW1, s_qd + kQdW4, s_tight[0][0], s_tight[0][1], tq, tau,
-                        s_app, q0, seg, s_hist, s_stats);
+            defer_flush(s_dq[wave], qn, a, p, s_qd + kQdW1, s_qd + kQdW4, d_tA, d_tB, tq, tau, s_app, q0, seg,
+                        s_hist, s_stats);
             qn = 0;
           }
           if ((surv >> lane) & 1ull) {
