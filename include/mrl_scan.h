@@ -61,7 +61,7 @@ typedef enum mrl_strata_depth {
   MRL_STRATA_FULL64B = 2
 } mrl_strata_depth;
 
-/* EdenFit (src/eden.rs:386-395).  `mean` has `dim` floats. */
+/* EdenFit (src/eden.rs:105-113).  `mean` has `dim` floats. */
 typedef struct mrl_eden_fit {
   uint32_t dim;
   uint32_t bits;

@@ -5,6 +5,11 @@ after every push, ring.rs:76-84).  ``search_exact`` scores them against a query
 on the device (mrl_ring_search), and ``merge_into`` pushes each query's ring
 hits into the device-resident scan shortlists the way
 IndexEngine::query_filtered does (src/engine.rs:584-594).
+
+``push`` / ``flush_partial`` are a thin host-side holder of the pending rows
+(ring.rs:76-93), kept only so that the pending rows exist for
+``search_exact`` and the merge; their block encoding is the host encoder's
+and is not part of the scan path.
 """
 from __future__ import annotations
 

@@ -189,6 +189,30 @@ def test_lloyd_max_codebooks_are_the_normal_centroids(bits):
     assert np.max(np.abs(centroid - cb)) < 2e-6
 
 
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_lloyd_max_codebooks_bit_exact_to_reference_literals(bits):
+    """Every codebook entry has the binary32 bits of the reference's decimal
+    literal (eden.rs:15-44, rounded directly to f32 by
+    tests/golden/make_codebooks.py), not just a value within 2e-6."""
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "eden_codebooks.json")) as f:
+        fx = json.load(f)
+    want = np.array([int(h, 16) for h in fx[f"B{bits}"]["f32_bits"]], dtype=np.uint32)
+    p = C.POINTER(C.c_float)()
+    n = L.ora_lloyd_max_normal(bits, C.byref(p))
+    got = np.array([p[i] for i in range(n)], dtype=np.float32).view(np.uint32)
+    assert np.array_equal(got, want)
+    # the fixture's bits are the nearest binary32 of each decimal literal
+    from fractions import Fraction
+    for lit, h in zip(fx[f"B{bits}"]["decimal"], want):
+        v = np.array(h, dtype=np.uint32).view(np.float32)
+        up = np.nextafter(v, np.float32(np.inf))
+        dn = np.nextafter(v, np.float32(-np.inf))
+        e = abs(Fraction(float(v)) - Fraction(lit))
+        assert e <= abs(Fraction(float(up)) - Fraction(lit)) and e <= abs(Fraction(float(dn)) - Fraction(lit))
+
+
 def test_nearest_centroid_matches_brute_force_with_lower_index_ties():
     p = C.POINTER(C.c_float)()
     n = L.ora_lloyd_max_normal(4, C.byref(p))
