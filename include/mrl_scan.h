@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MRL_ABI_VERSION 1
+#define MRL_ABI_VERSION 2
 #define MRL_BLOCK_BYTES 4096
 #define MRL_VECTORS_PER_BLOCK 64
 #define MRL_MAX_SHORTLIST 4096
@@ -100,7 +100,11 @@ typedef struct mrl_time_range {
  * MFMA-bounded path (RaBitQ mid-band, admissible weights) count
  * after_prefix = pairs whose f16 bound reached the floor, after_s1 =
  * after_s4_budget = pairs scored exactly, pushed = exactly scored pairs
- * kept as candidates. */
+ * kept as candidates.  The last two fields have no reference counterpart:
+ * reruns_safe counts queries whose final floor (taken from a sample of the
+ * index) left fewer than K candidates, reruns_dense queries whose candidate
+ * lists overflowed; mrl_results_fetch re-runs those of the last scan (at
+ * the safe floor / densely), so results never depend on the sample. */
 typedef struct mrl_scan_stats {
   uint64_t blocks;
   uint64_t active_vecs;
@@ -108,6 +112,8 @@ typedef struct mrl_scan_stats {
   uint64_t after_s1;
   uint64_t after_s4_budget;
   uint64_t pushed;
+  uint64_t reruns_safe;
+  uint64_t reruns_dense;
 } mrl_scan_stats;
 
 /* QueryPlan (src/scan.rs:20-71) with every reference field, followed by the
@@ -231,6 +237,17 @@ int mrl_scan_async(mrl_ctx *ctx, const mrl_index *index, const mrl_plans *plans,
 /* Waits for the stream, then copies results (any pointer may be NULL). */
 int mrl_results_fetch(mrl_ctx *ctx, mrl_results *res, uint64_t *out_ids, float *out_scores,
                       uint32_t *out_counts, mrl_scan_stats *stats);
+/* Diagnostic (no reference counterpart): for each query of the last scan on
+ * res, after mrl_results_fetch, the floor its list was selected at: every
+ * vector whose stage checks (src/scan.rs:453-634) fail at that threshold, or
+ * whose score is below it, was dropped; -inf when no floor was used.  Where
+ * the reference's stage bounds are admissible (RaBitQ mid-band, alpha >= 1,
+ * 0 <= w_s4 <= alpha / 2.4) the floor is <= the K-th best score and the list
+ * is the reference's top K.  Otherwise (EdenB1, other alpha / w_s4) the
+ * reference's own result depends on its running threshold's order; the list
+ * is then the top K of the vectors the stage functions keep at this fixed
+ * floor, scored by them.  out_floors: one float per query. */
+int mrl_results_floors(mrl_ctx *ctx, mrl_results *res, float *out_floors);
 
 /* Diagnostic scan at a fixed threshold per query: the stage functions of
  * src/scan.rs:453-634 composed as scan_block_stats does (709-799) with

@@ -204,6 +204,9 @@ struct mrl_results {
   mrl_scan_config last_cfg{};
   mrl_time_range last_time{};
   bool pending = false;
+  // per query of the last scan, the floor its list was selected at:
+  // 0 none (-inf), 1 the final floor (d_tau_hi), 2 the safe floor (d_tau)
+  std::vector<uint8_t> floor_kind;
   // rerank of the shortlists (allocated by the first mrl_results_rerank):
   // scores/rows scratch, sorted rows/scores, status
   void* d_rr = nullptr;
@@ -892,8 +895,8 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
     HIP_TRY(launch_scan_mma(a, 0, s, ps.ev()));
     ps.commit(a.n_pos != 0 && n_q != 0);
     ProfScope pt(ctx, MRL_KERNEL_THRESH, (int)si, 0, n_q);
-    HIP_TRY(launch_mma_floors(pb.hist, n_q, final_rank(K, stages[si].n_pos, B), K, pb.tau_hi, pb.tau, si != 0, s,
-                              pt.ev()));
+    HIP_TRY(launch_mma_floors(pb.hist, a.luts, n_q, final_rank(K, stages[si].n_pos, B), K, pb.tau_hi, pb.tau,
+                              si != 0, s, pt.ev()));
     pt.commit(n_q != 0);
   }
   const int final_pass = (int)stages.size();
@@ -939,6 +942,7 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
     ps.commit(n_q != 0);
   }
   SelectArgs sa{};
+  sa.luts = plans->d_luts + (size_t)plans_first * kQData;
   sa.cand_score = pb.cand_score;
   sa.cand_row = pb.cand_row;
   sa.seg_count = pb.seg_count;
@@ -950,6 +954,7 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
   sa.out_ids = pb.out_ids;
   sa.out_scores = pb.out_scores;
   sa.out_counts = pb.out_counts;
+  sa.stats = stats;
   sa.hist = sampled ? pb.hist : nullptr;
   sa.tau_final = pb.tau_hi;
   sa.tau_safe = pb.tau;
@@ -1015,6 +1020,7 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
     ps.commit(a.n_pos != 0 && n_q != 0);
   }
   SelectArgs sa{};
+  sa.luts = plans->d_luts + (size_t)plans_first * kQData;
   sa.cand_score = pb.cand_score;
   sa.cand_row = pb.cand_row;
   sa.seg_count = pb.seg_count;
@@ -1026,6 +1032,7 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
   sa.out_ids = pb.out_ids;
   sa.out_scores = pb.out_scores;
   sa.out_counts = pb.out_counts;
+  sa.stats = stats;
   sa.hist = sampled ? pb.hist : nullptr;
   sa.tau_final = pb.tau_hi;
   sa.tau_safe = pb.tau;
@@ -1077,6 +1084,7 @@ extern "C" int mrl_scan_async(mrl_ctx* ctx, const mrl_index* index, const mrl_pl
   res->last_cfg = *cfg;
   res->last_time = time ? *time : mrl_time_range{0, 0, 0, 0};
   res->pending = true;
+  res->floor_kind.assign(plans->n_q, 0);
   if (plans->n_q == 0) return MRL_OK;
   if (ix->n_blocks == 0) {
     HIP_TRY(hipMemsetAsync(res->d_counts, 0, plans->n_q * sizeof(uint32_t), ctx->stream));
@@ -1085,7 +1093,11 @@ extern "C" int mrl_scan_async(mrl_ctx* ctx, const mrl_index* index, const mrl_pl
   }
   LevelPlan* lp;
   if ((rc = get_levels(ix, K, &lp))) return rc;
-  return enqueue_scan(ctx, ix, plans, 0, plans->n_q, sp, K, *lp, results_buffers(res), res->d_stats);
+  const PassBuffers pb = results_buffers(res);
+  const bool sampled = mma_ok(plans, plans->n_q, sp, pb) ? !mma_stages(ix->n_blocks, plans->n_q).empty()
+                                                         : lp->passes.size() > 1;
+  res->floor_kind.assign(plans->n_q, sampled ? 1 : 0);
+  return enqueue_scan(ctx, ix, plans, 0, plans->n_q, sp, K, *lp, pb, res->d_stats);
 }
 
 // Exhaustive single pass for one query whose candidate list overflowed
@@ -1173,10 +1185,12 @@ static int rerun_query(mrl_ctx* ctx, mrl_results* r, uint32_t q, uint32_t status
   int rc;
   if (status & 4u) {
     if ((rc = safe_rerun(ctx, r, q, &status))) return rc;
+    if (q < r->floor_kind.size()) r->floor_kind[q] = 2;
     *rerun = true;
   }
   if (status & 1u) *nan = true;
   if (status & 2u) {
+    if (q < r->floor_kind.size()) r->floor_kind[q] = 0;
     rc = dense_rerun(ctx, r, q);
     if (rc == MRL_ERR_NAN) *nan = true;
     else if (rc) return rc;
@@ -1273,8 +1287,29 @@ extern "C" int mrl_results_fetch(mrl_ctx* ctx, mrl_results* res, uint64_t* out_i
     stats->after_s1 = st[kStatS1] - res->stats_seen[kStatS1];
     stats->after_s4_budget = st[kStatS4Budget] - res->stats_seen[kStatS4Budget];
     stats->pushed = st[kStatPushed] - res->stats_seen[kStatPushed];
+    stats->reruns_safe = st[kStatRerunSafe] - res->stats_seen[kStatRerunSafe];
+    stats->reruns_dense = st[kStatRerunDense] - res->stats_seen[kStatRerunDense];
   }
   memcpy(res->stats_seen, st, sizeof(st));
+  return MRL_OK;
+}
+
+extern "C" int mrl_results_floors(mrl_ctx* ctx, mrl_results* res, float* out_floors) {
+  if (!ctx || !res || !out_floors) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (res->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "results belong to another context");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  if (res->pending) return fail(MRL_ERR_INVALID_ARG, "the last scan on these results has not been fetched");
+  HIP_TRY(hipSetDevice(ctx->device));
+  const size_t n = res->floor_kind.size();
+  if (!n) return MRL_OK;
+  std::vector<float> fin(n), safe(n);
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  HIP_TRY(hipMemcpy(fin.data(), res->d_tau_hi, n * sizeof(float), hipMemcpyDeviceToHost));
+  HIP_TRY(hipMemcpy(safe.data(), res->d_tau, n * sizeof(float), hipMemcpyDeviceToHost));
+  for (size_t q = 0; q < n; ++q) {
+    const uint8_t k = res->floor_kind[q];
+    out_floors[q] = k == 1 ? fin[q] : (k == 2 ? safe[q] : -INFINITY);
+  }
   return MRL_OK;
 }
 

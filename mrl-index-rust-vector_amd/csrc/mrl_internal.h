@@ -60,6 +60,12 @@ constexpr int kQdW1 = 1024;
 constexpr int kQdW4 = 1152;
 constexpr int kQdU1 = 1216;
 constexpr int kQdU4 = 1217;
+// Histogram scale of the query: scores are binned as s * 2^-e with
+// e = round(log2 |q|) clamped to [-60, 60] (0 for a zero or non-finite
+// query), so the bins cover [-2, 2) x |q| at 512 / |q| bins per unit score
+// whatever the query's norm.  kQdHistInv holds 2^-e, kQdHistScale 2^e.
+constexpr int kQdHistInv = 1218;
+constexpr int kQdHistScale = 1219;
 constexpr int kQData = 1280;
 
 // Scan-time parameters passed by value to the kernels.
@@ -88,7 +94,19 @@ struct PlanConsts {
 };
 
 // Per-query statistic counters (ScanStats) accumulated on the device.
-enum { kStatBlocks = 0, kStatActive, kStatPrefix, kStatS1, kStatS4Budget, kStatPushed, kStatCount };
+// kStatRerunSafe / kStatRerunDense count the queries a final selection
+// flagged for a re-run at the safe floor / a dense re-run.
+enum {
+  kStatBlocks = 0,
+  kStatActive,
+  kStatPrefix,
+  kStatS1,
+  kStatS4Budget,
+  kStatPushed,
+  kStatRerunSafe,
+  kStatRerunDense,
+  kStatCount
+};
 // Workgroup w adds its counts into copy w % kStatCopies of the counters (one
 // address per counter would serialise the atomics of every workgroup); the
 // reader sums the copies.
@@ -113,9 +131,10 @@ struct PlanArgs {
 // Candidate lists: per query, kSegs segments with their own counters.  A
 // workgroup stages its appends in LDS and flushes them with one atomic on
 // its segment.  Sampling passes append nothing: they count the exact scores
-// of their survivors in a per-query histogram, bin = trunc(clamp((s + 2) *
-// 512, 0, 2047)); the lower edge of the bin holding the K-th best counted
-// score is <= the final K-th score.
+// of their survivors in a per-query histogram, bin = trunc(clamp((s * 2^-e +
+// 2) * 512, 0, 2047)) with the query's histogram scale e (kQdHistInv); the
+// lower edge of the bin holding the K-th best counted score is <= the final
+// K-th score.
 constexpr int kSegs = 16;
 // A one-query final pass may instead give every workgroup a segment of its
 // own (ScanArgs::excl): then nseg = the grid (at most kMaxSegs), and a
@@ -213,8 +232,15 @@ struct ScanArgs {
 // cleared.  k_exact, over the whole GPU: the reference's f32 score of every
 // listed candidate, appended to the query's segments (at or above the final
 // floor) for k_select.
-constexpr int kFinCap = 8192;     // exact-scoring list room per query
+constexpr int kFinCap = 32768;    // exact-scoring list room per query (at most 256 work items)
 constexpr int kExactItem = 256;   // list entries per k_exact work item (one per thread)
+// The list room of a query whose candidate area holds nseg * seg_cap entries
+// (its first entry holds the count).
+__host__ __device__ inline uint32_t fin_room(uint32_t nseg, uint32_t seg_cap) {
+  const uint64_t room = (uint64_t)nseg * seg_cap - 1u;
+  return room < (uint64_t)kFinCap ? (uint32_t)room : (uint32_t)kFinCap;
+}
+static_assert(kFinCap / kExactItem <= 256, "a work item holds its chunk index in 8 bits");
 struct FinishArgs {
   const uint8_t* idx;
   uint64_t n_blocks;
@@ -238,6 +264,7 @@ struct FinishArgs {
 };
 
 struct SelectArgs {
+  const float* luts;      // [n_q][kQData] scan constants (the histogram scale of each query)
   const float* cand_score;
   const uint32_t* cand_row;
   uint32_t* seg_count;    // consumed and zeroed
@@ -253,6 +280,7 @@ struct SelectArgs {
   uint64_t* out_ids;      // [n_q][k]
   float* out_scores;
   uint32_t* out_counts;
+  unsigned long long* stats;  // [kStatCopies][kStatCount] or null: flagged re-runs are counted here
 };
 
 // GPU encoder (mrl_encode.hip): rows -> PaxBlock64 records in the reference layout.
@@ -340,8 +368,8 @@ hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const Lau
 // Floors of a sampling stage from its histogram (which is then cleared): rank
 // `rank` into floor_out and rank safe_rank into safe_out, each raised to the
 // previous stage's value when `prev` is set (those arrays hold it on entry).
-hipError_t launch_mma_floors(uint32_t* hist, uint32_t n_q, uint32_t rank, uint32_t safe_rank, float* floor_out,
-                             float* safe_out, bool prev, hipStream_t s, const LaunchEvents& ev = {});
+hipError_t launch_mma_floors(uint32_t* hist, const float* luts, uint32_t n_q, uint32_t rank, uint32_t safe_rank,
+                             float* floor_out, float* safe_out, bool prev, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_finish(const FinishArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_exact(const FinishArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
 

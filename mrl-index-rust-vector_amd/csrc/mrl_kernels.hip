@@ -318,7 +318,7 @@ __global__ __launch_bounds__(192) void k_plan(PlanArgs a) {
   __shared__ __align__(16) float s_mid[128];
   __shared__ __align__(16) float s_eden[64];
   __shared__ __align__(16) float s_terms[9][128];
-  __shared__ float s_sums[10];
+  __shared__ float s_sums[11];
 
   const uint32_t q = blockIdx.x;
   const int t = threadIdx.x;
@@ -389,6 +389,11 @@ __global__ __launch_bounds__(192) void k_plan(PlanArgs a) {
     s_terms[3][64 + lane] = has_mid ? mv1 * mm1 : 0.0f;
     s_terms[4][lane] = mv0 * mv0;
     s_terms[4][64 + lane] = mv1 * mv1;
+    // squared prefix norm, for the histogram scale only (any summation order)
+    float psq = v * v;
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) psq += __shfl_xor(psq, h);
+    if (lane == 0) s_sums[10] = psq;
     if (lane < 16) p->eden_codebook[lane] = has_eden ? a.c.eden_codebook[lane] : 0.0f;
     if (lane < 27) p->pad[lane] = 0.0f;
     if (lane == 0) {
@@ -532,6 +537,17 @@ __global__ __launch_bounds__(192) void k_plan(PlanArgs a) {
     p->q_mid_norm = sqrtf(mid_sq);
     p->q_after_prefix = sqrtf(mid_sq + tail_sq);
     p->q_after_s1 = qt;
+    // histogram scale: e = round(log2 |q|), clamped to [-60, 60]
+    const float nrm = sqrtf(s_sums[10] + mid_sq + tail_sq);
+    int e = 0;
+    if (nrm > 0.0f && nrm - nrm == 0.0f) {
+      int ex;
+      const float mant = frexpf(nrm, &ex);  // nrm = mant * 2^ex, mant in [0.5, 1)
+      e = mant >= 0.70710678f ? ex : ex - 1;
+      e = e < -60 ? -60 : (e > 60 ? 60 : e);
+    }
+    qd[kQdHistInv] = ldexpf(1.0f, -e);
+    qd[kQdHistScale] = ldexpf(1.0f, e);
   }
 }
 
@@ -735,9 +751,12 @@ __device__ __forceinline__ uint64_t eval_block(const CONST_AS uint8_t* blk, uint
   return surv;
 }
 
-// Histogram bin of an appended score (monotone non-decreasing in s).
-__device__ __forceinline__ uint32_t hist_bin(float s) {
-  float x = (s + 2.0f) * 512.0f;
+// Histogram bin of an appended score (monotone non-decreasing in s): the
+// score times the query's power-of-two histogram scale inv = 2^-e (exact
+// unless it underflows, and monotone either way), then 512 bins per unit over
+// [-2, 2).
+__device__ __forceinline__ uint32_t hist_bin(float s, float inv) {
+  float x = (s * inv + 2.0f) * 512.0f;
   x = fminf(fmaxf(x, 0.0f), (float)(kHistBins - 1));
   return (uint32_t)x;
 }
@@ -757,6 +776,12 @@ __device__ __forceinline__ float bin_floor(uint32_t b) {
   }
   return f;
 }
+// The floor of bin b for a query of histogram scale 2^e (scale = 2^e): an
+// exact power-of-two multiple of bin_floor(b), whose magnitude stays in the
+// normal range for |e| <= 60.  hist_bin(s, 2^-e) >= b implies s * 2^-e >=
+// bin_floor(b) (when s * 2^-e underflows, |s * 2^-e| < 2^-126 lies above
+// every finite bin floor), so s >= bin_floor(b) * 2^e.
+__device__ __forceinline__ float bin_floor(uint32_t b, float scale) { return bin_floor(b) * scale; }
 
 // One wave: the bin floor of the need-th best count of a histogram (-inf
 // when it holds fewer than need).  Lane l holds bins 32(63-l) .. +31, so the
@@ -879,8 +904,9 @@ __device__ __forceinline__ void take_floors(const ScanArgs& a, uint32_t q0, int 
       const int qi = it >> 1;
       const bool safe = it & 1;
       const uint32_t need = safe ? a.safe_rank : a.floor_rank;
-      const float f = it == wave ? floor_of(first, need)
-                                 : wave_floor(a.floor_hist + (uint64_t)(q0 + qi) * kHistBins, need);
+      const float sc = a.luts[(uint64_t)(q0 + qi) * kQData + kQdHistScale];
+      const float f = (it == wave ? floor_of(first, need)
+                                  : wave_floor(a.floor_hist + (uint64_t)(q0 + qi) * kHistBins, need)) * sc;
       if (lane == 0) {
         if (!safe) s_floor[qi] = f;
         if (blockIdx.x == 0) (safe ? a.safe_out : a.floor_out)[q0 + qi] = f;
@@ -1014,7 +1040,7 @@ __device__ __forceinline__ void defer_flush(const DeferQ& dq, uint32_t qn, const
                                          const CONST_AS mrl_query_plan* p, const float* __restrict__ w1,
                                          const float* __restrict__ w4, float tA, float tB, float tq, float tau,
                                          Staging<1>& st, uint32_t q, uint32_t seg, uint32_t* s_hist,
-                                         unsigned int* s_stats) {
+                                         unsigned int* s_stats, float hinv) {
   const uint32_t lane = __lane_id();
   const ScanParams& sp = a.sp;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1063,7 +1089,7 @@ __device__ __forceinline__ void defer_flush(const DeferQ& dq, uint32_t qn, const
     atomicAdd(&s_stats[kStatPushed], (unsigned)__popcll(k3));
   }
   if (a.hist) {
-    if (keep) atomicAdd(&s_hist[hist_bin(score)], 1u);
+    if (keep) atomicAdd(&s_hist[hist_bin(score, hinv)], 1u);
   } else {
     if (ballot(keep && score != score) != 0 && lane == 0) atomicOr(a.err + q, 1u);
     const uint64_t pm = ballot(keep && score >= tq);
@@ -1084,6 +1110,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   constexpr bool kLdsHist = QT == 1 && !DIAG;  // sampling-pass counts gathered per workgroup
   __shared__ uint32_t s_hist[kLdsHist ? kHistBins : 1];
   __shared__ float s_floor[QT];
+  __shared__ float s_hinv[QT];  // histogram scale of each query (2^-e)
   __shared__ float s_tight[QT][2];
   constexpr bool DEFER = QT == 1 && !DIAG && !L0;  // S1 / S4 through the per-wave survivor queue
   __shared__ DeferQ s_dq[DEFER ? 4 : 1];
@@ -1122,8 +1149,9 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     }
   }
   const float fr0 = a.flag_tabs[tid], fr1 = a.flag_tabs[256 + tid];
-  float tu1 = 0.0f, tu4 = 0.0f;
+  float tu1 = 0.0f, tu4 = 0.0f, hinv = 1.0f;
   int t_b1 = 0, t_tail = 0;
+  if (!DIAG && tid < nq) hinv = a.luts[(uint64_t)(q0 + tid) * kQData + kQdHistInv];
   if (!DIAG && !L0 && tid < nq) {
     const float* qd = a.luts + (uint64_t)(q0 + tid) * kQData;
     const mrl_query_plan* pq = a.plans + q0 + tid;
@@ -1156,6 +1184,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   }
   s_rho[tid] = fr0;
   s_midf[tid] = fr1;
+  if (tid < nq) s_hinv[tid] = hinv;
   if (kLdsHist && a.hist)
     for (int i = tid; i < kHistBins; i += 256) s_hist[i] = 0u;
   if (!DIAG && !L0 && tid < nq) {  // diagnostic scans keep the reference's checks
@@ -1175,6 +1204,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   // (the loop's stores would otherwise make the compiler reload them per block).
   bool d_eden = false;
   float d_mean = 0.0f, d_psum = 0.0f, d_qmid = 0.0f, d_qtail = 0.0f, d_tq = 0.0f, d_tA = 0.0f, d_tB = 0.0f;
+  float d_hinv = 1.0f;
   if constexpr (DEFER) {
     const CONST_AS mrl_query_plan* p = cview<mrl_query_plan>(a.plans + q0);
     d_eden = p->prefix_codec == MRL_PREFIX_EDEN_PROD;
@@ -1185,6 +1215,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     d_tq = s_floor[0];
     d_tA = s_tight[0][0];
     d_tB = s_tight[0][1];
+    d_hinv = s_hinv[0];
     // (through an empty asm: held in registers, not re-read from the plan)
     asm volatile("" : "+s"(d_mean), "+s"(d_psum), "+s"(d_qmid), "+s"(d_qtail));
   }
@@ -1254,7 +1285,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
           const uint32_t n = (uint32_t)__popcll(surv);
           if (qn + n > 64u) {
             defer_flush(s_dq[wave], qn, a, p, s_qd + kQdW1, s_qd + kQdW4, d_tA, d_tB, tq, tau, s_app, q0, seg,
-                        s_hist, s_stats);
+                        s_hist, s_stats, d_hinv);
             qn = 0;
           }
           if ((surv >> lane) & 1ull) {
@@ -1315,8 +1346,8 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
           if (a.hist) {
             // sampling pass: count the survivors' exact scores
             if (mine) {
-              if constexpr (kLdsHist) atomicAdd(&s_hist[hist_bin(score)], 1u);
-              else atomicAdd(a.hist + (uint64_t)q * kHistBins + hist_bin(score), 1u);
+              if constexpr (kLdsHist) atomicAdd(&s_hist[hist_bin(score, s_hinv[qi])], 1u);
+              else atomicAdd(a.hist + (uint64_t)q * kHistBins + hist_bin(score, s_hinv[qi]), 1u);
             }
           } else {
             if (ballot(mine && score != score) != 0 && lane == 0) atomicOr(a.err + q, 1u);
@@ -1346,7 +1377,8 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   if constexpr (DEFER) {
     if (qn != 0)
       defer_flush(s_dq[wave], qn, a, cview<mrl_query_plan>(a.plans + q0), s_qd + kQdW1, s_qd + kQdW4, s_tight[0][0],
-                  s_tight[0][1], s_floor[0], sp.exhaustive ? -INFINITY : s_floor[0], s_app, q0, seg, s_hist, s_stats);
+                  s_tight[0][1], s_floor[0], sp.exhaustive ? -INFINITY : s_floor[0], s_app, q0, seg, s_hist, s_stats,
+                  s_hinv[0]);
   }
   flush_appends<QT, DIAG>(s_app, a, q0, nq, seg, s_stats);
   if (kLdsHist && a.hist) {
@@ -1460,6 +1492,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
   __shared__ unsigned int s_stats[kStatCount];
   __shared__ Staging<QT> s_app;
   __shared__ float s_floor[QT];
+  __shared__ float s_hinv[QT];  // histogram scale of each query (2^-e)
 
   const int tid = threadIdx.x;
   const uint32_t q0 = blockIdx.y * QT;
@@ -1491,6 +1524,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
     if (d < 128) s_w1[e] = w;
     else s_w4[e - 128 * QT] = w;
   }
+  if (tid < nq) s_hinv[tid] = a.luts[(uint64_t)(q0 + tid) * kQData + kQdHistInv];
   take_floors<QT>(a, q0, nq, wave, lane, s_floor, fl);
   __syncthreads();
   if (tid < QT) {
@@ -1684,7 +1718,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
         if (a.stats) c_s4b += (uint32_t)__popcll(pushed);
         if (pushed == 0) continue;
         if (a.hist) {
-          if (mine) atomicAdd(a.hist + (uint64_t)q * kHistBins + hist_bin(score[qi]), 1u);
+          if (mine) atomicAdd(a.hist + (uint64_t)q * kHistBins + hist_bin(score[qi], s_hinv[qi]), 1u);
           continue;
         }
         const float tq = s_qc[qi * kQcCount + kQcTauPush];
@@ -1920,10 +1954,10 @@ __device__ __forceinline__ void for_each_pair_short(const CandView& v, const Sho
 }
 
 // LDS histogram of the appended scores of one query (all segments).
-__device__ __forceinline__ void build_hist(uint32_t* hist, const CandView& v) {
+__device__ __forceinline__ void build_hist(uint32_t* hist, const CandView& v, float hinv) {
   for (int i = threadIdx.x; i < kHistBins; i += blockDim.x) hist[i] = 0u;
   __syncthreads();
-  for_each_cand(v, [&](float sc, uint32_t) { atomicAdd(&hist[hist_bin(sc)], 1u); });
+  for_each_cand(v, [&](float sc, uint32_t) { atomicAdd(&hist[hist_bin(sc, hinv)], 1u); });
   __syncthreads();
 }
 
@@ -1977,6 +2011,9 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   // The set-up's reads go out together: the final pass's floor and the safe
   // one (for the shortfall check below) and this thread's segment count.
   const bool short_segs = a.nseg > (uint32_t)kSegs;
+  // the query's histogram scale (2^-e, 2^e)
+  const float hinv = a.luts[(uint64_t)q * kQData + kQdHistInv];
+  const float hscale = a.luts[(uint64_t)q * kQData + kQdHistScale];
   float fl_safe = 0.0f, fl_final = 0.0f;
   if (a.hist && tid == 0) {
     fl_safe = a.tau_safe[q];
@@ -2010,7 +2047,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     for (int i = tid; i < kHistBins; i += kSelThreads) s_hist[i] = 0u;
     __syncthreads();
     auto take = [&](float sc, uint32_t row, uint32_t dense) {
-      atomicAdd(&s_hist[hist_bin(sc)], 1u);
+      atomicAdd(&s_hist[hist_bin(sc, hinv)], 1u);
       s_buf[dense] = composite(score_key(sc), row);
     };
     if (short_segs && a.seg_cap >= (uint32_t)kShortPre) for_each_pair_short(v, pre, take);
@@ -2019,7 +2056,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     find_boundary(s_hist, kHistBins, K, true, &s_misc[0], &s_misc[1], s_ws);
     if (tid == 0) s_misc[2] = 0;
     __syncthreads();
-    const uint32_t fkey = score_key(bin_floor(s_misc[0]));
+    const uint32_t fkey = score_key(bin_floor(s_misc[0], hscale));
     for (uint32_t i = tid; i < total; i += kSelThreads) {
       const uint64_t c = s_buf[i];
       if ((uint32_t)(c >> 32) >= fkey) {
@@ -2032,10 +2069,10 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     if (m <= (uint32_t)kSelCap) sb = s_sel;
     else m = total;  // sort every entry
   } else {
-  build_hist(s_hist, v);
+  build_hist(s_hist, v, hinv);
   find_boundary(s_hist, kHistBins, K, true, &s_misc[0], &s_misc[1], s_ws);
   __syncthreads();
-  const float floor_t = bin_floor(s_misc[0]);
+  const float floor_t = bin_floor(s_misc[0], hscale);
 
   // entries >= floor_t as (score key, candidate index); the rows of the
   // gathered entries are then loaded all at once
@@ -2127,7 +2164,8 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     // serves as the scatter cursor.
     for (int i = tid; i < kHistBins; i += kSelThreads) s_hist[i] = 0u;
     __syncthreads();
-    for (uint32_t i = tid; i < m; i += kSelThreads) atomicAdd(&s_hist[hist_bin(key_score((uint32_t)(sb[i] >> 32)))], 1u);
+    for (uint32_t i = tid; i < m; i += kSelThreads)
+      atomicAdd(&s_hist[hist_bin(key_score((uint32_t)(sb[i] >> 32)), hinv)], 1u);
     __syncthreads();
     {  // start[b] = entries in bins above b; thread t owns bins 2047 - 2t and 2046 - 2t
       const uint32_t b0 = kHistBins - 1 - 2u * (uint32_t)tid, b1 = b0 - 1;
@@ -2142,13 +2180,13 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     __syncthreads();
     for (uint32_t i = tid; i < m; i += kSelThreads) {
       const uint64_t c = sb[i];
-      const uint32_t b = hist_bin(key_score((uint32_t)(c >> 32)));
+      const uint32_t b = hist_bin(key_score((uint32_t)(c >> 32)), hinv);
       s_buf[s_start[b] + atomicAdd(&s_hist[b], 1u)] = c;
     }
     __syncthreads();
     for (uint32_t i = tid; i < m; i += kSelThreads) {
       const uint64_t c = s_buf[i];
-      const uint32_t b = hist_bin(key_score((uint32_t)(c >> 32)));
+      const uint32_t b = hist_bin(key_score((uint32_t)(c >> 32)), hinv);
       const uint32_t lo = s_start[b], hi = lo + s_hist[b];
       uint32_t r = lo, j = lo;
       for (; j + 4 <= hi; j += 4) {  // four independent reads in flight
@@ -2207,6 +2245,11 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     a.out_counts[q] = keep;
     a.status[q] = (a.err[q] & 1u) | s_misc[7] | short_k;
     a.err[q] = 0u;
+    if (a.stats && (short_k | s_misc[7])) {
+      unsigned long long* st = a.stats + (q % (uint32_t)kStatCopies) * kStatCount;
+      if (short_k) atomicAdd(st + kStatRerunSafe, 1ull);
+      if (s_misc[7] & 2u) atomicAdd(st + kStatRerunDense, 1ull);
+    }
   }
 }
 
@@ -2366,13 +2409,14 @@ __global__ __launch_bounds__(64) void k_mma_prep(MmaPrepArgs a) {
 // `prev` (a later stage counts only lower bounds at or above the previous
 // floor, so its own floor is -inf when too few were counted).  The histogram
 // is left zeroed for the next stage.
-__global__ __launch_bounds__(64) void k_mma_floors(uint32_t* hist, uint32_t rank, uint32_t safe_rank,
-                                                   float* floor_out, float* safe_out, int prev) {
+__global__ __launch_bounds__(64) void k_mma_floors(uint32_t* hist, const float* luts, uint32_t rank,
+                                                   uint32_t safe_rank, float* floor_out, float* safe_out, int prev) {
   const uint32_t q = blockIdx.x, lane = __lane_id();
   uint32_t* h = hist + (uint64_t)q * kHistBins;
   const HistRow r = hist_row(h);
-  float f = floor_of(r, rank);
-  float sf = floor_of(r, safe_rank);
+  const float sc = luts[(uint64_t)q * kQData + kQdHistScale];  // the query's histogram scale 2^e
+  float f = floor_of(r, rank) * sc;
+  float sf = floor_of(r, safe_rank) * sc;
   uint4* mine = reinterpret_cast<uint4*>(h + (63u - lane) * 32u);  // the bins hist_row gave this lane
 #pragma unroll
   for (int k = 0; k < 8; ++k) mine[k] = make_uint4(0u, 0u, 0u, 0u);
@@ -2559,6 +2603,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   __shared__ float s_flag[512];      // rho = f / 255, then sqrt(max(1 - rho^2, 0))
   __shared__ __align__(16) float s_c[kMmaQ];
   __shared__ __align__(16) float s_qk[kMmaQ][8];  // tau, 1/s, eP, e1, e4, eO, e0 (with the tau term), ok
+  __shared__ float s_hinv[kMmaQ];                 // histogram scale of each query (2^-e, sampling passes)
   __shared__ unsigned int s_stats[kStatCount];
   __shared__ uint32_t s_anyall;  // sampling: some query counts every lower bound
   __shared__ Staging s_st;
@@ -2627,6 +2672,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
     s_c[qi] = C;
 #pragma unroll
     for (int i = 0; i < 8; ++i) s_qk[qi][i] = qk[i];
+    s_hinv[qi] = (MODE == 0 && qi < nq) ? a.luts[(uint64_t)(q0 + qi) * kQData + kQdHistInv] : 1.0f;
   }
   // Query operands, element e: tile t, K-step st, lane ln -> query
   // q0 + 32 t + ln % 32, K-half ln / 32.  Every thread's loads go out first (from a clamped query
@@ -2795,7 +2841,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
             L = L - (fabsf(L) + fabsf(k.x)) * (1.0f / 4194304.0f);
             uint32_t qq = q0 + qi;  // through an empty asm: no hoisted per-register addresses
             asm volatile("" : "+v"(qq));
-            atomicAdd(a.hist + (uint64_t)qq * kHistBins + hist_bin(L), 1u);
+            atomicAdd(a.hist + (uint64_t)qq * kHistBins + hist_bin(L, s_hinv[qi]), 1u);
           }
       } else {
         // Absent queries and those with unusable operands start at C = -inf,
@@ -2949,10 +2995,9 @@ __device__ __forceinline__ uint64_t dist_bin_top(uint32_t b) {
 // reaches it, their exact scores, and those at or above the final floor
 // written back as the query's candidate list (segments in order) for
 // k_select.  A query whose candidate list overflowed, whose operands were
-// not finite, or with more than kFinCap such candidates gets a count past
+// not finite, or with more such candidates than its list room gets a count past
 // the segment room, which k_select reports as an overflow (dense re-run).
 __global__ __launch_bounds__(kFinThreads, 8) void k_finish(FinishArgs a) {
-  __shared__ uint32_t s_frow[kFinCap];
   __shared__ uint32_t s_hist[2048];
   __shared__ uint32_t s_off[kSegs + 1];
   __shared__ uint32_t s_coff[kSegs + 1];
@@ -3003,24 +3048,25 @@ __global__ __launch_bounds__(kFinThreads, 8) void k_finish(FinishArgs a) {
     tkey = dhi < (uint64_t)kmax ? kmax - (uint32_t)dhi : 0u;
   }
   // candidates whose upper bound reaches it, listed over the lower-bound area
-  // (every read of it is done)
+  // (every read of it is done): count at list[0], rows from list[1], room
+  // for fin_cap of them
+  const uint32_t fin_cap = fin_room(a.nseg, a.seg_cap);
   const CandView vu{a.cand_score + qbase, a.cand_row + qbase, a.seg_cap, a.nseg, s_off, s_coff};
   for_each_pair(vu, [&](float u, uint32_t row, uint32_t) {
     if (score_key(u) >= tkey) {
       const uint32_t slot = atomicAdd(&s_misc[2], 1u);
-      if (slot < (uint32_t)kFinCap) s_frow[slot] = row;
+      if (slot < fin_cap) list[1 + slot] = row;
     }
   });
   __syncthreads();
   const uint32_t nf = s_misc[2];
-  if (nf > (uint32_t)kFinCap) {
+  if (nf > fin_cap) {
     if (tid == 0) {
       qcount[0] = a.seg_cap + 1u;
       list[0] = 0u;
     }
     return;
   }
-  for (uint32_t i = tid; i < nf; i += kFinThreads) list[1 + i] = s_frow[i];
   if (tid == 0) {
     list[0] = nf;
     // k_exact's work items of this query: (q, chunk) for every kExactItem entries
@@ -3066,11 +3112,12 @@ __global__ __launch_bounds__(kExactItem) void k_exact(FinishArgs a) {
     const uint64_t qbase = (uint64_t)q * a.nseg * a.seg_cap;
     const uint32_t* list = reinterpret_cast<const uint32_t*>(a.cand_lower + qbase);
     // the count, this thread's row (read whether or not it is below the
-    // count: the list area holds 1 + kFinCap entries), the floor and the
+    // count: the list area holds 1 + fin_room entries), the floor and the
     // tables all go out together
+    const uint32_t room = fin_room(a.nseg, a.seg_cap);
     const uint32_t i = c * (uint32_t)kExactItem + (uint32_t)tid;
     const uint32_t nf_raw = list[0];
-    const uint32_t row_raw = list[1 + min(i, (uint32_t)kFinCap - 1u)];
+    const uint32_t row_raw = list[1 + min(i, room - 1u)];
     const float floor_t = a.tau_final ? a.tau_final[q] : -INFINITY;
     if (q != q_have) {
       const float4* qd4 = reinterpret_cast<const float4*>(a.luts + (uint64_t)q * kQData);
@@ -3082,7 +3129,7 @@ __global__ __launch_bounds__(kExactItem) void k_exact(FinishArgs a) {
       __syncthreads();
       q_have = q;
     }
-    const uint32_t nf = min(nf_raw, (uint32_t)kFinCap);
+    const uint32_t nf = min(nf_raw, room);
     if (c * (uint32_t)kExactItem >= nf) continue;
     bool keep = false;
     float sc = 0.0f;
@@ -3257,10 +3304,10 @@ hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const Lau
   return hipGetLastError();
 }
 
-hipError_t launch_mma_floors(uint32_t* hist, uint32_t n_q, uint32_t rank, uint32_t safe_rank, float* floor_out,
-                             float* safe_out, bool prev, hipStream_t s, const LaunchEvents& ev) {
+hipError_t launch_mma_floors(uint32_t* hist, const float* luts, uint32_t n_q, uint32_t rank, uint32_t safe_rank,
+                             float* floor_out, float* safe_out, bool prev, hipStream_t s, const LaunchEvents& ev) {
   if (n_q == 0) return hipSuccess;
-  launch(k_mma_floors, dim3(n_q), dim3(64), s, ev, hist, rank, safe_rank, floor_out, safe_out, prev ? 1 : 0);
+  launch(k_mma_floors, dim3(n_q), dim3(64), s, ev, hist, luts, rank, safe_rank, floor_out, safe_out, prev ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -73,6 +73,8 @@ class ScanStatsC(C.Structure):
         ("after_s1", C.c_uint64),
         ("after_s4_budget", C.c_uint64),
         ("pushed", C.c_uint64),
+        ("reruns_safe", C.c_uint64),
+        ("reruns_dense", C.c_uint64),
     ]
 
 
@@ -179,6 +181,7 @@ SIGNATURES = {
     "mrl_results_destroy": (None, [_P]),
     "mrl_scan_async": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), C.POINTER(TimeRangeC), _P]),
     "mrl_results_fetch": (C.c_int, [_P, _P, _U64, _F, _U32, C.POINTER(ScanStatsC)]),
+    "mrl_results_floors": (C.c_int, [_P, _P, _F]),
     "mrl_scan_fixed_tau": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), C.POINTER(TimeRangeC), _F, _U64,
                                      _F, _F]),
     "mrl_scan_mma_bounds": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), C.POINTER(TimeRangeC), _F, _F]),

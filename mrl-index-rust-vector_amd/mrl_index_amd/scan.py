@@ -245,9 +245,17 @@ class ScanStats:
     after_s1: int = 0
     after_s4_budget: int = 0
     pushed: int = 0
+    # no reference counterpart: queries the final selection flagged for a
+    # re-run at the safe floor / a dense re-run (mrl_scan_stats)
+    reruns_safe: int = 0
+    reruns_dense: int = 0
+
+    @classmethod
+    def from_c(cls, st: "_lib.ScanStatsC") -> "ScanStats":
+        return cls(*[getattr(st, f) for f, _ in _lib.ScanStatsC._fields_])
 
     def merge(self, other: "ScanStats") -> None:
-        for f in ("blocks", "active_vecs", "after_prefix", "after_s1", "after_s4_budget", "pushed"):
+        for f, _ in _lib.ScanStatsC._fields_:
             setattr(self, f, getattr(self, f) + getattr(other, f))
 
     def summary(self) -> str:
@@ -302,8 +310,7 @@ def scan_batch(blocks: Union["DeviceIndex", np.ndarray], plan: QueryPlan, cfg, t
         t = _time(time_lo, time_hi)
         _lib.check(_lib.lib.mrl_scan(plan.device.handle, idx.handle, plan.handle, C.byref(c), C.byref(t),
                                      _lib.u64ptr(ids), _lib.fptr(scores), _lib.u32ptr(counts), C.byref(st)))
-        stats = ScanStats(st.blocks, st.active_vecs, st.after_prefix, st.after_s1, st.after_s4_budget, st.pushed)
-        return ScanResult(ids, scores, counts, stats)
+        return ScanResult(ids, scores, counts, ScanStats.from_c(st))
     finally:
         if owned:
             idx.close()
@@ -358,8 +365,14 @@ class DeviceResults:
         st = _lib.ScanStatsC()
         _lib.check(_lib.lib.mrl_results_fetch(self.device.handle, self._h, _lib.u64ptr(ids), _lib.fptr(scores),
                                               _lib.u32ptr(counts), C.byref(st)))
-        stats = ScanStats(st.blocks, st.active_vecs, st.after_prefix, st.after_s1, st.after_s4_budget, st.pushed)
-        return ScanResult(ids, scores, counts, stats)
+        return ScanResult(ids, scores, counts, ScanStats.from_c(st))
+
+    def floors(self) -> np.ndarray:
+        """Per query of the last fetched scan, the floor its list was selected
+        at (mrl_results_floors; -inf where none was used)."""
+        out = np.zeros(max(self._nq, 1), dtype=np.float32)
+        _lib.check(_lib.lib.mrl_results_floors(self.device.handle, self._h, _lib.fptr(out)))
+        return out[:self._nq]
 
     def rerank(self, store) -> "tuple[np.ndarray, np.ndarray, np.ndarray]":
         """scored_hits_to_row_ids + rerank_exact_rows (pipeline.rs:157-180) of

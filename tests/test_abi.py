@@ -34,7 +34,8 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_plan_layout():
-    assert _lib.lib.mrl_abi_version() == 1
+    assert _lib.lib.mrl_abi_version() == 2
+    assert C.sizeof(_lib.ScanStatsC) == 64
     assert _lib.lib.mrl_query_plan_size() == C.sizeof(_lib.QueryPlanC) == 6656
     assert ora.lib.ora_plan_size() == 6656
     # identical field layout with the oracle's plan (field by field)

@@ -50,6 +50,12 @@ def test_config1_cpu_bench_size(device):
     _check_config(device, 1, 1)
 
 
+def test_config2_1m_batch1_k256(device):
+    """The bench line's own workload at full size: 15,625 blocks, one query,
+    K = 256, against the oracle's sharded scan_blocks."""
+    _check_config(device, 2, 1)
+
+
 def test_config3_1m_batch256(device):
     _check_config(device, 3, 8)
 
