@@ -38,6 +38,7 @@ extern "C" {
 #define MRL_VECTORS_PER_BLOCK 64
 #define MRL_MAX_SHORTLIST 4096
 #define MRL_MAX_DIMS 8192
+#define MRL_NOALLOC_MAX_QUERIES 64
 
 typedef enum mrl_status {
   MRL_OK = 0,
@@ -248,6 +249,28 @@ int mrl_results_fetch(mrl_ctx *ctx, mrl_results *res, uint64_t *out_ids, float *
  * is then the top K of the vectors the stage functions keep at this fixed
  * floor, scored by them.  out_floors: one float per query. */
 int mrl_results_floors(mrl_ctx *ctx, mrl_results *res, float *out_floors);
+
+/* Allocation-free variant of mrl_scan_async.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It allocates nothing: the scan's scratch (candidate lists,
+ * histograms, floors, counters) lives in a fixed 13 MiB device array of the
+ * library, one per GPU, held until the process ends.  The caller passes the
+ * inputs and device-memory outputs: d_out_ids / d_out_scores [n_queries][K]
+ * (K = max(shortlist_cand, 1)), d_out_counts and d_out_status [n_queries].
+ * Enqueued on the context stream; returns without waiting.  Results are
+ * those of mrl_scan_async + mrl_results_fetch: a query whose final floor
+ * left it short of K is re-run at the safe floor on the device.  Status bits
+ * per query: 1 a NaN score (mrl_results_fetch reports MRL_ERR_NAN), 2 a
+ * candidate list overflowed (massive exact ties; that query's list is not
+ * exact: scan it with mrl_scan, which re-runs it densely).  At most
+ * MRL_NOALLOC_MAX_QUERIES queries per call (more: MRL_ERR_INVALID_ARG).
+ * Every call on one GPU shares that GPU's array, which keeps the last call's
+ * contents: calls on one context are ordered on its stream, but calls from
+ * two contexts on the same GPU that overlap in time race. */
+int mrl_scan_noalloc(mrl_ctx *ctx, const mrl_index *index, const mrl_plans *plans,
+                     const mrl_scan_config *cfg, const mrl_time_range *time, uint64_t *d_out_ids,
+                     float *d_out_scores, uint32_t *d_out_counts, uint32_t *d_out_status);
 
 /* Diagnostic scan at a fixed threshold per query: the stage functions of
  * src/scan.rs:453-634 composed as scan_block_stats does (709-799) with

@@ -75,7 +75,37 @@ struct mrl_ctx {
   void* h_stage = nullptr;            // pinned host staging for result read-back
   size_t h_stage_cap = 0;
   mrl_results* spare = nullptr;       // result buffers kept between synchronous mrl_scan calls
+  uint8_t* scratch = nullptr;         // this device's copy of `scratch` (mrl_scan_noalloc)
 };
+
+// ---------------------------------------------------------------------------
+// scratch of the allocation-free scan (mrl_scan_noalloc)
+// ---------------------------------------------------------------------------
+// A fixed array in the library's code object: each GPU the library runs on
+// holds its own copy, at its own address, until the process ends.  In host
+// code its name is only a stand-in for the symbol, never a device address:
+// host code uses the address hipGetSymbolAddress gives for the device
+// (looked up once per device, when a context is created on it).
+constexpr size_t kNaScratchBytes = (size_t)13 << 20;  // 13 MiB
+static __device__ __align__(256) uint8_t scratch[kNaScratchBytes];
+
+static std::mutex g_scratch_mu;
+static std::vector<uint8_t*> g_scratch_ptr;  // per device id
+
+// The device address of `scratch` on `device`, which is current.
+static int scratch_address(int device, uint8_t** out) {
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if ((size_t)device >= g_scratch_ptr.size()) g_scratch_ptr.resize((size_t)device + 1, nullptr);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(MRL_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[device] = static_cast<uint8_t*>(p);
+  }
+  *out = g_scratch_ptr[device];
+  return MRL_OK;
+}
 
 // Pinned host buffer of at least `bytes` (grown on demand; every read-back
 // into it is waited for before the call returns).  Caller holds the lock.
@@ -259,6 +289,12 @@ extern "C" int mrl_ctx_create(int device, mrl_ctx** out) {
   }
   HIP_TRY(hipMalloc(&c->d_flag_tabs, sizeof(tabs)));
   HIP_TRY(hipMemcpy(c->d_flag_tabs, tabs, sizeof(tabs), hipMemcpyHostToDevice));
+  int rc = scratch_address(device, &c->scratch);
+  if (rc) {
+    dev_free(c->d_flag_tabs);
+    (void)hipStreamDestroy(c->stream);
+    return rc;
+  }
   *out = c.release();
   return MRL_OK;
 }
@@ -1349,6 +1385,167 @@ extern "C" int mrl_scan(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* p
   }
   if (old) mrl_results_destroy(old);
   return rc;
+}
+
+// ---------------------------------------------------------------------------
+// allocation-free scan
+// ---------------------------------------------------------------------------
+// Buffers of one mrl_scan_noalloc call inside the device's scratch array.
+// The candidate room per query shrinks with the batch: 16 segments of 4096
+// entries up to 16 queries (the room mrl_results gives), 2048 up to 32,
+// 1024 up to MRL_NOALLOC_MAX_QUERIES.
+struct NaLayout {
+  uint32_t seg_cap;
+  float *cand_score, *cand_lower;
+  uint32_t *cand_row, *seg_count, *hist, *err;
+  float *tau, *tau_hi;
+  uint8_t* mma;
+  uint32_t* zero_begin;  // seg_count .. err: the words a call clears first
+  uint64_t zero_words;
+  size_t bytes;          // end of the last buffer
+};
+static NaLayout na_layout(uint32_t n_q, uint8_t* base) {
+  NaLayout L{};
+  L.seg_cap = n_q <= 16 ? 4096u : (n_q <= 32 ? 2048u : 1024u);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    uint8_t* p = base + off;
+    off += (bytes + 255) & ~(size_t)255;
+    return p;
+  };
+  const size_t cands = (size_t)n_q * kSegs * L.seg_cap;
+  L.cand_score = reinterpret_cast<float*>(take(cands * 4));
+  L.cand_lower = reinterpret_cast<float*>(take(cands * 4));
+  L.cand_row = reinterpret_cast<uint32_t*>(take(cands * 4));
+  // seg_count, hist and err are contiguous (their sizes are multiples of 256 B
+  // except err's, which comes last): one fill clears them
+  L.seg_count = reinterpret_cast<uint32_t*>(take((size_t)n_q * kMaxSegs * 4));
+  L.hist = reinterpret_cast<uint32_t*>(take((size_t)n_q * kHistBins * 4));
+  L.err = reinterpret_cast<uint32_t*>(take((size_t)n_q * 4));
+  L.zero_begin = L.seg_count;
+  L.zero_words = (uint64_t)n_q * (kMaxSegs + kHistBins + 1);
+  L.tau = reinterpret_cast<float*>(take((size_t)n_q * 4));
+  L.tau_hi = reinterpret_cast<float*>(take((size_t)n_q * 4));
+  L.mma = take(mma_bytes(n_q));
+  L.bytes = off;
+  return L;
+}
+
+// Safe-floor re-run decided on the device: the final pass at the safe floor
+// for every query whose selection flagged a shortfall (bit 2 of its status),
+// then its selection; both launches exit at once for every other query.
+// Caller holds the lock.
+static int enqueue_gated_rerun(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t n_q,
+                               const ScanParams& sp, uint32_t K, const PassBuffers& pb) {
+  ScanArgs a{};
+  a.idx = ix->d_blocks;
+  a.recs = ix->recs();
+  a.n_blocks = ix->n_blocks;
+  a.n_pos = (uint32_t)ix->n_blocks;
+  a.shift = 0;
+  a.prev_shift = -1;
+  a.plans = plans->d_plans;
+  a.luts = plans->d_luts;
+  a.n_q = n_q;
+  a.flag_tabs = ctx->d_flag_tabs;
+  a.sp = sp;
+  a.tau = pb.tau;  // the safe floors
+  a.floor_out = pb.tau_hi;
+  a.safe_out = pb.tau;
+  a.cand_score = pb.cand_score;
+  a.cand_row = pb.cand_row;
+  a.seg_count = pb.seg_count;
+  a.nseg = pb.nseg;
+  a.seg_cap = pb.seg_cap;
+  a.err = pb.err;
+  a.gate = pb.status;
+  if (sp.strata != MRL_STRATA_L0_ONLY) {
+    a.excl = 1;
+    const uint32_t g = scan_grid(a, false);
+    if (g >= 1 && g <= (uint32_t)kMaxSegs) {
+      a.nseg = g;
+      a.seg_cap = std::min<uint32_t>(pb.nseg * pb.seg_cap / g, kExclCap);
+    } else {
+      a.excl = 0;
+    }
+  }
+  HIP_TRY(launch_scan(a, false, ctx->stream));
+  SelectArgs sa{};
+  sa.luts = plans->d_luts;
+  sa.cand_score = pb.cand_score;
+  sa.cand_row = pb.cand_row;
+  sa.seg_count = pb.seg_count;
+  sa.nseg = a.nseg;
+  sa.seg_cap = a.seg_cap;
+  sa.err = pb.err;
+  sa.k = K;
+  sa.status = pb.status;
+  sa.out_ids = pb.out_ids;
+  sa.out_scores = pb.out_scores;
+  sa.out_counts = pb.out_counts;
+  sa.tau_final = pb.tau_hi;
+  sa.tau_safe = pb.tau;
+  sa.gate = pb.status;
+  HIP_TRY(launch_select(sa, n_q, ctx->stream));
+  return MRL_OK;
+}
+
+extern "C" int mrl_scan_noalloc(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* plans,
+                                const mrl_scan_config* cfg, const mrl_time_range* time, uint64_t* d_out_ids,
+                                float* d_out_scores, uint32_t* d_out_counts, uint32_t* d_out_status) {
+  if (!ctx || !index || !plans) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (index->ctx != ctx || plans->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "objects belong to another context");
+  uint32_t K;
+  int rc = check_cfg(cfg, &K);
+  if (rc) return rc;
+  const uint32_t n_q = plans->n_q;
+  if (n_q > MRL_NOALLOC_MAX_QUERIES)
+    return fail(MRL_ERR_INVALID_ARG, "mrl_scan_noalloc takes at most " + std::to_string(MRL_NOALLOC_MAX_QUERIES) +
+                                         " queries per call (its scratch has a fixed size)");
+  if (n_q && (!d_out_ids || !d_out_scores || !d_out_counts || !d_out_status))
+    return fail(MRL_ERR_INVALID_ARG, "null output");
+  if (!n_q) return MRL_OK;
+  if (!ctx->scratch) return fail(MRL_ERR_HIP, "no scratch address for this device");
+  const NaLayout L = na_layout(n_q, ctx->scratch);
+  if (L.bytes > kNaScratchBytes) return fail(MRL_ERR_INVALID_ARG, "batch exceeds the scratch array");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  hipStream_t s = ctx->stream;
+  mrl_index* ix = const_cast<mrl_index*>(index);
+  // The array keeps the previous call's contents: the pass state starts from zero.
+  HIP_TRY(launch_fill_u32(L.zero_begin, L.zero_words, 0u, s));
+  if (ix->n_blocks == 0) {
+    HIP_TRY(launch_fill_u32(d_out_counts, n_q, 0u, s));
+    HIP_TRY(launch_fill_u32(d_out_status, n_q, 0u, s));
+    return MRL_OK;
+  }
+  PassBuffers pb;
+  pb.cand_score = L.cand_score;
+  pb.cand_row = L.cand_row;
+  pb.cand_lower = L.cand_lower;
+  pb.mma_ops = reinterpret_cast<uint4*>(L.mma);
+  pb.mma_consts = reinterpret_cast<float*>(L.mma + (size_t)n_q * 2 * kMmaSteps * 16);
+  pb.mma_work = reinterpret_cast<uint32_t*>(L.mma + (size_t)n_q * (2 * kMmaSteps * 16 + kMcCount * 4));
+  pb.seg_count = L.seg_count;
+  pb.nseg = kSegs;
+  pb.seg_cap = L.seg_cap;
+  pb.err = L.err;
+  pb.tau = L.tau;
+  pb.tau_hi = L.tau_hi;
+  pb.hist = L.hist;
+  pb.status = d_out_status;
+  pb.out_ids = d_out_ids;
+  pb.out_scores = d_out_scores;
+  pb.out_counts = d_out_counts;
+  const ScanParams sp = make_params(cfg, time);
+  LevelPlan* lp;
+  if ((rc = get_levels(ix, K, &lp))) return rc;
+  const bool sampled =
+      mma_ok(plans, n_q, sp, pb) ? !mma_stages(ix->n_blocks, n_q).empty() : lp->passes.size() > 1;
+  if ((rc = enqueue_scan(ctx, ix, plans, 0, n_q, sp, K, *lp, pb, nullptr))) return rc;
+  // without a sampling pass no query can be flagged
+  if (sampled && (rc = enqueue_gated_rerun(ctx, ix, plans, n_q, sp, K, pb))) return rc;
+  return MRL_OK;
 }
 
 extern "C" int mrl_scan_fixed_tau(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* plans,

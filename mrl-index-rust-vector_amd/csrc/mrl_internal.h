@@ -223,6 +223,9 @@ struct ScanArgs {
   const uint4* mma_ops;
   const float* mma_consts;
   float* cand_lower;
+  // Gated re-run (one-query kernel only): a workgroup of query q exits at
+  // once unless bit 2 of gate[q] (a final floor left the query short of K) is set.
+  const uint32_t* gate;
 };
 
 // Exact finishing of the MFMA path.  k_finish, one workgroup per query: a
@@ -281,6 +284,9 @@ struct SelectArgs {
   float* out_scores;
   uint32_t* out_counts;
   unsigned long long* stats;  // [kStatCopies][kStatCount] or null: flagged re-runs are counted here
+  // Gated re-run: query q is selected only if bit 2 of gate[q] is set
+  // (gate is the status array this launch rewrites); null: every query.
+  const uint32_t* gate;
 };
 
 // GPU encoder (mrl_encode.hip): rows -> PaxBlock64 records in the reference layout.
@@ -360,6 +366,8 @@ int scan_query_tile(uint32_t n_q);  // queries per workgroup of the non-tile ker
 uint32_t scan_grid(const ScanArgs& a, bool diag);
 hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
+// Sets n words at p to v (a kernel, so that a caller may capture it in a graph).
+hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t s);
 // MFMA path: mode 0 samples (lower bounds into the histogram), 1 appends the
 // pairs whose upper bound reaches the floor in a.tau, 2 appends every active pair.
 hipError_t launch_mma_prep(const MmaPrepArgs& a, hipStream_t s, const LaunchEvents& ev = {});

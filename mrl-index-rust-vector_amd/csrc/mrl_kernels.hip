@@ -1120,6 +1120,8 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   const int nq = (int)min((uint32_t)QT, a.n_q - q0);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t lane = lane_id();
+  // gated re-run (QT == 1): only a query its final selection flagged
+  if (QT == 1 && a.gate && (a.gate[q0] & 4u) == 0u) return;
 
   // This wave's blocks: positions pos = first + k * stride of the pass.  The
   // stride is odd (one wave of the grid stays idle), so the positions of a
@@ -2005,6 +2007,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   const uint32_t q = blockIdx.x;
   const int tid = threadIdx.x;
   const uint32_t K = a.k;
+  if (a.gate && (a.gate[q] & 4u) == 0u) return;  // gated re-run: only a flagged query
   const uint32_t* qcount = a.seg_count + (uint64_t)q * a.nseg;
   const CandView v{a.cand_score + (uint64_t)q * a.nseg * a.seg_cap, a.cand_row + (uint64_t)q * a.nseg * a.seg_cap,
                    a.seg_cap, a.nseg, s_off, s_coff};
@@ -3208,8 +3211,8 @@ static uint32_t resident_groups(K kernel) {
 // Workgroups along x of a scan launch (the same for every query tile).
 uint32_t scan_grid(const ScanArgs& a, bool diag) {
   const bool l0 = a.sp.strata == MRL_STRATA_L0_ONLY;
-  const bool tile = a.n_q >= 8 && !diag && !l0;
-  const int qt = tile ? kTileQ : scan_query_tile(a.n_q);
+  const bool tile = a.n_q >= 8 && !diag && !l0 && !a.gate;
+  const int qt = tile ? kTileQ : (a.gate ? 1 : scan_query_tile(a.n_q));
   const uint32_t tiles = (a.n_q + qt - 1) / qt;
   // One round of resident workgroups (each wave then loops over blocks),
   // but at least one workgroup per candidate segment of a query.
@@ -3230,8 +3233,9 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const Launch
   const bool l0 = a.sp.strata == MRL_STRATA_L0_ONLY;
   // batched: the tile kernel; otherwise one query per workgroup, or the
   // 8-query workgroups of the diagnostic and L0Only paths
-  const bool tile = a.n_q >= 8 && !diag && !l0;
-  const int qt = tile ? kTileQ : scan_query_tile(a.n_q);
+  const bool tile = a.n_q >= 8 && !diag && !l0 && !a.gate;
+  const int qt = tile ? kTileQ : (a.gate ? 1 : scan_query_tile(a.n_q));
+  if (a.gate && diag) return hipErrorInvalidValue;
   const uint32_t tiles = (a.n_q + qt - 1) / qt;
   const uint32_t grid = scan_grid(a, diag);
   // exclusive segments: the one-query kernel, one segment per workgroup
@@ -3259,6 +3263,17 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const Launch
       else launch(k_scan<1, false, false>, g, dim3(256), s, ev, a);
     }
   }
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_fill_u32(uint32_t* p, uint64_t n, uint32_t v) {
+  for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256u) p[i] = v;
+}
+
+hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const uint64_t groups = (n + 255) / 256;
+  hipLaunchKernelGGL(k_fill_u32, dim3((uint32_t)(groups < 2048 ? groups : 2048)), dim3(256), 0, s, p, n, v);
   return hipGetLastError();
 }
 

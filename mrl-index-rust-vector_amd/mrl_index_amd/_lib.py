@@ -182,6 +182,7 @@ SIGNATURES = {
     "mrl_scan_async": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), C.POINTER(TimeRangeC), _P]),
     "mrl_results_fetch": (C.c_int, [_P, _P, _U64, _F, _U32, C.POINTER(ScanStatsC)]),
     "mrl_results_floors": (C.c_int, [_P, _P, _F]),
+    "mrl_scan_noalloc": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), C.POINTER(TimeRangeC), _P, _P, _P, _P]),
     "mrl_scan_fixed_tau": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), C.POINTER(TimeRangeC), _F, _U64,
                                      _F, _F]),
     "mrl_scan_mma_bounds": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), C.POINTER(TimeRangeC), _F, _F]),
