@@ -4,24 +4,35 @@
 A step is one pass of the hot path over one batch of queries: the batched
 query-plan kernel on the resident queries, then every scan pass + top-K
 selection, all enqueued on the library's stream with the index already in
-HBM.  Default workload: BASELINE configs[1] (1M x 768, EDEN-prod prefix,
-batch 1, K_cand 256).  --config 1..5 selects another BASELINE workload.
+HBM.  The default run measures the two workloads BASELINE's metric is quoted
+on: the headline is configs[3] (8.8M x 768 clustered, batch 64, K_cand 256,
+the north-star target); configs[1] (1M x 768, batch 1, K_cand 256) is
+reported beside it under "batch1".  --config N runs BASELINE configs[N-1]
+alone as the headline.
 
 `roofline` uses the dominant kernel's durations from HIP events that each
 dispatch records at its own start and end (hipExtLaunchKernelGGL), from a
 second run of the same steps after the timed one (events stay out of the
 timed region), on the library's stream; `traffic` is the committed rocprofv3
-FETCH_SIZE + WRITE_SIZE reading for the same workload.  Batch 1 (and batches
-under 8) run the one-query k_scan, HBM-bound: 4096 B per block scanned.
-Batches of 8+ run the MFMA-bounded scan, whose final pass (k_scan_mma over
-every block) dominates: 2 x 261 f16 MACs per (query, vector) pair against
-the dense f16 MFMA peak, with that launch's HBM rate beside it.
+FETCH_SIZE + WRITE_SIZE reading for the same workload.  Batches under 8 run
+the one-query k_scan, HBM-bound: 4096 B per block scanned.  Batches of 8+
+run the MFMA-bounded scan, whose final pass (k_scan_mma over every block)
+dominates: 2 x 261 f16 MACs per (query, vector) pair against the dense f16
+MFMA peak, with that launch's HBM rate beside it.  `cold_cache` repeats the
+profiled steps with a 1 GiB read before each (the L2s and the 256 MB
+Infinity Cache evicted).  `reruns_per_step` counts the queries whose final
+floor needed a re-run (safe) or whose list overflowed (dense); those re-runs
+happen at fetch time, outside the timed step, so a non-zero count would mean
+the timed step left work out.
 `cpu_baseline` times the C restatement of the reference's scan_blocks
 (oracle/, Rayon-equivalent sharding on host threads) on query 0 of the same
-index, which also cross-checks the GPU top-K for that query.  `host_boundary`
-is the PCIe-inclusive rate of the synchronous host-buffer calls.  `rerank`
-reranks every query's device-resident shortlist at fp32 / fp16 / int8 after
-the scan; `encode` runs the GPU encoder over the workload's rows.
+index, on the host's cores and on one thread; the batch figure is the time
+of the same batch pass with queries one after another (the reference has no
+batch API).  The same run checks the GPU top-K of query 0 (`parity_query0`).
+`host_boundary` is the PCIe-inclusive rate of the synchronous host-buffer
+calls.  `rerank` reranks every query's device-resident shortlist at fp32 /
+fp16 / int8 after the scan; `encode` runs the GPU encoder over the
+workload's rows (1M-vector workloads only).
 """
 import argparse
 import ctypes as C
@@ -38,10 +49,31 @@ MFMA_F16_PEAK_TFS = 2500.0  # dense f16 MFMA, MI355X
 # MACs per (query, vector) pair of the MFMA bound: 64 prefix dims, 128 S1
 # bits, 64 S4 bits and the 5 meta / error columns of the last K-step
 MMA_MACS_PER_PAIR = 64 + 128 + 64 + 5
+EVICT_BYTES = 1 << 30  # cold-cache runs read this much between steps
+KIND_NAMES = {0: "plan", 1: "scan", 2: "select", 3: "thresh", 6: "finish", 7: "mma_prep", 8: "exact"}
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def host_threads():
+    """Threads for host work: the box's CPU share (OMP_NUM_THREADS there) or the core count."""
+    n = os.cpu_count() or 1
+    share = os.environ.get("OMP_NUM_THREADS")
+    if share and share.isdigit() and int(share) > 0:
+        n = min(n, int(share))
+    return max(1, min(n, 64))
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main():
@@ -49,10 +81,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--config", type=int, default=0, choices=[0, 1, 2, 3, 4, 5],
+                    help="0 (default): configs 4 and 2 (BASELINE configs[3] and [1]); N: that config alone")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-rerank", action="store_true", help="skip the post-scan rerank leg")
+    ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache runs")
+    ap.add_argument("--no-rerank", action="store_true", help="skip the post-scan rerank and encode legs")
     ap.add_argument("--rerank-reps", type=int, default=100)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (PMC byte-counter calibration) and exit")
@@ -66,85 +100,43 @@ def main():
         copy_calibration(args.copy_calibration)
         return
 
-    import numpy as np
     import mrl_index_amd as m
-    from mrl_index_amd import _lib, synth
-
-    w = synth.CONFIGS[args.config]
-    n_threads = min(os.cpu_count() or 1, 16)
-    t0 = time.time()
-    fit = synth.eden_fit(w)
-    log(f"generating + encoding {w.name}: {w.n_docs} x {w.dims} on {n_threads} threads")
-    blocks = synth.encode(w, fit, n_threads)
-    queries, _ = synth.queries(w)
-    log(f"corpus ready in {time.time() - t0:.1f}s ({blocks.nbytes / 1e6:.1f} MB of codes)")
-
+    n_threads = host_threads()
     dev = m.default_device()
-    ix = m.DeviceIndex.upload(blocks, dev)
-    plan = m.QueryPlan.from_query_codec(queries, w.dims, w.prefix_codec, m.MidCodec.RABITQ, fit, None, dev)
-    cfg = m.ScanConfig(shortlist_cand=w.k, strata_depth=w.strata, exhaustive=w.exhaustive)
-    ccfg = cfg.to_c()
-    tr = _lib.TimeRangeC(0, 0, 0, 0)
-    nq = w.n_queries
-    res = C.c_void_p()
-    _lib.check(_lib.lib.mrl_results_create(dev.handle, nq, w.k, C.byref(res)))
-    L = _lib.lib
+    head_id = args.config or 4
+    out = run_workload(head_id, args, m, dev, n_threads, legs=not args.no_rerank and m_rows_fit(head_id))
+    if args.config == 0:
+        out["batch1"] = run_workload(2, args, m, dev, n_threads, legs=not args.no_rerank)
+        for k in ("rerank", "encode", "host_boundary"):
+            if k in out["batch1"]:
+                out[k] = out["batch1"].pop(k)
+    print(json.dumps(out), flush=True)
 
-    def step():
-        _lib.check(L.mrl_plans_rebuild(dev.handle, plan.handle))
-        _lib.check(L.mrl_scan_async(dev.handle, ix.handle, plan.handle, C.byref(ccfg), C.byref(tr), res))
 
-    ids = np.zeros((nq, w.k), dtype=np.uint64)
-    scores = np.zeros((nq, w.k), dtype=np.float32)
-    counts = np.zeros(nq, dtype=np.uint32)
-    st = _lib.ScanStatsC()
+def m_rows_fit(cfg_id):
+    from mrl_index_amd import synth
+    return synth.CONFIGS[cfg_id].n_docs <= 2_000_000
 
-    log(f"warmup {args.warmup} steps")
-    for _ in range(args.warmup):
-        step()
-    _lib.check(L.mrl_results_fetch(dev.handle, res, _lib.u64ptr(ids), _lib.fptr(scores), _lib.u32ptr(counts),
-                                   C.byref(st)))
 
-    log(f"timed {args.steps} steps")
-    dev.synchronize()
-    t_start = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    dev.synchronize()
-    t_end = time.perf_counter()
-    _lib.check(L.mrl_results_fetch(dev.handle, res, _lib.u64ptr(ids), _lib.fptr(scores), _lib.u32ptr(counts),
-                                   C.byref(st)))
-    # Per-kernel durations: the same steps again with dispatch-recorded events
-    # (kept out of the timed region above).
-    prof_steps = min(args.steps, 100)
-    log(f"profiled {prof_steps} steps")
-    _lib.check(L.mrl_ctx_set_profiling(dev.handle, 1))
-    for _ in range(prof_steps):
-        step()
-    dev.synchronize()
-    _lib.check(L.mrl_ctx_set_profiling(dev.handle, 0))
-    cap = 64 * prof_steps + 64
+def kernel_groups(L, _lib, dev, cap):
+    """Collects the recorded launches: {(kind, pass): {"ms": [...], "blocks": [...]}}."""
     kt = (_lib.KernelTimeC * cap)()
     nrec = C.c_uint32()
     _lib.check(L.mrl_ctx_profile_collect(dev.handle, kt, cap, C.byref(nrec)))
-    _lib.check(L.mrl_results_fetch(dev.handle, res, None, None, None, None))
-
-    ms_step = (t_end - t_start) * 1000.0 / args.steps
-    vec_per_s = w.n_docs / (ms_step / 1000.0)
-
-    # per-kernel durations over the profiled steps
     groups = {}
     for i in range(min(nrec.value, cap)):
         r = kt[i]
-        key = ({0: "plan", 1: "scan", 2: "select", 3: "thresh", 6: "finish", 7: "mma_prep", 8: "exact"}[r.kind], r.pass_)
-        g = groups.setdefault(key, {"ms": [], "blocks": []})
+        g = groups.setdefault((KIND_NAMES.get(r.kind, str(r.kind)), r.pass_), {"ms": [], "blocks": []})
         g["ms"].append(r.ms)
         g["blocks"].append(r.n_blocks)
-    kernels = {}
-    for (kind, p), g in sorted(groups.items()):
-        kernels[f"{kind}[{p}]"] = {"avg_ms": float(np.mean(g["ms"])), "launches": len(g["ms"]),
-                                   "avg_blocks": float(np.mean(g["blocks"])), "total_ms": float(np.sum(g["ms"]))}
+    return groups
+
+
+def roofline_of(groups, nq, prof_steps, w, cold=False):
+    """The dominant kernel's roofline from the recorded launches."""
+    import numpy as np
     mma = any(kind == "mma_prep" for kind, _ in groups)
+    src = {}
     if not mma:
         # One-query path: the dominant kernel is k_scan (every pass launches
         # it); its roofline is taken over all of its launches, as rocprofv3's
@@ -155,12 +147,18 @@ def main():
         avg_ms = float(np.mean(scan_ms))
         bytes_per_launch = 4096.0 * float(np.mean(scan_blk))
         achieved = bytes_per_launch / (avg_ms / 1000.0) / 1e9
-        traffic = committed_traffic("k_scan", w.name)
-        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4),
-                    "traffic": traffic["bytes_per_launch"] if traffic else None,
-                    "kernel": "k_scan", "launches_per_step": len(scan_ms) / prof_steps,
-                    "kernel_avg_ms": round(avg_ms, 5), "algorithmic_bytes_per_launch": bytes_per_launch}
+        traffic = None if cold else committed_traffic("k_scan", w.name)
+        r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+             "frac": round(achieved / HBM_PEAK_GBS, 4),
+             "traffic": traffic["bytes_per_launch"] if traffic else None,
+             "kernel": "k_scan", "launches_per_step": len(scan_ms) / prof_steps,
+             "kernel_avg_ms": round(avg_ms, 5), "algorithmic_bytes_per_launch": bytes_per_launch}
+        final = max(p for kind, p in groups if kind == "scan")
+        g = groups[("scan", final)]
+        fb = 4096.0 * float(np.mean(g["blocks"]))
+        fm = float(np.mean(g["ms"]))
+        r["final_pass"] = {"avg_ms": round(fm, 5), "achieved_gb_s": round(fb / (fm / 1000.0) / 1e9, 1),
+                           "frac": round(fb / (fm / 1000.0) / 1e9 / HBM_PEAK_GBS, 4)}
     else:
         # MFMA path: the final pass (the highest pass index) scans every
         # block once for every query of the batch.
@@ -172,17 +170,91 @@ def main():
         achieved = flops / (avg_ms / 1000.0) / 1e12
         bytes_per_launch = 4096.0 * float(np.mean(g["blocks"]))
         hbm = bytes_per_launch / (avg_ms / 1000.0) / 1e9
-        traffic = committed_traffic("k_scan_mma", w.name)
-        roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
-                    "frac": round(achieved / MFMA_F16_PEAK_TFS, 4),
-                    "traffic": traffic["bytes_per_launch"] if traffic else None,
-                    "kernel": "k_scan_mma (final pass)", "launches_per_step": len(g["ms"]) / prof_steps,
-                    "kernel_avg_ms": round(avg_ms, 5), "algorithmic_flops_per_launch": flops,
-                    "algorithmic_bytes_per_launch": bytes_per_launch, "hbm_achieved_gb_s": round(hbm, 1),
-                    "hbm_frac": round(hbm / HBM_PEAK_GBS, 4)}
+        traffic = None if cold else committed_traffic("k_scan_mma", w.name)
+        r = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
+             "frac": round(achieved / MFMA_F16_PEAK_TFS, 4),
+             "traffic": traffic["bytes_per_launch"] if traffic else None,
+             "kernel": "k_scan_mma (final pass)", "launches_per_step": len(g["ms"]) / prof_steps,
+             "kernel_avg_ms": round(avg_ms, 5), "algorithmic_flops_per_launch": flops,
+             "algorithmic_bytes_per_launch": bytes_per_launch, "hbm_achieved_gb_s": round(hbm, 1),
+             "hbm_frac": round(hbm / HBM_PEAK_GBS, 4)}
     if traffic:
-        roofline["traffic_source"] = traffic["source"]
+        r["traffic_source"] = traffic["source"]
+    return r
 
+
+def kernels_of(groups):
+    import numpy as np
+    return {f"{kind}[{p}]": {"avg_ms": round(float(np.mean(g["ms"])), 5), "launches": len(g["ms"]),
+                             "avg_blocks": float(np.mean(g["blocks"]))}
+            for (kind, p), g in sorted(groups.items())}
+
+
+def run_workload(cfg_id, args, m, dev, n_threads, legs):
+    import numpy as np
+    from mrl_index_amd import _lib, synth
+    L = _lib.lib
+    w = synth.CONFIGS[cfg_id]
+    t0 = time.time()
+    fit = synth.eden_fit(w)
+    log(f"config {cfg_id}: generating + encoding {w.name}: {w.n_docs} x {w.dims} on {n_threads} threads")
+    blocks = synth.encode(w, fit, n_threads)
+    queries, _ = synth.queries(w)
+    log(f"corpus ready in {time.time() - t0:.1f}s ({blocks.nbytes / 1e6:.1f} MB of codes)")
+
+    ix = m.DeviceIndex.upload(blocks, dev)
+    plan = m.QueryPlan.from_query_codec(queries, w.dims, w.prefix_codec, m.MidCodec.RABITQ, fit, None, dev)
+    cfg = m.ScanConfig(shortlist_cand=w.k, strata_depth=w.strata, exhaustive=w.exhaustive)
+    ccfg = cfg.to_c()
+    tr = _lib.TimeRangeC(0, 0, 0, 0)
+    nq = w.n_queries
+    res = C.c_void_p()
+    _lib.check(L.mrl_results_create(dev.handle, nq, w.k, C.byref(res)))
+
+    def step():
+        _lib.check(L.mrl_plans_rebuild(dev.handle, plan.handle))
+        _lib.check(L.mrl_scan_async(dev.handle, ix.handle, plan.handle, C.byref(ccfg), C.byref(tr), res))
+
+    ids = np.zeros((nq, w.k), dtype=np.uint64)
+    scores = np.zeros((nq, w.k), dtype=np.float32)
+    counts = np.zeros(nq, dtype=np.uint32)
+    st = _lib.ScanStatsC()
+
+    def fetch(with_out=True):
+        _lib.check(L.mrl_results_fetch(dev.handle, res, _lib.u64ptr(ids) if with_out else None,
+                                       _lib.fptr(scores) if with_out else None,
+                                       _lib.u32ptr(counts) if with_out else None, C.byref(st)))
+
+    log(f"warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        step()
+    fetch()
+
+    log(f"timed {args.steps} steps")
+    dev.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dev.synchronize()
+    t_end = time.perf_counter()
+    fetch()
+    timed_stats = {f: getattr(st, f) for f, _ in _lib.ScanStatsC._fields_}
+
+    # Per-kernel durations: the same steps again with dispatch-recorded events
+    # (kept out of the timed region above).
+    prof_steps = min(args.steps, 100)
+    log(f"profiled {prof_steps} steps")
+    _lib.check(L.mrl_ctx_set_profiling(dev.handle, 1))
+    for _ in range(prof_steps):
+        step()
+    dev.synchronize()
+    _lib.check(L.mrl_ctx_set_profiling(dev.handle, 0))
+    groups = kernel_groups(L, _lib, dev, 64 * prof_steps + 64)
+    fetch(False)
+
+    ms_step = (t_end - t_start) * 1000.0 / args.steps
+    vec_per_s = w.n_docs / (ms_step / 1000.0)
+    step_bytes = 4096.0 * blocks.shape[0] + 4 * w.dims * nq + 12 * w.k * nq
     out = {
         "metric": "scan Mvec/s (vectors scored per second per query batch pass)",
         "value": round(vec_per_s / 1e6, 2),
@@ -196,29 +268,58 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": w.name, "baseline_config": args.config, "n_vectors": w.n_docs, "dims": w.dims,
+        "config": {"workload": w.name, "baseline_config": cfg_id, "n_vectors": w.n_docs, "dims": w.dims,
                    "blocks": int(blocks.shape[0]), "queries_per_step": nq, "k_cand": w.k,
                    "prefix_codec": w.prefix_codec.name.lower(), "strata": w.strata.name.lower(),
                    "pruning": "off (exhaustive)" if w.exhaustive else "on",
                    "query_noise": f"isotropic, norm {w.query_noise}" if not w.fresh_queries else "fresh draw"},
         "queries_per_s": round(nq / (ms_step / 1000.0), 1),
         "pairs_per_s": round(w.n_docs * nq / (ms_step / 1000.0), 1),
-        "step_algorithmic_gb_s": round((4096.0 * blocks.shape[0] + 4 * w.dims * nq + 12 * w.k * nq)
-                                       / (ms_step / 1000.0) / 1e9, 1),
-        "roofline": roofline,
-        "kernels": kernels,
-        "scan_stats_per_step": {f: getattr(st, f) // args.steps for f, _ in _lib.ScanStatsC._fields_},
+        "step_algorithmic_gb_s": round(step_bytes / (ms_step / 1000.0) / 1e9, 1),
+        "step_hbm_frac": round(step_bytes / (ms_step / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": roofline_of(groups, nq, prof_steps, w),
+        "kernels": kernels_of(groups),
+        "scan_stats_per_step": {f: v / args.steps for f, v in timed_stats.items()},
+        "reruns_per_step": {"safe": timed_stats["reruns_safe"] / args.steps,
+                            "dense": timed_stats["reruns_dense"] / args.steps},
     }
 
-    out["host_boundary"] = host_boundary_rate(L, _lib, dev, ix, queries, fit, w, ccfg, tr)
-    if not args.no_rerank:
+    if not args.no_cold:
+        # the same steps, each after a 1 GiB read: per-kernel durations with cold caches
+        log(f"cold-cache {prof_steps} steps")
+        _lib.check(L.mrl_ctx_evict_caches(dev.handle, EVICT_BYTES))
+        dev.synchronize()
+        _lib.check(L.mrl_ctx_set_profiling(dev.handle, 1))
+        for _ in range(prof_steps):
+            _lib.check(L.mrl_ctx_evict_caches(dev.handle, EVICT_BYTES))
+            step()
+        dev.synchronize()
+        _lib.check(L.mrl_ctx_set_profiling(dev.handle, 0))
+        cg = kernel_groups(L, _lib, dev, 64 * prof_steps + 64)
+        fetch(False)
+        kernel_ms = sum(float(np.sum(g["ms"])) for g in cg.values()) / prof_steps
+        warm_ms = sum(float(np.sum(g["ms"])) for g in groups.values()) / prof_steps
+        out["cold_cache"] = {
+            "method": f"{EVICT_BYTES >> 20} MiB device read before each step (L2 and Infinity Cache evicted); "
+                      "durations from the dispatch-recorded events of the scan's kernels",
+            "kernel_ms_per_step": round(kernel_ms, 5), "warm_kernel_ms_per_step": round(warm_ms, 5),
+            "value": round(w.n_docs / (kernel_ms / 1000.0) / 1e6, 2), "unit": "Mvec/s",
+            "step_algorithmic_gb_s": round(step_bytes / (kernel_ms / 1000.0) / 1e9, 1),
+            "roofline": roofline_of(cg, nq, prof_steps, w, cold=True), "kernels": kernels_of(cg)}
+
+    if legs:
+        out["host_boundary"] = host_boundary_rate(L, _lib, dev, ix, queries, fit, w, ccfg, tr)
         out["rerank"], out["encode"] = rerank_leg(L, _lib, m, dev, w, step, res, queries, args.rerank_reps,
                                                   n_threads, not args.no_cpu_baseline, fit, blocks)
-
     if not args.no_cpu_baseline:
+        step()
+        fetch()
         out["cpu_baseline"], out["parity_query0"] = cpu_baseline(w, blocks, queries, fit, ids[0], scores[0],
                                                                  int(counts[0]), args.cpu_seconds, n_threads)
-    print(json.dumps(out), flush=True)
+    L.mrl_results_destroy(res)
+    plan.close()
+    ix.close()
+    return out
 
 
 def encode_leg(m, dev, w, rows, fit, blocks, n_threads, with_cpu, reps=5):
@@ -403,23 +504,27 @@ def committed_traffic(kernel, workload):
 
 def cpu_baseline(w, blocks, queries, fit, gpu_ids, gpu_scores, gpu_count, seconds, n_threads):
     """The oracle's scan_blocks (restated reference, sharded like Rayon) on
-    query 0; also the parity check of the GPU top-K for that query."""
+    query 0, on n_threads host threads and on one; also the parity check of
+    the GPU top-K for that query."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import ora
     fitc = ora.Fit(fit.mean, 4, fit.seed, fit.n_observed) if fit is not None else None
     op = ora.plan_build(queries[0], w.dims, int(w.prefix_codec), 0, fitc, None)
-    cfg = ora.scan_config(w.k, depth=int(w.strata), sharding=True, threads=n_threads)
-    times = []
-    t_end = time.time() + seconds
-    ref = None
-    while time.time() < t_end or len(times) < 2:
-        t = time.perf_counter()
-        ref = ora.scan_blocks(blocks, op, cfg)
-        times.append(time.perf_counter() - t)
-        if len(times) >= 50:
-            break
-    t_med = float(np.median(times[1:] if len(times) > 1 else times))
+
+    def timed(threads, budget, min_runs, max_runs):
+        cfg = ora.scan_config(w.k, depth=int(w.strata), sharding=True, threads=threads)
+        ref = ora.scan_blocks(blocks, op, cfg)  # warm-up pass (mrl_index.rs:663-664)
+        times = []
+        t_end = time.time() + budget
+        while (time.time() < t_end or len(times) < min_runs) and len(times) < max_runs:
+            t = time.perf_counter()
+            ref = ora.scan_blocks(blocks, op, cfg)
+            times.append(time.perf_counter() - t)
+        return float(np.median(times)), len(times), ref
+
+    t_med, n_runs, ref = timed(n_threads, seconds, 5, 50)
+    t_one, n_one, _ = timed(1, seconds / 2, 3, 10)
     ref_ids, ref_scores = ref
     # tie-aware top-K comparison (scores bit-exact)
     n = gpu_count
@@ -429,9 +534,16 @@ def cpu_baseline(w, blocks, queries, fit, gpu_ids, gpu_scores, gpu_count, second
         ok = np.array_equal(np.sort(gs).view(np.uint32), np.sort(rs).view(np.uint32))
         kth = np.sort(rs)[0] if len(rs) >= w.k else -np.inf
         ok = ok and set(gpu_ids[:n][gs > kth].tolist()) == set(ref_ids[rs > kth].tolist())
-    base = {"value": round(w.n_docs / t_med / 1e6, 2), "unit": "Mvec/s", "cores": n_threads, "kind": "port",
-            "sample": f"query 0 of this workload over the full index, {len(times)} runs of the oracle's "
-                      f"sharded scan_blocks, median {t_med * 1000:.1f} ms"}
+    nq = w.n_queries
+    base = {"value": round(w.n_docs / (t_med * nq) / 1e6, 3), "unit": "Mvec/s", "cores": n_threads, "kind": "port",
+            "per_query_mvec_s": round(w.n_docs / t_med / 1e6, 2), "ms_per_query": round(t_med * 1000, 3),
+            "one_thread": {"value": round(w.n_docs / (t_one * nq) / 1e6, 3),
+                           "per_query_mvec_s": round(w.n_docs / t_one / 1e6, 2), "ms_per_query": round(t_one * 1000, 3),
+                           "runs": n_one},
+            "host_cpus": os.cpu_count(), "cpu_model": cpu_model(),
+            "sample": f"query 0 of this workload over the full index: the oracle's sharded scan_blocks, one warm-up "
+                      f"then {n_runs} runs on {n_threads} threads ({n_one} on one), median; value = N / ({nq} x "
+                      f"the per-query time), the batch pass with queries one after another"}
     return base, {"checked": True, "identical_topk": bool(ok)}
 
 

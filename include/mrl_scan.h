@@ -403,6 +403,11 @@ int mrl_ctx_set_profiling(mrl_ctx *ctx, int enable);
 /* Waits for the stream, returns up to max recorded launches (oldest first),
  * total count in *n_recorded, and clears the record. */
 int mrl_ctx_profile_collect(mrl_ctx *ctx, mrl_kernel_time *out, uint32_t max, uint32_t *n_recorded);
+/* Measurement helper (no reference counterpart): enqueues a read of `bytes`
+ * (at most 4 GiB) of a device buffer the context owns (allocated on first
+ * use), which evicts the L2 caches and the Infinity Cache before a
+ * cold-cache measurement.  Not timed as a scan kernel. */
+int mrl_ctx_evict_caches(mrl_ctx *ctx, uint64_t bytes);
 
 /* ---------------------------------------------------------------- */
 /* ingest-side helpers (host C++, multi-threaded)                   */

@@ -71,6 +71,8 @@ struct mrl_ctx {
   std::vector<ProfRecord> prof;       // recorded, not yet collected
   std::vector<hipEvent_t> event_pool; // reusable events
   uint32_t* d_crc = nullptr;          // encoder CRC tables: [256] byte table, then [64][32] carry map
+  uint8_t* d_evict = nullptr;         // cache-eviction buffer (mrl_ctx_evict_caches), zero-filled
+  uint64_t evict_bytes = 0;
   uint32_t crc_const = 0;
   void* h_stage = nullptr;            // pinned host staging for result read-back
   size_t h_stage_cap = 0;
@@ -308,6 +310,7 @@ extern "C" void mrl_ctx_destroy(mrl_ctx* ctx) {
   results_release(ctx->spare);
   dev_free(ctx->d_flag_tabs);
   dev_free(ctx->d_crc);
+  dev_free(ctx->d_evict);
   for (auto& r : ctx->prof) {
     (void)hipEventDestroy(r.start);
     (void)hipEventDestroy(r.stop);
@@ -330,6 +333,26 @@ extern "C" int mrl_ctx_set_profiling(mrl_ctx* ctx, int enable) {
   if (!ctx) return fail(MRL_ERR_INVALID_ARG, "ctx is null");
   std::lock_guard<std::mutex> g(ctx->mu);
   ctx->profiling = enable != 0;
+  return MRL_OK;
+}
+
+extern "C" int mrl_ctx_evict_caches(mrl_ctx* ctx, uint64_t bytes) {
+  if (!ctx) return fail(MRL_ERR_INVALID_ARG, "ctx is null");
+  if (bytes > ((uint64_t)4 << 30)) return fail(MRL_ERR_INVALID_ARG, "at most 4 GiB");
+  bytes = (bytes + 15) & ~(uint64_t)15;
+  if (!bytes) return MRL_OK;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  if (bytes > ctx->evict_bytes) {
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    dev_free(ctx->d_evict);
+    ctx->d_evict = nullptr;
+    ctx->evict_bytes = 0;
+    if (hipMalloc(&ctx->d_evict, bytes) != hipSuccess) return fail(MRL_ERR_OUT_OF_MEMORY, "eviction buffer");
+    ctx->evict_bytes = bytes;
+    HIP_TRY(launch_fill_u32(reinterpret_cast<uint32_t*>(ctx->d_evict), bytes / 4, 0u, ctx->stream));
+  }
+  HIP_TRY(launch_read_sweep(reinterpret_cast<uint4*>(ctx->d_evict), bytes / 16, ctx->stream));
   return MRL_OK;
 }
 

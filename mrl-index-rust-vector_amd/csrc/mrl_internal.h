@@ -368,6 +368,9 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const Launch
 hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
 // Sets n words at p to v (a kernel, so that a caller may capture it in a graph).
 hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t s);
+// Reads n uint4 at p (evicts the caches; the loads are kept alive by a store
+// whose condition never holds for the data written by launch_fill_u32).
+hipError_t launch_read_sweep(uint4* p, uint64_t n, hipStream_t s);
 // MFMA path: mode 0 samples (lower bounds into the histogram), 1 appends the
 // pairs whose upper bound reaches the floor in a.tau, 2 appends every active pair.
 hipError_t launch_mma_prep(const MmaPrepArgs& a, hipStream_t s, const LaunchEvents& ev = {});

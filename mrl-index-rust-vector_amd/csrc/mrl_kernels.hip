@@ -3277,6 +3277,24 @@ hipError_t launch_fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Cache eviction sweep: every thread xors its share of the buffer; the
+// buffer holds zeros, so the final store never happens, but the compiler must
+// keep the loads.
+__global__ __launch_bounds__(256) void k_read_sweep(uint4* p, uint64_t n) {
+  uint32_t x = 0u;
+  for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256u) {
+    const uint4 v = p[i];
+    x ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (x == 0x9e3779b9u) p[0].x = x;
+}
+
+hipError_t launch_read_sweep(uint4* p, uint64_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_read_sweep, dim3(4096), dim3(256), 0, s, p, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev) {
   if (n_q == 0) return hipSuccess;
   launch(k_select, dim3(n_q), dim3(kSelThreads), s, ev, a);
