@@ -50,7 +50,7 @@ MFMA_F16_PEAK_TFS = 2500.0  # dense f16 MFMA, MI355X
 # bits, 64 S4 bits and the 5 meta / error columns of the last K-step
 MMA_MACS_PER_PAIR = 64 + 128 + 64 + 5
 EVICT_BYTES = 1 << 30  # cold-cache runs read this much between steps
-KIND_NAMES = {0: "plan", 1: "scan", 2: "select", 3: "thresh", 6: "finish", 7: "mma_prep", 8: "exact"}
+KIND_NAMES = {0: "plan", 1: "scan", 2: "select", 3: "thresh", 6: "finish", 7: "mma_prep", 8: "exact", 9: "bounds"}
 
 
 def log(msg):
@@ -87,6 +87,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache runs")
     ap.add_argument("--no-rerank", action="store_true", help="skip the post-scan rerank and encode legs")
+    ap.add_argument("--layout", choices=["standard", "clustered"], default="standard",
+                    help="with --config N: the documents in row order (standard) or grouped by centroid (clustered)")
+    ap.add_argument("--no-cluster-layout", action="store_true",
+                    help="default run: skip config 4 in the cluster-grouped layout")
     ap.add_argument("--rerank-reps", type=int, default=100)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (PMC byte-counter calibration) and exit")
@@ -104,7 +108,12 @@ def main():
     n_threads = host_threads()
     dev = m.default_device()
     head_id = args.config or 4
-    out = run_workload(head_id, args, m, dev, n_threads, legs=not args.no_rerank and m_rows_fit(head_id))
+    out = run_workload(head_id, args, m, dev, n_threads, legs=not args.no_rerank and m_rows_fit(head_id),
+                       layout=args.layout if args.config else "standard")
+    if args.config == 0 and not args.no_cluster_layout:
+        # the same documents and queries grouped by centroid: block skipping
+        out["cluster_layout"] = run_workload(4, args, m, dev, n_threads, legs=False, layout="clustered",
+                                             cpu_seconds=0.5)
     if args.config == 0:
         out["batch1"] = run_workload(2, args, m, dev, n_threads, legs=not args.no_rerank)
         for k in ("rerank", "encode", "host_boundary"):
@@ -190,15 +199,24 @@ def kernels_of(groups):
             for (kind, p), g in sorted(groups.items())}
 
 
-def run_workload(cfg_id, args, m, dev, n_threads, legs):
+def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_seconds=None):
+    """One workload as a bench record.  layout "clustered": the documents of a
+    clustered corpus grouped by centroid (mrl_synth_encode_clustered), so the
+    index carries block bounds and the final passes skip blocks no query of
+    the batch can reach; the queries are the same."""
     import numpy as np
     from mrl_index_amd import _lib, synth
     L = _lib.lib
     w = synth.CONFIGS[cfg_id]
     t0 = time.time()
     fit = synth.eden_fit(w)
-    log(f"config {cfg_id}: generating + encoding {w.name}: {w.n_docs} x {w.dims} on {n_threads} threads")
-    blocks = synth.encode(w, fit, n_threads)
+    log(f"config {cfg_id} ({layout}): generating + encoding {w.name}: {w.n_docs} x {w.dims} on {n_threads} threads")
+    if layout == "clustered":
+        if not w.n_centroids:
+            raise SystemExit(f"config {cfg_id} has no clusters")
+        blocks, _ = synth.encode_clustered(w, fit, n_threads)
+    else:
+        blocks = synth.encode(w, fit, n_threads)
     queries, _ = synth.queries(w)
     log(f"corpus ready in {time.time() - t0:.1f}s ({blocks.nbytes / 1e6:.1f} MB of codes)")
 
@@ -268,7 +286,8 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs):
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": w.name, "baseline_config": cfg_id, "n_vectors": w.n_docs, "dims": w.dims,
+        "config": {"workload": w.name + ("-cluster-grouped" if layout == "clustered" else ""),
+                   "baseline_config": cfg_id, "layout": layout, "n_vectors": w.n_docs, "dims": w.dims,
                    "blocks": int(blocks.shape[0]), "queries_per_step": nq, "k_cand": w.k,
                    "prefix_codec": w.prefix_codec.name.lower(), "strata": w.strata.name.lower(),
                    "pruning": "off (exhaustive)" if w.exhaustive else "on",
@@ -283,6 +302,9 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs):
         "reruns_per_step": {"safe": timed_stats["reruns_safe"] / args.steps,
                             "dense": timed_stats["reruns_dense"] / args.steps},
     }
+    if layout == "clustered":
+        # blocks the final pass scanned per query, against the index's
+        out["final_pass_blocks_per_query"] = round(timed_stats["blocks"] / args.steps / nq, 1)
 
     if not args.no_cold:
         # the same steps, each after a 1 GiB read: per-kernel durations with cold caches
@@ -314,8 +336,9 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs):
     if not args.no_cpu_baseline:
         step()
         fetch()
-        out["cpu_baseline"], out["parity_query0"] = cpu_baseline(w, blocks, queries, fit, ids[0], scores[0],
-                                                                 int(counts[0]), args.cpu_seconds, n_threads)
+        out["cpu_baseline"], out["parity_query0"] = cpu_baseline(
+            w, blocks, queries, fit, ids[0], scores[0], int(counts[0]),
+            args.cpu_seconds if cpu_seconds is None else cpu_seconds, n_threads)
     L.mrl_results_destroy(res)
     plan.close()
     ix.close()

@@ -39,6 +39,8 @@ extern "C" {
 #define MRL_MAX_SHORTLIST 4096
 #define MRL_MAX_DIMS 8192
 #define MRL_NOALLOC_MAX_QUERIES 64
+/* block_flags bit of the cluster-grouped layout (see mrl_encode_corpus_clustered) */
+#define MRL_BLOCK_FLAG_ONE_CLUSTER 0x0001u
 
 typedef enum mrl_status {
   MRL_OK = 0,
@@ -295,6 +297,15 @@ int mrl_scan_mma_bounds(mrl_ctx *ctx, const mrl_index *index, const mrl_plans *p
                         const mrl_scan_config *cfg, const mrl_time_range *time, float *out_upper,
                         float *out_lower);
 
+/* Diagnostic of block skipping (no reference counterpart): for every
+ * (query, block) the upper bound on the full score (src/scan.rs:453-634,
+ * every stage run) of the block's active slots that the scan compares with
+ * the query's floor to skip the block.  out_bounds is [query][block]; blocks
+ * without bounds (no MRL_BLOCK_FLAG_ONE_CLUSTER, or an index with none) read
+ * NaN.  Requires the RaBitQ mid-band and an S1 stage. */
+int mrl_index_block_bounds(mrl_ctx *ctx, const mrl_index *index, const mrl_plans *plans,
+                           const mrl_scan_config *cfg, float *out_bounds);
+
 /* ---------------------------------------------------------------- */
 /* post-scan rerank (src/pipeline.rs:157-180, src/lowprec.rs:18-121) */
 /* ---------------------------------------------------------------- */
@@ -385,7 +396,8 @@ typedef enum mrl_kernel_kind {
   MRL_KERNEL_RERANK_SORT = 5, /* stable sort of the reranked shortlist */
   MRL_KERNEL_FINISH = 6,      /* candidates of the MFMA-bounded scan to score exactly */
   MRL_KERNEL_MMA_PREP = 7,    /* query operands of the MFMA-bounded scan */
-  MRL_KERNEL_EXACT = 8        /* exact scores of those candidates */
+  MRL_KERNEL_EXACT = 8,       /* exact scores of those candidates */
+  MRL_KERNEL_BOUNDS = 9       /* block bounds: cluster x query table (pass 0), block lists (pass 1) */
 } mrl_kernel_kind;
 
 typedef struct mrl_kernel_time {
@@ -423,6 +435,18 @@ int mrl_encode_block(const float *vectors, uint32_t n, uint32_t dims, const uint
 int mrl_encode_corpus(const float *matrix, uint64_t n, uint32_t dims, uint32_t default_source,
                       const mrl_eden_fit *eden, const mrl_eden_fit *eden_mid, int n_threads,
                       void *out_blocks);
+/* Cluster-grouped layout (no reference counterpart; an encoder convention
+ * for block skipping): mrl_encode_corpus with cluster[i] the coarse cluster
+ * of row i, rows grouped by cluster.  A block whose rows all share one
+ * cluster below 65536 records it in coarse_cluster_id (src/block.rs:38) and
+ * sets MRL_BLOCK_FLAG_ONE_CLUSTER in block_flags (block.rs:39).  The
+ * reference's scan reads neither field, so the records stay valid PaxBlock64
+ * blocks; every other byte, the CRC aside, equals mrl_encode_corpus's.  An
+ * index of such blocks gets per-block score bounds at upload
+ * (mrl_index_upload), which let every scan skip blocks no query can reach. */
+int mrl_encode_corpus_clustered(const float *matrix, uint64_t n, uint32_t dims, const uint32_t *cluster,
+                                uint32_t default_source, const mrl_eden_fit *eden, const mrl_eden_fit *eden_mid,
+                                int n_threads, void *out_blocks);
 /* encode_f32_corpus_par (src/encoder.rs:195-219) on the GPU: n rows of `dims`
  * floats already in device memory -> ceil(n/64) records in device memory, in
  * the reference byte layout with the CRC set, byte-identical to
@@ -430,6 +454,12 @@ int mrl_encode_corpus(const float *matrix, uint64_t n, uint32_t dims, uint32_t d
 int mrl_encode_corpus_device(mrl_ctx *ctx, const float *d_matrix, uint64_t n, uint32_t dims,
                              uint32_t default_source, const mrl_eden_fit *eden,
                              const mrl_eden_fit *eden_mid, void *d_out_blocks);
+/* mrl_encode_corpus_device with the cluster-grouped layout: d_cluster holds
+ * the n rows' clusters in device memory; byte-identical to
+ * mrl_encode_corpus_clustered. */
+int mrl_encode_corpus_device_clustered(mrl_ctx *ctx, const float *d_matrix, uint64_t n, uint32_t dims,
+                                       const uint32_t *d_cluster, uint32_t default_source,
+                                       const mrl_eden_fit *eden, const mrl_eden_fit *eden_mid, void *d_out_blocks);
 /* Device memory on the context's GPU, for callers without a HIP allocator of
  * their own (no reference counterpart).  Copies are synchronous. */
 int mrl_device_alloc(mrl_ctx *ctx, size_t bytes, void **out);

@@ -42,6 +42,12 @@ int mrl_synth_eden_fit(const mrl_synth_spec *spec, uint64_t n_rows, float *out_m
 /* Generate and encode all documents: ceil(n_docs/64) blocks, timestamp = row. */
 int mrl_synth_encode(const mrl_synth_spec *spec, const mrl_eden_fit *eden, const mrl_eden_fit *eden_mid,
                      uint32_t default_source, int n_threads, void *out_blocks);
+/* The same documents of a clustered corpus in the cluster-grouped layout
+ * (mrl_encode_corpus_clustered): rows ordered by (centroid, row), timestamp
+ * = position in that order; out_rows[p] (may be NULL) = the row at
+ * position p. */
+int mrl_synth_encode_clustered(const mrl_synth_spec *spec, const mrl_eden_fit *eden, const mrl_eden_fit *eden_mid,
+                               uint32_t default_source, int n_threads, void *out_blocks, uint64_t *out_rows);
 
 #ifdef __cplusplus
 }

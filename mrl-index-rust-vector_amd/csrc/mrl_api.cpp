@@ -189,6 +189,19 @@ struct mrl_index {
   uint64_t n_blocks = 0;
   const uint4* recs() const { return d_recs; }
   std::map<uint32_t, LevelPlan> levels;
+  // Block bounds (blocks with MRL_BLOCK_FLAG_ONE_CLUSTER): one allocation
+  // holding the cluster centers [n_cl][kBndStride], their part norms
+  // [n_cl][4], each block's dense cluster (~0u: unbounded) and radii [4].
+  uint32_t n_cl = 0;
+  uint8_t* d_bounds = nullptr;
+  float* d_center = nullptr;
+  float* d_cnorm = nullptr;
+  uint32_t* d_bcl = nullptr;
+  float* d_brad = nullptr;
+  // per-scan scratch of the block selection (grown on demand): the cluster x
+  // query table, query norms, block lists and counts
+  uint8_t* d_bsel = nullptr;
+  size_t bsel_bytes = 0;
 };
 
 struct mrl_plans {
@@ -252,6 +265,8 @@ struct mrl_rerank_store {
   void* d_data = nullptr;       // 768 dims: accumulator-major rows; else row-major f32
   uint16_t* d_scales = nullptr; // int8: f16 scale bits per row
 };
+
+static int build_bounds(mrl_ctx* ctx, mrl_index* ix);
 
 static void dev_free(void* p) {
   if (p) (void)hipFree(p);
@@ -442,6 +457,12 @@ extern "C" int mrl_index_upload(mrl_ctx* ctx, const void* blocks, uint64_t n_blo
       }
     }
     dev_free(staging);
+    int rc = build_bounds(ctx, ix.get());
+    if (rc) {
+      dev_free(ix->d_blocks);
+      dev_free(ix->d_recs);
+      return rc;
+    }
   }
   *out = ix.release();
   return MRL_OK;
@@ -509,7 +530,86 @@ extern "C" void mrl_index_destroy(mrl_index* index) {
   (void)hipStreamSynchronize(index->ctx->stream);
   dev_free(index->d_blocks);
   dev_free(index->d_recs);
+  dev_free(index->d_bounds);
+  dev_free(index->d_bsel);
   delete index;
+}
+
+// Block bounds of an uploaded index: every block whose header carries
+// MRL_BLOCK_FLAG_ONE_CLUSTER belongs to the cluster in coarse_cluster_id
+// (header dword 3 = coarse_cluster_id | block_flags << 16, src/block.rs:38-39).
+// Builds the centers and radii on the device (k_bound_centers,
+// k_bound_radii); no flagged block: no bounds.  Caller holds the lock.
+static int build_bounds(mrl_ctx* ctx, mrl_index* ix) {
+  const uint64_t B = ix->n_blocks;
+  if (!B) return MRL_OK;
+  std::vector<uint32_t> h3(B);
+  HIP_TRY(hipMemcpy2DAsync(h3.data(), 4, ix->d_blocks + 12, kBlockBytes, 4, B, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  std::map<uint32_t, uint32_t> dense;
+  std::vector<uint32_t> bcl(B, ~0u);
+  for (uint64_t b = 0; b < B; ++b)
+    if ((h3[b] >> 16) & kBlockFlagOneCluster) {
+      auto it = dense.emplace(h3[b] & 0xffffu, (uint32_t)dense.size()).first;
+      bcl[b] = it->second;
+    }
+  const uint32_t n_cl = (uint32_t)dense.size();
+  if (!n_cl) return MRL_OK;
+  std::vector<uint32_t> start(n_cl + 1, 0), blocks;
+  for (uint64_t b = 0; b < B; ++b)
+    if (bcl[b] != ~0u) ++start[bcl[b] + 1];
+  for (uint32_t c = 0; c < n_cl; ++c) start[c + 1] += start[c];
+  blocks.resize(start[n_cl]);
+  {
+    std::vector<uint32_t> fill(start.begin(), start.end() - 1);
+    for (uint64_t b = 0; b < B; ++b)
+      if (bcl[b] != ~0u) blocks[fill[bcl[b]]++] = (uint32_t)b;
+  }
+  const size_t center_bytes = (size_t)n_cl * kBndStride * 4, cnorm_bytes = (size_t)n_cl * 16;
+  const size_t bcl_bytes = ((B * 4 + 15) / 16) * 16, brad_bytes = B * 16;
+  const size_t bytes = center_bytes + cnorm_bytes + bcl_bytes + brad_bytes;
+  uint32_t* d_csr = nullptr;
+  if (hipMalloc(&ix->d_bounds, bytes) != hipSuccess) {
+    ix->d_bounds = nullptr;
+    return fail(MRL_ERR_OUT_OF_MEMORY, "block bounds");
+  }
+  if (hipMalloc(&d_csr, (start.size() + blocks.size()) * 4) != hipSuccess) {
+    dev_free(ix->d_bounds);
+    ix->d_bounds = nullptr;
+    return fail(MRL_ERR_OUT_OF_MEMORY, "block bounds");
+  }
+  ix->d_center = reinterpret_cast<float*>(ix->d_bounds);
+  ix->d_cnorm = reinterpret_cast<float*>(ix->d_bounds + center_bytes);
+  ix->d_bcl = reinterpret_cast<uint32_t*>(ix->d_bounds + center_bytes + cnorm_bytes);
+  ix->d_brad = reinterpret_cast<float*>(ix->d_bounds + center_bytes + cnorm_bytes + bcl_bytes);
+  hipError_t e = hipMemcpyAsync(ix->d_bcl, bcl.data(), B * 4, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(d_csr, start.data(), start.size() * 4, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(d_csr + start.size(), blocks.data(), blocks.size() * 4, hipMemcpyHostToDevice, ctx->stream);
+  BoundBuildArgs a{};
+  a.idx = ix->d_blocks;
+  a.recs = ix->recs();
+  a.n_blocks = B;
+  a.cl_start = d_csr;
+  a.cl_blocks = d_csr + start.size();
+  a.n_cl = n_cl;
+  a.flag_tabs = ctx->d_flag_tabs;
+  for (int i = 0; i < 16; ++i) a.cb[i] = ctx->consts.eden_codebook[i];
+  a.center = ix->d_center;
+  a.cnorm = ix->d_cnorm;
+  a.bcl = ix->d_bcl;
+  a.brad = ix->d_brad;
+  if (e == hipSuccess) e = launch_bound_build(a, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  dev_free(d_csr);
+  if (e != hipSuccess) {
+    dev_free(ix->d_bounds);
+    ix->d_bounds = nullptr;
+    return fail(MRL_ERR_HIP, std::string("block bounds: ") + hipGetErrorString(e));
+  }
+  ix->n_cl = n_cl;
+  return MRL_OK;
 }
 
 // Pass schedule (the same for every K).  When the index has more than 256
@@ -835,6 +935,7 @@ struct PassBuffers {
   uint64_t* out_ids;
   float* out_scores;
   uint32_t* out_counts;
+  bool block_lists = true;  // false: never skip blocks (the block selection allocates its scratch)
 };
 
 // Floor rank for the final pass: the rank-th best score of a sample of n_s
@@ -898,6 +999,101 @@ static std::vector<MmaStage> mma_stages(uint64_t B, uint32_t n_q) {
   return st;
 }
 
+// Block bounds apply to scans whose score is the code-space dot product the
+// bounds were built for: the RaBitQ mid-band, an S1 stage, and pruning on.
+static bool bounds_ok(const mrl_index* ix, const mrl_plans* plans, const ScanParams& sp, const PassBuffers& pb) {
+  return pb.block_lists && ix->n_cl != 0 && plans->mid_codec == MRL_MID_RABITQ &&
+         (sp.strata == MRL_STRATA_L1_RABITQ || sp.strata == MRL_STRATA_FULL64B) && !sp.exhaustive;
+}
+
+// Scratch of the block selection of one scan, in the index (grown on demand):
+// the cluster x query table, the query norms, two count arrays (one per
+// block list of the scan) and the block lists, n_chunks of n_blocks each.
+struct BoundSel {
+  float* table;
+  float* qn;
+  uint32_t* bcount;  // [2][n_chunks]
+  uint32_t* blist;
+  uint32_t n_chunks;
+  uint32_t chunk;
+};
+
+// The cluster x query table of a scan whose workgroups take `chunk` queries
+// each; clears both count arrays.  Caller holds the lock.
+static int enqueue_bound_table(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t plans_first,
+                               uint32_t n_q, const ScanParams& sp, uint32_t chunk, BoundSel* sel) {
+  const uint32_t n_chunks = (n_q + chunk - 1) / chunk;
+  const size_t table_bytes = ((size_t)ix->n_cl * n_q * 4 + 255) & ~(size_t)255;
+  const size_t qn_bytes = ((size_t)n_q * 16 + 255) & ~(size_t)255;
+  const size_t count_bytes = ((size_t)2 * n_chunks * 4 + 255) & ~(size_t)255;
+  const size_t need = table_bytes + qn_bytes + count_bytes + (size_t)n_chunks * ix->n_blocks * 4;
+  if (need > ix->bsel_bytes) {
+    HIP_TRY(hipStreamSynchronize(ctx->stream));  // an earlier scan may still read the old lists
+    dev_free(ix->d_bsel);
+    ix->d_bsel = nullptr;
+    ix->bsel_bytes = 0;
+    if (hipMalloc(&ix->d_bsel, need) != hipSuccess) {
+      ix->d_bsel = nullptr;
+      return fail(MRL_ERR_OUT_OF_MEMORY, "block selection");
+    }
+    ix->bsel_bytes = need;
+  }
+  sel->table = reinterpret_cast<float*>(ix->d_bsel);
+  sel->qn = reinterpret_cast<float*>(ix->d_bsel + table_bytes);
+  sel->bcount = reinterpret_cast<uint32_t*>(ix->d_bsel + table_bytes + qn_bytes);
+  sel->blist = reinterpret_cast<uint32_t*>(ix->d_bsel + table_bytes + qn_bytes + count_bytes);
+  sel->n_chunks = n_chunks;
+  sel->chunk = chunk;
+  BoundScanArgs b{};
+  b.center = ix->d_center;
+  b.cnorm = ix->d_cnorm;
+  b.n_cl = ix->n_cl;
+  b.n_q = n_q;
+  b.plans = plans->d_plans + plans_first;
+  b.luts = plans->d_luts + (size_t)plans_first * kQData;
+  b.sp = sp;
+  b.eden = plans->prefix_codec == MRL_PREFIX_EDEN_PROD;
+  b.table = sel->table;
+  b.qn = sel->qn;
+  b.bcount = sel->bcount;
+  b.chunk = chunk;
+  ProfScope ps(ctx, MRL_KERNEL_BOUNDS, 0, 0, n_q);
+  HIP_TRY(launch_bound_table(b, ctx->stream, ps.ev()));
+  ps.commit(true);
+  return MRL_OK;
+}
+
+// Block list `which` (0 or 1) of the pass over blocks pos << shift, pos <
+// n_pos, at the floors in `floor`; points the block-list fields of *a at it.
+// Caller holds the lock.
+static int enqueue_block_select(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t n_q,
+                                const BoundSel& sel, int which, const float* floor, uint32_t n_pos, uint32_t shift,
+                                ScanArgs* a) {
+  BoundScanArgs b{};
+  b.n_cl = ix->n_cl;
+  b.bcl = ix->d_bcl;
+  b.brad = ix->d_brad;
+  b.n_blocks = ix->n_blocks;
+  b.n_q = n_q;
+  b.eden = plans->prefix_codec == MRL_PREFIX_EDEN_PROD;
+  b.table = sel.table;
+  b.qn = sel.qn;
+  b.floor = floor;
+  b.n_pos = n_pos;
+  b.shift = shift;
+  b.chunk = sel.chunk;
+  b.bcount = sel.bcount + (size_t)which * sel.n_chunks;
+  b.blist = sel.blist;
+  b.stride = (uint32_t)ix->n_blocks;
+  ProfScope ps(ctx, MRL_KERNEL_BOUNDS, 1 + which, n_pos, n_q);
+  HIP_TRY(launch_block_select(b, ctx->stream, ps.ev()));
+  ps.commit(n_pos != 0);
+  a->blist = b.blist;
+  a->bcount = b.bcount;
+  a->blist_stride = b.stride;
+  return MRL_OK;
+}
+
 // MFMA-bounded scan of n_q plans: operands (k_mma_prep); the sampling stages,
 // each followed by k_mma_floors (final floor at rank final_rank, safe floor
 // at rank K); the final pass, which appends (upper, lower, row) for the pairs
@@ -944,12 +1140,23 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
   a.err = pb.err;
   a.mma_ops = pb.mma_ops;
   a.mma_consts = pb.mma_consts;
+  // block bounds: the table once; a block list for every stage with a floor
+  const bool bounded = sampled && bounds_ok(ix, plans, sp, pb);
+  BoundSel sel{};
+  int rc;
+  if (bounded && (rc = enqueue_bound_table(ctx, ix, plans, plans_first, n_q, sp, kMmaQ, &sel))) return rc;
   for (size_t si = 0; si < stages.size(); ++si) {
     a.n_pos = stages[si].n_pos;
     a.shift = stages[si].shift;
     a.tau = si ? pb.tau_hi : nullptr;  // count only lower bounds at or above the previous floor
     a.hist = pb.hist;
     a.stats = nullptr;
+    a.blist = nullptr;
+    a.bcount = nullptr;
+    // a block whose bound lies below the previous floor adds no count
+    if (si && bounded &&
+        (rc = enqueue_block_select(ctx, ix, plans, n_q, sel, 0, pb.tau_hi, a.n_pos, a.shift, &a)))
+      return rc;
     ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)si, stages[si].n_pos, n_q);
     HIP_TRY(launch_scan_mma(a, 0, s, ps.ev()));
     ps.commit(a.n_pos != 0 && n_q != 0);
@@ -965,6 +1172,9 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
   a.tau = floor;
   a.hist = nullptr;
   a.stats = stats;
+  a.blist = nullptr;
+  a.bcount = nullptr;
+  if (bounded && (rc = enqueue_block_select(ctx, ix, plans, n_q, sel, 1, floor, (uint32_t)B, 0u, &a))) return rc;
   {
     ProfScope ps(ctx, MRL_KERNEL_SCAN, final_pass, (uint32_t)B, n_q);
     HIP_TRY(launch_scan_mma(a, floor ? 1 : 2, s, ps.ev()));
@@ -1074,6 +1284,20 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
     }
     a.stats = last ? stats : nullptr;
     a.err = pb.err;
+    if (last && sampled && bounds_ok(ix, plans, sp, pb)) {
+      // floors from the sampling counts first (as take_floors would), then
+      // the blocks some query of a workgroup's tile can reach
+      ProfScope pt(ctx, MRL_KERNEL_THRESH, (int)pi, 0, n_q);
+      HIP_TRY(launch_mma_floors(pb.hist, a.luts, n_q, rank, K, pb.tau_hi, pb.tau, false, s, pt.ev()));
+      pt.commit(n_q != 0);
+      a.floor_hist = nullptr;
+      a.tau = pb.tau_hi;
+      const uint32_t chunk = n_q >= 8 ? (uint32_t)kTileQ : (uint32_t)scan_query_tile(n_q);
+      BoundSel sel{};
+      int rc = enqueue_bound_table(ctx, ix, plans, plans_first, n_q, sp, chunk, &sel);
+      if (!rc) rc = enqueue_block_select(ctx, ix, plans, n_q, sel, 1, pb.tau_hi, (uint32_t)ix->n_blocks, 0u, &a);
+      if (rc) return rc;
+    }
     ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)pi, lp.passes[pi].n_new, n_q);
     HIP_TRY(launch_scan(a, false, s, ps.ev()));
     ps.commit(a.n_pos != 0 && n_q != 0);
@@ -1560,6 +1784,7 @@ extern "C" int mrl_scan_noalloc(mrl_ctx* ctx, const mrl_index* index, const mrl_
   pb.out_ids = d_out_ids;
   pb.out_scores = d_out_scores;
   pb.out_counts = d_out_counts;
+  pb.block_lists = false;
   const ScanParams sp = make_params(cfg, time);
   LevelPlan* lp;
   if ((rc = get_levels(ix, K, &lp))) return rc;
@@ -1629,6 +1854,65 @@ extern "C" int mrl_scan_fixed_tau(mrl_ctx* ctx, const mrl_index* index, const mr
 // one segment per query with room for every slot; the host scatters the
 // appended pairs to out[q][row].  Pairs not appended (inactive slots, queries
 // with unusable operands) read NaN.
+extern "C" int mrl_index_block_bounds(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* plans,
+                                      const mrl_scan_config* cfg, float* out_bounds) {
+  if (!ctx || !index || !plans) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (index->ctx != ctx || plans->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "objects belong to another context");
+  uint32_t K;
+  int rc = check_cfg(cfg, &K);
+  if (rc) return rc;
+  ScanParams sp = make_params(cfg, nullptr);
+  if (plans->mid_codec != MRL_MID_RABITQ || sp.strata == MRL_STRATA_L0_ONLY)
+    return fail(MRL_ERR_INVALID_ARG, "block bounds need the RaBitQ mid-band and an S1 stage");
+  const uint64_t nq = plans->n_q, B = index->n_blocks;
+  if (!nq || !B) return MRL_OK;
+  if (!out_bounds) return fail(MRL_ERR_INVALID_ARG, "null output");
+  const float nan = std::numeric_limits<float>::quiet_NaN();
+  if (!index->n_cl) {
+    std::fill(out_bounds, out_bounds + nq * B, nan);
+    return MRL_OK;
+  }
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  float *d_table = nullptr, *d_qn = nullptr, *d_out = nullptr;
+  auto cleanup = [&]() {
+    dev_free(d_table);
+    dev_free(d_qn);
+    dev_free(d_out);
+  };
+  if (hipMalloc(&d_table, (size_t)index->n_cl * nq * 4) != hipSuccess || hipMalloc(&d_qn, nq * 16) != hipSuccess ||
+      hipMalloc(&d_out, nq * B * 4) != hipSuccess) {
+    cleanup();
+    return fail(MRL_ERR_OUT_OF_MEMORY, "bounds buffers");
+  }
+  sp.exhaustive = 0;
+  BoundScanArgs b{};
+  b.center = index->d_center;
+  b.cnorm = index->d_cnorm;
+  b.n_cl = index->n_cl;
+  b.bcl = index->d_bcl;
+  b.brad = index->d_brad;
+  b.n_blocks = B;
+  b.plans = plans->d_plans;
+  b.luts = plans->d_luts;
+  b.n_q = (uint32_t)nq;
+  b.sp = sp;
+  b.eden = plans->prefix_codec == MRL_PREFIX_EDEN_PROD;
+  b.table = d_table;
+  b.qn = d_qn;
+  b.chunk = 64;
+  b.n_pos = (uint32_t)B;
+  b.shift = 0;
+  b.out_bound = d_out;
+  hipError_t e = launch_bound_table(b, ctx->stream);
+  if (e == hipSuccess) e = launch_block_select(b, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(out_bounds, d_out, nq * B * 4, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  cleanup();
+  if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("block bounds: ") + hipGetErrorString(e));
+  return MRL_OK;
+}
+
 extern "C" int mrl_scan_mma_bounds(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* plans,
                                    const mrl_scan_config* cfg, const mrl_time_range* time, float* out_upper,
                                    float* out_lower) {
@@ -2161,6 +2445,17 @@ extern "C" int mrl_encode_corpus(const float* matrix, uint64_t n, uint32_t dims,
   return rc ? fail(rc, "encode_corpus: invalid arguments") : MRL_OK;
 }
 
+extern "C" int mrl_encode_corpus_clustered(const float* matrix, uint64_t n, uint32_t dims, const uint32_t* cluster,
+                                           uint32_t default_source, const mrl_eden_fit* eden,
+                                           const mrl_eden_fit* eden_mid, int n_threads, void* out_blocks) {
+  if ((n && (!matrix || !out_blocks || !cluster))) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  EdenFitView e, m;
+  int rc = encode_corpus(matrix, n, dims, default_source, fit_view(eden, &e) ? &e : nullptr,
+                         fit_view(eden_mid, &m) ? &m : nullptr, n_threads, static_cast<uint8_t*>(out_blocks),
+                         cluster);
+  return rc ? fail(rc, "encode_corpus: invalid arguments") : MRL_OK;
+}
+
 
 // CRC-32 tables for the GPU encoder.  raw(c, M) is the reflected CRC register
 // after bytes M starting from register c (no initial or final xor); it is
@@ -2192,9 +2487,9 @@ static const CrcTables& crc_tables() {
   return t;
 }
 
-extern "C" int mrl_encode_corpus_device(mrl_ctx* ctx, const float* d_matrix, uint64_t n, uint32_t dims,
-                                        uint32_t default_source, const mrl_eden_fit* eden,
-                                        const mrl_eden_fit* eden_mid, void* d_out_blocks) {
+static int encode_device(mrl_ctx* ctx, const float* d_matrix, uint64_t n, uint32_t dims, const uint32_t* d_cluster,
+                         uint32_t default_source, const mrl_eden_fit* eden, const mrl_eden_fit* eden_mid,
+                         void* d_out_blocks) {
   if (!ctx || (n && (!d_matrix || !d_out_blocks))) return fail(MRL_ERR_INVALID_ARG, "null argument");
   if (dims < (uint32_t)(kPrefixDims + kRabitqDims)) return fail(MRL_ERR_INVALID_ARG, "dims < 192");
   if (eden && (eden->dim != 64 || eden->bits != 4 || !eden->mean))
@@ -2219,6 +2514,7 @@ extern "C" int mrl_encode_corpus_device(mrl_ctx* ctx, const float* d_matrix, uin
   a.x = d_matrix;
   a.n = n;
   a.dims = dims;
+  a.cluster = d_cluster;
   a.source = default_source;
   a.eden_mean = eden ? d_means : nullptr;
   a.eden_seed = eden ? eden->seed : 0;
@@ -2237,6 +2533,20 @@ extern "C" int mrl_encode_corpus_device(mrl_ctx* ctx, const float* d_matrix, uin
   dev_free(d_means);
   if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("encode: ") + hipGetErrorString(e));
   return MRL_OK;
+}
+
+extern "C" int mrl_encode_corpus_device(mrl_ctx* ctx, const float* d_matrix, uint64_t n, uint32_t dims,
+                                        uint32_t default_source, const mrl_eden_fit* eden,
+                                        const mrl_eden_fit* eden_mid, void* d_out_blocks) {
+  return encode_device(ctx, d_matrix, n, dims, nullptr, default_source, eden, eden_mid, d_out_blocks);
+}
+
+extern "C" int mrl_encode_corpus_device_clustered(mrl_ctx* ctx, const float* d_matrix, uint64_t n, uint32_t dims,
+                                                  const uint32_t* d_cluster, uint32_t default_source,
+                                                  const mrl_eden_fit* eden, const mrl_eden_fit* eden_mid,
+                                                  void* d_out_blocks) {
+  if (n && !d_cluster) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  return encode_device(ctx, d_matrix, n, dims, d_cluster, default_source, eden, eden_mid, d_out_blocks);
 }
 
 // Device memory for callers without a HIP allocator of their own (plain
@@ -2299,6 +2609,12 @@ extern "C" int mrl_index_from_device(mrl_ctx* ctx, const void* d_blocks, uint64_
       dev_free(ix->d_blocks);
       dev_free(ix->d_recs);
       return fail(MRL_ERR_HIP, std::string("index from device: ") + hipGetErrorString(e));
+    }
+    int rc = build_bounds(ctx, ix.get());
+    if (rc) {
+      dev_free(ix->d_blocks);
+      dev_free(ix->d_recs);
+      return rc;
     }
   }
   *out = ix.release();
@@ -2381,6 +2697,48 @@ extern "C" int mrl_synth_encode(const mrl_synth_spec* spec, const mrl_eden_fit* 
         src[r - start] = default_source;
       }
       int rc = encode_block(rows.data(), (uint32_t)(end - start), s.dims, ts, src, ep, mp, out + b * kBlockBytes);
+      if (rc) status.store(rc);
+    }
+  });
+  return status.load() ? fail(status.load(), "synth encode failed") : MRL_OK;
+}
+
+extern "C" int mrl_synth_encode_clustered(const mrl_synth_spec* spec, const mrl_eden_fit* eden,
+                                          const mrl_eden_fit* eden_mid, uint32_t default_source, int n_threads,
+                                          void* out_blocks, uint64_t* out_rows) {
+  if (!spec || !out_blocks) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  SynthSpec s = to_spec(spec);
+  if (s.n_centroids == 0) return fail(MRL_ERR_INVALID_ARG, "the corpus has no clusters");
+  // rows in (cluster, row) order: a counting sort of the row clusters
+  std::vector<uint32_t> cl(s.n_docs);
+  parallel_for(s.n_docs, n_threads, [&](uint64_t r0, uint64_t r1) {
+    for (uint64_t r = r0; r < r1; ++r) cl[r] = synth_cluster(s, r);
+  });
+  std::vector<uint64_t> start(s.n_centroids + 1, 0);
+  for (uint64_t r = 0; r < s.n_docs; ++r) ++start[cl[r] + 1];
+  for (uint32_t c = 0; c < s.n_centroids; ++c) start[c + 1] += start[c];
+  std::vector<uint64_t> order(s.n_docs);
+  for (uint64_t r = 0; r < s.n_docs; ++r) order[start[cl[r]]++] = r;
+  if (out_rows) memcpy(out_rows, order.data(), s.n_docs * sizeof(uint64_t));
+  EdenFitView e, m;
+  const EdenFitView* ep = fit_view(eden, &e) ? &e : nullptr;
+  const EdenFitView* mp = fit_view(eden_mid, &m) ? &m : nullptr;
+  const uint64_t n_blocks = (s.n_docs + 63) / 64;
+  std::atomic<int> status{MRL_OK};
+  uint8_t* out = static_cast<uint8_t*>(out_blocks);
+  parallel_for(n_blocks, n_threads, [&](uint64_t b0, uint64_t b1) {
+    std::vector<float> rows(64 * (size_t)s.dims);
+    uint32_t ts[64], src[64], bc[64];
+    for (uint64_t b = b0; b < b1; ++b) {
+      const uint64_t start_p = b * 64, end = std::min(s.n_docs, start_p + 64);
+      for (uint64_t p = start_p; p < end; ++p) {
+        synth_doc(s, order[p], rows.data() + (p - start_p) * s.dims);
+        ts[p - start_p] = (uint32_t)p;  // the row's position in the encoded order (encoder.rs:184-189)
+        src[p - start_p] = default_source;
+        bc[p - start_p] = cl[order[p]];
+      }
+      int rc = encode_block(rows.data(), (uint32_t)(end - start_p), s.dims, ts, src, ep, mp, out + b * kBlockBytes,
+                            block_cluster(bc, end - start_p));
       if (rc) status.store(rc);
     }
   });

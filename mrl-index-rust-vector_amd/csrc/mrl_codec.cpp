@@ -237,7 +237,7 @@ static inline void put16(uint8_t* p, uint16_t v) {
 static inline void or_bit(uint8_t* block, int off, int d, int slot) { block[off + 8 * d + (slot >> 3)] |= (uint8_t)(1u << (slot & 7)); }
 
 int encode_block(const float* vecs, uint32_t n, uint32_t dims, const uint32_t* ts, const uint32_t* src,
-                 const EdenFitView* eden, const EdenFitView* eden_mid, uint8_t* block) {
+                 const EdenFitView* eden, const EdenFitView* eden_mid, uint8_t* block, uint32_t cluster) {
   if (n == 0 || n > 64 || dims < (uint32_t)(kPrefixDims + kRabitqDims)) return MRL_ERR_INVALID_ARG;
   if (eden && (eden->dim != 64 || eden->bits != 4)) return MRL_ERR_INVALID_ARG;
   if (eden_mid && (!eden || eden_mid->dim != 128 || eden_mid->bits != 1)) return MRL_ERR_INVALID_ARG;
@@ -309,6 +309,10 @@ int encode_block(const float* vecs, uint32_t n, uint32_t dims, const uint32_t* t
   memcpy(block + kOrigMaxTs, &max_ts, 4);
   memcpy(block + 8, &smask, 4);
   memcpy(block + kOrigTombstone, &tomb, 8);
+  if (cluster < 65536u) {  // coarse_cluster_id, block_flags (block.rs:38-39)
+    put16(block + 12, (uint16_t)cluster);
+    put16(block + 14, (uint16_t)kBlockFlagOneCluster);
+  }
   uint32_t crc = crc32(block, kBlockBytes);  // recompute_crc (block.rs:186-190)
   memcpy(block + kOrigCrc, &crc, 4);
   return MRL_OK;
@@ -336,8 +340,16 @@ int parallel_for(uint64_t n, int n_threads, const std::function<void(uint64_t, u
   return 0;
 }
 
+uint32_t block_cluster(const uint32_t* c, uint64_t n) {
+  if (n == 0 || c[0] >= 65536u) return kNoCluster;
+  for (uint64_t i = 1; i < n; ++i)
+    if (c[i] != c[0]) return kNoCluster;
+  return c[0];
+}
+
 int encode_corpus(const float* matrix, uint64_t n, uint32_t dims, uint32_t default_source,
-                  const EdenFitView* eden, const EdenFitView* eden_mid, int n_threads, uint8_t* out) {
+                  const EdenFitView* eden, const EdenFitView* eden_mid, int n_threads, uint8_t* out,
+                  const uint32_t* cluster) {
   const uint64_t n_blocks = (n + 63) / 64;
   std::atomic<int> status{MRL_OK};
   parallel_for(n_blocks, n_threads, [&](uint64_t b0, uint64_t b1) {
@@ -348,8 +360,9 @@ int encode_corpus(const float* matrix, uint64_t n, uint32_t dims, uint32_t defau
         ts[j - start] = (uint32_t)j;  // encoder.rs:184-189
         src[j - start] = default_source;
       }
+      const uint32_t cl = cluster ? block_cluster(cluster + start, end - start) : kNoCluster;
       int rc = encode_block(matrix + start * dims, (uint32_t)(end - start), dims, ts, src, eden, eden_mid,
-                            out + b * kBlockBytes);
+                            out + b * kBlockBytes, cl);
       if (rc != MRL_OK) status.store(rc);
     }
   });
@@ -407,12 +420,16 @@ static void base_vector(uint64_t seed, uint64_t stream, uint64_t row, uint32_t d
   l2_normalize(out, dims);
 }
 
+uint32_t synth_cluster(const SynthSpec& s, uint64_t row) {
+  return s.n_centroids ? (uint32_t)(mix64(mix64(s.seed_assign) ^ (row * 0xD1B54A32D192ED03ull)) % s.n_centroids) : 0u;
+}
+
 void synth_doc(const SynthSpec& s, uint64_t row, float* out) {
   if (s.n_centroids == 0) {
     base_vector(s.seed, 1, row, s.dims, s.mean_offset, out);
     return;
   }
-  const uint64_t c = mix64(mix64(s.seed_assign) ^ (row * 0xD1B54A32D192ED03ull)) % s.n_centroids;
+  const uint64_t c = synth_cluster(s, row);
   base_vector(s.seed_centroids, 2, c, s.dims, s.mean_offset, out);
   std::vector<float> noise(s.dims);
   gaussian_row(s.seed, 3, row, s.dims, noise.data());

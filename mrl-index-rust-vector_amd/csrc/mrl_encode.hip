@@ -264,6 +264,14 @@ __global__ __launch_bounds__(64) void k_encode(EncodeArgs a) {
       h[4] = (uint32_t)tomb;
       h[5] = (uint32_t)(tomb >> 32);
     }
+    if (a.cluster) {
+      // cluster-grouped convention: coarse_cluster_id and block_flags (block.rs:38-39) when every row of the
+      // block is in one cluster below 65536
+      const uint32_t c = lane < rows ? a.cluster[row0 + lane] : 0u;
+      const uint32_t c0 = __shfl(c, 0);
+      const bool one = __ballot(lane < rows && c != c0) == 0 && c0 < 65536u;
+      if (lane == 0 && one) reinterpret_cast<uint32_t*>(img)[3] = c0 | (kBlockFlagOneCluster << 16);
+    }
     __syncthreads();
 
     // ---- CRC-32 (recompute_crc, block.rs:186-190) over the block with crc = 0

@@ -147,6 +147,7 @@ constexpr int kHistBins = 2048;
 // its S1 bits (dword k = dims 32k..32k+31); kRecS4Meta: {S4 dword 0, S4
 // dword 1, scale | offset << 16, tail_norm | flags << 16} (f16 bits).
 constexpr int kRecWords = 4;
+constexpr uint32_t kBlockFlagOneCluster = 0x0001;  // block_flags bit: every row of the block is in coarse_cluster_id
 constexpr int kRecLev0 = 0, kRecLev1 = 1, kRecS1 = 2, kRecS4Meta = 3;
 
 // MFMA-bounded batched scan (k_mma_prep, k_scan_mma, k_mma_floors, k_finish).
@@ -157,6 +158,7 @@ constexpr int kMmaSteps = 17;   // K-steps of a tile: prefix 4, S1 8, S4 4, erro
 constexpr int kMmaQ = 64;       // queries per workgroup (two 32-query tiles per wave)
 constexpr int kMmaWaves = 8;    // waves per MFMA scan workgroup (four waves per SIMD)
 constexpr int kMmaMinQ = 8;     // batches of at least this many queries take the MFMA path
+constexpr int kTileQ = 8;       // queries per tile of the batched exact kernel (k_scan_tile)
 // Per-query constants written by k_mma_prep (floats).
 enum {
   kMcS = 0,   // power-of-two scale of the query operand
@@ -226,6 +228,12 @@ struct ScanArgs {
   // Gated re-run (one-query kernel only): a workgroup of query q exits at
   // once unless bit 2 of gate[q] (a final floor left the query short of K) is set.
   const uint32_t* gate;
+  // Block lists (final passes on an index with block bounds): the pass
+  // scans blist[y * blist_stride + pos] for pos < bcount[y], y = the
+  // launch's query tile (blockIdx.y), instead of pos << shift.
+  const uint32_t* blist;
+  const uint32_t* bcount;
+  uint32_t blist_stride;
 };
 
 // Exact finishing of the MFMA path.  k_finish, one workgroup per query: a
@@ -294,6 +302,7 @@ struct EncodeArgs {
   const float* x;          // [n][dims] row-major, device
   uint64_t n;
   uint32_t dims;
+  const uint32_t* cluster; // [n] coarse cluster of each row (device) or null: the cluster-grouped convention
   uint32_t source;         // source id of every row
   const float* eden_mean;  // 64 floats (device) or null: MinMax4 prefix
   uint64_t eden_seed;
@@ -350,6 +359,63 @@ struct RingMergeArgs {
   uint32_t* out_counts;       // [n_q]
 };
 
+// Block bounds of an index with cluster-grouped blocks (MRL_BLOCK_FLAG_ONE_CLUSTER).
+// The full score of a slot (scan.rs:453-634, every stage run) is, in real
+// arithmetic, mean_ip + <rho_v, c_q>: a code-space row per slot against a
+// column per query.  The row's parts, by stage:
+//   [kBndEden, +64)  EdenProd prefix: scale * codebook[level_d]   (column: prefix_weight)
+//   [kBndMm, +64)    MinMax4 prefix: scale * level_d               (column: q_d)
+//   kBndOff          MinMax4: offset                               (column: prefix_sum)
+//   [kBndS1, +128)   S1: mid_n * (2 bit_d - 1)                     (column: rabitq_weights2 / 2)
+//   [kBndS4, +64)    S4: hn * (2 bit_d - 1)                        (column: w_s4 tail_fold_weights2 / 2)
+// At upload each cluster gets its center (the mean row of its slots) and
+// each flagged block one radius per stage (the largest distance of its
+// slots' stage part from the center's); by Cauchy-Schwarz every slot's score
+// is at most mean_ip + <center, c_q> + sum_stages radius * |c_q stage part|,
+// plus a relative margin of 2^-10 for f32 rounding (the reference's own
+// stage sums round by less than 2^-14 of the summed magnitudes).
+constexpr int kBndEden = 0, kBndMm = 64, kBndOff = 128, kBndS1 = 129, kBndS4 = 257, kBndDims = 321;
+constexpr int kBndStride = 324;  // floats per center
+constexpr float kBndMargin = 1.0f / 1024.0f;
+// radius / norm slots: 0 EdenProd prefix, 1 MinMax4 prefix with the offset, 2 S1, 3 S4
+struct BoundBuildArgs {
+  const uint8_t* idx;
+  const uint4* recs;
+  uint64_t n_blocks;
+  const uint32_t* cl_start;   // [n_cl + 1] offsets into cl_blocks
+  const uint32_t* cl_blocks;  // the flagged blocks of each cluster, grouped
+  uint32_t n_cl;
+  const float* flag_tabs;     // rho and sqrt(1 - rho^2) per flags byte
+  float cb[16];               // EdenProd codebook (eden.rs:27-44)
+  float* center;              // [n_cl][kBndStride]
+  float* cnorm;               // [n_cl][4] norms of the center's parts
+  const uint32_t* bcl;        // [n_blocks] dense cluster of a flagged block, ~0u otherwise
+  float* brad;                // [n_blocks][4] radii (upper bounds, +inf when a slot is not finite)
+};
+struct BoundScanArgs {
+  const float* center;
+  const float* cnorm;
+  uint32_t n_cl;
+  const uint32_t* bcl;
+  const float* brad;
+  uint64_t n_blocks;
+  const mrl_query_plan* plans;
+  const float* luts;
+  uint32_t n_q;
+  ScanParams sp;
+  int32_t eden;               // prefix codec of the plans is EdenProd
+  float* table;               // [n_cl][n_q] mean_ip + <center, c_q> + margin
+  float* qn;                  // [n_q][4] norms of the column parts (prefix, S1, S4) raised by the margin
+  const float* floor;         // [n_q] floors of the pass (null: the diagnostic)
+  uint32_t n_pos;             // the pass's blocks: pos << shift for pos < n_pos
+  uint32_t shift;
+  uint32_t chunk;             // queries per block list (one list per chunk of queries)
+  uint32_t* blist;            // [n_chunks][stride] blocks some query of the chunk can reach
+  uint32_t* bcount;           // [n_chunks]
+  uint32_t stride;
+  float* out_bound;           // diagnostic [n_q][n_blocks] bounds (NaN: unbounded block), or null
+};
+
 // Launchers (mrl_kernels.hip).
 // Optional start/stop events written by the dispatch itself (kernel-only
 // duration, the same interval a kernel-trace profiler reports).
@@ -357,6 +423,12 @@ struct LaunchEvents {
   hipEvent_t start = nullptr;
   hipEvent_t stop = nullptr;
 };
+
+// Block bounds: centers and radii at upload; per scan the cluster x query
+// table, then the block lists of a final pass (BoundScanArgs).
+hipError_t launch_bound_build(const BoundBuildArgs& a, hipStream_t s);
+hipError_t launch_bound_table(const BoundScanArgs& a, hipStream_t s, const LaunchEvents& ev = {});
+hipError_t launch_block_select(const BoundScanArgs& a, hipStream_t s, const LaunchEvents& ev = {});
 
 // to_device also writes each slot's record (recs, may be null).
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device, hipStream_t s,

@@ -1131,9 +1131,12 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
   const uint32_t stride = gridDim.x * 4 - 1;
   const uint32_t first = blockIdx.x * 4 + wave;
   const uint32_t cover = a.prev_shift >= 0 ? (1u << a.prev_shift) - 1u : 0u;
-  uint32_t b_cur = first << a.shift;
+  // position -> block: pos << shift, or this query tile's block list
+  const uint32_t* bl = a.blist ? a.blist + (uint64_t)blockIdx.y * a.blist_stride : nullptr;
+  const uint32_t n_pos = first < stride ? (bl ? a.bcount[blockIdx.y] : a.n_pos) : 0u;
+  auto block_of = [&](uint32_t pos) -> uint32_t { return bl ? bl[pos] : pos << a.shift; };
+  uint32_t b_cur = first < n_pos ? block_of(first) : 0u;
   RawLane cur;
-  const uint32_t n_pos = first < stride ? a.n_pos : 0u;
   // The set-up's reads go out first (memory returns loads in order, so the
   // set-up below then waits for them alone), then the first blocks' loads.
   const HistRow fl = floor_prefetch(a, q0, nq, wave);
@@ -1170,7 +1173,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
 #pragma unroll
   for (int k = 0; k + 1 < kAhead; ++k) {
     const uint32_t pk = first + (uint32_t)(k + 1) * stride;
-    b_pf[k] = pk < n_pos ? pk << a.shift : b_cur;
+    b_pf[k] = pk < n_pos ? block_of(pk) : b_cur;
     if (first < n_pos) pf[k] = load_raw<false>(a.idx + (uint64_t)b_pf[k] * kBlockBytes);
   }
 
@@ -1228,7 +1231,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     // is loaded again, so the loads are unconditional and the wait before
     // this block's compute covers only this block's own loads.
     const uint32_t ahead = (uint32_t)kAhead * stride;
-    const uint32_t b_nxt = pos + ahead < n_pos ? (pos + ahead) << a.shift : b_cur;
+    const uint32_t b_nxt = pos + ahead < n_pos ? block_of(pos + ahead) : b_cur;
     const RawLane nxt = load_raw<!DEFER>(a.idx + (uint64_t)b_nxt * kBlockBytes);
 
     const uint32_t b = b_cur;
@@ -1406,7 +1409,6 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
 //    becomes the execution mask and the tile's weights are added under it.  These sums run for every active lane; a lane takes part in a
 //    query's stage only through that query's survivor mask, so a survivor's
 //    sum is the reference's and other lanes are never pushed.
-constexpr int kTileQ = 8;  // queries per tile of the batched kernel
 
 // s[i] += w[i] on the lanes set in p (and in the incoming execution mask).
 __device__ __forceinline__ void masked_add_tile(float (&s)[8], uint64_t p, const float4* w) {
@@ -1505,8 +1507,10 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
   const uint32_t stride = gridDim.x * 4 - 1;  // odd: see k_scan
   const uint32_t first = blockIdx.x * 4 + wave;
   const uint32_t cover = a.prev_shift >= 0 ? (1u << a.prev_shift) - 1u : 0u;
-  const uint32_t n_pos = first < stride ? a.n_pos : 0u;
-  uint32_t b_cur = first << a.shift;
+  const uint32_t* bl = a.blist ? a.blist + (uint64_t)blockIdx.y * a.blist_stride : nullptr;
+  const uint32_t n_pos = first < stride ? (bl ? a.bcount[blockIdx.y] : a.n_pos) : 0u;
+  auto block_of = [&](uint32_t pos) -> uint32_t { return bl ? bl[pos] : pos << a.shift; };
+  uint32_t b_cur = first < n_pos ? block_of(first) : 0u;
   RawLane cur;
   if (first < n_pos) cur = load_raw(a.idx + (uint64_t)b_cur * kBlockBytes);
   const HistRow fl = floor_prefetch(a, q0, nq, wave);
@@ -1576,7 +1580,7 @@ __global__ __launch_bounds__(256) void k_scan_tile(ScanArgs a) {
   uint32_t c_blocks = 0, c_active = 0, c_prefix = 0, c_s1 = 0, c_s4b = 0;
 
   for (uint32_t pos = first; pos < n_pos; pos += stride) {
-    const uint32_t b_nxt = pos + stride < n_pos ? (pos + stride) << a.shift : b_cur;
+    const uint32_t b_nxt = pos + stride < n_pos ? block_of(pos + stride) : b_cur;
     const RawLane nxt = load_raw(a.idx + (uint64_t)b_nxt * kBlockBytes);
     const uint32_t b = b_cur;
     const uint32_t min_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 0);
@@ -2619,13 +2623,21 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   if (tid == 0) s_anyall = 0u;
   __syncthreads();
 
-  const uint32_t n_items = 2u * a.n_pos;
+  // item i: half i % 2 of the block at position i / 2 (pos << shift, or
+  // this query chunk's block list)
+  const uint32_t* bl = a.blist ? a.blist + (uint64_t)blockIdx.y * a.blist_stride : nullptr;
+  const uint32_t n_items = 2u * (bl ? a.bcount[blockIdx.y] : a.n_pos);
+  auto block_of = [&](uint32_t pos) -> uint64_t { return bl ? (uint64_t)bl[pos] : (uint64_t)pos << a.shift; };
   const uint32_t stride = gridDim.x * WPG - 1;  // odd: see k_scan
   const uint32_t first = blockIdx.x * WPG + wave;
   const uint32_t n_it = first < stride ? n_items : 0u;
   uint32_t it_cur = first;
+  uint64_t b_cur = 0;
   MmaRaw cur{};
-  if (first < n_it) cur = mma_load(a.idx, a.recs, (uint64_t)(first >> 1) << a.shift, first & 1u);
+  if (first < n_it) {
+    b_cur = block_of(first >> 1);
+    cur = mma_load(a.idx, a.recs, b_cur, first & 1u);
+  }
 
   if (tid < 256) {  // byte -> (f16 cb[low nibble], f16 cb[high nibble])
     const mrl_query_plan* p0 = a.plans + q0;
@@ -2725,8 +2737,9 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
 
   for (uint32_t it = first; it < n_it; it += stride) {
     const uint32_t it_nxt = it + stride < n_it ? it + stride : it_cur;
-    const MmaRaw nxt = mma_load(a.idx, a.recs, (uint64_t)(it_nxt >> 1) << a.shift, it_nxt & 1u);
-    const uint32_t b = (it_cur >> 1) << a.shift, h = it_cur & 1u;
+    const uint64_t b_nxt = it + stride < n_it ? block_of(it_nxt >> 1) : b_cur;
+    const MmaRaw nxt = mma_load(a.idx, a.recs, b_nxt, it_nxt & 1u);
+    const uint32_t b = (uint32_t)b_cur, h = it_cur & 1u;
     const uint32_t min_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 0);
     const uint32_t max_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 1);
     const uint64_t tomb = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(cur.hdr, 3) << 32) |
@@ -2880,6 +2893,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
     }
     cur = nxt;
     it_cur = it_nxt;
+    b_cur = b_nxt;
   }
   if (a.stats && lane == 0) {
     atomicAdd(&s_stats[kStatBlocks], c_blocks);
@@ -3168,6 +3182,383 @@ __global__ __launch_bounds__(kExactItem) void k_exact(FinishArgs a) {
 // ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
+template <typename K, typename... Args>
+static void launch(K kernel, dim3 grid, dim3 block, hipStream_t s, const LaunchEvents& ev, Args... args);
+
+// ---------------------------------------------------------------------------
+// block bounds (cluster-grouped indexes)
+// ---------------------------------------------------------------------------
+// One slot's meta as the scan decodes it (block.rs:61-99): scale, offset,
+// mid_n = max(mid_norm, 1e-6), hn = max(high_n, 1e-6); false if one is not finite.
+__device__ __forceinline__ bool slot_meta(uint4 x, const float* flag_tabs, float* scale, float* offset, float* mid_n,
+                                          float* hn) {
+  *scale = h2f((uint16_t)(x.z & 0xffffu));
+  *offset = h2f((uint16_t)(x.z >> 16));
+  const float t = fmaxf(h2f((uint16_t)(x.w & 0xffffu)), 0.0f);
+  const uint32_t fl = (x.w >> 16) & 0xffu;
+  *mid_n = fmaxf(flag_tabs[256 + fl] * t, 1e-6f);
+  *hn = fmaxf(fmaxf(flag_tabs[fl] * t, 0.0f), 1e-6f);
+  const float sum = *scale + *offset + *mid_n + *hn;
+  return sum - sum == 0.0f;
+}
+
+// Record dword and bit position behind code-space dimension d (< kBndDims):
+// prefix levels are nibbles of dwords 0..7, S1 bits of dwords 8..11, S4 bits
+// of dwords 12..13 (the record layout of k_relayout_to_device).
+__device__ __forceinline__ void bnd_source(int d, int* word, int* shift) {
+  if (d < kBndOff) {
+    const int dd = d & 63;
+    *word = dd >> 3;
+    *shift = 4 * (dd & 7);
+  } else if (d == kBndOff) {
+    *word = -1;
+    *shift = 0;
+  } else if (d < kBndS4) {
+    const int k = d - kBndS1;
+    *word = 8 + (k >> 5);
+    *shift = k & 31;
+  } else {
+    const int k = d - kBndS4;
+    *word = 12 + (k >> 5);
+    *shift = k & 31;
+  }
+}
+
+__device__ __forceinline__ float bnd_value(int d, uint32_t w, int shift, float scale, float offset, float mid_n,
+                                           float hn, const float* cb) {
+  if (d < kBndMm) return scale * cb[(w >> shift) & 15u];
+  if (d < kBndOff) return scale * (float)((w >> shift) & 15u);
+  if (d == kBndOff) return offset;
+  const bool bit = (w >> shift) & 1u;
+  if (d < kBndS4) return bit ? mid_n : -mid_n;
+  return bit ? hn : -hn;
+}
+
+// Stage slot (0 EdenProd prefix, 1 MinMax4 prefix + offset, 2 S1, 3 S4) of dimension d.
+__device__ __forceinline__ int bnd_stage(int d) {
+  return d < kBndMm ? 0 : (d <= kBndOff ? 1 : (d < kBndS4 ? 2 : 3));
+}
+
+// Cluster centers: one workgroup per cluster, thread t owns dimensions t and
+// t + 256; the sum runs over the cluster's blocks and active slots with
+// finite meta in a fixed order (the center need not be exact: the radii are
+// measured from the stored center).
+__global__ __launch_bounds__(256) void k_bound_centers(BoundBuildArgs a) {
+  __shared__ float s_cb[16];
+  __shared__ float s_part[4][256];
+  const uint32_t c = blockIdx.x;
+  const int tid = threadIdx.x;
+  if (tid < 16) s_cb[tid] = a.cb[tid];
+  __syncthreads();
+  constexpr int kPer = 2;
+  int word[kPer], shift[kPer];
+  float sum[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int d = tid + 256 * k;
+    bnd_source(d < kBndDims ? d : 0, &word[k], &shift[k]);
+    sum[k] = 0.0f;
+  }
+  uint32_t count = 0;
+  for (uint32_t i = a.cl_start[c]; i < a.cl_start[c + 1]; ++i) {
+    const uint64_t b = a.cl_blocks[i];
+    const uint8_t* blk = a.idx + b * kBlockBytes;
+    const uint64_t tomb = *reinterpret_cast<const uint64_t*>(blk + kOrigTombstone);
+    for (int v = 0; v < 64; ++v) {
+      if ((tomb >> v) & 1ull) continue;
+      const uint32_t* rw = reinterpret_cast<const uint32_t*>(a.recs + (b * 64u + (uint32_t)v) * kRecWords);
+      const uint4 x = a.recs[(b * 64u + (uint32_t)v) * kRecWords + kRecS4Meta];
+      float scale, offset, mid_n, hn;
+      if (!slot_meta(x, a.flag_tabs, &scale, &offset, &mid_n, &hn)) continue;
+      ++count;
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int d = tid + 256 * k;
+        if (d < kBndDims) {
+          const uint32_t w = word[k] >= 0 ? rw[word[k]] : 0u;
+          sum[k] += bnd_value(d, w, shift[k], scale, offset, mid_n, hn, s_cb);
+        }
+      }
+    }
+  }
+  const float inv = count ? 1.0f / (float)count : 0.0f;
+  float* cen = a.center + (uint64_t)c * kBndStride;
+  float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int d = tid + 256 * k;
+    if (d < kBndStride) {
+      const float m = d < kBndDims ? sum[k] * inv : 0.0f;
+      cen[d] = m;
+      if (d < kBndDims) part[bnd_stage(d)] += m * m;
+    }
+  }
+#pragma unroll
+  for (int st = 0; st < 4; ++st) s_part[st][tid] = part[st];
+  __syncthreads();
+  if (tid < 4) {
+    float t = 0.0f;
+    for (int i = 0; i < 256; ++i) t += s_part[tid][i];
+    a.cnorm[(uint64_t)c * 4 + tid] = sqrtf(t) * (1.0f + kBndMargin);
+  }
+}
+
+// Per-block radii: one wave per block, lane = slot; the largest distance of
+// an active slot's stage part from its cluster center's, raised by the
+// margin; +inf when an active slot's meta is not finite.  Blocks without the
+// one-cluster flag are left unbounded (+inf).
+__global__ __launch_bounds__(256) void k_bound_radii(BoundBuildArgs a) {
+  __shared__ float s_cb[16];
+  const int tid = threadIdx.x;
+  if (tid < 16) s_cb[tid] = a.cb[tid];
+  __syncthreads();
+  const uint64_t b = (uint64_t)blockIdx.x * 4 + (tid >> 6);
+  const uint32_t lane = __lane_id();
+  if (b >= a.n_blocks) return;
+  const uint32_t cl = a.bcl[b];
+  float r[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+  if (cl != ~0u) {
+    const uint8_t* blk = a.idx + b * kBlockBytes;
+    const uint64_t tomb = *reinterpret_cast<const uint64_t*>(blk + kOrigTombstone);
+    const bool act = !((tomb >> lane) & 1ull);
+    const uint4* rec = a.recs + (b * 64u + lane) * kRecWords;
+    const uint4 q0 = rec[0], q1 = rec[1], q2 = rec[2], q3 = rec[3];
+    const uint32_t rw[14] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w, q2.x, q2.y, q2.z, q2.w, q3.x, q3.y};
+    float scale, offset, mid_n, hn;
+    const bool fin = slot_meta(q3, a.flag_tabs, &scale, &offset, &mid_n, &hn);
+    const float* cen = a.center + (uint64_t)cl * kBndStride;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int d = 0; d < kBndDims; ++d) {
+      int w, sh;
+      bnd_source(d, &w, &sh);
+      const float x = bnd_value(d, w >= 0 ? rw[w] : 0u, sh, scale, offset, mid_n, hn, s_cb) - cen[d];
+      acc[bnd_stage(d)] += x * x;
+    }
+    const bool bad = act && !fin;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      float v = act && fin ? acc[st] : 0.0f;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+      r[st] = sqrtf(v) * (1.0f + kBndMargin) + 1e-30f;
+    }
+    if (__ballot(bad) != 0) r[0] = r[1] = r[2] = r[3] = INFINITY;
+  }
+  if (lane < 4) a.brad[b * 4 + lane] = lane == 0 ? r[0] : lane == 1 ? r[1] : lane == 2 ? r[2] : r[3];
+}
+
+hipError_t launch_bound_build(const BoundBuildArgs& a, hipStream_t s) {
+  if (a.n_cl) hipLaunchKernelGGL(k_bound_centers, dim3(a.n_cl), dim3(256), 0, s, a);
+  if (a.n_blocks) hipLaunchKernelGGL(k_bound_radii, dim3((uint32_t)((a.n_blocks + 3) / 4)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+// Query columns of the bound table, kBndCols per query: 65 prefix columns
+// (EdenProd: prefix_weight and a zero; MinMax4: q_d and prefix_sum), 128 S1
+// columns (rabitq_weights2 / 2), 64 S4 columns (w_s4 tail_fold_weights2 / 2).
+// Column k multiplies center dimension bnd_center_dim(k).
+constexpr int kBndCols = 65 + 128 + 64;
+__device__ __forceinline__ int bnd_center_dim(int k, bool eden) {
+  return k < 65 ? (eden ? k : kBndMm + k) : kBndS1 + (k - 65);
+}
+
+// Per (cluster, query): mean_ip + <center, c_q> + margin; per query the norms
+// of its column parts (raised by the margin).  Grid (clusters / 4, queries /
+// 64): a workgroup stages its 64 queries' columns (float4 loads of the S1 and
+// S4 weights, all of a thread's loads in flight together) and its 4 clusters'
+// centers in LDS, then each wave takes one cluster, lane = query.  Workgroup
+// (0, 0) also clears the block-list counts.
+constexpr int kBndTableClusters = 4;
+constexpr int kBndColsPad = (kBndCols + 3) & ~3;  // columns past kBndCols are zero
+static_assert(64 + 64 * (kBndColsPad - kBndCols) <= 256 && kQdW4 + 64 <= kQData, "table staging");
+__global__ __launch_bounds__(256) void k_bound_table(BoundScanArgs a) {
+  __shared__ float s_col[kBndColsPad][65];  // [column][query], padded: conflict-free both ways
+  __shared__ __align__(16) float s_cen[kBndTableClusters][kBndColsPad];
+  __shared__ float s_mean[64], s_ws4[64], s_s1[64];
+  const int tid = threadIdx.x;
+  const uint32_t lane = __lane_id();
+  const int wave = tid >> 6;
+  const uint32_t q0 = blockIdx.y * 64;
+  const uint32_t c0 = blockIdx.x * kBndTableClusters;
+  const uint32_t nq = min(64u, a.n_q - q0);
+  const bool eden = a.eden != 0;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && a.bcount) {
+    // the counts of both block lists of a scan (a sampling stage's and the final pass's)
+    const uint32_t n_chunks = (a.n_q + a.chunk - 1) / a.chunk;
+    for (uint32_t i = (uint32_t)tid; i < 2 * n_chunks; i += 256) a.bcount[i] = 0u;
+  }
+  // per-query fields and column 64 (MinMax4: prefix_sum), then the rest
+  if (tid < 64) {
+    const bool have = (uint32_t)tid < nq;
+    const mrl_query_plan* p = a.plans + q0 + (have ? tid : 0);
+    const float ws4 = (a.sp.strata == MRL_STRATA_FULL64B && p->has_tail_fold) ? a.sp.w_s4 : 0.0f;
+    s_ws4[tid] = have ? 0.5f * ws4 : 0.0f;
+    s_s1[tid] = have && a.sp.strata != MRL_STRATA_L0_ONLY ? 0.5f : 0.0f;
+    s_mean[tid] = have && eden ? p->eden_mean_ip : 0.0f;
+    s_col[64][tid] = have && !eden ? p->prefix_sum : 0.0f;
+  } else if (tid < 64 + 64 * (kBndColsPad - kBndCols)) {  // the zero rows past kBndCols
+    const int i = tid - 64;
+    s_col[kBndCols + (i >> 6)][i & 63] = 0.0f;
+  }
+  for (int i = tid; i < kBndTableClusters * kBndColsPad; i += 256) {
+    const int j = i / kBndColsPad, k = i - j * kBndColsPad;
+    const uint32_t c = c0 + (uint32_t)j;
+    s_cen[j][k] = (c < a.n_cl && k < kBndCols) ? a.center[(uint64_t)c * kBndStride + bnd_center_dim(k, eden)] : 0.0f;
+  }
+  __syncthreads();
+  // prefix columns 0..63: plan prefix_weight (one float per thread and query);
+  // S1 columns 65..192 and S4 columns 193..256: 48 float4 per query
+  {
+    constexpr int kP = 64 * 64 / 256, kV = 64 * 48 / 256;
+    float pv[kP];
+    float4 wv[kV];
+#pragma unroll
+    for (int u = 0; u < kP; ++u) {
+      const uint32_t i = (uint32_t)tid + 256u * u, qi = i >> 6, k = i & 63u;
+      pv[u] = qi < nq ? a.plans[q0 + qi].prefix_weight[k] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kV; ++u) {
+      const uint32_t i = (uint32_t)tid + 256u * u, qi = i / 48u, k4 = i - qi * 48u;
+      const float* qd = a.luts + (uint64_t)(q0 + (qi < nq ? qi : 0)) * kQData;
+      wv[u] = qi < nq ? *reinterpret_cast<const float4*>(qd + (k4 < 32 ? kQdW1 + 4 * k4 : kQdW4 + 4 * (k4 - 32)))
+                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int u = 0; u < kP; ++u) {
+      const uint32_t i = (uint32_t)tid + 256u * u;
+      s_col[i & 63u][i >> 6] = pv[u];
+    }
+#pragma unroll
+    for (int u = 0; u < kV; ++u) {
+      const uint32_t i = (uint32_t)tid + 256u * u, qi = i / 48u, k4 = i - qi * 48u;
+      const float f = k4 < 32 ? s_s1[qi] : s_ws4[qi];
+      const uint32_t k = 65u + 4u * k4;
+      s_col[k][qi] = f * wv[u].x;
+      s_col[k + 1][qi] = f * wv[u].y;
+      s_col[k + 2][qi] = f * wv[u].z;
+      s_col[k + 3][qi] = f * wv[u].w;
+    }
+  }
+  __syncthreads();
+  // lane = query: the norms of its column parts (raised by the margin)
+  float n0 = 0.0f, n1 = 0.0f, n2 = 0.0f;
+  for (int k = 0; k < 65; ++k) n0 += s_col[k][lane] * s_col[k][lane];
+  for (int k = 65; k < 65 + 128; ++k) n1 += s_col[k][lane] * s_col[k][lane];
+  for (int k = 65 + 128; k < kBndCols; ++k) n2 += s_col[k][lane] * s_col[k][lane];
+  const float up = 1.0f + kBndMargin;
+  const float nq0 = sqrtf(n0) * up, nq1 = sqrtf(n1) * up, nq2 = sqrtf(n2) * up, mean = s_mean[lane];
+  const uint32_t q = q0 + lane;
+  if (blockIdx.x == 0 && wave == 0 && q < a.n_q) {
+    const float4 n = make_float4(nq0, nq1, nq2, 0.0f);
+    *reinterpret_cast<float4*>(a.qn + (uint64_t)q * 4) = n;
+  }
+  const uint32_t c = c0 + (uint32_t)wave;
+  if (c >= a.n_cl || q >= a.n_q) return;
+  float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll 4
+  for (int k = 0; k < kBndColsPad; k += 4) {
+    const float4 cv = *reinterpret_cast<const float4*>(&s_cen[wave][k]);
+    d0 += cv.x * s_col[k][lane] + cv.y * s_col[k + 1][lane];
+    d1 += cv.z * s_col[k + 2][lane] + cv.w * s_col[k + 3][lane];
+  }
+  const float* cn = a.cnorm + (uint64_t)c * 4;
+  const float margin = kBndMargin * (fabsf(mean) + (eden ? cn[0] : cn[1]) * nq0 + cn[2] * nq1 + cn[3] * nq2) + 1e-30f;
+  a.table[(uint64_t)c * a.n_q + q] = (mean + (d0 + d1)) + margin;
+}
+
+hipError_t launch_bound_table(const BoundScanArgs& a, hipStream_t s, const LaunchEvents& ev) {
+  if (a.n_cl == 0 || a.n_q == 0) return hipSuccess;
+  launch(k_bound_table, dim3((a.n_cl + kBndTableClusters - 1) / kBndTableClusters, (a.n_q + 63) / 64), dim3(256), s,
+         ev, a);
+  return hipGetLastError();
+}
+
+// Block selection over the pass's blocks (pos << shift, pos < n_pos): a block
+// is listed for a chunk of queries (at most 64) unless every query's bound on
+// it lies below that query's floor (blocks without bounds are always listed).
+// Lane = block; the chunk's query norms and floors sit in LDS; a workgroup
+// reserves room for its listed blocks with one atomic and writes them in
+// position order.  With out_bound (the diagnostic) every bound is written
+// instead.
+constexpr int kSelBlocksPerGroup = 256;
+__global__ __launch_bounds__(256) void k_block_select(BoundScanArgs a) {
+  __shared__ float4 s_q[64];  // norms of the column parts, floor
+  __shared__ uint32_t s_wn[4], s_base;
+  const int tid = threadIdx.x;
+  const uint32_t lane = __lane_id();
+  const int wave = tid >> 6;
+  const uint32_t chunk = blockIdx.y;
+  const uint32_t qc0 = chunk * a.chunk;
+  const uint32_t nq = min(min(a.chunk, 64u), a.n_q - qc0);
+  if ((uint32_t)tid < nq) {
+    const float4 n = *reinterpret_cast<const float4*>(a.qn + (uint64_t)(qc0 + tid) * 4);
+    s_q[tid] = make_float4(n.x, n.y, n.z, a.floor ? a.floor[qc0 + tid] : 0.0f);
+  }
+  __syncthreads();
+  const uint32_t pos = blockIdx.x * kSelBlocksPerGroup + (uint32_t)tid;
+  const bool have = pos < a.n_pos;
+  const uint64_t b = (uint64_t)pos << a.shift;
+  const uint32_t cl = have ? a.bcl[b] : ~0u;
+  if (a.out_bound) {  // the diagnostic: every bound (NaN: unbounded block)
+    if (!have) return;
+    const float4 r = cl != ~0u ? *reinterpret_cast<const float4*>(a.brad + b * 4) : make_float4(0, 0, 0, 0);
+    for (uint32_t i = 0; i < nq; ++i) {
+      float bound = __builtin_nanf("");
+      if (cl != ~0u) {
+        const float4 qv = s_q[i];
+        bound = a.table[(uint64_t)cl * a.n_q + qc0 + i] + ((a.eden ? r.x : r.y) * qv.x + r.z * qv.y + r.w * qv.z);
+        if (!(bound == bound)) bound = INFINITY;
+      }
+      a.out_bound[(uint64_t)(qc0 + i) * a.n_blocks + b] = bound;
+    }
+    return;
+  }
+  bool need = have;
+  if (cl != ~0u) {
+    const float4 r = *reinterpret_cast<const float4*>(a.brad + b * 4);
+    const float re = a.eden ? r.x : r.y;
+    const float* trow = a.table + (uint64_t)cl * a.n_q + qc0;
+    bool any = false;
+    constexpr int kB = 16;  // table loads in flight together
+    for (uint32_t i0 = 0; i0 < nq; i0 += kB) {
+      float t[kB];
+#pragma unroll
+      for (int u = 0; u < kB; ++u) t[u] = i0 + u < nq ? trow[i0 + u] : -INFINITY;
+#pragma unroll
+      for (int u = 0; u < kB; ++u) {
+        const float4 qv = s_q[min(i0 + (uint32_t)u, 63u)];
+        const float bound = t[u] + (re * qv.x + r.z * qv.y + r.w * qv.z);
+        // NaN bounds keep the block; past the chunk t = -inf
+        any |= (i0 + u < nq) && !(bound < qv.w);
+      }
+    }
+    need = any;
+  }
+  const uint64_t m = __ballot(need);
+  if (lane == 0) s_wn[wave] = (uint32_t)__popcll(m);
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t cnt = s_wn[0] + s_wn[1] + s_wn[2] + s_wn[3];
+    s_base = cnt ? atomicAdd(a.bcount + chunk, cnt) : 0u;
+  }
+  __syncthreads();
+  if (need) {
+    uint32_t off = s_base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+    for (int w = 0; w < wave; ++w) off += s_wn[w];
+    a.blist[(uint64_t)chunk * a.stride + off] = (uint32_t)b;
+  }
+}
+
+hipError_t launch_block_select(const BoundScanArgs& a, hipStream_t s, const LaunchEvents& ev) {
+  if (a.n_pos == 0 || a.n_q == 0) return hipSuccess;
+  const uint32_t chunks = (a.n_q + a.chunk - 1) / a.chunk;
+  launch(k_block_select, dim3((a.n_pos + kSelBlocksPerGroup - 1) / kSelBlocksPerGroup, chunks), dim3(256), s, ev,
+         a);
+  return hipGetLastError();
+}
+
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, uint64_t n_blocks, bool to_device,
                            hipStream_t s, uint4* recs) {
   if (n_blocks == 0) return hipSuccess;

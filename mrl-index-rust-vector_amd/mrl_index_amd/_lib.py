@@ -132,7 +132,7 @@ class KernelTimeC(C.Structure):
 
 
 (KERNEL_PLAN, KERNEL_SCAN, KERNEL_SELECT, KERNEL_THRESH, KERNEL_RERANK, KERNEL_RERANK_SORT, KERNEL_FINISH,
- KERNEL_MMA_PREP, KERNEL_EXACT) = 0, 1, 2, 3, 4, 5, 6, 7, 8
+ KERNEL_MMA_PREP, KERNEL_EXACT, KERNEL_BOUNDS) = 0, 1, 2, 3, 4, 5, 6, 7, 8, 9
 
 
 class SynthSpecC(C.Structure):
@@ -186,6 +186,7 @@ SIGNATURES = {
     "mrl_scan_fixed_tau": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), C.POINTER(TimeRangeC), _F, _U64,
                                      _F, _F]),
     "mrl_scan_mma_bounds": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), C.POINTER(TimeRangeC), _F, _F]),
+    "mrl_index_block_bounds": (C.c_int, [_P, _P, _P, C.POINTER(ScanConfigC), _F]),
     "mrl_ctx_set_profiling": (C.c_int, [_P, C.c_int]),
     "mrl_ctx_profile_collect": (C.c_int, [_P, C.POINTER(KernelTimeC), C.c_uint32, _U32]),
     "mrl_ctx_evict_caches": (C.c_int, [_P, C.c_uint64]),
@@ -196,6 +197,10 @@ SIGNATURES = {
     "mrl_eden_fit_band": (C.c_int, [_F, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, _F]),
     "mrl_encode_corpus_device": (C.c_int, [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, C.POINTER(EdenFitC),
                                            C.POINTER(EdenFitC), _P]),
+    "mrl_encode_corpus_clustered": (C.c_int, [_F, C.c_uint64, C.c_uint32, _U32, C.c_uint32, C.POINTER(EdenFitC),
+                                              C.POINTER(EdenFitC), C.c_int, _P]),
+    "mrl_encode_corpus_device_clustered": (C.c_int, [_P, _P, C.c_uint64, C.c_uint32, _P, C.c_uint32,
+                                                     C.POINTER(EdenFitC), C.POINTER(EdenFitC), _P]),
     "mrl_index_from_device": (C.c_int, [_P, _P, C.c_uint64, _PP]),
     "mrl_device_alloc": (C.c_int, [_P, C.c_size_t, _PP]),
     "mrl_device_free": (None, [_P, _P]),
@@ -214,6 +219,8 @@ SIGNATURES = {
     "mrl_synth_eden_fit": (C.c_int, [C.POINTER(SynthSpecC), C.c_uint64, _F]),
     "mrl_synth_encode": (C.c_int, [C.POINTER(SynthSpecC), C.POINTER(EdenFitC), C.POINTER(EdenFitC),
                                    C.c_uint32, C.c_int, _P]),
+    "mrl_synth_encode_clustered": (C.c_int, [C.POINTER(SynthSpecC), C.POINTER(EdenFitC), C.POINTER(EdenFitC),
+                                             C.c_uint32, C.c_int, _P, _U64]),
 }
 
 

@@ -427,6 +427,19 @@ def scan_fixed_tau(blocks, plan: QueryPlan, cfg, tau, time_lo=None, time_hi=None
             idx.close()
 
 
+def index_block_bounds(index: "DeviceIndex", plan: QueryPlan, cfg) -> np.ndarray:
+    """Upper bounds of every (query, block) pair's full scores on a
+    cluster-grouped index (mrl_index_block_bounds): float32 [query, block],
+    NaN for blocks without a bound."""
+    sc = _scan_cfg(cfg)
+    nq, nb = plan.n_queries, index.block_count()
+    out = np.zeros((nq, nb), dtype=np.float32)
+    c = sc.to_c()
+    _lib.check(_lib.lib.mrl_index_block_bounds(plan.device.handle, index.handle, plan.handle, C.byref(c),
+                                               _lib.fptr(out)))
+    return out
+
+
 def scan_mma_bounds(blocks, plan: QueryPlan, cfg, time_lo=None, time_hi=None):
     """Upper and lower bounds of every (query, slot) pair's full score from
     the batched path's f16 MFMA tiles (mrl_scan_mma_bounds): two float32

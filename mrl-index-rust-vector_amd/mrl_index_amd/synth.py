@@ -90,6 +90,19 @@ def queries(w: Workload, n_queries: Optional[int] = None, seed: int = SEED_QUERI
     return out, src
 
 
+def encode_clustered(w: Workload, fit: Optional[EdenFit], n_threads: int = 0):
+    """The same documents in the cluster-grouped layout
+    (mrl_synth_encode_clustered): (blocks, rows) with rows[p] the document at
+    position p (its id in `encode`'s layout)."""
+    out = np.zeros(((w.n_docs + 63) // 64, BLOCK_BYTES), dtype=np.uint8)
+    rows = np.zeros(w.n_docs, dtype=np.uint64)
+    spec = w.spec()
+    f = fit.to_c() if fit is not None else None
+    _lib.check(_lib.lib.mrl_synth_encode_clustered(C.byref(spec), C.byref(f) if f else None, None, source.DOC,
+                                                   n_threads, _lib.vptr(out), _lib.u64ptr(rows)))
+    return out, rows
+
+
 def encode(w: Workload, fit: Optional[EdenFit], n_threads: int = 0) -> np.ndarray:
     out = np.zeros(((w.n_docs + 63) // 64, BLOCK_BYTES), dtype=np.uint8)
     spec = w.spec()
