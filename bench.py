@@ -89,6 +89,8 @@ def main():
     ap.add_argument("--no-rerank", action="store_true", help="skip the post-scan rerank and encode legs")
     ap.add_argument("--layout", choices=["standard", "clustered"], default="standard",
                     help="with --config N: the documents in row order (standard) or grouped by centroid (clustered)")
+    ap.add_argument("--stratum4-weight", type=float, default=None,
+                    help="with --config N: EngineConfig.stratum4_weight (default: the reference's 0.20)")
     ap.add_argument("--no-cluster-layout", action="store_true",
                     help="default run: skip config 4 in the cluster-grouped layout")
     ap.add_argument("--rerank-reps", type=int, default=100)
@@ -223,6 +225,8 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
     ix = m.DeviceIndex.upload(blocks, dev)
     plan = m.QueryPlan.from_query_codec(queries, w.dims, w.prefix_codec, m.MidCodec.RABITQ, fit, None, dev)
     cfg = m.ScanConfig(shortlist_cand=w.k, strata_depth=w.strata, exhaustive=w.exhaustive)
+    if args.stratum4_weight is not None:
+        cfg.stratum4_weight = args.stratum4_weight
     ccfg = cfg.to_c()
     tr = _lib.TimeRangeC(0, 0, 0, 0)
     nq = w.n_queries
@@ -291,6 +295,7 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
                    "blocks": int(blocks.shape[0]), "queries_per_step": nq, "k_cand": w.k,
                    "prefix_codec": w.prefix_codec.name.lower(), "strata": w.strata.name.lower(),
                    "pruning": "off (exhaustive)" if w.exhaustive else "on",
+                   "stratum4_weight": round(float(cfg.stratum4_weight), 4),
                    "query_noise": f"isotropic, norm {w.query_noise}" if not w.fresh_queries else "fresh draw"},
         "queries_per_s": round(nq / (ms_step / 1000.0), 1),
         "pairs_per_s": round(w.n_docs * nq / (ms_step / 1000.0), 1),

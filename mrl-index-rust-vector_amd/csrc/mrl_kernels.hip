@@ -2882,12 +2882,23 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
 #pragma unroll
         for (int t = 0; t < NQT; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const uint64_t pm = (MODE == 2 ? ballot((okbits >> (16 * t + r)) & 1u) : ballot(acc[t][r] >= 0.0f)) & actm;
-            if (pm == 0) continue;
-            const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
-            c_app += (uint32_t)__popcll(pm);
-            mma_append(s_st, a, s_qk, s_flag, wave, &fill, q0, (uint32_t)qi, seg, pm, acc[t][r], row);
+          for (int g = 0; g < 4; ++g) {
+            // MODE 1: one compare per group of four registers (four queries)
+            // first; fmaxf passes a group whenever a register of it passes
+            if (MODE == 1) {
+              const float m4 = fmaxf(fmaxf(acc[t][4 * g], acc[t][4 * g + 1]), fmaxf(acc[t][4 * g + 2], acc[t][4 * g + 3]));
+              if ((ballot(m4 >= 0.0f) & actm) == 0) continue;
+            }
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+              const int r = 4 * g + rr;
+              const uint64_t pm =
+                  (MODE == 2 ? ballot((okbits >> (16 * t + r)) & 1u) : ballot(acc[t][r] >= 0.0f)) & actm;
+              if (pm == 0) continue;
+              const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
+              c_app += (uint32_t)__popcll(pm);
+              mma_append(s_st, a, s_qk, s_flag, wave, &fill, q0, (uint32_t)qi, seg, pm, acc[t][r], row);
+            }
           }
       }
     }
