@@ -399,7 +399,8 @@ extern "C" int mrl_ctx_profile_collect(mrl_ctx* ctx, mrl_kernel_time* out, uint3
 // ---------------------------------------------------------------------------
 // index
 // ---------------------------------------------------------------------------
-static int verify_crcs(const uint8_t* blocks, uint64_t n_blocks) {
+// CRC check of n_blocks blocks whose first is block `first` of the index (for the message).
+static int verify_crcs(const uint8_t* blocks, uint64_t n_blocks, uint64_t first = 0) {
   std::atomic<int64_t> bad{-1};
   parallel_for(n_blocks, 0, [&](uint64_t b0, uint64_t b1) {
     for (uint64_t b = b0; b < b1; ++b)
@@ -408,7 +409,8 @@ static int verify_crcs(const uint8_t* blocks, uint64_t n_blocks) {
         bad.compare_exchange_strong(expect, (int64_t)b);
       }
   });
-  return bad.load() < 0 ? MRL_OK : fail(MRL_ERR_CORRUPT, "crc32 mismatch in block " + std::to_string(bad.load()));
+  return bad.load() < 0 ? MRL_OK
+                        : fail(MRL_ERR_CORRUPT, "crc32 mismatch in block " + std::to_string(first + bad.load()));
 }
 
 extern "C" int mrl_index_upload(mrl_ctx* ctx, const void* blocks, uint64_t n_blocks, int verify_crc,
@@ -468,8 +470,12 @@ extern "C" int mrl_index_upload(mrl_ctx* ctx, const void* blocks, uint64_t n_blo
   return MRL_OK;
 }
 
+// Segment blocks per staging chunk of mrl_index_open_segment (16 MiB).
+static const uint64_t kSegChunkBlocks = 4096;
+
 extern "C" int mrl_index_open_segment(mrl_ctx* ctx, const char* path, int verify_crc, mrl_index** out) {
   if (!ctx || !path || !out) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  *out = nullptr;
   FILE* f = fopen(path, "rb");
   if (!f) return mrl_index_upload(ctx, nullptr, 0, 0, out);  // segment.rs:94-101: absent file = empty
   if (fseek(f, 0, SEEK_END) != 0) {
@@ -485,12 +491,100 @@ extern "C" int mrl_index_open_segment(mrl_ctx* ctx, const char* path, int verify
     fclose(f);
     return fail(MRL_ERR_CORRUPT, "corrupt segment size " + std::to_string(len) + " (not multiple of 4096)");
   }
-  std::vector<uint8_t> buf((size_t)len);
+  const uint64_t n_blocks = (uint64_t)len / kBlockBytes;
+  if (n_blocks == 0) {
+    fclose(f);
+    return mrl_index_upload(ctx, nullptr, 0, 0, out);
+  }
+  if (n_blocks > (1ull << 26)) {
+    fclose(f);
+    return fail(MRL_ERR_INVALID_ARG, "n_blocks exceeds 2^26 (32-bit row ids)");
+  }
   fseek(f, 0, SEEK_SET);
-  size_t got = len ? fread(buf.data(), 1, (size_t)len, f) : 0;
-  fclose(f);
-  if (got != (size_t)len) return fail(MRL_ERR_IO, "short read");
-  return mrl_index_upload(ctx, buf.data(), (uint64_t)len / kBlockBytes, verify_crc, out);
+  // The file streams through two pinned host chunks: while the GPU copies
+  // chunk i and re-lays it out into the index, the host reads (and checks)
+  // chunk i + 1.  No whole-file host copy is made.
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  std::unique_ptr<mrl_index> ix(new mrl_index());
+  ix->ctx = ctx;
+  ix->n_blocks = n_blocks;
+  const uint64_t chunk = std::min<uint64_t>(n_blocks, kSegChunkBlocks);
+  uint8_t* host[2] = {nullptr, nullptr};
+  uint8_t* dstage[2] = {nullptr, nullptr};
+  hipEvent_t done[2] = {nullptr, nullptr};
+  auto cleanup = [&](bool keep_index) {
+    (void)hipStreamSynchronize(ctx->stream);  // nothing may still read the staging
+    for (int k = 0; k < 2; ++k) {
+      if (host[k]) (void)hipHostFree(host[k]);
+      dev_free(dstage[k]);
+      if (done[k]) (void)hipEventDestroy(done[k]);
+    }
+    if (!keep_index) {
+      dev_free(ix->d_blocks);
+      dev_free(ix->d_recs);
+    }
+    fclose(f);
+  };
+  int rc = MRL_OK;
+  std::string msg;
+  if (hipMalloc(&ix->d_blocks, (size_t)n_blocks * kBlockBytes) != hipSuccess ||
+      hipMalloc(&ix->d_recs, (size_t)n_blocks * 64 * kRecWords * 16) != hipSuccess) {
+    rc = MRL_ERR_OUT_OF_MEMORY;
+    msg = "hipMalloc index";
+  }
+  for (int k = 0; k < 2 && !rc; ++k) {
+    if (hipHostMalloc((void**)&host[k], chunk * kBlockBytes, hipHostMallocDefault) != hipSuccess ||
+        hipMalloc(&dstage[k], chunk * kBlockBytes) != hipSuccess ||
+        hipEventCreateWithFlags(&done[k], hipEventDisableTiming) != hipSuccess) {
+      rc = MRL_ERR_OUT_OF_MEMORY;
+      msg = "segment staging";
+    }
+  }
+  for (uint64_t b = 0, i = 0; b < n_blocks && !rc; b += chunk, ++i) {
+    const int k = (int)(i & 1u);
+    const uint64_t nb = std::min(chunk, n_blocks - b);
+    if (i >= 2 && hipEventSynchronize(done[k]) != hipSuccess) {  // chunk i - 2 left these buffers
+      rc = MRL_ERR_HIP;
+      msg = "segment staging wait";
+      break;
+    }
+    if (fread(host[k], 1, nb * kBlockBytes, f) != nb * kBlockBytes) {
+      rc = MRL_ERR_IO;
+      msg = "short read";
+      break;
+    }
+    if (verify_crc) {
+      rc = verify_crcs(host[k], nb, b);
+      if (rc) break;
+    }
+    hipError_t e = hipMemcpyAsync(dstage[k], host[k], nb * kBlockBytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess)
+      e = launch_relayout(dstage[k], ix->d_blocks + b * kBlockBytes, nb, true, ctx->stream,
+                          ix->d_recs + b * 64 * kRecWords);
+    if (e == hipSuccess) e = hipEventRecord(done[k], ctx->stream);
+    if (e != hipSuccess) {
+      rc = MRL_ERR_HIP;
+      msg = std::string("segment upload: ") + hipGetErrorString(e);
+    }
+  }
+  if (!rc && hipStreamSynchronize(ctx->stream) != hipSuccess) {
+    rc = MRL_ERR_HIP;
+    msg = "segment upload";
+  }
+  if (rc) {
+    cleanup(false);
+    return msg.empty() ? rc : fail(rc, msg);  // verify_crcs has set its own message
+  }
+  cleanup(true);
+  rc = build_bounds(ctx, ix.get());
+  if (rc) {
+    dev_free(ix->d_blocks);
+    dev_free(ix->d_recs);
+    return rc;
+  }
+  *out = ix.release();
+  return MRL_OK;
 }
 
 extern "C" int mrl_index_block_count(const mrl_index* index, uint64_t* out) {

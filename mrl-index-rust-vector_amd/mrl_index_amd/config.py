@@ -5,6 +5,7 @@ from dataclasses import dataclass, field, replace
 from enum import IntEnum
 
 from . import _lib
+from .jsonf32 import f32_from_text, f32_text
 
 
 class PrefixCodec(IntEnum):
@@ -120,3 +121,87 @@ class EngineConfig:
 
     def copy(self, **kw) -> "EngineConfig":
         return replace(self, **kw)
+
+    def to_serde(self) -> dict:
+        """The serde form of EngineConfig (config.rs:124-167): the Rust field
+        order, enums in snake_case (``exhaustive`` is this build's own and is
+        not written)."""
+        d = {}
+        for name, kind in _SERDE_FIELDS:
+            v = getattr(self, name)
+            if kind == "enum":
+                v = _SERDE_ENUMS[name][type(_SERDE_DEFAULTS_ENUM[name])(v)]
+            elif kind == "f32":
+                v = float(f32_text(v))  # the shortest text of the f32 (json.dumps writes it back)
+            elif kind == "bool":
+                v = bool(v)
+            elif kind == "residency":
+                if v not in _RESIDENCY:
+                    raise ValueError(f"slab_residency {v!r}")
+            else:
+                v = int(v)
+            d[name] = v
+        return d
+
+    @classmethod
+    def from_serde(cls, d: dict) -> "EngineConfig":
+        """Deserialize the serde form: every field is required except those
+        with #[serde(default)] (use_gemma2 false, prefix_codec min_max4 -- the
+        enum's own default, not EngineConfig::default's --, eden_seed 1,
+        mid_codec rabitq); unknown fields are ignored; f32 fields are rounded
+        once from their decimal text.  Type errors raise ValueError."""
+        if not isinstance(d, dict):
+            raise ValueError("config: expected an object")
+        kw = {}
+        for name, kind in _SERDE_FIELDS:
+            if name not in d:
+                if name in _SERDE_OPTIONAL:
+                    kw[name] = _SERDE_OPTIONAL[name]
+                    continue
+                raise ValueError(f"config: missing field `{name}`")
+            v = d[name]
+            if kind == "enum":
+                inv = {t: e for e, t in _SERDE_ENUMS[name].items()}
+                if v not in inv:
+                    raise ValueError(f"config: unknown variant {v!r} for `{name}`")
+                v = inv[v]
+            elif kind == "residency":
+                if v not in _RESIDENCY:
+                    raise ValueError(f"config: unknown variant {v!r} for `slab_residency`")
+            elif kind == "bool":
+                if not isinstance(v, bool):
+                    raise ValueError(f"config: `{name}` expects a bool")
+            elif kind == "f32":
+                if isinstance(v, bool) or not isinstance(v, (int, float, str)):
+                    raise ValueError(f"config: `{name}` expects a number")
+                v = float(f32_text(f32_from_text(str(v))))
+            else:
+                if isinstance(v, bool) or not isinstance(v, int) or v < 0:
+                    raise ValueError(f"config: `{name}` expects an unsigned integer")
+            kw[name] = v
+        return cls(**kw)
+
+
+# serde field order and kinds of EngineConfig (config.rs:124-167)
+_SERDE_FIELDS = (
+    ("strata_depth", "enum"), ("slab_residency", "residency"), ("numa_sharding", "bool"),
+    ("shortlist_cand", "usize"), ("cs_tolerance", "f32"), ("stratum4_weight", "f32"),
+    ("rabitq_confidence", "f32"), ("jit_batch_size", "usize"), ("io_read_workers", "usize"),
+    ("max_latency_budget_ms", "usize"), ("ring_buffer_size", "usize"), ("tombstone_compact_ratio", "f32"),
+    ("temporal_filter_enable", "bool"), ("embed_dims", "usize"), ("mrl_prefix", "usize"),
+    ("final_top_k", "usize"), ("use_gemma2", "bool"), ("prefix_codec", "enum"), ("eden_seed", "usize"),
+    ("mid_codec", "enum"),
+)
+# #[serde(rename_all = "snake_case")] variant names (config.rs:8-77)
+_SERDE_ENUMS = {
+    "strata_depth": {StrataDepth.L0_ONLY: "l0_only", StrataDepth.L1_RABITQ: "l1_rabitq",
+                     StrataDepth.FULL64B: "full64b"},
+    "prefix_codec": {PrefixCodec.MIN_MAX4: "min_max4", PrefixCodec.EDEN_PROD: "eden_prod"},
+    "mid_codec": {MidCodec.RABITQ: "rabitq", MidCodec.EDEN_B1: "eden_b1"},
+}
+_SERDE_DEFAULTS_ENUM = {"strata_depth": StrataDepth.FULL64B, "prefix_codec": PrefixCodec.MIN_MAX4,
+                        "mid_codec": MidCodec.RABITQ}
+_RESIDENCY = ("ram_locked", "mmap_willneed", "direct_nvme")
+# fields with #[serde(default)] (config.rs:155-166)
+_SERDE_OPTIONAL = {"use_gemma2": False, "prefix_codec": PrefixCodec.MIN_MAX4, "eden_seed": 1,
+                   "mid_codec": MidCodec.RABITQ}

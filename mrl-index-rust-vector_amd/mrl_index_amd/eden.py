@@ -1,4 +1,4 @@
-"""EdenFit (src/eden.rs:382-485): the corpus prefix mean shared by encode and query."""
+"""EdenFit (src/eden.rs:100-203): the corpus prefix mean shared by encode and query."""
 from __future__ import annotations
 
 import json
@@ -8,6 +8,7 @@ import numpy as np
 
 from . import _lib
 from .block import MRL_PREFIX_DIMS
+from .jsonf32 import f32_from_text, f32_text
 
 # eden.rs:15-44
 LLOYD_MAX = {
@@ -72,12 +73,43 @@ class EdenFit:
         return _lib.EdenFitC(self.dim, self.bits, self.seed, _lib.fptr(self.mean), self.n_observed)
 
     def save_json(self, path) -> None:
+        """eden.rs:193-197 (serde_json pretty form; f32 as shortest round-trip text)."""
         with open(path, "w") as f:
-            json.dump({"dim": self.dim, "bits": self.bits, "seed": self.seed,
-                       "mean": [float(v) for v in self.mean], "n_observed": self.n_observed}, f, indent=2)
+            f.write(self.to_json())
+
+    def to_json(self) -> str:
+        mean = ",\n".join("    " + f32_text(v) for v in self.mean)
+        return (f'{{\n  "dim": {int(self.dim)},\n  "bits": {int(self.bits)},\n  "seed": {int(self.seed)},\n'
+                f'  "mean": [\n{mean}\n  ],\n  "n_observed": {int(self.n_observed)}\n}}')
 
     @classmethod
     def load_json(cls, path) -> "EdenFit":
+        """eden.rs:199-202.  Each mean value is rounded once from its decimal
+        text to f32, as serde_json does; a missing n_observed is 0
+        (#[serde(default)]).  Malformed files raise ValueError."""
         with open(path) as f:
-            d = json.load(f)
-        return cls(d["dim"], d["bits"], d["seed"], np.array(d["mean"], dtype=np.float32), d.get("n_observed", 0))
+            return cls.from_json(f.read())
+
+    @classmethod
+    def from_json(cls, text: str) -> "EdenFit":
+        d = json.loads(text, parse_float=str)
+        try:
+            dim, bits, seed = _uint(d["dim"]), _uint(d["bits"], 255), _uint(d["seed"])
+            mean = np.array([f32_from_text(_num(v)) for v in d["mean"]], dtype=np.float32)
+            n_obs = _uint(d.get("n_observed", 0))
+        except (KeyError, TypeError) as e:
+            raise ValueError(f"eden fit json: {e!r}") from None
+        return cls(dim, bits, seed, mean, n_obs)
+
+
+def _uint(v, hi=2 ** 64 - 1) -> int:
+    if isinstance(v, bool) or not isinstance(v, int) or not 0 <= v <= hi:
+        raise ValueError(f"expected an unsigned integer, got {v!r}")
+    return v
+
+
+def _num(v) -> str:
+    # parse_float=str hands decimals over as text; integers arrive as int
+    if isinstance(v, bool) or not isinstance(v, (int, str)):
+        raise ValueError(f"expected a number, got {v!r}")
+    return str(v)

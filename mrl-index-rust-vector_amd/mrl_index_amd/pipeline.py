@@ -2,17 +2,24 @@
 caller of the reference goes through."""
 from __future__ import annotations
 
+import json
+import os
 import time
 from dataclasses import dataclass
-from typing import List, Optional
+from typing import List, Optional, Tuple
 
 import numpy as np
 
-from .block import VECTORS_PER_BLOCK, VectorId
+from .block import BLOCK_BYTES, VECTORS_PER_BLOCK, VectorId
 from .config import EngineConfig, MidCodec, PrefixCodec
 from .eden import EdenFit
 from .lowprec import RerankStore, rerank_rows
-from .scan import DeviceIndex, QueryPlan, ScanStats, ScoredHit, scan_blocks_stats
+from .scan import DeviceIndex, QueryPlan, ScanStats, ScoredHit, default_device, scan_blocks_stats
+from .shortlist import Shortlist
+
+EDEN_PREFIX_FILE = "eden_prefix.json"  # engine.rs:22
+MANIFEST_FILE = "manifest.json"
+SEGMENT_PATH = os.path.join("segments", "000001.pax")  # engine.rs:143
 
 
 @dataclass
@@ -57,6 +64,15 @@ class QueryPipeline:
         n = blocks.block_count() if isinstance(blocks, DeviceIndex) else len(np.asarray(blocks).reshape(-1, 4096))
         return ScanPhase(plan, hits, ms, n)
 
+    def scan_segments_into(self, plan: QueryPlan, reader: DeviceIndex, shortlist: Shortlist, time_lo=None,
+                           time_hi=None) -> int:
+        """pipeline.rs:104-133: scans the segment (resident in HBM) and pushes
+        every hit, best first, into the caller's shortlist; the caller merges
+        ring hits afterwards and calls into_sorted.  Returns the block count."""
+        for hit in scan_blocks_stats(reader, plan, self.cfg, time_lo, time_hi, None):
+            shortlist.push(hit)
+        return reader.block_count()
+
     def scan_segments(self, query, index: DeviceIndex, time_lo=None, time_hi=None):
         """pipeline.rs:136-154 for a segment opened with DeviceIndex.open_segment."""
         plan = self.build_plan(query)
@@ -83,6 +99,77 @@ class QueryPipeline:
         finally:
             store.close()
         return [(uniq[r], s) for r, s in ranked]
+
+
+@dataclass
+class IndexManifest:
+    """engine.rs:38-44 (manifest.json)."""
+    version: str
+    config: EngineConfig
+    next_passage_id: int
+    blocks_written: int
+
+    @classmethod
+    def load(cls, path) -> "IndexManifest":
+        with open(path) as f:
+            d = json.loads(f.read(), parse_float=str)
+        try:
+            ver, cfg = d["version"], d["config"]
+            npid, bw = d["next_passage_id"], d["blocks_written"]
+        except (KeyError, TypeError) as e:
+            raise ValueError(f"manifest: missing {e}") from None
+        if not isinstance(ver, str):
+            raise ValueError("manifest: `version` expects a string")
+        for name, v, hi in (("next_passage_id", npid, 2 ** 64 - 1), ("blocks_written", bw, 2 ** 32 - 1)):
+            if isinstance(v, bool) or not isinstance(v, int) or not 0 <= v <= hi:
+                raise ValueError(f"manifest: `{name}` expects an unsigned integer")
+        return cls(ver, EngineConfig.from_serde(cfg), npid, bw)
+
+    def save(self, path) -> None:
+        """engine.rs:213-225 (pretty JSON)."""
+        d = {"version": self.version, "config": self.config.to_serde(), "next_passage_id": int(self.next_passage_id),
+             "blocks_written": int(self.blocks_written)}
+        with open(path, "w") as f:
+            f.write(json.dumps(d, indent=2))
+
+
+def live_slots(segment_path) -> int:
+    """Slots not tombstoned in a segment file (the id_map rebuild of
+    engine.rs:149-161 counts them): tombstone bits are the u64 at byte 16 of
+    each block header (block.rs:34-44)."""
+    if not os.path.exists(segment_path):
+        return 0
+    size = os.path.getsize(segment_path)
+    if size == 0 or size % BLOCK_BYTES:
+        return 0
+    mm = np.memmap(segment_path, dtype=np.uint8, mode="r")
+    tomb = np.ascontiguousarray(mm.reshape(-1, BLOCK_BYTES)[:, 16:24]).view("<u8").ravel()
+    del mm
+    return int(VECTORS_PER_BLOCK * tomb.size - int(np.unpackbits(tomb.view(np.uint8)).sum()))
+
+
+def open_index(directory, device=None, verify_crc: bool = False) -> Tuple[QueryPipeline, DeviceIndex, IndexManifest]:
+    """The scan path of IndexEngine::open (engine.rs:132-192) on an index
+    directory: manifest.json's config (validated), segments/000001.pax
+    streamed into HBM, and the prefix fit -- eden_prefix.json if present,
+    else EdenFit::default_prefix(eden_seed) -- when the codec is EdenProd.
+    The reopen check compares the segment's live slots with the manifest's
+    next_passage_id (the passage count it was written with; the passage store
+    itself is not part of the scan path).  Errors raise ValueError (config,
+    JSON, reopen check) or MrlError (segment)."""
+    directory = str(directory)
+    man = IndexManifest.load(os.path.join(directory, MANIFEST_FILE))
+    man.config.validate()
+    seg = os.path.join(directory, SEGMENT_PATH)
+    live = live_slots(seg)
+    if live > man.next_passage_id:
+        raise ValueError(f"segment/passage mismatch: {live} live slots vs {man.next_passage_id} passages")
+    index = DeviceIndex.open_segment(seg, device or default_device(), verify_crc)
+    fit = None
+    if man.config.prefix_codec == PrefixCodec.EDEN_PROD:
+        path = os.path.join(directory, EDEN_PREFIX_FILE)
+        fit = EdenFit.load_json(path) if os.path.exists(path) else EdenFit.default_prefix(man.config.eden_seed)
+    return QueryPipeline(man.config, fit, None), index, man
 
 
 def scored_hits_to_row_ids(hits: List[ScoredHit]) -> List[int]:
