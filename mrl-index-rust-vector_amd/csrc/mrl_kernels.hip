@@ -1997,8 +1997,8 @@ __device__ __forceinline__ void bitonic_desc(uint64_t* s, int n2) {
 // exact ties) when the gathered set exceeds the sort buffer.  Leaves the
 // query's counters, histogram and error flag zeroed for the next scan.
 __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
-  __shared__ uint64_t s_buf[kSortCap];
-  __shared__ uint64_t s_sel[kSelCap + 16];
+  __shared__ __align__(16) uint64_t s_buf[kSortCap];  // read as 16-byte pairs by the rank sort
+  __shared__ __align__(16) uint64_t s_sel[kSelCap + 16];
   __shared__ uint32_t s_start[kHistBins];
   __shared__ uint32_t s_hist[2048];
   __shared__ uint32_t s_misc[8];
