@@ -143,8 +143,11 @@ def kernel_groups(L, _lib, dev, cap):
     return groups
 
 
-def roofline_of(groups, nq, prof_steps, w, cold=False):
-    """The dominant kernel's roofline from the recorded launches."""
+def roofline_of(groups, nq, prof_steps, w, cold=False, scanned=None):
+    """The dominant kernel's roofline from the recorded launches.  scanned:
+    the (block, query) pairs the MFMA final pass actually scored per step (its
+    ScanStats.blocks counter), which a cluster-grouped index's block lists make
+    fewer than blocks x queries; by default every block for every query."""
     import numpy as np
     mma = any(kind == "mma_prep" for kind, _ in groups)
     src = {}
@@ -176,10 +179,12 @@ def roofline_of(groups, nq, prof_steps, w, cold=False):
         final = max(p for kind, p in groups if kind == "scan")
         g = groups[("scan", final)]
         avg_ms = float(np.mean(g["ms"]))
-        pairs = 64.0 * float(np.mean(g["blocks"])) * nq
+        block_queries = float(scanned) if scanned is not None else float(np.mean(g["blocks"])) * nq
+        pairs = 64.0 * block_queries
         flops = 2.0 * MMA_MACS_PER_PAIR * pairs
         achieved = flops / (avg_ms / 1000.0) / 1e12
-        bytes_per_launch = 4096.0 * float(np.mean(g["blocks"]))
+        # the blocks one query scanned (a block shared by the batch is read once)
+        bytes_per_launch = 4096.0 * block_queries / nq
         hbm = bytes_per_launch / (avg_ms / 1000.0) / 1e9
         traffic = None if cold else committed_traffic("k_scan_mma", w.name)
         r = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
@@ -301,7 +306,8 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
         "pairs_per_s": round(w.n_docs * nq / (ms_step / 1000.0), 1),
         "step_algorithmic_gb_s": round(step_bytes / (ms_step / 1000.0) / 1e9, 1),
         "step_hbm_frac": round(step_bytes / (ms_step / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": roofline_of(groups, nq, prof_steps, w),
+        "roofline": roofline_of(groups, nq, prof_steps, w,
+                                scanned=timed_stats["blocks"] / args.steps if layout == "clustered" else None),
         "kernels": kernels_of(groups),
         "scan_stats_per_step": {f: v / args.steps for f, v in timed_stats.items()},
         "reruns_per_step": {"safe": timed_stats["reruns_safe"] / args.steps,
@@ -332,7 +338,9 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
             "kernel_ms_per_step": round(kernel_ms, 5), "warm_kernel_ms_per_step": round(warm_ms, 5),
             "value": round(w.n_docs / (kernel_ms / 1000.0) / 1e6, 2), "unit": "Mvec/s",
             "step_algorithmic_gb_s": round(step_bytes / (kernel_ms / 1000.0) / 1e9, 1),
-            "roofline": roofline_of(cg, nq, prof_steps, w, cold=True), "kernels": kernels_of(cg)}
+            "roofline": roofline_of(cg, nq, prof_steps, w, cold=True,
+                                    scanned=timed_stats["blocks"] / args.steps if layout == "clustered" else None),
+            "kernels": kernels_of(cg)}
 
     if legs:
         out["host_boundary"] = host_boundary_rate(L, _lib, dev, ix, queries, fit, w, ccfg, tr)

@@ -21,13 +21,15 @@
  *    follow from single set bits; the pruned scan against the exhaustive
  *    top-K (admissibility); stage-mask monotonicity and stats consistency.
  *  - EDEN nearest_centroid: brute force incl. the lower-index tie rule.
+ *  - ora_lloyd_max_normal (eden.rs:15-44): the f32 bits of every level equal
+ *    the reference's literals, parsed from eden.rs by
+ *    tests/golden/make_codebooks.py into tests/golden/eden_codebooks.json;
+ *    each level is also within 2e-6 of the N(0,1) Lloyd-Max centroid.
  * Parity unpinned (no independent check fixes the exact bits):
  *  - ora_rademacher_diag / ora_tail_rademacher (eden.rs:357-370,
  *    rotate.rs:53-67): the SplitMix-style sign sequence is checked only
  *    against a second restatement, for balance, and through the rotations'
  *    orthogonality, which any sign sequence satisfies.
- *  - ora_lloyd_max_normal (eden.rs:27-44): each level is within 2e-6 of the
- *    N(0,1) Lloyd-Max centroid; the literal f32 bits are as read.
  *  - ora_scan_blocks with sharding on: which of several exactly tied scores
  *    survive at the K boundary (Rayon's merge order, scan.rs:846-865).
  *  - ora_dot for n != 768: the sign of an exactly zero sum (Sum for f32
