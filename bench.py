@@ -186,7 +186,8 @@ def roofline_of(groups, nq, prof_steps, w, cold=False, scanned=None):
         # the blocks one query scanned (a block shared by the batch is read once)
         bytes_per_launch = 4096.0 * block_queries / nq
         hbm = bytes_per_launch / (avg_ms / 1000.0) / 1e9
-        traffic = None if cold else committed_traffic("k_scan_mma", w.name)
+        # (the committed counters cover the standard layout; a block-listed pass reads other bytes)
+        traffic = None if cold or scanned is not None else committed_traffic("k_scan_mma", w.name)
         r = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
              "frac": round(achieved / MFMA_F16_PEAK_TFS, 4),
              "traffic": traffic["bytes_per_launch"] if traffic else None,
