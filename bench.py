@@ -50,7 +50,8 @@ MFMA_F16_PEAK_TFS = 2500.0  # dense f16 MFMA, MI355X
 # bits, 64 S4 bits and the 5 meta / error columns of the last K-step
 MMA_MACS_PER_PAIR = 64 + 128 + 64 + 5
 EVICT_BYTES = 1 << 30  # cold-cache runs read this much between steps
-KIND_NAMES = {0: "plan", 1: "scan", 2: "select", 3: "thresh", 6: "finish", 7: "mma_prep", 8: "exact", 9: "bounds"}
+KIND_NAMES = {0: "plan", 1: "scan", 2: "select", 3: "thresh", 6: "finish", 7: "mma_prep", 8: "exact", 9: "bounds",
+              10: "plan+scan"}
 
 
 def log(msg):
@@ -153,9 +154,10 @@ def roofline_of(groups, nq, prof_steps, w, cold=False, scanned=None):
     src = {}
     if not mma:
         # One-query path: the dominant kernel is k_scan (every pass launches
-        # it); its roofline is taken over all of its launches, as rocprofv3's
-        # per-kernel average is: algorithmic bytes per launch = 4096 B x
-        # blocks scanned by that launch.
+        # it; a sampling pass that also builds the plan is its own
+        # instantiation, "plan+scan"); its roofline is taken over all of its
+        # launches, as rocprofv3's per-kernel average is: algorithmic bytes
+        # per launch = 4096 B x blocks scanned by that launch.
         scan_ms = [ms for (kind, _), g in groups.items() if kind == "scan" for ms in g["ms"]]
         scan_blk = [b for (kind, _), g in groups.items() if kind == "scan" for b in g["blocks"]]
         avg_ms = float(np.mean(scan_ms))

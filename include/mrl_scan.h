@@ -397,7 +397,8 @@ typedef enum mrl_kernel_kind {
   MRL_KERNEL_FINISH = 6,      /* candidates of the MFMA-bounded scan to score exactly */
   MRL_KERNEL_MMA_PREP = 7,    /* query operands of the MFMA-bounded scan */
   MRL_KERNEL_EXACT = 8,       /* exact scores of those candidates */
-  MRL_KERNEL_BOUNDS = 9       /* block bounds: cluster x query table (pass 0), block lists (pass 1) */
+  MRL_KERNEL_BOUNDS = 9,      /* block bounds: cluster x query table (pass 0), block lists (passes 1, 2) */
+  MRL_KERNEL_PLAN_SCAN = 10   /* a one-query sampling pass that also built the query's plan */
 } mrl_kernel_kind;
 
 typedef struct mrl_kernel_time {

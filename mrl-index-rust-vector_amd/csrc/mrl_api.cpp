@@ -218,6 +218,9 @@ struct mrl_plans {
   float* d_queries = nullptr;  // owned copy, n_q * dims
   float* d_luts = nullptr;     // n_q * kQData scan constants written by the plan kernel
   uint8_t* d_block = nullptr;  // one allocation holding all of the above
+  // The plans are built lazily: by the next call that reads them (flush_plans),
+  // or inside a one-query sampling pass (k_scan's fused plan).
+  mutable bool pending = false;
 };
 
 // The per-query outputs sit in one device block, read back with one copy:
@@ -752,8 +755,7 @@ static int check_fit(const mrl_eden_fit* f, uint32_t dim, uint32_t bits, const c
 }
 
 // Plan kernel over the plan set's resident queries.  Caller holds the lock.
-static int enqueue_plan(mrl_ctx* ctx, mrl_plans* p) {
-  if (!p->n_q) return MRL_OK;
+static PlanArgs plan_args(const mrl_ctx* ctx, const mrl_plans* p) {
   PlanArgs a;
   a.queries = p->d_queries;
   a.n_q = p->n_q;
@@ -767,10 +769,25 @@ static int enqueue_plan(mrl_ctx* ctx, mrl_plans* p) {
   a.c = ctx->consts;
   a.out = p->d_plans;
   a.luts = p->d_luts;
+  return a;
+}
+
+static int enqueue_plan(mrl_ctx* ctx, mrl_plans* p) {
+  if (!p->n_q) return MRL_OK;
+  const PlanArgs a = plan_args(ctx, p);
   ProfScope ps(ctx, MRL_KERNEL_PLAN, 0, 0, p->n_q);
   HIP_TRY(launch_plan(a, ctx->stream, ps.ev()));
   ps.commit(p->n_q != 0);
   return MRL_OK;
+}
+
+// Builds plans whose build is still pending (the lazy build of
+// mrl_plans_build / _rebuild).  Caller holds the lock.
+static int flush_plans(mrl_ctx* ctx, const mrl_plans* plans) {
+  if (!plans || !plans->pending) return MRL_OK;
+  int rc = enqueue_plan(ctx, const_cast<mrl_plans*>(plans));
+  if (!rc) plans->pending = false;
+  return rc;
 }
 
 static int plans_build_impl(mrl_ctx* ctx, const float* queries, bool on_device, uint32_t n_q, uint32_t dims,
@@ -840,7 +857,8 @@ static int plans_build_impl(mrl_ctx* ctx, const float* queries, bool on_device, 
     dev_free(p->d_block);
     return fail(MRL_ERR_HIP, "plan inputs copy");
   }
-  int rc2 = enqueue_plan(ctx, p.get());
+  int rc2 = MRL_OK;
+  p->pending = true;  // built by the first call that reads the plans
   // The pinned inputs are reused by the next call: wait for the copy (host path).
   if (!rc2 && !on_device && hipStreamSynchronize(ctx->stream) != hipSuccess) rc2 = fail(MRL_ERR_HIP, "plan build");
   if (rc2) {
@@ -869,7 +887,8 @@ extern "C" int mrl_plans_rebuild(mrl_ctx* ctx, mrl_plans* plans) {
   if (plans->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "plans belong to another context");
   std::lock_guard<std::mutex> g(ctx->mu);
   HIP_TRY(hipSetDevice(ctx->device));
-  return enqueue_plan(ctx, plans);
+  plans->pending = true;  // built by the next call that reads the plans
+  return MRL_OK;
 }
 
 extern "C" int mrl_plans_count(const mrl_plans* plans, uint32_t* out) {
@@ -884,6 +903,8 @@ extern "C" int mrl_plans_export(mrl_ctx* ctx, const mrl_plans* plans, uint32_t f
   if ((uint64_t)first + count > plans->n_q) return fail(MRL_ERR_INVALID_ARG, "plan range out of bounds");
   std::lock_guard<std::mutex> g(ctx->mu);
   HIP_TRY(hipSetDevice(ctx->device));
+  int rc = flush_plans(ctx, plans);
+  if (rc) return rc;
   HIP_TRY(hipStreamSynchronize(ctx->stream));
   if (count) HIP_TRY(hipMemcpy(out, plans->d_plans + first, sizeof(mrl_query_plan) * count, hipMemcpyDeviceToHost));
   return MRL_OK;
@@ -1116,6 +1137,7 @@ struct BoundSel {
 // each; clears both count arrays.  Caller holds the lock.
 static int enqueue_bound_table(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t plans_first,
                                uint32_t n_q, const ScanParams& sp, uint32_t chunk, BoundSel* sel) {
+  if (int rc = flush_plans(ctx, plans)) return rc;
   const uint32_t n_chunks = (n_q + chunk - 1) / chunk;
   const size_t table_bytes = ((size_t)ix->n_cl * n_q * 4 + 255) & ~(size_t)255;
   const size_t qn_bytes = ((size_t)n_q * 16 + 255) & ~(size_t)255;
@@ -1330,6 +1352,15 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
 static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t plans_first, uint32_t n_q,
                         const ScanParams& sp, uint32_t K, const LevelPlan& lp, const PassBuffers& pb,
                         unsigned long long* stats, bool rerun_safe = false) {
+  // A pending plan build of one query goes into its sampling pass (the fused
+  // k_scan); otherwise the plans are built first.
+  const bool fuse = plans->pending && n_q == 1 && plans_first == 0 && plans->n_q == 1 && !rerun_safe &&
+                    lp.passes.size() > 1 && sp.strata != MRL_STRATA_L0_ONLY && plans->dims <= (uint32_t)kFuseMaxDims &&
+                    !mma_ok(plans, n_q, sp, pb);
+  if (!fuse) {
+    int rc = flush_plans(ctx, plans);
+    if (rc) return rc;
+  }
   if (mma_ok(plans, n_q, sp, pb)) return enqueue_scan_mma(ctx, ix, plans, plans_first, n_q, sp, K, pb, stats, rerun_safe);
   hipStream_t s = ctx->stream;
   const size_t np = lp.passes.size();
@@ -1392,9 +1423,14 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
       if (!rc) rc = enqueue_block_select(ctx, ix, plans, n_q, sel, 1, pb.tau_hi, (uint32_t)ix->n_blocks, 0u, &a);
       if (rc) return rc;
     }
-    ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)pi, lp.passes[pi].n_new, n_q);
+    if (fuse && pi == 0) {
+      a.fuse_plan = 1;
+      a.plan = plan_args(ctx, plans);
+    }
+    ProfScope ps(ctx, a.fuse_plan ? MRL_KERNEL_PLAN_SCAN : MRL_KERNEL_SCAN, (int)pi, lp.passes[pi].n_new, n_q);
     HIP_TRY(launch_scan(a, false, s, ps.ev()));
     ps.commit(a.n_pos != 0 && n_q != 0);
+    if (a.fuse_plan) plans->pending = false;
   }
   SelectArgs sa{};
   sa.luts = plans->d_luts + (size_t)plans_first * kQData;
@@ -1778,6 +1814,7 @@ static NaLayout na_layout(uint32_t n_q, uint8_t* base) {
 // Caller holds the lock.
 static int enqueue_gated_rerun(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t n_q,
                                const ScanParams& sp, uint32_t K, const PassBuffers& pb) {
+  if (int rc = flush_plans(ctx, plans)) return rc;
   ScanArgs a{};
   a.idx = ix->d_blocks;
   a.recs = ix->recs();
@@ -1902,6 +1939,7 @@ extern "C" int mrl_scan_fixed_tau(mrl_ctx* ctx, const mrl_index* index, const mr
   if (!out_masks || !out_prefix_ip || !out_scores) return fail(MRL_ERR_INVALID_ARG, "null output");
   std::lock_guard<std::mutex> g(ctx->mu);
   HIP_TRY(hipSetDevice(ctx->device));
+  if (int rc = flush_plans(ctx, plans)) return rc;
   float* d_tau = nullptr;
   uint64_t* d_masks = nullptr;
   float *d_prefix = nullptr, *d_score = nullptr;
@@ -1968,6 +2006,7 @@ extern "C" int mrl_index_block_bounds(mrl_ctx* ctx, const mrl_index* index, cons
   }
   std::lock_guard<std::mutex> g(ctx->mu);
   HIP_TRY(hipSetDevice(ctx->device));
+  if (int rc = flush_plans(ctx, plans)) return rc;
   float *d_table = nullptr, *d_qn = nullptr, *d_out = nullptr;
   auto cleanup = [&]() {
     dev_free(d_table);
@@ -2023,6 +2062,7 @@ extern "C" int mrl_scan_mma_bounds(mrl_ctx* ctx, const mrl_index* index, const m
   if (N > (1ull << 24)) return fail(MRL_ERR_INVALID_ARG, "MFMA bounds dump is limited to 2^24 slots");
   std::lock_guard<std::mutex> g(ctx->mu);
   HIP_TRY(hipSetDevice(ctx->device));
+  if (int rc = flush_plans(ctx, plans)) return rc;
   float *d_u = nullptr, *d_l = nullptr, *d_consts = nullptr;
   uint32_t *d_row = nullptr, *d_cnt = nullptr, *d_work = nullptr;
   uint4* d_ops = nullptr;

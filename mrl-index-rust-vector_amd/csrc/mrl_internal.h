@@ -159,6 +159,7 @@ constexpr int kMmaQ = 64;       // queries per workgroup (two 32-query tiles per
 constexpr int kMmaWaves = 8;    // waves per MFMA scan workgroup (four waves per SIMD)
 constexpr int kMmaMinQ = 8;     // batches of at least this many queries take the MFMA path
 constexpr int kTileQ = 8;       // queries per tile of the batched exact kernel (k_scan_tile)
+constexpr int kFuseMaxDims = 1024;  // queries up to this many dims may build their plan inside the sampling pass
 // Per-query constants written by k_mma_prep (floats).
 enum {
   kMcS = 0,   // power-of-two scale of the query operand
@@ -194,6 +195,8 @@ struct ScanArgs {
   uint32_t n_pos;
   uint32_t shift;
   int32_t prev_shift;
+  int32_t fuse_plan;  // one-query sampling pass that also builds the query's plan (`plan`)
+  PlanArgs plan;
   const mrl_query_plan* plans;
   const float* luts;           // [n_q][kQData] scan constants (prefix LUT, stage weights, sum bounds)
   uint32_t n_q;

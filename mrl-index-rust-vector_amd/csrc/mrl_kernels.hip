@@ -312,15 +312,27 @@ __device__ __forceinline__ void wave_lds_sync() {
 // Each sum is a chain of f32 additions in the reference's order (scan.rs:
 // 132-233, 528-531) whose terms are the reference's single rounded f32
 // operations; `x -= y` is accumulated as `x + (-y)`, the same IEEE operation.
-__global__ __launch_bounds__(192) void k_plan(PlanArgs a) {
-  __shared__ __align__(16) float s_q[MRL_MAX_DIMS];
-  __shared__ __align__(16) float s_sq[MRL_MAX_DIMS - kTailStart];
-  __shared__ __align__(16) float s_mid[128];
-  __shared__ __align__(16) float s_eden[64];
-  __shared__ __align__(16) float s_terms[9][128];
-  __shared__ float s_sums[11];
+// The LDS of one query's plan for queries of at most MAXD dims.
+template <int MAXD>
+struct PlanLds {
+  __align__(16) float q[MAXD];
+  __align__(16) float sq[MAXD - kTailStart];
+  __align__(16) float mid[128];
+  __align__(16) float eden[64];
+  __align__(16) float terms[9][128];
+  float sums[11];
+};
 
-  const uint32_t q = blockIdx.x;
+// One query's plan (plan record and scan constants) by threads 0..191 of the
+// workgroup; every thread of the workgroup must call it (it has barriers).
+template <int MAXD>
+__device__ __forceinline__ void plan_body(const PlanArgs& a, uint32_t q, PlanLds<MAXD>& sh) {
+  float* s_q = sh.q;
+  float* s_sq = sh.sq;
+  float* s_mid = sh.mid;
+  float* s_eden = sh.eden;
+  float (*s_terms)[128] = sh.terms;
+  float* s_sums = sh.sums;
   const int t = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const uint32_t lane = (uint32_t)t & 63u;
@@ -339,7 +351,7 @@ __global__ __launch_bounds__(192) void k_plan(PlanArgs a) {
   const float c1 = has_mid ? a.c.eden_mid_codebook[1] : 0.0f;
 
   // four loads in flight per thread (index clamped), then the stores
-  for (uint32_t i0 = t; i0 < dims; i0 += 4u * 192u) {
+  for (uint32_t i0 = t; t < 192 && i0 < dims; i0 += 4u * 192u) {
     float v[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -357,7 +369,9 @@ __global__ __launch_bounds__(192) void k_plan(PlanArgs a) {
   }
   __syncthreads();
 
-  if (wave == 1) {
+  if (wave >= 3) {
+    // (a wider workgroup's other waves only meet the barriers)
+  } else if (wave == 1) {
     // q_tail_sq: the squares formed by every lane, then the chain on one
     for (int i = (int)lane; i < tail_n; i += 64) s_sq[i] = s_q[kTailStart + i] * s_q[kTailStart + i];
     wave_lds_sync();
@@ -407,7 +421,10 @@ __global__ __launch_bounds__(192) void k_plan(PlanArgs a) {
       p->eden_mid_codebook[1] = c1;
       p->rabitq_scale = rs;
     }
-    for (int e = kQdU4 + 1 + (int)lane; e < kQData; e += 64) qd[e] = 0.0f;
+    // the unused tail; every address is written once, with its final value,
+    // so a fused pass may read it while other workgroups still write it
+    static_assert(kQdHistInv == kQdU4 + 1 && kQdHistScale == kQdU4 + 2, "scan constant layout");
+    for (int e = kQdHistScale + 1 + (int)lane; e < kQData; e += 64) qd[e] = 0.0f;
     wave_lds_sync();
     // Prefix LUT: lut[d*16 + level] = codebook[level] * weight[d] (or
     // level * weight[d]), the product scan.rs:476-484 forms per (d, level).
@@ -549,6 +566,11 @@ __global__ __launch_bounds__(192) void k_plan(PlanArgs a) {
     qd[kQdHistInv] = ldexpf(1.0f, -e);
     qd[kQdHistScale] = ldexpf(1.0f, e);
   }
+}
+
+__global__ __launch_bounds__(192) void k_plan(PlanArgs a) {
+  __shared__ PlanLds<MRL_MAX_DIMS> sh;
+  plan_body<MRL_MAX_DIMS>(a, blockIdx.x, sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -1100,8 +1122,18 @@ __device__ __forceinline__ void defer_flush(const DeferQ& dq, uint32_t qn, const
 // One pass of the strata scan.  Workgroup = 4 waves; wave = one block at a
 // time (lane v = slot v), blocks pos = first + k * stride of the pass order.
 // QT queries share each block's loads.  L0 selects the L0Only stage set.
-template <int QT, bool DIAG, bool L0>
+// FUSE (one query, a sampling pass): the workgroup first builds the query's
+// plan itself (plan_body, the work of k_plan); every workgroup writes the same
+// plan record and scan constants, and each reads them only after its own
+// writes, so the pass needs no separate plan launch.
+template <int QT, bool DIAG, bool L0, bool FUSE = false>
 __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
+  static_assert(!FUSE || (QT == 1 && !DIAG && !L0), "the plan is fused into one-query scans only");
+  if constexpr (FUSE) {
+    __shared__ PlanLds<kFuseMaxDims> s_pl;
+    plan_body<kFuseMaxDims>(a.plan, blockIdx.y, s_pl);
+    __syncthreads();
+  }
   __shared__ __align__(16) float s_qd[L0 ? 1 : QT * kQData];  // scan constants of each query
   __shared__ float s_rho[256];
   __shared__ float s_midf[256];
@@ -3638,6 +3670,8 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const Launch
   const bool tile = a.n_q >= 8 && !diag && !l0 && !a.gate;
   const int qt = tile ? kTileQ : (a.gate ? 1 : scan_query_tile(a.n_q));
   if (a.gate && diag) return hipErrorInvalidValue;
+  if (a.fuse_plan && (a.n_q != 1 || diag || l0 || a.gate || a.plan.dims > (uint32_t)kFuseMaxDims || a.plan.n_q != 1))
+    return hipErrorInvalidValue;
   const uint32_t tiles = (a.n_q + qt - 1) / qt;
   const uint32_t grid = scan_grid(a, diag);
   // exclusive segments: the one-query kernel, one segment per workgroup
@@ -3662,6 +3696,7 @@ hipError_t launch_scan(const ScanArgs& a, bool diag, hipStream_t s, const Launch
       else launch(k_scan<1, false, true>, g, dim3(256), s, ev, a);
     } else {
       if (diag) launch(k_scan<1, true, false>, g, dim3(256), s, ev, a);
+      else if (a.fuse_plan) launch(k_scan<1, false, false, true>, g, dim3(256), s, ev, a);
       else launch(k_scan<1, false, false>, g, dim3(256), s, ev, a);
     }
   }
