@@ -51,7 +51,7 @@ MFMA_F16_PEAK_TFS = 2500.0  # dense f16 MFMA, MI355X
 MMA_MACS_PER_PAIR = 64 + 128 + 64 + 5
 EVICT_BYTES = 1 << 30  # cold-cache runs read this much between steps
 KIND_NAMES = {0: "plan", 1: "scan", 2: "select", 3: "thresh", 6: "finish", 7: "mma_prep", 8: "exact", 9: "bounds",
-              10: "plan+scan"}
+              10: "plan+scan", 11: "plan+mma_prep"}
 
 
 def log(msg):

@@ -398,7 +398,8 @@ typedef enum mrl_kernel_kind {
   MRL_KERNEL_MMA_PREP = 7,    /* query operands of the MFMA-bounded scan */
   MRL_KERNEL_EXACT = 8,       /* exact scores of those candidates */
   MRL_KERNEL_BOUNDS = 9,      /* block bounds: cluster x query table (pass 0), block lists (passes 1, 2) */
-  MRL_KERNEL_PLAN_SCAN = 10   /* a one-query sampling pass that also built the query's plan */
+  MRL_KERNEL_PLAN_SCAN = 10,  /* a one-query sampling pass that also built the query's plan */
+  MRL_KERNEL_PLAN_PREP = 11   /* the batch's plans and the MFMA query operands, in one launch */
 } mrl_kernel_kind;
 
 typedef struct mrl_kernel_time {

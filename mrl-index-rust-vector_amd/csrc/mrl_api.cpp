@@ -1219,7 +1219,7 @@ static int enqueue_block_select(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* pl
 // top K.  rerun_safe: the final pass alone at the safe floor.
 static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t plans_first, uint32_t n_q,
                             const ScanParams& sp, uint32_t K, const PassBuffers& pb, unsigned long long* stats,
-                            bool rerun_safe) {
+                            bool rerun_safe, bool fuse_prep = false) {
   hipStream_t s = ctx->stream;
   const uint64_t B = ix->n_blocks;
   const std::vector<MmaStage> stages = rerun_safe ? std::vector<MmaStage>() : mma_stages(B, n_q);
@@ -1233,9 +1233,16 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
     pa.ops = pb.mma_ops;
     pa.consts = pb.mma_consts;
     pa.work = pb.mma_work;
-    ProfScope ps(ctx, MRL_KERNEL_MMA_PREP, 0, 0, n_q);
-    HIP_TRY(launch_mma_prep(pa, s, ps.ev()));
-    ps.commit(n_q != 0);
+    if (fuse_prep) {  // the batch's pending plans first, in the same launch
+      ProfScope ps(ctx, MRL_KERNEL_PLAN_PREP, 0, 0, n_q);
+      HIP_TRY(launch_plan_mma_prep(plan_args(ctx, plans), pa, s, ps.ev()));
+      ps.commit(n_q != 0);
+      plans->pending = false;
+    } else {
+      ProfScope ps(ctx, MRL_KERNEL_MMA_PREP, 0, 0, n_q);
+      HIP_TRY(launch_mma_prep(pa, s, ps.ev()));
+      ps.commit(n_q != 0);
+    }
   }
   ScanArgs a{};
   a.idx = ix->d_blocks;
@@ -1354,14 +1361,17 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
                         unsigned long long* stats, bool rerun_safe = false) {
   // A pending plan build of one query goes into its sampling pass (the fused
   // k_scan); otherwise the plans are built first.
+  const bool mma = mma_ok(plans, n_q, sp, pb);
   const bool fuse = plans->pending && n_q == 1 && plans_first == 0 && plans->n_q == 1 && !rerun_safe &&
                     lp.passes.size() > 1 && sp.strata != MRL_STRATA_L0_ONLY && plans->dims <= (uint32_t)kFuseMaxDims &&
-                    !mma_ok(plans, n_q, sp, pb);
-  if (!fuse) {
+                    !mma;
+  // the MFMA path builds a pending plan of the whole batch with the query operands
+  const bool fuse_prep = mma && plans->pending && plans_first == 0 && n_q == plans->n_q;
+  if (!fuse && !fuse_prep) {
     int rc = flush_plans(ctx, plans);
     if (rc) return rc;
   }
-  if (mma_ok(plans, n_q, sp, pb)) return enqueue_scan_mma(ctx, ix, plans, plans_first, n_q, sp, K, pb, stats, rerun_safe);
+  if (mma) return enqueue_scan_mma(ctx, ix, plans, plans_first, n_q, sp, K, pb, stats, rerun_safe, fuse_prep);
   hipStream_t s = ctx->stream;
   const size_t np = lp.passes.size();
   const bool sampled = np > 1 && !rerun_safe;

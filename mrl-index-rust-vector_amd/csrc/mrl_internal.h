@@ -449,6 +449,8 @@ hipError_t launch_read_sweep(uint4* p, uint64_t n, hipStream_t s);
 // MFMA path: mode 0 samples (lower bounds into the histogram), 1 appends the
 // pairs whose upper bound reaches the floor in a.tau, 2 appends every active pair.
 hipError_t launch_mma_prep(const MmaPrepArgs& a, hipStream_t s, const LaunchEvents& ev = {});
+// k_plan then k_mma_prep for every query of the batch, in one launch (pa.n_q == ma.n_q)
+hipError_t launch_plan_mma_prep(const PlanArgs& pa, const MmaPrepArgs& ma, hipStream_t s, const LaunchEvents& ev = {});
 uint32_t mma_scan_grid(const ScanArgs& a);
 hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const LaunchEvents& ev = {});
 // Floors of a sampling stage from its histogram (which is then cleared): rank

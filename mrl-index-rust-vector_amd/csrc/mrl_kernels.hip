@@ -2355,74 +2355,86 @@ __device__ __forceinline__ uint32_t f16_bits(float x) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
-// Query operands and error coefficients, one wave per query.
-__global__ __launch_bounds__(64) void k_mma_prep(MmaPrepArgs a) {
-  __shared__ float s_w[64], s_w1[128], s_w4[64], s_ex[8];
-  const uint32_t q = blockIdx.x, lane = threadIdx.x;
-  const mrl_query_plan* p = a.plans + q;
-  const float* qd = a.luts + (uint64_t)q * kQData;
-  const bool eden = p->prefix_codec == MRL_PREFIX_EDEN_PROD;
-  const bool s1on = a.sp.strata != MRL_STRATA_L0_ONLY;
-  const bool tail = a.sp.strata == MRL_STRATA_FULL64B && p->has_tail_fold != 0;
-  const float w = p->prefix_weight[lane];
-  const float w1a = s1on ? qd[kQdW1 + lane] : 0.0f, w1b = s1on ? qd[kQdW1 + 64 + lane] : 0.0f;
-  const float w4 = tail ? qd[kQdW4 + lane] : 0.0f;
-  s_w[lane] = w;
-  s_w1[lane] = w1a;
-  s_w1[64 + lane] = w1b;
-  s_w4[lane] = w4;
-  const float cbv = lane < 16 ? (eden ? fabsf(p->eden_codebook[lane]) : (float)lane) : 0.0f;
-  float l1w = fabsf(w), l1w2 = fabsf(w1a) + fabsf(w1b), l1w4 = fabsf(w4), cbm = cbv;
-  float mx = fmaxf(fmaxf(fabsf(w), fabsf(w4)), fmaxf(fabsf(w1a), fabsf(w1b)));
-  const bool fin_l = w - w == 0.0f && w1a - w1a == 0.0f && w1b - w1b == 0.0f && w4 - w4 == 0.0f && cbv - cbv == 0.0f;
+// Query operands and error coefficients of query q, by the first wave of
+// the workgroup (threads 0..63; it has a workgroup barrier, so every thread
+// of the workgroup must call it).
+struct MmaPrepLds {
+  float w[64], w1[128], w4[64], ex[8];
+};
+__device__ __forceinline__ void mma_prep_body(const MmaPrepArgs& a, uint32_t q, MmaPrepLds& sh) {
+  float* s_w = sh.w;
+  float* s_w1 = sh.w1;
+  float* s_w4 = sh.w4;
+  float* s_ex = sh.ex;
+  const uint32_t lane = threadIdx.x;
+  float s = 0.0f, psum = 0.0f;  // operand scale and prefix_sum, for the operand step below
+  if (lane < 64) {
+    const mrl_query_plan* p = a.plans + q;
+    const float* qd = a.luts + (uint64_t)q * kQData;
+    const bool eden = p->prefix_codec == MRL_PREFIX_EDEN_PROD;
+    const bool s1on = a.sp.strata != MRL_STRATA_L0_ONLY;
+    const bool tail = a.sp.strata == MRL_STRATA_FULL64B && p->has_tail_fold != 0;
+    const float w = p->prefix_weight[lane];
+    const float w1a = s1on ? qd[kQdW1 + lane] : 0.0f, w1b = s1on ? qd[kQdW1 + 64 + lane] : 0.0f;
+    const float w4 = tail ? qd[kQdW4 + lane] : 0.0f;
+    s_w[lane] = w;
+    s_w1[lane] = w1a;
+    s_w1[64 + lane] = w1b;
+    s_w4[lane] = w4;
+    const float cbv = lane < 16 ? (eden ? fabsf(p->eden_codebook[lane]) : (float)lane) : 0.0f;
+    float l1w = fabsf(w), l1w2 = fabsf(w1a) + fabsf(w1b), l1w4 = fabsf(w4), cbm = cbv;
+    float mx = fmaxf(fmaxf(fabsf(w), fabsf(w4)), fmaxf(fabsf(w1a), fabsf(w1b)));
+    const bool fin_l = w - w == 0.0f && w1a - w1a == 0.0f && w1b - w1b == 0.0f && w4 - w4 == 0.0f && cbv - cbv == 0.0f;
 #pragma unroll
-  for (int h = 1; h < 64; h <<= 1) {
-    l1w += __shfl_xor(l1w, h);
-    l1w2 += __shfl_xor(l1w2, h);
-    l1w4 += __shfl_xor(l1w4, h);
-    mx = fmaxf(mx, __shfl_xor(mx, h));
-    cbm = fmaxf(cbm, __shfl_xor(cbm, h));
-  }
-  const float mean = eden ? p->eden_mean_ip : 0.0f;
-  const float psum = eden ? 0.0f : p->prefix_sum;
-  const float ws4 = tail ? a.sp.w_s4 : 0.0f;
-  // The f32 sums above run over at most 128 terms: relative error < 2^-17.
-  const float up = 1.0f + 1.0f / 1024.0f;
-  // s: every query-operand value times s stays below 2^14 in magnitude
-  const float bm = fmaxf(mx, fabsf(psum));
-  int ex = 0;
-  if (bm > 0.0f && bm - bm == 0.0f) (void)frexpf(bm, &ex);
-  ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
-  const float s = ldexpf(1.0f, 14 - ex), inv_s = ldexpf(1.0f, ex - 14);
-  const float t25 = 2.98023223876953125e-8f;  // 2^-25
-  const float eP = (cbm * l1w * (1.0f / 256.0f) + t25 * (64.0f * cbm + 1.0f) * inv_s) * up;
-  const float e1 = s1on ? (l1w2 * (1.0f / 512.0f) + t25 * 65.0f * inv_s) * up : 0.0f;
-  const float e4 = tail ? (ws4 * l1w4 * (1.0f / 512.0f) + t25 * (32.0f * ws4 + 1.0f) * inv_s) * up : 0.0f;
-  const float eO = eden ? 0.0f : (fabsf(psum) * (1.0f / 512.0f) + t25 * 2.0f * inv_s) * up;
-  const float e0 =
-      (fabsf(mean) * (1.0f / 16384.0f) + t25 * (l1w + l1w2 + l1w4 + fabsf(psum) + eP + e1 + e4 + eO)) * up +
-      1e-18f;
-  const float R = 2.0f * (fabsf(mean) +
-                          kMmaSafe * (cbm * l1w + l1w2 + ws4 * l1w4 + fabsf(psum) + eP + e1 + e4 + eO) + e0 + 1.0f);
-  const bool fin = ballot(!fin_l) == 0 && mean - mean == 0.0f && psum - psum == 0.0f && R - R == 0.0f;
-  if (q == 0 && lane == 0) a.work[0] = 0u;  // k_exact's item count, filled by k_finish
-  if (lane == 0) {
-    s_ex[0] = eP;
-    s_ex[1] = e1;
-    s_ex[2] = e4;
-    s_ex[3] = eO;
-    float* mc = a.consts + (uint64_t)q * kMcCount;
-    mc[kMcS] = s;
-    mc[kMcInvS] = inv_s;
-    mc[kMcMean] = mean;
-    mc[kMcEP] = eP;
-    mc[kMcE1] = e1;
-    mc[kMcE4] = e4;
-    mc[kMcEO] = eO;
-    mc[kMcE0] = e0;
-    mc[kMcR] = R;
-    mc[kMcOk] = fin ? 1.0f : 0.0f;
-    for (int i = kMcOk + 1; i < kMcCount; ++i) mc[i] = 0.0f;
+    for (int h = 1; h < 64; h <<= 1) {
+      l1w += __shfl_xor(l1w, h);
+      l1w2 += __shfl_xor(l1w2, h);
+      l1w4 += __shfl_xor(l1w4, h);
+      mx = fmaxf(mx, __shfl_xor(mx, h));
+      cbm = fmaxf(cbm, __shfl_xor(cbm, h));
+    }
+    const float mean = eden ? p->eden_mean_ip : 0.0f;
+    psum = eden ? 0.0f : p->prefix_sum;
+    const float ws4 = tail ? a.sp.w_s4 : 0.0f;
+    // The f32 sums above run over at most 128 terms: relative error < 2^-17.
+    const float up = 1.0f + 1.0f / 1024.0f;
+    // s: every query-operand value times s stays below 2^14 in magnitude
+    const float bm = fmaxf(mx, fabsf(psum));
+    int ex = 0;
+    if (bm > 0.0f && bm - bm == 0.0f) (void)frexpf(bm, &ex);
+    ex = ex < -100 ? -100 : (ex > 100 ? 100 : ex);
+    s = ldexpf(1.0f, 14 - ex);
+    const float inv_s = ldexpf(1.0f, ex - 14);
+    const float t25 = 2.98023223876953125e-8f;  // 2^-25
+    const float eP = (cbm * l1w * (1.0f / 256.0f) + t25 * (64.0f * cbm + 1.0f) * inv_s) * up;
+    const float e1 = s1on ? (l1w2 * (1.0f / 512.0f) + t25 * 65.0f * inv_s) * up : 0.0f;
+    const float e4 = tail ? (ws4 * l1w4 * (1.0f / 512.0f) + t25 * (32.0f * ws4 + 1.0f) * inv_s) * up : 0.0f;
+    const float eO = eden ? 0.0f : (fabsf(psum) * (1.0f / 512.0f) + t25 * 2.0f * inv_s) * up;
+    const float e0 =
+        (fabsf(mean) * (1.0f / 16384.0f) + t25 * (l1w + l1w2 + l1w4 + fabsf(psum) + eP + e1 + e4 + eO)) * up +
+        1e-18f;
+    const float R = 2.0f * (fabsf(mean) +
+                            kMmaSafe * (cbm * l1w + l1w2 + ws4 * l1w4 + fabsf(psum) + eP + e1 + e4 + eO) + e0 + 1.0f);
+    const bool fin = ballot(!fin_l) == 0 && mean - mean == 0.0f && psum - psum == 0.0f && R - R == 0.0f;
+    if (q == 0 && lane == 0) a.work[0] = 0u;  // k_exact's item count, filled by k_finish
+    if (lane == 0) {
+      s_ex[0] = eP;
+      s_ex[1] = e1;
+      s_ex[2] = e4;
+      s_ex[3] = eO;
+      float* mc = a.consts + (uint64_t)q * kMcCount;
+      mc[kMcS] = s;
+      mc[kMcInvS] = inv_s;
+      mc[kMcMean] = mean;
+      mc[kMcEP] = eP;
+      mc[kMcE1] = e1;
+      mc[kMcE4] = e4;
+      mc[kMcEO] = eO;
+      mc[kMcE0] = e0;
+      mc[kMcR] = R;
+      mc[kMcOk] = fin ? 1.0f : 0.0f;
+      for (int i = kMcOk + 1; i < kMcCount; ++i) mc[i] = 0.0f;
+    }
   }
   __syncthreads();
   if (lane < 2 * kMmaSteps) {
@@ -2441,6 +2453,23 @@ __global__ __launch_bounds__(64) void k_mma_prep(MmaPrepArgs a) {
     a.ops[(uint64_t)q * (2 * kMmaSteps) + lane] =
         make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
   }
+}
+
+__global__ __launch_bounds__(64) void k_mma_prep(MmaPrepArgs a) {
+  __shared__ MmaPrepLds sh;
+  mma_prep_body(a, blockIdx.x, sh);
+}
+
+// The plan of query blockIdx.x (k_plan's work), then its MFMA operands from
+// that plan (k_mma_prep's): one launch where a batch's plan is still to be
+// built.  The plan record and scan constants are written to global memory
+// by this workgroup and read back after its barrier.
+__global__ __launch_bounds__(192) void k_plan_mma_prep(PlanArgs pa, MmaPrepArgs ma) {
+  __shared__ PlanLds<MRL_MAX_DIMS> sh;
+  __shared__ MmaPrepLds sp;
+  plan_body<MRL_MAX_DIMS>(pa, blockIdx.x, sh);
+  __syncthreads();
+  mma_prep_body(ma, blockIdx.x, sp);
 }
 
 // Floors of a sampling stage from its histogram, one wave per query: rank
@@ -3741,6 +3770,13 @@ hipError_t launch_select(const SelectArgs& a, uint32_t n_q, hipStream_t s, const
 hipError_t launch_mma_prep(const MmaPrepArgs& a, hipStream_t s, const LaunchEvents& ev) {
   if (a.n_q == 0) return hipSuccess;
   launch(k_mma_prep, dim3(a.n_q), dim3(64), s, ev, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_plan_mma_prep(const PlanArgs& pa, const MmaPrepArgs& ma, hipStream_t s, const LaunchEvents& ev) {
+  if (ma.n_q == 0) return hipSuccess;
+  if (pa.n_q != ma.n_q) return hipErrorInvalidValue;
+  launch(k_plan_mma_prep, dim3(ma.n_q), dim3(192), s, ev, pa, ma);
   return hipGetLastError();
 }
 

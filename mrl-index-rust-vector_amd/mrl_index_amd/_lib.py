@@ -132,7 +132,7 @@ class KernelTimeC(C.Structure):
 
 
 (KERNEL_PLAN, KERNEL_SCAN, KERNEL_SELECT, KERNEL_THRESH, KERNEL_RERANK, KERNEL_RERANK_SORT, KERNEL_FINISH,
- KERNEL_MMA_PREP, KERNEL_EXACT, KERNEL_BOUNDS, KERNEL_PLAN_SCAN) = 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10
+ KERNEL_MMA_PREP, KERNEL_EXACT, KERNEL_BOUNDS, KERNEL_PLAN_SCAN, KERNEL_PLAN_PREP) = 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11
 
 
 class SynthSpecC(C.Structure):
