@@ -1280,13 +1280,27 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
     if (si && bounded &&
         (rc = enqueue_block_select(ctx, ix, plans, n_q, sel, 0, pb.tau_hi, a.n_pos, a.shift, &a)))
       return rc;
+    // The first stage (no previous floor) counts every pair: it stores the
+    // lower bounds in the MFMA lower-bound area (free until the final pass)
+    // and the floors kernel builds the histograms, instead of contended
+    // global histogram atomics.
+    const uint32_t lb_stride = pb.nseg * pb.seg_cap;
+    const bool store = si == 0 && (uint64_t)stages[si].n_pos * 64u <= lb_stride;
+    a.lbuf = store ? pb.cand_lower : nullptr;
+    a.lbuf_stride = store ? lb_stride : 0u;
     ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)si, stages[si].n_pos, n_q);
     HIP_TRY(launch_scan_mma(a, 0, s, ps.ev()));
     ps.commit(a.n_pos != 0 && n_q != 0);
     ProfScope pt(ctx, MRL_KERNEL_THRESH, (int)si, 0, n_q);
-    HIP_TRY(launch_mma_floors(pb.hist, a.luts, n_q, final_rank(K, stages[si].n_pos, B), K, pb.tau_hi, pb.tau,
-                              si != 0, s, pt.ev()));
+    if (store)
+      HIP_TRY(launch_mma_floors_lb(pb.cand_lower, lb_stride, stages[si].n_pos * 64u, a.luts, n_q,
+                                   final_rank(K, stages[si].n_pos, B), K, pb.tau_hi, pb.tau, s, pt.ev()));
+    else
+      HIP_TRY(launch_mma_floors(pb.hist, a.luts, n_q, final_rank(K, stages[si].n_pos, B), K, pb.tau_hi, pb.tau,
+                                si != 0, s, pt.ev()));
     pt.commit(n_q != 0);
+    a.lbuf = nullptr;
+    a.lbuf_stride = 0u;
   }
   const int final_pass = (int)stages.size();
   const float* floor = rerun_safe ? pb.tau : (sampled ? pb.tau_hi : nullptr);
@@ -1365,8 +1379,10 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
   const bool fuse = plans->pending && n_q == 1 && plans_first == 0 && plans->n_q == 1 && !rerun_safe &&
                     lp.passes.size() > 1 && sp.strata != MRL_STRATA_L0_ONLY && plans->dims <= (uint32_t)kFuseMaxDims &&
                     !mma;
-  // the MFMA path builds a pending plan of the whole batch with the query operands
-  const bool fuse_prep = mma && plans->pending && plans_first == 0 && n_q == plans->n_q;
+  // the MFMA path builds a pending plan of the whole batch with the query
+  // operands (up to one workgroup per CU: larger batches run the plan kernel
+  // and the lighter operand kernel at their own occupancies)
+  const bool fuse_prep = mma && plans->pending && plans_first == 0 && n_q == plans->n_q && n_q <= 256u;
   if (!fuse && !fuse_prep) {
     int rc = flush_plans(ctx, plans);
     if (rc) return rc;

@@ -237,6 +237,12 @@ struct ScanArgs {
   const uint32_t* blist;
   const uint32_t* bcount;
   uint32_t blist_stride;
+  // MFMA sampling pass without a previous floor: instead of counting the
+  // lower bounds in a.hist, store every pair's (-inf for pairs that do not
+  // count) at lbuf[q * lbuf_stride + 64 pos + slot]; k_mma_floors_lb then
+  // builds each query's histogram from them.
+  float* lbuf;
+  uint32_t lbuf_stride;
 };
 
 // Exact finishing of the MFMA path.  k_finish, one workgroup per query: a
@@ -458,6 +464,11 @@ hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const Lau
 // previous stage's value when `prev` is set (those arrays hold it on entry).
 hipError_t launch_mma_floors(uint32_t* hist, const float* luts, uint32_t n_q, uint32_t rank, uint32_t safe_rank,
                              float* floor_out, float* safe_out, bool prev, hipStream_t s, const LaunchEvents& ev = {});
+// The floors of a first sampling stage that stored its lower bounds (n_s per
+// query, rows of lbuf_stride floats) instead of counting them.
+hipError_t launch_mma_floors_lb(const float* lbuf, uint32_t lbuf_stride, uint32_t n_s, const float* luts,
+                                uint32_t n_q, uint32_t rank, uint32_t safe_rank, float* floor_out, float* safe_out,
+                                hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_finish(const FinishArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_exact(const FinishArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
 

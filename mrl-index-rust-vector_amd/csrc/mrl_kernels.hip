@@ -2653,6 +2653,43 @@ __device__ __forceinline__ void mma_wave_flush(ST& st, const ScanArgs& a, const 
   wave_lds_sync();  // the region is read before it is refilled
 }
 
+// Floors of a first sampling stage that stored its lower bounds: the
+// query's histogram is built in LDS from its n_s values (the bins and the
+// values that count are those k_scan_mma's counting form would have added to
+// the global histogram), then the floors at `rank` and the safe rank K.
+__global__ __launch_bounds__(256) void k_mma_floors_lb(const float* lbuf, uint32_t lbuf_stride, uint32_t n_s,
+                                                      const float* luts, uint32_t rank, uint32_t safe_rank,
+                                                      float* floor_out, float* safe_out) {
+  __shared__ __align__(16) uint32_t s_h[kHistBins];
+  const uint32_t q = blockIdx.x, tid = threadIdx.x;
+  const float hinv = luts[(uint64_t)q * kQData + kQdHistInv];
+  const float sc = luts[(uint64_t)q * kQData + kQdHistScale];
+  for (uint32_t i = tid; i < (uint32_t)kHistBins; i += 256u) s_h[i] = 0u;
+  __syncthreads();
+  const float* row = lbuf + (uint64_t)q * lbuf_stride;
+  for (uint32_t i0 = 0; i0 < n_s; i0 += 256u * 8u) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const uint32_t i = i0 + 256u * (uint32_t)u + tid;
+      v[u] = i < n_s ? row[i] : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (v[u] > -INFINITY) atomicAdd(&s_h[hist_bin(v[u], hinv)], 1u);
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const HistRow r = hist_row(s_h);
+    const float f = floor_of(r, rank) * sc;
+    const float sf = floor_of(r, safe_rank) * sc;
+    if (tid == 0) {
+      floor_out[q] = f;
+      safe_out[q] = sf;
+    }
+  }
+}
+
 // One pass of the MFMA-bounded scan.  Workgroup = 8 waves over the same 64
 // queries (blockIdx.y); a wave takes one 32-vector tile (half a block) at a
 // time, items i = first + k * stride with block (i / 2) << shift and half
@@ -2660,11 +2697,14 @@ __device__ __forceinline__ void mma_wave_flush(ST& st, const ScanArgs& a, const 
 // read one K-step ahead of the MFMAs that use them, which keeps the register
 // file small enough for four waves per SIMD.
 // MODE 0: sampling pass, the lower bounds of every active pair go into the
-// query's histogram; 1: final pass, pairs with U >= the floor in a.tau are
-// appended; 2: single pass, every active pair is appended.
+// query's histogram; 3: the same pass storing every pair's lower bound at
+// a.lbuf (-inf where it does not count) for k_mma_floors_lb; 1: final pass,
+// pairs with U >= the floor in a.tau are appended; 2: single pass, every
+// active pair is appended.
 template <int NQT, int MODE>
 __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   constexpr int WPG = kMmaWaves;  // waves per workgroup
+  constexpr bool SAMPLE = MODE == 0 || MODE == 3;  // a sampling pass (lower bounds, no appends)
   using Staging = MmaStaging<WPG, 256>;
   __shared__ __align__(16) uint4 s_qa[NQT][kMmaSteps][64];
   __shared__ uint32_t s_tab[256];
@@ -2729,13 +2769,13 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
       if (MODE != 2) {
         tau = a.tau ? a.tau[q0 + qi] : -INFINITY;
         if (!(tau >= -R)) {
-          all = MODE == 0;
-          tau = MODE == 0 ? 0.0f : -R;  // MODE 1 without a floor: below every score of a vector with safe magnitudes
+          all = SAMPLE;
+          tau = SAMPLE ? 0.0f : -R;  // MODE 1 without a floor: below every score of a vector with safe magnitudes
         }
       }
       if (all) atomicOr(&s_anyall, 1u);
       const float e0q = mc[kMcE0] + fabsf(tau) * (1.0f / 65536.0f);
-      if (ok) C = sc * ((mean - tau) + (MODE == 0 ? -e0q : e0q));
+      if (ok) C = sc * ((mean - tau) + (SAMPLE ? -e0q : e0q));
       qk[0] = tau;
       qk[1] = mc[kMcInvS];
       qk[2] = mc[kMcEP];
@@ -2748,7 +2788,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
     s_c[qi] = C;
 #pragma unroll
     for (int i = 0; i < 8; ++i) s_qk[qi][i] = qk[i];
-    s_hinv[qi] = (MODE == 0 && qi < nq) ? a.luts[(uint64_t)(q0 + qi) * kQData + kQdHistInv] : 1.0f;
+    s_hinv[qi] = (SAMPLE && qi < nq) ? a.luts[(uint64_t)(q0 + qi) * kQData + kQdHistInv] : 1.0f;
   }
   // Query operands, element e: tile t, K-step st, lane ln -> query
   // q0 + 32 t + ln % 32, K-half ln / 32.  Every thread's loads go out first (from a clamped query
@@ -2768,7 +2808,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
     if (e < kQaN) {
       const int t = e / (kMmaSteps * 64), st = (e / 64) % kMmaSteps, ln = e & 63;
       uint4 v = 32 * t + (ln & 31) < nq ? qav[k] : make_uint4(0u, 0u, 0u, 0u);
-      if (MODE == 0 && (ln >> 5) == 0 && st == kMmaSteps - 1) {  // the sampling pass subtracts the error columns
+      if (SAMPLE && (ln >> 5) == 0 && st == kMmaSteps - 1) {  // the sampling pass subtracts the error columns
         v.x ^= 0x80008000u;
         v.y ^= 0x80008000u;
       }
@@ -2785,7 +2825,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   // bit 16 t + r: register r of tile t belongs to a query of the batch with
   // usable operands (read only on the rare paths that force candidates)
   uint32_t okbits = 0u;
-  if constexpr (MODE != 0) {
+  if constexpr (!SAMPLE) {
 #pragma unroll
     for (int t = 0; t < NQT; ++t)
 #pragma unroll
@@ -2811,6 +2851,17 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
       if (a.sp.has_hi && min_ts > a.sp.hi) skip = true;
     }
     const uint32_t active = (uint32_t)(~tomb >> (32u * h));  // this tile's slots
+    if (MODE == 3 && (skip || active == 0)) {
+      // a skipped tile stores no lower bounds that count
+      float* lrow = a.lbuf + (uint64_t)(q0 + 4u * kh) * a.lbuf_stride + 32u * it_cur + vl;
+#pragma unroll
+      for (int t = 0; t < NQT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
+          if (qi < nq) lrow[(uint64_t)(32 * t + 8 * (r >> 2) + (r & 3)) * a.lbuf_stride] = -INFINITY;
+        }
+    }
     if (!skip && active != 0) {
       if (h == 0) {
         c_blocks += (uint32_t)nq;
@@ -2897,7 +2948,23 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
           acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ac[t]), as_h8(bo), acc[t], 0, 0, 0);
       }
       // Register r of tile t holds query 32 t + 8 (r / 4) + 4 kh + r % 4.
-      if constexpr (MODE == 0) {
+      if constexpr (MODE == 3) {
+        // store every pair's lower bound (sample 32 it + lane % 32 of the query)
+        const bool cnt = act && safe;
+        float* lrow = a.lbuf + (uint64_t)(q0 + 4u * kh) * a.lbuf_stride + 32u * it_cur + vl;
+#pragma unroll
+        for (int t = 0; t < NQT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
+            if (qi >= nq) continue;
+            const float2 k = *reinterpret_cast<const float2*>(&s_qk[qi][0]);  // tau, 1/s
+            float L = k.x + acc[t][r] * k.y;
+            L = L - (fabsf(L) + fabsf(k.x)) * (1.0f / 4194304.0f);
+            if (!cnt || s_qk[qi][7] == 0.0f || !(acc[t][r] >= 0.0f || s_anyall != 0u)) L = -INFINITY;
+            lrow[(uint64_t)(32 * t + 8 * (r >> 2) + (r & 3)) * a.lbuf_stride] = L;
+          }
+      } else if constexpr (MODE == 0) {
         // Tile value = s (L - tau): the pairs at or above the previous floor
         // pass a compare; without one (some query counts all) every pair of
         // a present query is counted.  L = tau + value / s, less a margin
@@ -2972,7 +3039,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
     atomicAdd(&s_stats[kStatActive], c_active);
     atomicAdd(&s_stats[kStatPrefix], c_app);
   }
-  if constexpr (MODE != 0) {
+  if constexpr (!SAMPLE) {
     if (lane == 0) s_st.n[wave] = min(fill, (uint32_t)Staging::kCap);
     __syncthreads();
     for (int w = 0; w < WPG; ++w)
@@ -3797,7 +3864,10 @@ hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const Lau
   if (a.n_pos == 0 || a.n_q == 0) return hipSuccess;
   const dim3 g(mma_scan_grid(a), (a.n_q + kMmaQ - 1) / kMmaQ), b(kMmaWaves * 64);
   const bool two = a.n_q > 32;  // one 32-query tile per wave suffices up to 32 queries
-  if (mode == 0) {
+  if (mode == 0 && a.lbuf) {
+    if (two) launch(k_scan_mma<2, 3>, g, b, s, ev, a);
+    else launch(k_scan_mma<1, 3>, g, b, s, ev, a);
+  } else if (mode == 0) {
     if (two) launch(k_scan_mma<2, 0>, g, b, s, ev, a);
     else launch(k_scan_mma<1, 0>, g, b, s, ev, a);
   } else if (mode == 1) {
@@ -3807,6 +3877,16 @@ hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const Lau
     if (two) launch(k_scan_mma<2, 2>, g, b, s, ev, a);
     else launch(k_scan_mma<1, 2>, g, b, s, ev, a);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_mma_floors_lb(const float* lbuf, uint32_t lbuf_stride, uint32_t n_s, const float* luts,
+                                uint32_t n_q, uint32_t rank, uint32_t safe_rank, float* floor_out, float* safe_out,
+                                hipStream_t s, const LaunchEvents& ev) {
+  if (n_q == 0) return hipSuccess;
+  if (n_s > lbuf_stride) return hipErrorInvalidValue;
+  launch(k_mma_floors_lb, dim3(n_q), dim3(256), s, ev, lbuf, lbuf_stride, n_s, luts, rank, safe_rank, floor_out,
+         safe_out);
   return hipGetLastError();
 }
 
