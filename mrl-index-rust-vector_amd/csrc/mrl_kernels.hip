@@ -2311,11 +2311,21 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
 // +-mid_n / 2 and +-hn w_s4 / 2 from the sign of each S1 / S4 bit, and a last
 // step of error columns.  The accumulator starts at C = s (mean_ip - tau + e0).
 //   E(v, q) = |scale| eP + mid_n e1 + hn e4 + |offset| eO + e0
-// bounds |tile value / s - (reference's f32 score - tau)|: the f16 rounding of
-// both operands (2^-11 relative, 2^-25 absolute below the normal range), the
-// MFMA's f32 accumulation (measured below 2^-21 of the summed magnitudes) and
-// the reference's own f32 rounding (< 300 ulp of the summed magnitudes), each
-// covered two times or more.  With the error columns added the tile holds
+// bounds |tile value / s - (reference's f32 score - tau)|.  With u = 2^-11
+// (f16 rounding, relative; 2^-25 absolute below the normal range, covered by
+// the t25 terms and e0) and M the summed magnitudes of a part's products:
+//  - prefix: a query weight rounded once, scale * cb rounded twice (cb, then
+//    the packed product): <= (3u + 3u^2 + u^3) M, M <= |scale| cbm l1w;
+//  - S1 / S4 / offset * prefix_sum: two roundings (one for the offset):
+//    <= (2u + u^2) M, M = mid_n l1w2 / 2, hn w_s4 l1w4 / 2, |offset psum|;
+//  - the MFMA's f32 accumulation of the 272 products and the start value C,
+//    in any order: <= 271 * 2^-24 < 2^-15 of all the magnitudes;
+//  - the reference's own sequential f32 sums (at most 129 terms each):
+//    < 2^-16 of their magnitudes.
+// eP = cbm l1w / 600 (needs 1 / 661), e1 = l1w2 / 1800 (needs 1 / 1957),
+// e4 = w_s4 l1w4 / 1800, eO = |psum| / 1700 (needs 1 / 1872), each times
+// 1 + 2^-10 for its own f32 evaluation; C's share is in e0 (|mean_ip| /
+// 16384, |tau| / 16384).  With the error columns added the tile holds
 // s (U - tau), U = approximation + E >= score; the sampling pass subtracts
 // them and gets s L, L = approximation - E <= score.  Under the settings
 // tight_coef() accepts, the reference's top K is the top K by full score, so
@@ -2406,10 +2416,10 @@ __device__ __forceinline__ void mma_prep_body(const MmaPrepArgs& a, uint32_t q, 
     s = ldexpf(1.0f, 14 - ex);
     const float inv_s = ldexpf(1.0f, ex - 14);
     const float t25 = 2.98023223876953125e-8f;  // 2^-25
-    const float eP = (cbm * l1w * (1.0f / 256.0f) + t25 * (64.0f * cbm + 1.0f) * inv_s) * up;
-    const float e1 = s1on ? (l1w2 * (1.0f / 512.0f) + t25 * 65.0f * inv_s) * up : 0.0f;
-    const float e4 = tail ? (ws4 * l1w4 * (1.0f / 512.0f) + t25 * (32.0f * ws4 + 1.0f) * inv_s) * up : 0.0f;
-    const float eO = eden ? 0.0f : (fabsf(psum) * (1.0f / 512.0f) + t25 * 2.0f * inv_s) * up;
+    const float eP = (cbm * l1w * (1.0f / 600.0f) + t25 * (64.0f * cbm + 1.0f) * inv_s) * up;
+    const float e1 = s1on ? (l1w2 * (1.0f / 1800.0f) + t25 * 65.0f * inv_s) * up : 0.0f;
+    const float e4 = tail ? (ws4 * l1w4 * (1.0f / 1800.0f) + t25 * (32.0f * ws4 + 1.0f) * inv_s) * up : 0.0f;
+    const float eO = eden ? 0.0f : (fabsf(psum) * (1.0f / 1700.0f) + t25 * 2.0f * inv_s) * up;
     const float e0 =
         (fabsf(mean) * (1.0f / 16384.0f) + t25 * (l1w + l1w2 + l1w4 + fabsf(psum) + eP + e1 + e4 + eO)) * up +
         1e-18f;
@@ -2774,7 +2784,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
         }
       }
       if (all) atomicOr(&s_anyall, 1u);
-      const float e0q = mc[kMcE0] + fabsf(tau) * (1.0f / 65536.0f);
+      const float e0q = mc[kMcE0] + fabsf(tau) * (1.0f / 16384.0f);
       if (ok) C = sc * ((mean - tau) + (SAMPLE ? -e0q : e0q));
       qk[0] = tau;
       qk[1] = mc[kMcInvS];
