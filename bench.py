@@ -150,7 +150,7 @@ def roofline_of(groups, nq, prof_steps, w, cold=False, scanned=None):
     ScanStats.blocks counter), which a cluster-grouped index's block lists make
     fewer than blocks x queries; by default every block for every query."""
     import numpy as np
-    mma = any(kind == "mma_prep" for kind, _ in groups)
+    mma = any(kind in ("mma_prep", "plan+mma_prep") for kind, _ in groups)
     src = {}
     if not mma:
         # One-query path: the dominant kernel is k_scan (every pass launches
