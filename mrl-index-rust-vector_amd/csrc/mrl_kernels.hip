@@ -2319,11 +2319,12 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
 //  - S1 / S4 / offset * prefix_sum: two roundings (one for the offset):
 //    <= (2u + u^2) M, M = mid_n l1w2 / 2, hn w_s4 l1w4 / 2, |offset psum|;
 //  - the MFMA's f32 accumulation of the 272 products and the start value C,
-//    in any order: <= 271 * 2^-24 < 2^-15 of all the magnitudes;
-//  - the reference's own sequential f32 sums (at most 129 terms each):
-//    < 2^-16 of their magnitudes.
-// eP = cbm l1w / 600 (needs 1 / 661), e1 = l1w2 / 1800 (needs 1 / 1957),
-// e4 = w_s4 l1w4 / 1800, eO = |psum| / 1700 (needs 1 / 1872), each times
+//    in any order, each addition rounding to nearest or truncating:
+//    <= gamma_273 ~ 2^-14.9 of all the magnitudes;
+//  - the reference's own sequential f32 sums (at most 128 terms each):
+//    <= gamma_128 ~ 2^-17 of their magnitudes.
+// eP = cbm l1w / 600 (needs 1 / 664), e1 = l1w2 / 1800 (needs 1 / 1966),
+// e4 = w_s4 l1w4 / 1800, eO = |psum| / 1700 (needs 1 / 1892), each times
 // 1 + 2^-10 for its own f32 evaluation; C's share is in e0 (|mean_ip| /
 // 16384, |tau| / 16384).  With the error columns added the tile holds
 // s (U - tau), U = approximation + E >= score; the sampling pass subtracts
