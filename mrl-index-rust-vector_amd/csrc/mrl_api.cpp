@@ -1098,6 +1098,9 @@ static bool mma_ok(const mrl_plans* plans, uint32_t n_q, const ScanParams& sp, c
 // final_rank of a much larger sample) is much tighter.  (Every 16th block
 // gave a slightly tighter floor, but that stage cost more than the final
 // pass saved on the 1M..8.8M-vector benchmark indexes.)
+// Per-workgroup list room below which a later sampling stage counts into the
+// global histogram instead.
+static const uint32_t kMinListCap = 16;
 struct MmaStage {
   uint32_t shift;
   uint32_t n_pos;
@@ -1284,10 +1287,22 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
     // lower bounds in the MFMA lower-bound area (free until the final pass)
     // and the floors kernel builds the histograms, instead of contended
     // global histogram atomics.
+    // A later stage over block lists (counting only the bounds at or above
+    // the previous floor, which on a cluster-grouped index concentrates them
+    // on a few histogram bins) lists them per workgroup in the same area, the
+    // list lengths in the candidate-row area (also free until the final
+    // pass), when every workgroup's list gets kMinListCap entries or more.
+    // (Without block lists the global histogram atomics cost no more than
+    // the lists: 1M..8.8M-vector benchmark indexes, batches 64..1024.)
     const uint32_t lb_stride = pb.nseg * pb.seg_cap;
     const bool store = si == 0 && (uint64_t)stages[si].n_pos * 64u <= lb_stride;
-    a.lbuf = store ? pb.cand_lower : nullptr;
-    a.lbuf_stride = store ? lb_stride : 0u;
+    const uint32_t n_wg = mma_scan_grid(a);
+    const uint32_t lcap = n_wg ? lb_stride / n_wg : 0u;
+    const bool lists = si != 0 && a.blist && lcap >= kMinListCap && n_wg <= (uint32_t)kMaxListWg;
+    a.lbuf = store || lists ? pb.cand_lower : nullptr;
+    a.lbuf_stride = store || lists ? lb_stride : 0u;
+    a.lcount = lists ? pb.cand_row : nullptr;
+    a.lcap = lists ? lcap : 0u;
     ProfScope ps(ctx, MRL_KERNEL_SCAN, (int)si, stages[si].n_pos, n_q);
     HIP_TRY(launch_scan_mma(a, 0, s, ps.ev()));
     ps.commit(a.n_pos != 0 && n_q != 0);
@@ -1295,12 +1310,17 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
     if (store)
       HIP_TRY(launch_mma_floors_lb(pb.cand_lower, lb_stride, stages[si].n_pos * 64u, a.luts, n_q,
                                    final_rank(K, stages[si].n_pos, B), K, pb.tau_hi, pb.tau, s, pt.ev()));
+    else if (lists)
+      HIP_TRY(launch_mma_floors_seg(pb.cand_lower, pb.cand_row, lb_stride, n_wg, lcap, pb.hist, a.luts, n_q,
+                                    final_rank(K, stages[si].n_pos, B), K, pb.tau_hi, pb.tau, s, pt.ev()));
     else
       HIP_TRY(launch_mma_floors(pb.hist, a.luts, n_q, final_rank(K, stages[si].n_pos, B), K, pb.tau_hi, pb.tau,
                                 si != 0, s, pt.ev()));
     pt.commit(n_q != 0);
     a.lbuf = nullptr;
     a.lbuf_stride = 0u;
+    a.lcount = nullptr;
+    a.lcap = 0u;
   }
   const int final_pass = (int)stages.size();
   const float* floor = rerun_safe ? pb.tau : (sampled ? pb.tau_hi : nullptr);

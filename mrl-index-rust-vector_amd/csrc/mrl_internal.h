@@ -243,7 +243,15 @@ struct ScanArgs {
   // builds each query's histogram from them.
   float* lbuf;
   uint32_t lbuf_stride;
+  // MFMA sampling pass with a previous floor, when lcount is set: workgroup
+  // w lists the lower bounds that count for query q at
+  // lbuf[q * lbuf_stride + w * lcap + i], i < lcount[q * lbuf_stride + w]
+  // (past lcap entries they go to a.hist); k_mma_floors_seg builds each
+  // query's histogram from the lists and a.hist.
+  uint32_t* lcount;
+  uint32_t lcap;
 };
+constexpr int kMaxListWg = 1024;  // workgroup lists per query a later sampling stage may keep
 
 // Exact finishing of the MFMA path.  k_finish, one workgroup per query: a
 // key at or below the K-th best lower bound among the query's candidates, and
@@ -469,6 +477,14 @@ hipError_t launch_mma_floors(uint32_t* hist, const float* luts, uint32_t n_q, ui
 hipError_t launch_mma_floors_lb(const float* lbuf, uint32_t lbuf_stride, uint32_t n_s, const float* luts,
                                 uint32_t n_q, uint32_t rank, uint32_t safe_rank, float* floor_out, float* safe_out,
                                 hipStream_t s, const LaunchEvents& ev = {});
+// Floors of a later sampling stage that listed its counted lower bounds per
+// workgroup (ScanArgs::lcount): the query's histogram from its n_wg lists
+// and the global histogram (left zeroed), floors at rank and safe_rank, each
+// at least the previous stage's.
+hipError_t launch_mma_floors_seg(const float* lbuf, const uint32_t* lcount, uint32_t lbuf_stride, uint32_t n_wg,
+                                 uint32_t lcap, uint32_t* hist, const float* luts, uint32_t n_q, uint32_t rank,
+                                 uint32_t safe_rank, float* floor_out, float* safe_out, hipStream_t s,
+                                 const LaunchEvents& ev = {});
 hipError_t launch_finish(const FinishArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
 hipError_t launch_exact(const FinishArgs& a, uint32_t n_q, hipStream_t s, const LaunchEvents& ev = {});
 

@@ -2701,6 +2701,77 @@ __global__ __launch_bounds__(256) void k_mma_floors_lb(const float* lbuf, uint32
   }
 }
 
+// Floors of a later sampling stage that listed its counted lower bounds:
+// the query's histogram is built in LDS from the global row (the bounds past
+// a list's room; the row is then cleared) and the n_wg workgroup lists, then
+// the floors at `rank` and the safe rank K, each at least the previous
+// stage's (floor_out / safe_out hold it on entry).  The lists' lengths are
+// scanned into offsets, so the threads take the entries of all lists
+// together, kSegUnroll loads in flight per thread (entry e: the list whose
+// offsets bracket it, by binary search in LDS).
+constexpr int kSegThreads = 1024, kSegUnroll = 8;
+__global__ __launch_bounds__(kSegThreads) void k_mma_floors_seg(const float* lbuf, const uint32_t* lcount,
+                                                               uint32_t lbuf_stride, uint32_t n_wg, uint32_t lcap,
+                                                               uint32_t* hist, const float* luts, uint32_t rank,
+                                                               uint32_t safe_rank, float* floor_out,
+                                                               float* safe_out) {
+  static_assert(kMaxListWg == kSegThreads, "one list length per thread");
+  __shared__ __align__(16) uint32_t s_h[kHistBins];
+  __shared__ uint32_t s_off[2][kMaxListWg + 1];
+  const uint32_t q = blockIdx.x, tid = threadIdx.x;
+  const float hinv = luts[(uint64_t)q * kQData + kQdHistInv];
+  const float sc = luts[(uint64_t)q * kQData + kQdHistScale];
+  uint32_t* g = hist + (uint64_t)q * kHistBins;
+  const float* row = lbuf + (uint64_t)q * lbuf_stride;
+  const uint32_t len = tid < n_wg ? min(lcount[(uint64_t)q * lbuf_stride + tid], lcap) : 0u;
+  for (uint32_t i = tid; i < (uint32_t)kHistBins; i += kSegThreads) {
+    s_h[i] = g[i];
+    g[i] = 0u;
+  }
+  // inclusive scan of the lengths at offsets 1.. (Hillis-Steele)
+  s_off[0][tid + 1] = len;
+  if (tid == 0) s_off[0][0] = s_off[1][0] = 0u;
+  __syncthreads();
+  int cur = 0;
+  for (uint32_t d = 1; d < (uint32_t)kMaxListWg; d <<= 1) {
+    s_off[cur ^ 1][tid + 1] = s_off[cur][tid + 1] + (tid >= d ? s_off[cur][tid + 1 - d] : 0u);
+    cur ^= 1;
+    __syncthreads();
+  }
+  const uint32_t* off = s_off[cur];  // off[w] = entries of lists before w
+  const uint32_t total = off[n_wg];
+  for (uint32_t e0 = 0; e0 < total; e0 += kSegThreads * kSegUnroll) {
+    float v[kSegUnroll];
+#pragma unroll
+    for (int u = 0; u < kSegUnroll; ++u) {
+      const uint32_t e = e0 + kSegThreads * (uint32_t)u + tid;
+      v[u] = -INFINITY;
+      if (e < total) {
+        uint32_t lo = 0, hi = n_wg;  // the last w with off[w] <= e
+        while (hi - lo > 1u) {
+          const uint32_t mid = (lo + hi) >> 1;
+          if (off[mid] <= e) lo = mid;
+          else hi = mid;
+        }
+        v[u] = row[(uint64_t)lo * lcap + (e - off[lo])];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSegUnroll; ++u)
+      if (v[u] > -INFINITY) atomicAdd(&s_h[hist_bin(v[u], hinv)], 1u);
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const HistRow r = hist_row(s_h);
+    const float f = floor_of(r, rank) * sc;
+    const float sf = floor_of(r, safe_rank) * sc;
+    if (tid == 0) {
+      floor_out[q] = fmaxf(f, floor_out[q]);
+      safe_out[q] = fmaxf(sf, safe_out[q]);
+    }
+  }
+}
+
 // One pass of the MFMA-bounded scan.  Workgroup = 8 waves over the same 64
 // queries (blockIdx.y); a wave takes one 32-vector tile (half a block) at a
 // time, items i = first + k * stride with block (i / 2) << shift and half
@@ -2709,13 +2780,15 @@ __global__ __launch_bounds__(256) void k_mma_floors_lb(const float* lbuf, uint32
 // file small enough for four waves per SIMD.
 // MODE 0: sampling pass, the lower bounds of every active pair go into the
 // query's histogram; 3: the same pass storing every pair's lower bound at
-// a.lbuf (-inf where it does not count) for k_mma_floors_lb; 1: final pass,
+// a.lbuf (-inf where it does not count) for k_mma_floors_lb; 4: the
+// sampling pass listing the counted lower bounds per workgroup (a.lcount)
+// for k_mma_floors_seg; 1: final pass,
 // pairs with U >= the floor in a.tau are appended; 2: single pass, every
 // active pair is appended.
 template <int NQT, int MODE>
 __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   constexpr int WPG = kMmaWaves;  // waves per workgroup
-  constexpr bool SAMPLE = MODE == 0 || MODE == 3;  // a sampling pass (lower bounds, no appends)
+  constexpr bool SAMPLE = MODE == 0 || MODE == 3 || MODE == 4;  // a sampling pass (lower bounds, no appends)
   using Staging = MmaStaging<WPG, 256>;
   __shared__ __align__(16) uint4 s_qa[NQT][kMmaSteps][64];
   __shared__ uint32_t s_tab[256];
@@ -2975,6 +3048,41 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
             if (!cnt || s_qk[qi][7] == 0.0f || !(acc[t][r] >= 0.0f || s_anyall != 0u)) L = -INFINITY;
             lrow[(uint64_t)(32 * t + 8 * (r >> 2) + (r & 3)) * a.lbuf_stride] = L;
           }
+      } else if constexpr (MODE == 4) {
+        // As MODE 0, but a counted lower bound joins this workgroup's list
+        // for its query: one LDS reservation per half-wave (the two halves
+        // hold different queries), then a plain store; past the list's room
+        // it is counted in the global histogram instead.
+        const uint64_t cm = ballot(act && safe);
+        const bool all = s_anyall != 0u;
+#pragma unroll
+        for (int t = 0; t < NQT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            uint64_t pm = (all ? ~0ull : ballot(acc[t][r] >= 0.0f)) & cm;
+            if (pm == 0) continue;
+            const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
+            pm &= ballot(qi < nq && s_qk[qi][7] != 0.0f);
+            if (pm == 0) continue;
+            const uint32_t n_lo = (uint32_t)__popcll(pm & 0xffffffffull), n_hi = (uint32_t)__popcll(pm >> 32);
+            uint32_t qq = (uint32_t)qi;  // through an empty asm: no hoisted per-register addresses
+            asm volatile("" : "+v"(qq));
+            uint32_t base = 0u;
+            if ((lane == 0u && n_lo != 0u) || (lane == 32u && n_hi != 0u))
+              base = atomicAdd(&s_st.cnt[qq], kh ? n_hi : n_lo);
+            const uint32_t b_lo = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
+            const uint32_t b_hi = (uint32_t)__builtin_amdgcn_readlane((int)base, 32);
+            if (!((pm >> lane) & 1ull)) continue;
+            const uint32_t slot = (kh ? b_hi - n_lo : b_lo) + lanes_below(pm);
+            const float2 k = *reinterpret_cast<const float2*>(&s_qk[qq][0]);  // tau, 1/s
+            float L = k.x + acc[t][r] * k.y;
+            L = L - (fabsf(L) + fabsf(k.x)) * (1.0f / 4194304.0f);
+            const uint32_t q = q0 + qq;
+            if (slot < a.lcap)
+              a.lbuf[(uint64_t)q * a.lbuf_stride + blockIdx.x * a.lcap + slot] = L;
+            else
+              atomicAdd(a.hist + (uint64_t)q * kHistBins + hist_bin(L, s_hinv[qq]), 1u);
+          }
       } else if constexpr (MODE == 0) {
         // Tile value = s (L - tau): the pairs at or above the previous floor
         // pass a compare; without one (some query counts all) every pair of
@@ -3049,6 +3157,10 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
     atomicAdd(&s_stats[kStatBlocks], c_blocks);
     atomicAdd(&s_stats[kStatActive], c_active);
     atomicAdd(&s_stats[kStatPrefix], c_app);
+  }
+  if constexpr (MODE == 4) {  // the length of each query's list
+    __syncthreads();
+    if (tid < nq) a.lcount[(uint64_t)(q0 + tid) * a.lbuf_stride + blockIdx.x] = min(s_st.cnt[tid], a.lcap);
   }
   if constexpr (!SAMPLE) {
     if (lane == 0) s_st.n[wave] = min(fill, (uint32_t)Staging::kCap);
@@ -3875,7 +3987,12 @@ hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const Lau
   if (a.n_pos == 0 || a.n_q == 0) return hipSuccess;
   const dim3 g(mma_scan_grid(a), (a.n_q + kMmaQ - 1) / kMmaQ), b(kMmaWaves * 64);
   const bool two = a.n_q > 32;  // one 32-query tile per wave suffices up to 32 queries
-  if (mode == 0 && a.lbuf) {
+  if (mode == 0 && a.lbuf && a.lcount) {
+    // every workgroup's list fits in its query's row
+    if ((uint64_t)g.x * a.lcap > a.lbuf_stride || a.lcap == 0) return hipErrorInvalidValue;
+    if (two) launch(k_scan_mma<2, 4>, g, b, s, ev, a);
+    else launch(k_scan_mma<1, 4>, g, b, s, ev, a);
+  } else if (mode == 0 && a.lbuf) {
     if (two) launch(k_scan_mma<2, 3>, g, b, s, ev, a);
     else launch(k_scan_mma<1, 3>, g, b, s, ev, a);
   } else if (mode == 0) {
@@ -3898,6 +4015,18 @@ hipError_t launch_mma_floors_lb(const float* lbuf, uint32_t lbuf_stride, uint32_
   if (n_s > lbuf_stride) return hipErrorInvalidValue;
   launch(k_mma_floors_lb, dim3(n_q), dim3(256), s, ev, lbuf, lbuf_stride, n_s, luts, rank, safe_rank, floor_out,
          safe_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_mma_floors_seg(const float* lbuf, const uint32_t* lcount, uint32_t lbuf_stride, uint32_t n_wg,
+                                 uint32_t lcap, uint32_t* hist, const float* luts, uint32_t n_q, uint32_t rank,
+                                 uint32_t safe_rank, float* floor_out, float* safe_out, hipStream_t s,
+                                 const LaunchEvents& ev) {
+  if (n_q == 0) return hipSuccess;
+  if ((uint64_t)n_wg * lcap > lbuf_stride || n_wg > lbuf_stride || n_wg > (uint32_t)kMaxListWg)
+    return hipErrorInvalidValue;
+  launch(k_mma_floors_seg, dim3(n_q), dim3(kSegThreads), s, ev, lbuf, lcount, lbuf_stride, n_wg, lcap, hist, luts,
+         rank, safe_rank, floor_out, safe_out);
   return hipGetLastError();
 }
 

@@ -162,3 +162,31 @@ def test_cluster_grouped_scan_tile_kernel_contract(device, eden_index):
         rid, rsc = fixed_floor_topk(blocks, op, ora.scan_config(48, alpha=0.9), floors[qi], 48)
         n = int(out.counts[qi])
         assert_topk_equal(out.ids[qi, :n], out.scores[qi, :n], rid, rsc, 48, f"tile q={qi}")
+
+
+def test_cluster_grouped_mma_two_stage_lists(device):
+    """An index of more than 2048 blocks at 64 queries: the MFMA path's
+    second sampling stage runs over block lists and lists its counted lower
+    bounds per workgroup (k_mma_floors_seg); queries near 5 of the 40
+    clusters (each spans a few of the stage's every-32nd blocks, so its
+    floor comes from the query's own cluster), top K equal to the oracle's,
+    blocks skipped."""
+    rows, cl = clustered_rows(57, 40, 4400, 768)
+    fit = oracle_fit(rows[:8192])
+    pf = m.EdenFit(64, 4, 1, fit.mean, 8192)
+    blocks = m.encode_corpus_clustered(rows, cl, 8, pf)
+    nb = blocks.shape[0]
+    assert nb > 2048, nb
+    ix = m.DeviceIndex.upload(blocks, device)
+    rng = np.random.default_rng(58)
+    nq, k = 64, 128
+    near = np.nonzero(cl < 5)[0]
+    qs = rows[rng.choice(near, nq)] + np.float32(0.1 / np.sqrt(768)) * rng.standard_normal(
+        (nq, 768)).astype(np.float32)
+    plan = m.QueryPlan.from_query_eden(qs, 768, pf, device)
+    res = _scan_vs_oracle(device, blocks, ix, qs, plan,
+                          lambda q: ora.plan_build(q, 768, ora.PREFIX_EDEN_PROD, ora.MID_RABITQ, fit),
+                          m.ScanConfig(shortlist_cand=k), ora.scan_config(k), k, "two-stage lists")
+    assert res.stats.blocks < 0.5 * nb * nq, (res.stats.blocks, nb * nq)
+    assert res.stats.reruns_dense == 0
+    ix.close()
