@@ -1092,12 +1092,16 @@ static bool mma_ok(const mrl_plans* plans, uint32_t n_q, const ScanParams& sp, c
 
 // Sampling stages of the MFMA path: blocks b = pos << shift, pos < n_pos.
 // Above 256 blocks a first stage scores 16..128 blocks (fewer for larger
-// batches); when that is at most 1/64 of the index, a second stage scores
-// every 32nd block but counts only lower bounds at or above the first
-// stage's floor, so its histogram stays small while its floor (rank
-// final_rank of a much larger sample) is much tighter.  (Every 16th block
-// gave a slightly tighter floor, but that stage cost more than the final
-// pass saved on the 1M..8.8M-vector benchmark indexes.)
+// batches); when that is at most 1/128 of the index, a second stage scores
+// every 64th block (every 32nd when the index has fewer than 32 K blocks, or
+// the first stage is at most 1/64 of it) but counts only lower bounds at or
+// above the first stage's floor, so its histogram stays small while its
+// floor (rank final_rank of a much larger sample) is much tighter.  A
+// sparser second stage costs less but leaves a looser floor, so more pairs
+// are appended in the final pass; on the benchmark indexes every 64th block
+// paid when the index holds 32 K blocks or more (8.8M vectors, K 256:
+// 0.418 -> 0.413 ms per step; 1M, K 256: -1.5 us) and lost below
+// (1M, K 1024: +5 us), and every 16th block cost more than it saved.
 // Per-workgroup list room below which a later sampling stage counts into the
 // global histogram instead.
 static const uint32_t kMinListCap = 16;
@@ -1105,7 +1109,7 @@ struct MmaStage {
   uint32_t shift;
   uint32_t n_pos;
 };
-static std::vector<MmaStage> mma_stages(uint64_t B, uint32_t n_q) {
+static std::vector<MmaStage> mma_stages(uint64_t B, uint32_t n_q, uint32_t K) {
   std::vector<MmaStage> st;
   if (B <= 256) return st;
   // the first stage counts every pair: keep it near 4096 x 64 block-queries
@@ -1113,7 +1117,9 @@ static std::vector<MmaStage> mma_stages(uint64_t B, uint32_t n_q) {
   uint32_t s1 = 0;
   while (((B + (1ull << s1) - 1) >> s1) > cap) ++s1;
   st.push_back(MmaStage{s1, (uint32_t)((B + (1ull << s1) - 1) >> s1)});
-  if (s1 >= 6) st.push_back(MmaStage{5u, (uint32_t)((B + 31) >> 5)});  // >= 2x the first stage's blocks
+  // the second stage holds at least twice the first stage's blocks
+  const uint32_t s2 = B >= 32ull * K && s1 >= 7 ? 6u : 5u;
+  if (s1 >= s2 + 1) st.push_back(MmaStage{s2, (uint32_t)((B + (1ull << s2) - 1) >> s2)});
   return st;
 }
 
@@ -1225,7 +1231,7 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
                             bool rerun_safe, bool fuse_prep = false) {
   hipStream_t s = ctx->stream;
   const uint64_t B = ix->n_blocks;
-  const std::vector<MmaStage> stages = rerun_safe ? std::vector<MmaStage>() : mma_stages(B, n_q);
+  const std::vector<MmaStage> stages = rerun_safe ? std::vector<MmaStage>() : mma_stages(B, n_q, K);
   const bool sampled = !stages.empty();
   {
     MmaPrepArgs pa{};
@@ -1553,7 +1559,7 @@ extern "C" int mrl_scan_async(mrl_ctx* ctx, const mrl_index* index, const mrl_pl
   LevelPlan* lp;
   if ((rc = get_levels(ix, K, &lp))) return rc;
   const PassBuffers pb = results_buffers(res);
-  const bool sampled = mma_ok(plans, plans->n_q, sp, pb) ? !mma_stages(ix->n_blocks, plans->n_q).empty()
+  const bool sampled = mma_ok(plans, plans->n_q, sp, pb) ? !mma_stages(ix->n_blocks, plans->n_q, K).empty()
                                                          : lp->passes.size() > 1;
   res->floor_kind.assign(plans->n_q, sampled ? 1 : 0);
   return enqueue_scan(ctx, ix, plans, 0, plans->n_q, sp, K, *lp, pb, res->d_stats);
@@ -1966,7 +1972,7 @@ extern "C" int mrl_scan_noalloc(mrl_ctx* ctx, const mrl_index* index, const mrl_
   LevelPlan* lp;
   if ((rc = get_levels(ix, K, &lp))) return rc;
   const bool sampled =
-      mma_ok(plans, n_q, sp, pb) ? !mma_stages(ix->n_blocks, n_q).empty() : lp->passes.size() > 1;
+      mma_ok(plans, n_q, sp, pb) ? !mma_stages(ix->n_blocks, n_q, K).empty() : lp->passes.size() > 1;
   if ((rc = enqueue_scan(ctx, ix, plans, 0, n_q, sp, K, *lp, pb, nullptr))) return rc;
   // without a sampling pass no query can be flagged
   if (sampled && (rc = enqueue_gated_rerun(ctx, ix, plans, n_q, sp, K, pb))) return rc;
