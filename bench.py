@@ -7,8 +7,10 @@ selection, all enqueued on the library's stream with the index already in
 HBM.  The default run measures the two workloads BASELINE's metric is quoted
 on: the headline is configs[3] (8.8M x 768 clustered, batch 64, K_cand 256,
 the north-star target); configs[1] (1M x 768, batch 1, K_cand 256) is
-reported beside it under "batch1".  --config N runs BASELINE configs[N-1]
-alone as the headline.
+reported beside it under "batch1", and one GPU's share of configs[3]
+sharded over 8 GPUs by block range (the first 1.1M documents, the same 64
+queries) under "shard_1of8".  --config N runs BASELINE configs[N-1] alone as
+the headline.
 
 `roofline` uses the dominant kernel's durations from HIP events that each
 dispatch records at its own start and end (hipExtLaunchKernelGGL), from a
@@ -118,6 +120,8 @@ def main():
         out["cluster_layout"] = run_workload(4, args, m, dev, n_threads, legs=False, layout="clustered",
                                              cpu_seconds=0.5)
     if args.config == 0:
+        # one GPU's share of config 4 sharded over 8 GPUs by block range
+        out["shard_1of8"] = run_workload(4, args, m, dev, n_threads, legs=False, shard=8, cpu=False)
         out["batch1"] = run_workload(2, args, m, dev, n_threads, legs=not args.no_rerank)
         for k in ("rerank", "encode", "host_boundary"):
             if k in out["batch1"]:
@@ -209,15 +213,18 @@ def kernels_of(groups):
             for (kind, p), g in sorted(groups.items())}
 
 
-def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_seconds=None):
+def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_seconds=None, shard=1, cpu=True):
     """One workload as a bench record.  layout "clustered": the documents of a
     clustered corpus grouped by centroid (mrl_synth_encode_clustered), so the
     index carries block bounds and the final passes skip blocks no query of
-    the batch can reach; the queries are the same."""
+    the batch can reach; the queries are the same.  shard > 1: one GPU's
+    share of the index sharded by contiguous block range, the first
+    1/shard of the documents, scanned for the workload's full query batch."""
     import numpy as np
     from mrl_index_amd import _lib, synth
     L = _lib.lib
-    w = synth.CONFIGS[cfg_id]
+    wq = synth.CONFIGS[cfg_id]
+    w = wq.scaled(wq.n_docs // shard) if shard > 1 else wq
     t0 = time.time()
     fit = synth.eden_fit(w)
     log(f"config {cfg_id} ({layout}): generating + encoding {w.name}: {w.n_docs} x {w.dims} on {n_threads} threads")
@@ -227,7 +234,7 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
         blocks, _ = synth.encode_clustered(w, fit, n_threads)
     else:
         blocks = synth.encode(w, fit, n_threads)
-    queries, _ = synth.queries(w)
+    queries, _ = synth.queries(wq)
     log(f"corpus ready in {time.time() - t0:.1f}s ({blocks.nbytes / 1e6:.1f} MB of codes)")
 
     ix = m.DeviceIndex.upload(blocks, dev)
@@ -298,7 +305,8 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": w.name + ("-cluster-grouped" if layout == "clustered" else ""),
+        "config": {"workload": (wq.name + (f"-shard-1of{shard}" if shard > 1 else "") +
+                                ("-cluster-grouped" if layout == "clustered" else "")),
                    "baseline_config": cfg_id, "layout": layout, "n_vectors": w.n_docs, "dims": w.dims,
                    "blocks": int(blocks.shape[0]), "queries_per_step": nq, "k_cand": w.k,
                    "prefix_codec": w.prefix_codec.name.lower(), "strata": w.strata.name.lower(),
@@ -349,7 +357,7 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
         out["host_boundary"] = host_boundary_rate(L, _lib, dev, ix, queries, fit, w, ccfg, tr)
         out["rerank"], out["encode"] = rerank_leg(L, _lib, m, dev, w, step, res, queries, args.rerank_reps,
                                                   n_threads, not args.no_cpu_baseline, fit, blocks)
-    if not args.no_cpu_baseline:
+    if cpu and not args.no_cpu_baseline:
         step()
         fetch()
         out["cpu_baseline"], out["parity_query0"] = cpu_baseline(
