@@ -2197,14 +2197,46 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     a.out_scores[(uint64_t)q * K + r] = key_score((uint32_t)(c >> 32));
   };
   if (sb == s_sel) {
-    // Counting sort by histogram bin, descending: an entry's position is the
-    // number of selected entries in higher bins plus the number of larger
-    // keys in its own bin (keys are distinct).  s_hist counts per bin, then
-    // serves as the scatter cursor.
+    // Counting sort by bin, descending: an entry's position is the number of
+    // selected entries in higher bins plus the number of larger keys in its
+    // own bin (keys are distinct).  The bins split the selected entries' own
+    // score range [smin, smax] evenly (never wider than the sampling
+    // histogram's bins, and much finer when the selected scores crowd
+    // together, as for a query among near-duplicates).  s_hist counts per
+    // bin, then serves as the scatter cursor.
+    if (tid == 0) {
+      s_misc[3] = 0xFFFFFFFFu;
+      s_misc[4] = 0u;
+    }
     for (int i = tid; i < kHistBins; i += kSelThreads) s_hist[i] = 0u;
     __syncthreads();
-    for (uint32_t i = tid; i < m; i += kSelThreads)
-      atomicAdd(&s_hist[hist_bin(key_score((uint32_t)(sb[i] >> 32)), hinv)], 1u);
+    {  // the key range: per wave first, then one LDS atomic per wave
+      uint32_t lo_k = 0xFFFFFFFFu, hi_k = 0u;
+      for (uint32_t i = tid; i < m; i += kSelThreads) {
+        const uint32_t k = (uint32_t)(sb[i] >> 32);
+        lo_k = min(lo_k, k);
+        hi_k = max(hi_k, k);
+      }
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        lo_k = min(lo_k, (uint32_t)__shfl_xor((int)lo_k, o));
+        hi_k = max(hi_k, (uint32_t)__shfl_xor((int)hi_k, o));
+      }
+      if ((tid & 63) == 0 && lo_k <= hi_k) {
+        atomicMin(&s_misc[3], lo_k);
+        atomicMax(&s_misc[4], hi_k);
+      }
+    }
+    __syncthreads();
+    const float smin = key_score(s_misc[3]), smax = key_score(s_misc[4]);
+    // (bounded, so every product below is finite: 0 when the range overflows)
+    const float binv = m && smax > smin ? fminf((float)(kHistBins - 1) / (smax - smin), 1e30f) : 0.0f;
+    // monotone in the score: a larger score never takes a lower bin
+    auto lbin = [&](uint64_t c) -> uint32_t {
+      const float b = fminf((key_score((uint32_t)(c >> 32)) - smin) * binv, (float)(kHistBins - 1));
+      return (uint32_t)b;
+    };
+    for (uint32_t i = tid; i < m; i += kSelThreads) atomicAdd(&s_hist[lbin(sb[i])], 1u);
     __syncthreads();
     {  // start[b] = entries in bins above b; thread t owns bins 2047 - 2t and 2046 - 2t
       const uint32_t b0 = kHistBins - 1 - 2u * (uint32_t)tid, b1 = b0 - 1;
@@ -2219,13 +2251,13 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     __syncthreads();
     for (uint32_t i = tid; i < m; i += kSelThreads) {
       const uint64_t c = sb[i];
-      const uint32_t b = hist_bin(key_score((uint32_t)(c >> 32)), hinv);
+      const uint32_t b = lbin(c);
       s_buf[s_start[b] + atomicAdd(&s_hist[b], 1u)] = c;
     }
     __syncthreads();
     for (uint32_t i = tid; i < m; i += kSelThreads) {
       const uint64_t c = s_buf[i];
-      const uint32_t b = hist_bin(key_score((uint32_t)(c >> 32)), hinv);
+      const uint32_t b = lbin(c);
       const uint32_t lo = s_start[b], hi = lo + s_hist[b];
       uint32_t r = lo, j = lo;
       for (; j + 4 <= hi; j += 4) {  // four independent reads in flight
