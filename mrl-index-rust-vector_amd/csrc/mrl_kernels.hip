@@ -2399,8 +2399,7 @@ __device__ __forceinline__ uint32_t f16_bits(float x) {
 }
 
 // Query operands and error coefficients of query q, by the first wave of
-// the workgroup (threads 0..63; it has a workgroup barrier, so every thread
-// of the workgroup must call it).
+// the workgroup (threads 0..63; the other waves have nothing to do).
 struct MmaPrepLds {
   float w[64], w1[128], w4[64], ex[8];
 };
@@ -2479,18 +2478,25 @@ __device__ __forceinline__ void mma_prep_body(const MmaPrepArgs& a, uint32_t q, 
       for (int i = kMcOk + 1; i < kMcCount; ++i) mc[i] = 0.0f;
     }
   }
-  __syncthreads();
+  // The operands are read back from LDS by the same wave that wrote them
+  // (no workgroup barrier: the coefficient stores above need not complete
+  // first).  Each lane converts its 8 elements along one path: value, then
+  // f16 rounding to nearest, rounded up for the error columns.
+  if (lane >= 64) return;
+  wave_lds_sync();
   if (lane < 2 * kMmaSteps) {
     const int st = (int)lane >> 1, kh = (int)lane & 1;
+    const float* src = st < 4 ? s_w : (st < 12 ? s_w1 : s_w4);
     uint32_t hv[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      uint32_t h = 0u;
-      if (st < 4) h = f32_to_f16(s * s_w[mma_dim(st, kh, e)]);
-      else if (st < 12) h = f32_to_f16(s * s_w1[mma_dim(st, kh, e)]);
-      else if (st < 16) h = f32_to_f16(s * s_w4[mma_dim(st, kh, e)]);
-      else if (kh == 0 && e < 4) h = f16_up(s * s_ex[e]);       // error columns
-      else if (kh == 0 && e == 4) h = f32_to_f16(s * psum);     // offset * prefix_sum
+      float v = 0.0f;
+      if (st < 16) v = src[mma_dim(st, kh, e)];
+      else if (kh == 0 && e < 4) v = s_ex[e];   // error columns
+      else if (kh == 0 && e == 4) v = psum;     // offset * prefix_sum
+      const float x = s * v;
+      uint32_t h = f32_to_f16(x);
+      if (st == 16 && e < 4 && h2f((uint16_t)h) < x) h += 1u;  // f16_up: magnitude no smaller than x
       hv[e] = h;
     }
     a.ops[(uint64_t)q * (2 * kMmaSteps) + lane] =
