@@ -2079,7 +2079,16 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   const uint32_t total = s_off[a.nseg];
   uint32_t m;
   uint64_t* sb = s_buf;  // the entries the final sort reads
-  if (total <= (uint32_t)kSortCap) {
+  if (total <= (uint32_t)kSelCap) {
+    // Every entry fits the final sort: one walk loads (score, row) pairs
+    // into LDS, and all of them are sorted (no histogram, no threshold).
+    auto take = [&](float sc, uint32_t row, uint32_t dense) { s_sel[dense] = composite(score_key(sc), row); };
+    if (short_segs && a.seg_cap >= (uint32_t)kShortPre) for_each_pair_short(v, pre, take);
+    else for_each_pair(v, take);
+    __syncthreads();
+    m = total;
+    sb = s_sel;
+  } else if (total <= (uint32_t)kSortCap) {
     // Every entry fits in LDS: one walk loads (score, row) pairs and
     // histograms them; the entries at or above the K-th bin's floor are then
     // picked out of LDS.
