@@ -2212,10 +2212,16 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     // score range [smin, smax] evenly (never wider than the sampling
     // histogram's bins, and much finer when the selected scores crowd
     // together, as for a query among near-duplicates).  s_hist counts per
-    // bin, then serves as the scatter cursor.
+    // bin, then serves as the scatter cursor.  Only bins that start above
+    // position keep are placed and ranked: an entry in a bin with `keep`
+    // entries above it ranks at keep or lower.  These low bins are the
+    // crowded ones (the scores thin out towards the top), so skipping them
+    // also skips most same-bin LDS atomics.  s_misc[5]: the end of the bin
+    // that holds position keep - 1, m when keep == m.
     if (tid == 0) {
       s_misc[3] = 0xFFFFFFFFu;
       s_misc[4] = 0u;
+      s_misc[5] = m;
     }
     for (int i = tid; i < kHistBins; i += kSelThreads) s_hist[i] = 0u;
     __syncthreads();
@@ -2256,15 +2262,19 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
       s_start[b1] = excl + c0;
       s_hist[b0] = 0u;
       s_hist[b1] = 0u;
+      // at most one bin holds position keep - 1 (empty bins hold none)
+      if (excl < keep && excl + c0 >= keep) s_misc[5] = excl + c0;
+      if (excl + c0 < keep && excl + c0 + c1 >= keep) s_misc[5] = excl + c0 + c1;
     }
     __syncthreads();
     for (uint32_t i = tid; i < m; i += kSelThreads) {
       const uint64_t c = sb[i];
       const uint32_t b = lbin(c);
-      s_buf[s_start[b] + atomicAdd(&s_hist[b], 1u)] = c;
+      if (s_start[b] < keep) s_buf[s_start[b] + atomicAdd(&s_hist[b], 1u)] = c;
     }
     __syncthreads();
-    for (uint32_t i = tid; i < m; i += kSelThreads) {
+    const uint32_t placed = s_misc[5];
+    for (uint32_t i = tid; i < placed; i += kSelThreads) {
       const uint64_t c = s_buf[i];
       const uint32_t b = lbin(c);
       const uint32_t lo = s_start[b], hi = lo + s_hist[b];
