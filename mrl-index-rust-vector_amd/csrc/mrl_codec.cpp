@@ -142,7 +142,7 @@ static void fwht(float* a, int n) {  // rotate.rs:13-33
   for (int i = 0; i < n; ++i) a[i] *= scale;
 }
 
-static inline float mix_sign(uint64_t a, uint64_t i) {  // rotate.rs:53-67, eden.rs:357-370
+static inline float mix_sign(uint64_t a, uint64_t i) {  // rotate.rs:53-67, eden.rs:75-88
   uint64_t x = (a * 0x9E3779B97F4A7C15ull + i) * 0xBF58476D1CE4E5B9ull;
   x ^= x >> 30;
   x *= 0x94D049BB133111EBull;

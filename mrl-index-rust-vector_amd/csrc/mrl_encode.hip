@@ -31,7 +31,7 @@ __device__ __forceinline__ float zero_acc() {
   return z;
 }
 
-// tail_rademacher / rademacher_diag sign (rotate.rs:53-67, eden.rs:357-370)
+// tail_rademacher / rademacher_diag sign (rotate.rs:53-67, eden.rs:75-88)
 __device__ __forceinline__ float mix_sign(uint64_t a, uint64_t i) {
   uint64_t x = (a * 0x9E3779B97F4A7C15ull + i) * 0xBF58476D1CE4E5B9ull;
   x ^= x >> 30;

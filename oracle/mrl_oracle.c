@@ -203,7 +203,7 @@ void ora_rotate_mid_band(const float *mid128, float *out128) {
 /* rotate.rs:46-49; std::f32::consts::PI rounds to the same float as (float)M_PI. */
 float ora_rabitq_bit_scale(void) { return sqrtf(2.0f / (float)M_PI) / sqrtf((float)ORA_RABITQ_DIMS); }
 
-/* rotate.rs:53-67 and eden.rs:357-370 share this SplitMix-style mix. */
+/* rotate.rs:53-67 and eden.rs:75-88 share this SplitMix-style mix. */
 static float splitmix_sign(uint64_t a, uint64_t i) {
   uint64_t x = (a * 0x9E3779B97F4A7C15ull + i) * 0xBF58476D1CE4E5B9ull;
   x ^= x >> 30;

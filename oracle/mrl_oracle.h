@@ -25,11 +25,13 @@
  *    the reference's literals, parsed from eden.rs by
  *    tests/golden/make_codebooks.py into tests/golden/eden_codebooks.json;
  *    each level is also within 2e-6 of the N(0,1) Lloyd-Max centroid.
- * Parity unpinned (no independent check fixes the exact bits):
- *  - ora_rademacher_diag / ora_tail_rademacher (eden.rs:357-370,
- *    rotate.rs:53-67): the SplitMix-style sign sequence is checked only
- *    against a second restatement, for balance, and through the rotations'
- *    orthogonality, which any sign sequence satisfies.
+ *  - ora_rademacher_diag / ora_tail_rademacher (eden.rs:75-88,
+ *    rotate.rs:53-67): tests/golden/make_sign_hash.py parses both reference
+ *    function bodies into their 64-bit operation sequence
+ *    (tests/golden/sign_hash.json); the signs of every (seed, i) and
+ *    (block, dim) pair the path uses equal the ones that sequence gives.
+ * Not pinned bit for bit (no independent check fixes them; the parity
+ * contract excludes them):
  *  - ora_scan_blocks with sharding on: which of several exactly tied scores
  *    survive at the K boundary (Rayon's merge order, scan.rs:846-865).
  *  - ora_dot for n != 768: the sign of an exactly zero sum (Sum for f32

@@ -143,30 +143,6 @@ def test_operator_gram_structure_and_fold_amplification():
         assert np.max(np.abs(T @ z.astype(np.float64) - exp)) < 2e-5
 
 
-def test_tail_rademacher_signs_are_balanced_and_match_splitmix_restatement():
-    # parity of the 64-bit SplitMix-style mix is pinned only by restatement:
-    # Python's arbitrary-precision arithmetic reduced mod 2^64 against the C code
-    M = (1 << 64) - 1
-
-    def sign(a, i):
-        x = ((a * 0x9E3779B97F4A7C15 + i) * 0xBF58476D1CE4E5B9) & M
-        x ^= x >> 30
-        x = (x * 0x94D049BB133111EB) & M
-        x ^= x >> 27
-        return 1.0 if x & 1 == 0 else -1.0
-
-    vals = []
-    for b in range(9):
-        for d in range(64):
-            s = L.ora_tail_rademacher(b, d)
-            assert s == sign(b, d)
-            vals.append(s)
-    for seed in (1, 2, 12345):
-        for i in range(128):
-            assert L.ora_rademacher_diag(seed, i) == sign(seed, i)
-    assert abs(np.mean(vals)) < 0.15
-
-
 def test_bit_scales_closed_form():
     assert abs(L.ora_rabitq_bit_scale() - np.sqrt(2 / np.pi) / np.sqrt(128)) < 1e-8
     assert abs(L.ora_tail_fold_bit_scale() - np.sqrt(2 / np.pi) / np.sqrt(64)) < 1e-8
