@@ -171,7 +171,14 @@ int mrl_abi_version(void);
 const char *mrl_last_error(void);
 size_t mrl_query_plan_size(void);
 
-/* No reference counterpart (the reference scan runs on the global Rayon pool). */
+/* No reference counterpart (the reference scan runs on the global Rayon pool).
+ * Destroy order: every index, plans, results and rerank store made on a
+ * context keeps the context alive, so mrl_ctx_destroy and the objects'
+ * destroy calls may come in any order; the context's stream and buffers are
+ * freed with the last of them.  After mrl_ctx_destroy the handle may not be
+ * passed to any call (its objects' own destroy calls remain valid).  Memory
+ * from mrl_device_alloc is freed with mrl_device_free(ctx, ...) before
+ * mrl_ctx_destroy.  Destroy calls wait for the context's stream first. */
 int mrl_ctx_create(int device, mrl_ctx **out);
 void mrl_ctx_destroy(mrl_ctx *ctx);
 int mrl_ctx_synchronize(mrl_ctx *ctx);
@@ -263,9 +270,16 @@ int mrl_results_floors(mrl_ctx *ctx, mrl_results *res, float *out_floors);
  * Enqueued on the context stream; returns without waiting.  Results are
  * those of mrl_scan_async + mrl_results_fetch: a query whose final floor
  * left it short of K is re-run at the safe floor on the device.  Status bits
- * per query: 1 a NaN score (mrl_results_fetch reports MRL_ERR_NAN), 2 a
- * candidate list overflowed (massive exact ties; that query's list is not
- * exact: scan it with mrl_scan, which re-runs it densely).  At most
+ * per query: 1 a NaN score (mrl_results_fetch reports MRL_ERR_NAN); 2 a
+ * candidate list overflowed, so that query's list is not exact: scan it with
+ * mrl_scan, which re-runs it densely.  Besides massive exact ties, a
+ * safe-floor re-run can overflow: the room per query is 16 segments of 4096
+ * entries up to 16 queries, 2048 up to 32, 1024 up to 64, while about
+ * K x (blocks / sampled blocks) vectors reach the safe floor (some 16K at
+ * K = 256 on a 1M-vector index, more on larger ones).  8: fewer than K hits
+ * at a floor no tighter than the safe one, possible only where the stage
+ * bounds are not admissible (see mrl_results_floors); mrl_scan re-runs such
+ * a query with no floor.  At most
  * MRL_NOALLOC_MAX_QUERIES queries per call (more: MRL_ERR_INVALID_ARG).
  * Every call on one GPU shares that GPU's array, which keeps the last call's
  * contents: calls on one context are ordered on its stream, but calls from

@@ -77,8 +77,20 @@ struct mrl_ctx {
   void* h_stage = nullptr;            // pinned host staging for result read-back
   size_t h_stage_cap = 0;
   mrl_results* spare = nullptr;       // result buffers kept between synchronous mrl_scan calls
-  uint8_t* scratch = nullptr;         // this device's copy of `scratch` (mrl_scan_noalloc)
+  uint8_t* scratch = nullptr;         // this device's copy of `scratch` (mrl_scan_noalloc); null: lookup failed
+  // The caller's handle plus one per live object made on this context (index,
+  // plans, results, rerank store).  Each of those reaches the context through
+  // its `ctx` member when it is destroyed, so the context's stream and
+  // buffers are freed when the last reference goes, in whatever order the
+  // caller destroys the handles.
+  std::atomic<uint32_t> refs{1};
 };
+
+static void ctx_free(mrl_ctx* ctx);
+static void ctx_retain(mrl_ctx* ctx) { ctx->refs.fetch_add(1, std::memory_order_relaxed); }
+static void ctx_release(mrl_ctx* ctx) {
+  if (ctx->refs.fetch_sub(1, std::memory_order_acq_rel) == 1) ctx_free(ctx);
+}
 
 // ---------------------------------------------------------------------------
 // scratch of the allocation-free scan (mrl_scan_noalloc)
@@ -309,12 +321,10 @@ extern "C" int mrl_ctx_create(int device, mrl_ctx** out) {
   }
   HIP_TRY(hipMalloc(&c->d_flag_tabs, sizeof(tabs)));
   HIP_TRY(hipMemcpy(c->d_flag_tabs, tabs, sizeof(tabs), hipMemcpyHostToDevice));
-  int rc = scratch_address(device, &c->scratch);
-  if (rc) {
-    dev_free(c->d_flag_tabs);
-    (void)hipStreamDestroy(c->stream);
-    return rc;
-  }
+  // The scan entry points other than mrl_scan_noalloc do not need the
+  // scratch address: a failed lookup only makes that one entry point fail.
+  if (scratch_address(device, &c->scratch)) c->scratch = nullptr;
+  g_err.clear();
   *out = c.release();
   return MRL_OK;
 }
@@ -322,7 +332,10 @@ extern "C" int mrl_ctx_create(int device, mrl_ctx** out) {
 static void results_release(mrl_results* r);
 
 extern "C" void mrl_ctx_destroy(mrl_ctx* ctx) {
-  if (!ctx) return;
+  if (ctx) ctx_release(ctx);
+}
+
+static void ctx_free(mrl_ctx* ctx) {
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
   results_release(ctx->spare);
@@ -469,6 +482,7 @@ extern "C" int mrl_index_upload(mrl_ctx* ctx, const void* blocks, uint64_t n_blo
       return rc;
     }
   }
+  ctx_retain(ctx);
   *out = ix.release();
   return MRL_OK;
 }
@@ -586,6 +600,7 @@ extern "C" int mrl_index_open_segment(mrl_ctx* ctx, const char* path, int verify
     dev_free(ix->d_recs);
     return rc;
   }
+  ctx_retain(ctx);
   *out = ix.release();
   return MRL_OK;
 }
@@ -623,13 +638,15 @@ extern "C" int mrl_index_download(mrl_ctx* ctx, const mrl_index* index, void* ou
 
 extern "C" void mrl_index_destroy(mrl_index* index) {
   if (!index) return;
-  (void)hipSetDevice(index->ctx->device);
-  (void)hipStreamSynchronize(index->ctx->stream);
+  mrl_ctx* ctx = index->ctx;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
   dev_free(index->d_blocks);
   dev_free(index->d_recs);
   dev_free(index->d_bounds);
   dev_free(index->d_bsel);
   delete index;
+  ctx_release(ctx);
 }
 
 // Block bounds of an uploaded index: every block whose header carries
@@ -866,6 +883,7 @@ static int plans_build_impl(mrl_ctx* ctx, const float* queries, bool on_device, 
     dev_free(p->d_block);
     return rc2;
   }
+  ctx_retain(ctx);
   *out = p.release();
   return MRL_OK;
 }
@@ -912,10 +930,12 @@ extern "C" int mrl_plans_export(mrl_ctx* ctx, const mrl_plans* plans, uint32_t f
 
 extern "C" void mrl_plans_destroy(mrl_plans* plans) {
   if (!plans) return;
-  (void)hipSetDevice(plans->ctx->device);
-  (void)hipStreamSynchronize(plans->ctx->stream);
+  mrl_ctx* ctx = plans->ctx;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
   dev_free(plans->d_block);
   delete plans;
+  ctx_release(ctx);
 }
 
 // ---------------------------------------------------------------------------
@@ -973,7 +993,9 @@ static const uint32_t kSegCap = 4096;  // kSegs * kSegCap = 65536 candidates per
 static size_t mma_bytes_per_query() { return (size_t)2 * kMmaSteps * 16 + kMcCount * 4 + kFinCap / kExactItem * 4; }
 static size_t mma_bytes(uint32_t n_q) { return (size_t)std::max<uint32_t>(n_q, 1) * mma_bytes_per_query() + 16; }
 
-extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_results** out) {
+// A results object that holds no reference to its context (the context's
+// own spare, kept for mrl_scan); mrl_results_create adds the reference.
+static int results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_results** out) {
   if (!ctx || !out) return fail(MRL_ERR_INVALID_ARG, "null argument");
   if (k == 0 || k > MRL_MAX_SHORTLIST) return fail(MRL_ERR_INVALID_ARG, "k must be in [1, 4096]");
   *out = nullptr;
@@ -1023,12 +1045,25 @@ extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_re
   return MRL_OK;
 }
 
-extern "C" void mrl_results_destroy(mrl_results* res) {
-  if (!res) return;
+extern "C" int mrl_results_create(mrl_ctx* ctx, uint32_t n_q, uint32_t k, mrl_results** out) {
+  const int rc = results_create(ctx, n_q, k, out);
+  if (rc == MRL_OK) ctx_retain(ctx);
+  return rc;
+}
+
+// Frees a results object without touching its context's reference count.
+static void results_destroy(mrl_results* res) {
   (void)hipSetDevice(res->ctx->device);
   (void)hipStreamSynchronize(res->ctx->stream);
   results_free(res);
   delete res;
+}
+
+extern "C" void mrl_results_destroy(mrl_results* res) {
+  if (!res) return;
+  mrl_ctx* ctx = res->ctx;
+  results_destroy(res);
+  ctx_release(ctx);
 }
 
 // Buffers one scan writes its candidates into.
@@ -1390,6 +1425,7 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
   sa.hist = sampled ? pb.hist : nullptr;
   sa.tau_final = pb.tau_hi;
   sa.tau_safe = pb.tau;
+  sa.tau_used = floor;
   ProfScope ps(ctx, MRL_KERNEL_SELECT, final_pass, 0, n_q);
   HIP_TRY(launch_select(sa, n_q, s, ps.ev()));
   ps.commit(n_q != 0);
@@ -1501,6 +1537,7 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
   sa.hist = sampled ? pb.hist : nullptr;
   sa.tau_final = pb.tau_hi;
   sa.tau_safe = pb.tau;
+  sa.tau_used = rerun_safe ? pb.tau : (sampled ? pb.tau_hi : nullptr);
   ProfScope ps(ctx, MRL_KERNEL_SELECT, (int)np - 1, 0, n_q);
   HIP_TRY(launch_select(sa, n_q, s, ps.ev()));
   ps.commit(n_q != 0);
@@ -1644,8 +1681,10 @@ static int safe_rerun(mrl_ctx* ctx, mrl_results* r, uint32_t q, uint32_t* st) {
 }
 
 // Acts on one query's scan status: bit 2 (final floor too high) re-runs the
-// final pass at the safe floor, bit 1 (a segment overflowed) re-runs densely,
-// bit 0 (NaN) sets *nan.  *rerun is set if anything ran.  Caller holds the lock.
+// final pass at the safe floor; bit 1 (a segment overflowed) or bit 3 (short
+// of K at a floor no tighter than the safe one: bounds that are not
+// admissible) re-runs densely, with no floor; bit 0 (NaN) sets *nan.  *rerun
+// is set if anything ran.  Caller holds the lock.
 static int rerun_query(mrl_ctx* ctx, mrl_results* r, uint32_t q, uint32_t status, bool* nan, bool* rerun) {
   int rc;
   if (status & 4u) {
@@ -1654,7 +1693,7 @@ static int rerun_query(mrl_ctx* ctx, mrl_results* r, uint32_t q, uint32_t status
     *rerun = true;
   }
   if (status & 1u) *nan = true;
-  if (status & 2u) {
+  if (status & 10u) {
     if (q < r->floor_kind.size()) r->floor_kind[q] = 0;
     rc = dense_rerun(ctx, r, q);
     if (rc == MRL_ERR_NAN) *nan = true;
@@ -1795,12 +1834,12 @@ extern "C" int mrl_scan(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* p
       ctx->spare = nullptr;
     }
   }
-  if (!res && (rc = mrl_results_create(ctx, plans->n_q, K, &res))) return rc;
+  if (!res && (rc = results_create(ctx, plans->n_q, K, &res))) return rc;
   rc = mrl_scan_async(ctx, index, plans, cfg, time, res);
   if (!rc) rc = mrl_results_fetch(ctx, res, out_ids, out_scores, out_counts, stats);
   if (rc) {  // a failed scan may leave pass state behind: do not keep these buffers
     std::string msg = g_err;
-    mrl_results_destroy(res);
+    results_destroy(res);
     g_err = msg;
     return rc;
   }
@@ -1812,7 +1851,7 @@ extern "C" int mrl_scan(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* p
     old = ctx->spare;
     ctx->spare = res;
   }
-  if (old) mrl_results_destroy(old);
+  if (old) results_destroy(old);
   return rc;
 }
 
@@ -1915,6 +1954,7 @@ static int enqueue_gated_rerun(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* pla
   sa.out_counts = pb.out_counts;
   sa.tau_final = pb.tau_hi;
   sa.tau_safe = pb.tau;
+  sa.tau_used = pb.tau;
   sa.gate = pb.status;
   HIP_TRY(launch_select(sa, n_q, ctx->stream));
   return MRL_OK;
@@ -2270,14 +2310,18 @@ extern "C" int mrl_rerank_store_create(mrl_ctx* ctx, const float* rows, int rows
     return fail(MRL_ERR_INVALID_ARG, "fp16 / int8 rerank rows need 768 dims");  // lowprec.rs:50,73
   std::lock_guard<std::mutex> g(ctx->mu);
   HIP_TRY(hipSetDevice(ctx->device));
-  return store_create_locked(ctx, rows, rows_on_device, n_rows, dims, precision, out);
+  const int rc = store_create_locked(ctx, rows, rows_on_device, n_rows, dims, precision, out);
+  if (rc == MRL_OK) ctx_retain(ctx);
+  return rc;
 }
 
 extern "C" void mrl_rerank_store_destroy(mrl_rerank_store* store) {
   if (!store) return;
-  (void)hipSetDevice(store->ctx->device);
-  (void)hipStreamSynchronize(store->ctx->stream);
+  mrl_ctx* ctx = store->ctx;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
   store_free(store);
+  ctx_release(ctx);
 }
 
 extern "C" int mrl_rerank_store_download(mrl_ctx* ctx, const mrl_rerank_store* store, void* out_rows,
@@ -2803,6 +2847,7 @@ extern "C" int mrl_index_from_device(mrl_ctx* ctx, const void* d_blocks, uint64_
       return rc;
     }
   }
+  ctx_retain(ctx);
   *out = ix.release();
   return MRL_OK;
 }

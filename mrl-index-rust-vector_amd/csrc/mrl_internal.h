@@ -301,10 +301,13 @@ struct SelectArgs {
   uint32_t* err;          // consumed and zeroed
   uint32_t k;
   uint32_t* status;       // out per query: bit 0 NaN seen, bit 1 a segment overflowed,
-                          // bit 2 fewer than k candidates above a floor tighter than the safe one
+                          // bit 2 fewer than k candidates above a floor tighter than the safe one,
+                          // bit 3 fewer than k candidates above a finite floor no tighter than it
+                          // (stage bounds that are not admissible rejected vectors above the floor)
   uint32_t* hist;         // sampling histogram [n_q][kHistBins] (null: none); zeroed for the next scan
   const float* tau_final; // [n_q] floor of the final pass (with hist)
   const float* tau_safe;  // [n_q] safe floor (with hist)
+  const float* tau_used;  // [n_q] the floor the final pass used (null: -inf, no floor)
   uint64_t* out_ids;      // [n_q][k]
   float* out_scores;
   uint32_t* out_counts;

@@ -2038,7 +2038,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   __shared__ uint32_t s_coff[kMaxSegs + 1];
   __shared__ uint32_t s_ws[32];
 
-  __shared__ float s_fl[2];
+  __shared__ float s_fl[3];
 
   const uint32_t q = blockIdx.x;
   const int tid = threadIdx.x;
@@ -2053,11 +2053,12 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
   // the query's histogram scale (2^-e, 2^e)
   const float hinv = a.luts[(uint64_t)q * kQData + kQdHistInv];
   const float hscale = a.luts[(uint64_t)q * kQData + kQdHistScale];
-  float fl_safe = 0.0f, fl_final = 0.0f;
+  float fl_safe = 0.0f, fl_final = 0.0f, fl_used = -INFINITY;
   if (a.hist && tid == 0) {
     fl_safe = a.tau_safe[q];
     fl_final = a.tau_final[q];
   }
+  if (a.tau_used && tid == 0) fl_used = a.tau_used[q];
   const uint32_t c_own = tid < (int)a.nseg ? qcount[tid] : 0u;
   ShortPre pre;
   if (short_segs && tid < (int)a.nseg && a.seg_cap >= (uint32_t)kShortPre) {
@@ -2072,6 +2073,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     s_misc[7] = 0;
     s_fl[0] = fl_safe;
     s_fl[1] = fl_final;
+    s_fl[2] = fl_used;
   }
   __syncthreads();
   if (c_own > a.seg_cap) atomicOr(&s_misc[7], 2u);
@@ -2329,16 +2331,21 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     for (int i = tid; i < kHistBins; i += kSelThreads) a.hist[(uint64_t)q * kHistBins + i] = 0u;
   if (tid == 0) {
     // Fewer than K candidates above a floor tighter than the safe one: the
-    // top K may lie below it, so the host re-runs the final pass at the safe
-    // floor.
+    // top K may lie below it, so the final pass is re-run at the safe floor.
+    // Fewer than K above a finite floor no tighter than the safe one happens
+    // only when the stage bounds are not admissible (vectors above the floor
+    // were rejected): the query is re-run with no floor, as the reference's
+    // shortlist, whose threshold stays at -inf until it holds K, keeps
+    // min(K, active) hits.
     const uint32_t short_k = (a.hist && keep < K && s_fl[1] > s_fl[0]) ? 4u : 0u;
+    const uint32_t short_f = (!short_k && keep < K && s_fl[2] > -INFINITY) ? 8u : 0u;
     a.out_counts[q] = keep;
-    a.status[q] = (a.err[q] & 1u) | s_misc[7] | short_k;
+    a.status[q] = (a.err[q] & 1u) | s_misc[7] | short_k | short_f;
     a.err[q] = 0u;
-    if (a.stats && (short_k | s_misc[7])) {
+    if (a.stats && (short_k | short_f | s_misc[7])) {
       unsigned long long* st = a.stats + (q % (uint32_t)kStatCopies) * kStatCount;
       if (short_k) atomicAdd(st + kStatRerunSafe, 1ull);
-      if (s_misc[7] & 2u) atomicAdd(st + kStatRerunDense, 1ull);
+      if ((s_misc[7] & 2u) || short_f) atomicAdd(st + kStatRerunDense, 1ull);
     }
   }
 }
@@ -3932,6 +3939,11 @@ uint32_t scan_grid(const ScanArgs& a, bool diag) {
   const uint32_t res = tile ? rest : (qt == 8 ? res8 : res1);
   uint32_t grid = (a.n_pos + 4) / 4;  // 4 * grid - 1 >= n_pos waves carry positions
   uint32_t max_grid = res / tiles;
+  // A gated re-run scans for the few flagged queries only (the other
+  // queries' workgroups exit at once): each query gets at least a quarter of
+  // the one-query grid, not 1/n_q of the GPU.
+  const uint32_t g_rerun = (res1 < MRL_SCAN_GRID1 ? res1 : MRL_SCAN_GRID1) / 4u;
+  if (a.gate && max_grid < g_rerun) max_grid = g_rerun;
   if (!tile && qt == 1 && !diag && !l0 && max_grid > MRL_SCAN_GRID1) max_grid = MRL_SCAN_GRID1;
   if (!a.excl && max_grid < a.nseg) max_grid = a.nseg;
   if (grid > max_grid) grid = max_grid;

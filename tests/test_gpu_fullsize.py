@@ -1,9 +1,13 @@
 """GPU parity at the benchmark configurations' full sizes, plus the segment
 loader, the QueryPipeline seam and an exhaustive f16 meta decode check.
 
-Full-size checks: the GPU top-K equals the oracle's scan_blocks top-K (exact
-ties excepted) on a subset of queries, and for every query the returned
-scores are bit-identical to the oracle's score of those vectors."""
+Full-size checks: for every query of every configuration the GPU top-K
+equals the oracle's scan_blocks top-K (exact ties excepted) with bit-identical
+scores; the first queries against the sharded scan (scan.rs:838-886), the
+rest against the serial one (scan.rs:822-836), run query-parallel."""
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 import pytest
 
@@ -15,7 +19,26 @@ from helpers import assert_topk_equal
 pytestmark = pytest.mark.gpu
 
 
-def _check_config(device, cfg_id, n_checked, n_queries=None):
+def _oracle_all(blocks, qs, w, ofit, n_sharded):
+    """The oracle's top K of every query: the first n_sharded through the
+    sharded scan on all host threads, the others through serial scans, one
+    query per host thread."""
+    threads = max(1, min(16, os.cpu_count() or 1))
+    sharded = ora.scan_config(w.k, depth=int(w.strata), sharding=True, threads=threads)
+    serial = ora.scan_config(w.k, depth=int(w.strata), sharding=False)
+    b = np.ascontiguousarray(blocks)
+
+    def one(qi):
+        op = ora.plan_build(qs[qi], w.dims, int(w.prefix_codec), 0, ofit, None)
+        return ora.scan_blocks(b, op, sharded if qi < n_sharded else serial)
+
+    out = [one(qi) for qi in range(min(n_sharded, w.n_queries))]
+    with ThreadPoolExecutor(threads) as ex:
+        out += list(ex.map(one, range(len(out), w.n_queries)))
+    return out
+
+
+def _check_config(device, cfg_id, n_sharded, n_queries=None):
     w = synth.CONFIGS[cfg_id]
     if n_queries:
         w = w.scaled(w.n_docs, n_queries)
@@ -28,21 +51,13 @@ def _check_config(device, cfg_id, n_checked, n_queries=None):
     cfg = m.ScanConfig(shortlist_cand=w.k, strata_depth=w.strata, exhaustive=w.exhaustive)
     res = m.scan_batch(ix, plan, cfg)
     ofit = ora.Fit(fit.mean, 4, 1, fit.n_observed) if fit is not None else None
-    ocfg = ora.scan_config(w.k, depth=int(w.strata), sharding=True, threads=16)
+    refs = _oracle_all(blocks, qs, w, ofit, n_sharded)
     for qi in range(w.n_queries):
         n = int(res.counts[qi])
         ids, sc = res.ids[qi, :n], res.scores[qi, :n]
         assert n == min(w.k, w.n_docs)
         assert len(set(ids.tolist())) == n and np.all(sc[:-1] >= sc[1:])
-        op = ora.plan_build(qs[qi], w.dims, int(w.prefix_codec), 0, ofit, None)
-        if qi < n_checked:
-            rids, rsc = ora.scan_blocks(blocks, op, ocfg)
-            assert_topk_equal(ids, sc, rids, rsc, w.k, f"config {cfg_id} q={qi}")
-        else:  # every returned score is the oracle's exhaustive score of that vector
-            for i in range(0, n, max(1, n // 16)):
-                b, v = int(ids[i]) >> 16, int(ids[i]) & 0xFFFF
-                _, mk, _, osc = ora.block_stages(blocks[b], op, ora.scan_config(w.k, depth=int(w.strata)), -np.inf)
-                assert (int(mk[4]) >> v) & 1 and osc[v].view(np.uint32) == sc[i].view(np.uint32)
+        assert_topk_equal(ids, sc, refs[qi][0], refs[qi][1], w.k, f"config {cfg_id} q={qi}")
     return res
 
 

@@ -103,3 +103,38 @@ def test_inactive_and_out_of_range_slots(device):
     assert np.all(np.isposinf(up[:, 3 * 64 + 9])) and np.all(np.isneginf(lw[:, 3 * 64 + 9]))
     # timestamps are row indices: keep rows 1000 .. 4000
     _check(device, blocks, qs, 768, None, lo=1000, hi=4000, what="temporal")
+
+
+@pytest.mark.parametrize("eden", [True, False])
+def test_subnormal_operands(device, eden):
+    """Slots whose f16 scale, offset and tail norm lie in the f16 subnormal
+    range (so the prefix operands cb[l]*scale, the S1 / S4 operands
+    +-mid_n/2 and +-hn*w_s4/2, and the error-column entries are subnormal
+    f16 values), and MinMax4 queries whose prefix weights span 2^-40 .. 1
+    (the smallest become subnormal f16 operands after the query's
+    power-of-two scaling).  Every pair's score must stay inside its bounds.
+    Were subnormal operands flushed to zero, a slot with a subnormal scale
+    would lose its whole prefix term, far more than its error term
+    |scale| * eP, and the bracket would break."""
+    print(f"[mma bounds] subnormal operands, eden={eden}", flush=True)
+    rng = np.random.default_rng(36 + eden)
+    rows = normalized(rng, 40 * 64, 768)
+    fit = m.EdenFit.fit_prefix(rows[:2048], 4, 1) if eden else None
+    blocks = m.encode_corpus(rows, m.source.DOC, fit)
+    meta = blocks[:, 64:512].reshape(-1, 64, 7)
+    sub = lambda n: rng.integers(1, 0x400, size=n, dtype=np.uint16) | (rng.integers(0, 2, size=n, dtype=np.uint16) << 15)
+    for b in range(24):
+        for part, sel in ((0, b % 3 != 2), (1, b % 3 != 1), (2, b % 3 != 0)):
+            if sel:  # part 0: scale, 1: offset, 2: tail norm (kept positive)
+                v = sub(64)
+                if part == 2:
+                    v &= 0x7FFF
+                meta[b, :, 2 * part:2 * part + 2] = v.view(np.uint8).reshape(64, 2)
+    meta[:24, :, 6] = rng.integers(0, 256, size=(24, 64), dtype=np.uint8)   # any rho
+    qs = _queries(rows, rng, 16)
+    if not eden:
+        for qi in range(2, 16):
+            dims = rng.choice(64, 12, replace=False)
+            qs[qi, dims] *= np.float32(2.0) ** -rng.integers(20, 41, size=12).astype(np.float32)
+    up, lw = _check(device, blocks, qs, 768, fit, what=f"subnormal eden={eden}")
+    assert np.all(np.isfinite(up[:, :24 * 64])) and np.all(np.isfinite(lw[:, :24 * 64]))
