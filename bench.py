@@ -3,8 +3,14 @@
 
 A step is one pass of the hot path over one batch of queries: the batched
 query-plan kernel on the resident queries, then every scan pass + top-K
-selection, all enqueued on the library's stream with the index already in
-HBM.  The default run measures the two workloads BASELINE's metric is quoted
+selection, all enqueued on a context's stream with the index already in
+HBM.  The timed steps go round `--streams` contexts (default 3) that scan the
+one index, each with its own plans and results, so the latency-bound launches
+of one step (plan, sampling, selection) overlap another step's on the GPU:
+`ms_per_step` and `value` are that throughput (K steps between
+synchronisations of every stream), `single_stream_ms_per_step` the same K
+steps on one context, one batch in flight at a time (the latency of a step).
+The default run measures the two workloads BASELINE's metric is quoted
 on: the headline is configs[3] (8.8M x 768 clustered, batch 64, K_cand 256,
 the north-star target); configs[1] (1M x 768, batch 1, K_cand 256) is
 reported beside it under "batch1", and one GPU's share of configs[3]
@@ -88,6 +94,8 @@ def main():
                     help="0 (default): configs 4 and 2 (BASELINE configs[3] and [1]); N: that config alone")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--streams", type=int, default=3,
+                    help="contexts (one stream each) sharing the index; the timed steps go round them")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache runs")
     ap.add_argument("--no-rerank", action="store_true", help="skip the post-scan rerank and encode legs")
     ap.add_argument("--layout", choices=["standard", "clustered"], default="standard",
@@ -98,7 +106,7 @@ def main():
                     help="default run: skip config 4 in the cluster-grouped layout")
     ap.add_argument("--rerank-reps", type=int, default=100)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="only run a plain device copy of MIB MiB (PMC byte-counter calibration) and exit")
+                    help="only run the library's fill and read-sweep kernels over MIB MiB (PMC byte-counter calibration) and exit")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -247,10 +255,24 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
     nq = w.n_queries
     res = C.c_void_p()
     _lib.check(L.mrl_results_create(dev.handle, nq, w.k, C.byref(res)))
+    # Further contexts (one stream each) scanning the same index with their
+    # own plans and results: the timed steps go round them, so a step's
+    # latency-bound kernels overlap the next step's on the GPU.
+    lanes = [(dev, plan, res)]
+    for _ in range(1, max(1, args.streams)):
+        d = m.Device(dev.device)
+        p = m.QueryPlan.from_query_codec(queries, w.dims, w.prefix_codec, m.MidCodec.RABITQ, fit, None, d)
+        r = C.c_void_p()
+        _lib.check(L.mrl_results_create(d.handle, nq, w.k, C.byref(r)))
+        lanes.append((d, p, r))
+
+    def lane_step(i):
+        d, p, r = lanes[i]
+        _lib.check(L.mrl_plans_rebuild(d.handle, p.handle))
+        _lib.check(L.mrl_scan_async(d.handle, ix.handle, p.handle, C.byref(ccfg), C.byref(tr), r))
 
     def step():
-        _lib.check(L.mrl_plans_rebuild(dev.handle, plan.handle))
-        _lib.check(L.mrl_scan_async(dev.handle, ix.handle, plan.handle, C.byref(ccfg), C.byref(tr), res))
+        lane_step(0)
 
     ids = np.zeros((nq, w.k), dtype=np.uint64)
     scores = np.zeros((nq, w.k), dtype=np.float32)
@@ -262,20 +284,43 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
                                        _lib.fptr(scores) if with_out else None,
                                        _lib.u32ptr(counts) if with_out else None, C.byref(st)))
 
-    log(f"warmup {args.warmup} steps")
-    for _ in range(args.warmup):
-        step()
-    fetch()
+    def lane_stats(i):
+        s_i = _lib.ScanStatsC()
+        _lib.check(L.mrl_results_fetch(lanes[i][0].handle, lanes[i][2], None, None, None, C.byref(s_i)))
+        return {f: getattr(s_i, f) for f, _ in _lib.ScanStatsC._fields_}
 
-    log(f"timed {args.steps} steps")
-    dev.synchronize()
+    log(f"warmup {args.warmup} steps on each of {len(lanes)} streams")
+    for _ in range(args.warmup):
+        for i in range(len(lanes)):
+            lane_step(i)
+    fetch()
+    for i in range(1, len(lanes)):
+        lane_stats(i)
+
+    log(f"timed {args.steps} steps over {len(lanes)} streams")
+    for d, _, _ in lanes:
+        d.synchronize()
     t_start = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    dev.synchronize()
+    for k in range(args.steps):
+        lane_step(k % len(lanes))
+    for d, _, _ in lanes:
+        d.synchronize()
     t_end = time.perf_counter()
     fetch()
     timed_stats = {f: getattr(st, f) for f, _ in _lib.ScanStatsC._fields_}
+    for i in range(1, len(lanes)):
+        for f, v in lane_stats(i).items():
+            timed_stats[f] += v
+
+    # Latency: the same steps on one stream, one batch in flight at a time.
+    log(f"timed {args.steps} steps on one stream")
+    dev.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dev.synchronize()
+    single_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    fetch(False)
 
     # Per-kernel durations: the same steps again with dispatch-recorded events
     # (kept out of the timed region above).
@@ -300,6 +345,8 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
+        "streams": len(lanes),
+        "single_stream_ms_per_step": round(single_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -365,6 +412,10 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
             args.cpu_seconds if cpu_seconds is None else cpu_seconds, n_threads)
     L.mrl_results_destroy(res)
     plan.close()
+    for d, p, r in lanes[1:]:
+        L.mrl_results_destroy(r)
+        p.close()
+        d.close()
     ix.close()
     return out
 
@@ -522,16 +573,20 @@ def host_boundary_rate(L, _lib, dev, ix, queries, fit, w, ccfg, tr, reps=20):
 
 
 def copy_calibration(mib):
-    """A plain device-to-device copy of known size: under rocprofv3 --pmc its
-    FETCH_SIZE / WRITE_SIZE per dispatch give the counters' scale factor."""
-    import torch
+    """Kernels of known traffic for the PMC byte counters' scale factor, from
+    the library itself (no second HIP runtime in the process):
+    mrl_ctx_evict_caches allocates and fills a buffer of MIB MiB once
+    (k_fill_u32: MIB MiB written) and then reads all of it each call
+    (k_read_sweep: MIB MiB read); five calls."""
+    import mrl_index_amd as m
+    from mrl_index_amd import _lib
     n = mib << 20
-    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
-    dst = torch.empty_like(src)
+    dev = m.default_device()
     for _ in range(5):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    print(json.dumps({"copy_bytes_per_dispatch": n, "dispatches": 5}), flush=True)
+        _lib.check(_lib.lib.mrl_ctx_evict_caches(dev.handle, n))
+    dev.synchronize()
+    print(json.dumps({"k_fill_u32_bytes_written_per_dispatch": n, "k_fill_u32_dispatches": 1,
+                      "k_read_sweep_bytes_read_per_dispatch": n, "k_read_sweep_dispatches": 5}), flush=True)
 
 
 def committed_traffic(kernel, workload):

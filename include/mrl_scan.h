@@ -190,7 +190,13 @@ int mrl_ctx_synchronize(mrl_ctx *ctx);
  * (src/scan.rs:802-810, src/pipeline.rs:77-98, src/segment.rs:187-193).
  * Copies n_blocks * 4096 bytes to HBM once.  verify_crc=1 checks every block
  * like PaxBlock64::verify_crc (src/block.rs:192-197) and fails with
- * MRL_ERR_CORRUPT on a mismatch. */
+ * MRL_ERR_CORRUPT on a mismatch.
+ * Sharing: an index is read-only once made, so every context on its device
+ * may scan it, the way the reference's engine serves `&self` queries from
+ * many threads over one slab (src/engine.rs:572-580).  Each context's scans
+ * run on its own stream, so scans through two contexts overlap on the GPU.
+ * mrl_index_destroy waits for every stream of the device first; a scan
+ * enqueued after it is the caller's error. */
 int mrl_index_upload(mrl_ctx *ctx, const void *blocks, uint64_t n_blocks, int verify_crc,
                      mrl_index **out);
 /* Same, from a segments/NNNNNN.pax file (SegmentReader::open, src/segment.rs:89-162):

@@ -78,6 +78,10 @@ struct mrl_ctx {
   size_t h_stage_cap = 0;
   mrl_results* spare = nullptr;       // result buffers kept between synchronous mrl_scan calls
   uint8_t* scratch = nullptr;         // this device's copy of `scratch` (mrl_scan_noalloc); null: lookup failed
+  // per-scan scratch of the block selection (grown on demand): the cluster x
+  // query table, query norms, block lists and counts of this context's scans
+  uint8_t* d_bsel = nullptr;
+  size_t bsel_bytes = 0;
   // The caller's handle plus one per live object made on this context (index,
   // plans, results, rerank store).  Each of those reaches the context through
   // its `ctx` member when it is destroyed, so the context's stream and
@@ -200,6 +204,8 @@ struct mrl_index {
   uint4* d_recs = nullptr;  // each slot's 64-byte record (kRecWords uint4, slot-major)
   uint64_t n_blocks = 0;
   const uint4* recs() const { return d_recs; }
+  // Pass schedules by K, shared by every context that scans the index.
+  std::mutex levels_mu;
   std::map<uint32_t, LevelPlan> levels;
   // Block bounds (blocks with MRL_BLOCK_FLAG_ONE_CLUSTER): one allocation
   // holding the cluster centers [n_cl][kBndStride], their part norms
@@ -210,11 +216,11 @@ struct mrl_index {
   float* d_cnorm = nullptr;
   uint32_t* d_bcl = nullptr;
   float* d_brad = nullptr;
-  // per-scan scratch of the block selection (grown on demand): the cluster x
-  // query table, query norms, block lists and counts
-  uint8_t* d_bsel = nullptr;
-  size_t bsel_bytes = 0;
 };
+
+// An index is read-only once uploaded, so any context on its device may scan
+// it (each context's scans run on that context's own stream).
+static bool index_usable(const mrl_index* ix, const mrl_ctx* ctx) { return ix->ctx->device == ctx->device; }
 
 struct mrl_plans {
   mrl_ctx* ctx = nullptr;
@@ -342,6 +348,7 @@ static void ctx_free(mrl_ctx* ctx) {
   dev_free(ctx->d_flag_tabs);
   dev_free(ctx->d_crc);
   dev_free(ctx->d_evict);
+  dev_free(ctx->d_bsel);
   for (auto& r : ctx->prof) {
     (void)hipEventDestroy(r.start);
     (void)hipEventDestroy(r.stop);
@@ -613,7 +620,7 @@ extern "C" int mrl_index_block_count(const mrl_index* index, uint64_t* out) {
 
 extern "C" int mrl_index_download(mrl_ctx* ctx, const mrl_index* index, void* out_blocks) {
   if (!ctx || !index || (index->n_blocks && !out_blocks)) return fail(MRL_ERR_INVALID_ARG, "null argument");
-  if (index->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "index belongs to another context");
+  if (!index_usable(index, ctx)) return fail(MRL_ERR_INVALID_ARG, "index lives on another device");
   if (!index->n_blocks) return MRL_OK;
   std::lock_guard<std::mutex> g(ctx->mu);
   HIP_TRY(hipSetDevice(ctx->device));
@@ -640,11 +647,11 @@ extern "C" void mrl_index_destroy(mrl_index* index) {
   if (!index) return;
   mrl_ctx* ctx = index->ctx;
   (void)hipSetDevice(ctx->device);
-  (void)hipStreamSynchronize(ctx->stream);
+  // other contexts' streams may still read it
+  (void)hipDeviceSynchronize();
   dev_free(index->d_blocks);
   dev_free(index->d_recs);
   dev_free(index->d_bounds);
-  dev_free(index->d_bsel);
   delete index;
   ctx_release(ctx);
 }
@@ -732,6 +739,7 @@ static int build_bounds(mrl_ctx* ctx, mrl_index* ix) {
 // then scores every block.  Block ids are arithmetic, so a pass needs no
 // index list.
 static int get_levels(mrl_index* ix, uint32_t K, LevelPlan** out) {
+  std::lock_guard<std::mutex> g(ix->levels_mu);  // map nodes stay put: the pointer outlives the lock
   auto it = ix->levels.find(K);
   if (it != ix->levels.end()) {
     *out = &it->second;
@@ -1187,21 +1195,21 @@ static int enqueue_bound_table(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* pla
   const size_t qn_bytes = ((size_t)n_q * 16 + 255) & ~(size_t)255;
   const size_t count_bytes = ((size_t)2 * n_chunks * 4 + 255) & ~(size_t)255;
   const size_t need = table_bytes + qn_bytes + count_bytes + (size_t)n_chunks * ix->n_blocks * 4;
-  if (need > ix->bsel_bytes) {
+  if (need > ctx->bsel_bytes) {
     HIP_TRY(hipStreamSynchronize(ctx->stream));  // an earlier scan may still read the old lists
-    dev_free(ix->d_bsel);
-    ix->d_bsel = nullptr;
-    ix->bsel_bytes = 0;
-    if (hipMalloc(&ix->d_bsel, need) != hipSuccess) {
-      ix->d_bsel = nullptr;
+    dev_free(ctx->d_bsel);
+    ctx->d_bsel = nullptr;
+    ctx->bsel_bytes = 0;
+    if (hipMalloc(&ctx->d_bsel, need) != hipSuccess) {
+      ctx->d_bsel = nullptr;
       return fail(MRL_ERR_OUT_OF_MEMORY, "block selection");
     }
-    ix->bsel_bytes = need;
+    ctx->bsel_bytes = need;
   }
-  sel->table = reinterpret_cast<float*>(ix->d_bsel);
-  sel->qn = reinterpret_cast<float*>(ix->d_bsel + table_bytes);
-  sel->bcount = reinterpret_cast<uint32_t*>(ix->d_bsel + table_bytes + qn_bytes);
-  sel->blist = reinterpret_cast<uint32_t*>(ix->d_bsel + table_bytes + qn_bytes + count_bytes);
+  sel->table = reinterpret_cast<float*>(ctx->d_bsel);
+  sel->qn = reinterpret_cast<float*>(ctx->d_bsel + table_bytes);
+  sel->bcount = reinterpret_cast<uint32_t*>(ctx->d_bsel + table_bytes + qn_bytes);
+  sel->blist = reinterpret_cast<uint32_t*>(ctx->d_bsel + table_bytes + qn_bytes + count_bytes);
   sel->n_chunks = n_chunks;
   sel->chunk = chunk;
   BoundScanArgs b{};
@@ -1570,8 +1578,8 @@ static PassBuffers results_buffers(mrl_results* r) {
 extern "C" int mrl_scan_async(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* plans,
                               const mrl_scan_config* cfg, const mrl_time_range* time, mrl_results* res) {
   if (!ctx || !index || !plans || !res) return fail(MRL_ERR_INVALID_ARG, "null argument");
-  if (index->ctx != ctx || plans->ctx != ctx || res->ctx != ctx)
-    return fail(MRL_ERR_INVALID_ARG, "objects belong to another context");
+  if (!index_usable(index, ctx)) return fail(MRL_ERR_INVALID_ARG, "index lives on another device");
+  if (plans->ctx != ctx || res->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "objects belong to another context");
   uint32_t K;
   int rc = check_cfg(cfg, &K);
   if (rc) return rc;
@@ -1964,7 +1972,8 @@ extern "C" int mrl_scan_noalloc(mrl_ctx* ctx, const mrl_index* index, const mrl_
                                 const mrl_scan_config* cfg, const mrl_time_range* time, uint64_t* d_out_ids,
                                 float* d_out_scores, uint32_t* d_out_counts, uint32_t* d_out_status) {
   if (!ctx || !index || !plans) return fail(MRL_ERR_INVALID_ARG, "null argument");
-  if (index->ctx != ctx || plans->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "objects belong to another context");
+  if (!index_usable(index, ctx)) return fail(MRL_ERR_INVALID_ARG, "index lives on another device");
+  if (plans->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "objects belong to another context");
   uint32_t K;
   int rc = check_cfg(cfg, &K);
   if (rc) return rc;
@@ -2023,6 +2032,8 @@ extern "C" int mrl_scan_fixed_tau(mrl_ctx* ctx, const mrl_index* index, const mr
                                   const mrl_scan_config* cfg, const mrl_time_range* time, const float* tau,
                                   uint64_t* out_masks, float* out_prefix_ip, float* out_scores) {
   if (!ctx || !index || !plans || !tau) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (!index_usable(index, ctx)) return fail(MRL_ERR_INVALID_ARG, "index lives on another device");
+  if (plans->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "objects belong to another context");
   uint32_t K;
   int rc = check_cfg(cfg, &K);
   if (rc) return rc;
@@ -2081,7 +2092,8 @@ extern "C" int mrl_scan_fixed_tau(mrl_ctx* ctx, const mrl_index* index, const mr
 extern "C" int mrl_index_block_bounds(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* plans,
                                       const mrl_scan_config* cfg, float* out_bounds) {
   if (!ctx || !index || !plans) return fail(MRL_ERR_INVALID_ARG, "null argument");
-  if (index->ctx != ctx || plans->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "objects belong to another context");
+  if (!index_usable(index, ctx)) return fail(MRL_ERR_INVALID_ARG, "index lives on another device");
+  if (plans->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "objects belong to another context");
   uint32_t K;
   int rc = check_cfg(cfg, &K);
   if (rc) return rc;
@@ -2142,6 +2154,8 @@ extern "C" int mrl_scan_mma_bounds(mrl_ctx* ctx, const mrl_index* index, const m
                                    const mrl_scan_config* cfg, const mrl_time_range* time, float* out_upper,
                                    float* out_lower) {
   if (!ctx || !index || !plans) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  if (!index_usable(index, ctx)) return fail(MRL_ERR_INVALID_ARG, "index lives on another device");
+  if (plans->ctx != ctx) return fail(MRL_ERR_INVALID_ARG, "objects belong to another context");
   uint32_t K;
   int rc = check_cfg(cfg, &K);
   if (rc) return rc;
