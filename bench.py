@@ -29,9 +29,10 @@ dominates: 2 x 261 f16 MACs per (query, vector) pair against the dense f16
 MFMA peak, with that launch's HBM rate beside it.  `cold_cache` repeats the
 profiled steps with a 1 GiB read before each (the L2s and the 256 MB
 Infinity Cache evicted).  `reruns_per_step` counts the queries whose final
-floor needed a re-run (safe) or whose list overflowed (dense); those re-runs
-happen at fetch time, outside the timed step, so a non-zero count would mean
-the timed step left work out.
+floor needed a re-run (safe: done on the device inside the step, by two
+launches every sampled scan enqueues) or whose list overflowed (dense: done
+at fetch time, outside the timed step, so a non-zero count would mean the
+timed step left work out).
 `cpu_baseline` times the C restatement of the reference's scan_blocks
 (oracle/, Rayon-equivalent sharding on host threads) on query 0 of the same
 index, on the host's cores and on one thread; the batch figure is the time
@@ -170,8 +171,10 @@ def roofline_of(groups, nq, prof_steps, w, cold=False, scanned=None):
         # instantiation, "plan+scan"); its roofline is taken over all of its
         # launches, as rocprofv3's per-kernel average is: algorithmic bytes
         # per launch = 4096 B x blocks scanned by that launch.
-        scan_ms = [ms for (kind, _), g in groups.items() if kind == "scan" for ms in g["ms"]]
-        scan_blk = [b for (kind, _), g in groups.items() if kind == "scan" for b in g["blocks"]]
+        # (pass -1: the safe-floor re-run, which ends at once unless a query
+        # was flagged, is left out)
+        scan_ms = [ms for (kind, p), g in groups.items() if kind == "scan" and p >= 0 for ms in g["ms"]]
+        scan_blk = [b for (kind, p), g in groups.items() if kind == "scan" and p >= 0 for b in g["blocks"]]
         avg_ms = float(np.mean(scan_ms))
         bytes_per_launch = 4096.0 * float(np.mean(scan_blk))
         achieved = bytes_per_launch / (avg_ms / 1000.0) / 1e9

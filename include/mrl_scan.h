@@ -424,7 +424,7 @@ typedef enum mrl_kernel_kind {
 
 typedef struct mrl_kernel_time {
   int32_t kind;      /* mrl_kernel_kind */
-  int32_t pass;      /* pass index within its scan (0 for plans) */
+  int32_t pass;      /* pass index within its scan (0 for plans; -1: the safe-floor re-run an async scan enqueues) */
   uint32_t n_blocks; /* blocks this launch scanned */
   uint32_t n_queries;
   float ms;          /* kernel duration from events recorded by the dispatch itself */

@@ -1575,6 +1575,9 @@ static PassBuffers results_buffers(mrl_results* r) {
   return pb;
 }
 
+static int enqueue_gated_rerun(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uint32_t n_q,
+                               const ScanParams& sp, uint32_t K, const PassBuffers& pb);
+
 extern "C" int mrl_scan_async(mrl_ctx* ctx, const mrl_index* index, const mrl_plans* plans,
                               const mrl_scan_config* cfg, const mrl_time_range* time, mrl_results* res) {
   if (!ctx || !index || !plans || !res) return fail(MRL_ERR_INVALID_ARG, "null argument");
@@ -1607,7 +1610,13 @@ extern "C" int mrl_scan_async(mrl_ctx* ctx, const mrl_index* index, const mrl_pl
   const bool sampled = mma_ok(plans, plans->n_q, sp, pb) ? !mma_stages(ix->n_blocks, plans->n_q, K).empty()
                                                          : lp->passes.size() > 1;
   res->floor_kind.assign(plans->n_q, sampled ? 1 : 0);
-  return enqueue_scan(ctx, ix, plans, 0, plans->n_q, sp, K, *lp, pb, res->d_stats);
+  if ((rc = enqueue_scan(ctx, ix, plans, 0, plans->n_q, sp, K, *lp, pb, res->d_stats))) return rc;
+  // A query its selection left short of K above the sample's final floor is
+  // re-run on the device at the safe floor (two launches that end at once for
+  // every other query), so the step is complete when the stream is; only an
+  // overflowed list (or a shortfall at the safe floor) is left to
+  // mrl_results_fetch, which re-runs it with no floor.
+  return sampled ? enqueue_gated_rerun(ctx, ix, plans, plans->n_q, sp, K, pb) : MRL_OK;
 }
 
 // Exhaustive single pass for one query whose candidate list overflowed
@@ -1946,7 +1955,11 @@ static int enqueue_gated_rerun(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* pla
       a.excl = 0;
     }
   }
-  HIP_TRY(launch_scan(a, false, ctx->stream));
+  {
+    ProfScope ps(ctx, MRL_KERNEL_SCAN, -1, (uint32_t)ix->n_blocks, n_q);
+    HIP_TRY(launch_scan(a, false, ctx->stream, ps.ev()));
+    ps.commit(true);
+  }
   SelectArgs sa{};
   sa.luts = plans->d_luts;
   sa.cand_score = pb.cand_score;
@@ -1963,8 +1976,11 @@ static int enqueue_gated_rerun(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* pla
   sa.tau_final = pb.tau_hi;
   sa.tau_safe = pb.tau;
   sa.tau_used = pb.tau;
+  sa.floor_record = pb.tau_hi;  // a re-run query's list now stands at the safe floor
   sa.gate = pb.status;
-  HIP_TRY(launch_select(sa, n_q, ctx->stream));
+  ProfScope ps(ctx, MRL_KERNEL_SELECT, -1, 0, n_q);
+  HIP_TRY(launch_select(sa, n_q, ctx->stream, ps.ev()));
+  ps.commit(true);
   return MRL_OK;
 }
 

@@ -308,6 +308,7 @@ struct SelectArgs {
   const float* tau_final; // [n_q] floor of the final pass (with hist)
   const float* tau_safe;  // [n_q] safe floor (with hist)
   const float* tau_used;  // [n_q] the floor the final pass used (null: -inf, no floor)
+  float* floor_record;    // [n_q] or null: a selected query's tau_used is written here
   uint64_t* out_ids;      // [n_q][k]
   float* out_scores;
   uint32_t* out_counts;

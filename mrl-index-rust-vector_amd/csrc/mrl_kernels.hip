@@ -2340,6 +2340,7 @@ __global__ __launch_bounds__(kSelThreads) void k_select(SelectArgs a) {
     const uint32_t short_k = (a.hist && keep < K && s_fl[1] > s_fl[0]) ? 4u : 0u;
     const uint32_t short_f = (!short_k && keep < K && s_fl[2] > -INFINITY) ? 8u : 0u;
     a.out_counts[q] = keep;
+    if (a.floor_record) a.floor_record[q] = s_fl[2];
     a.status[q] = (a.err[q] & 1u) | s_misc[7] | short_k | short_f;
     a.err[q] = 0u;
     if (a.stats && (short_k | short_f | s_misc[7])) {

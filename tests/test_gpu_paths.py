@@ -206,30 +206,83 @@ def test_queries_far_from_unit_norm(device, corpus, nq):
     assert b <= 3 * u + 4 * k * nq, (u, b)
 
 
-def test_mfma_final_floor_shortfall_reruns_at_the_safe_floor(device):
-    """The MFMA path's sampling stage scores every 32nd block.  Each query's
-    near vectors all sit in sampled blocks, so the floor taken from the sample
-    lies above the true K-th score: every query is flagged, re-run at the safe
-    floor, and still returns the exact top K."""
-    rng = np.random.default_rng(16)
-    n_blocks, dims, k, nq = 4096, 192, 64, 8
+def _shortfall_corpus(nq, dims=192, n_blocks=4096, seed=16):
+    """Each query's 40 nearest vectors all sit in blocks that the sampling
+    stages score (block ids that are multiples of 32), so the floor taken
+    from the sample lies above the true K-th score."""
+    rng = np.random.default_rng(seed)
     rows = normalized(rng, n_blocks * 64, dims)
     qs = normalized(rng, nq, dims)
     for qi in range(nq):
-        # 8 slots in each of 5 sampled blocks (block ids that are multiples of 32)
+        # 8 slots in each of 5 sampled blocks
         blks = 32 * (5 * qi + np.arange(40) // 8)
         near = blks * 64 + np.arange(40) % 8
         rows[near] = qs[qi][None, :] + np.float32(0.02) * normalized(rng, 40, dims)
         rows[near] /= np.linalg.norm(rows[near], axis=1, keepdims=True).astype(np.float32)
-    blocks = m.encode_corpus(rows, 8)
-    plan = m.QueryPlan.from_query(qs, dims, device)
-    res = m.scan_batch(m.DeviceIndex.upload(blocks, device), plan, m.ScanConfig(shortlist_cand=k))
-    assert res.stats.reruns_safe >= 1
-    for qi in range(nq):
-        rid, rsc = ora.scan_blocks(blocks, ora.plan_build(qs[qi], dims), ora.scan_config(k))
+    return m.encode_corpus(rows, 8), qs
+
+
+def _check_exact(blocks, qs, res, k):
+    for qi in range(qs.shape[0]):
+        rid, rsc = ora.scan_blocks(blocks, ora.plan_build(qs[qi], qs.shape[1]), ora.scan_config(k))
         n = int(res.counts[qi])
         assert n == len(rid) == k
         assert_topk_equal(res.ids[qi, :n], res.scores[qi, :n], rid, rsc, k, f"q={qi}")
+
+
+def test_mfma_final_floor_shortfall_reruns_at_the_safe_floor(device):
+    """The MFMA path's sampling stage scores every 32nd block; every query is
+    flagged, re-run at the safe floor, and still returns the exact top K."""
+    k = 64
+    blocks, qs = _shortfall_corpus(8)
+    plan = m.QueryPlan.from_query(qs, qs.shape[1], device)
+    res = m.scan_batch(m.DeviceIndex.upload(blocks, device), plan, m.ScanConfig(shortlist_cand=k))
+    assert res.stats.reruns_safe >= 1
+    _check_exact(blocks, qs, res, k)
+
+
+def _records(dev):
+    import ctypes as C
+    L = m._lib.lib
+    kt = (m._lib.KernelTimeC * 512)()
+    n = C.c_uint32()
+    m._lib.check(L.mrl_ctx_profile_collect(dev.handle, kt, 512, C.byref(n)))
+    return [(kt[i].kind, kt[i].pass_) for i in range(min(n.value, 512))]
+
+
+@pytest.mark.parametrize("nq", [1, 8])
+def test_async_scan_reruns_on_the_device(device, nq):
+    """mrl_scan_async itself enqueues the safe-floor re-run (the gated scan
+    and selection, recorded as pass -1): once the stream is done the lists
+    are final, and mrl_results_fetch launches nothing more.  nq 1: the
+    one-query kernel; 8: the MFMA path."""
+    L = m._lib.lib
+    k = 64
+    blocks, qs = _shortfall_corpus(nq, seed=17 + nq)
+    dev = m.Device(0)
+    ix = m.DeviceIndex.upload(blocks, dev)
+    plan = m.QueryPlan.from_query(qs, qs.shape[1], dev)
+    res = m.DeviceResults(nq, k, dev)
+    m._lib.check(L.mrl_ctx_set_profiling(dev.handle, 1))
+    res.scan(ix, plan, m.ScanConfig(shortlist_cand=k))
+    dev.synchronize()
+    before = _records(dev)
+    out = res.fetch()
+    after = _records(dev)
+    m._lib.check(L.mrl_ctx_set_profiling(dev.handle, 0))
+    assert (1, -1) in before and (2, -1) in before, before
+    assert after == [], f"fetch launched {after}"
+    assert out.stats.reruns_safe >= 1 and out.stats.reruns_dense == 0
+    _check_exact(blocks, qs, out, k)
+    # the floors reported are the safe floors the lists were selected at
+    fl = res.floors()
+    assert np.all(np.isfinite(fl))
+    for qi in range(nq):
+        assert out.scores[qi, k - 1] >= fl[qi]
+    res.close()
+    plan.close()
+    ix.close()
+    dev.close()
 
 
 def test_mfma_k4096_sampled_clustered(device):
