@@ -488,6 +488,10 @@ int mrl_device_alloc(mrl_ctx *ctx, size_t bytes, void **out);
 void mrl_device_free(mrl_ctx *ctx, void *d_ptr);
 int mrl_copy_to_device(mrl_ctx *ctx, void *d_dst, const void *src, size_t bytes);
 int mrl_copy_to_host(mrl_ctx *ctx, void *dst, const void *d_src, size_t bytes);
+/* Free and total device memory of the context's GPU (hipMemGetInfo), after
+ * its stream is done; no reference counterpart (callers and tests that check
+ * that a path allocates nothing). */
+int mrl_device_mem_info(mrl_ctx *ctx, uint64_t *free_bytes, uint64_t *total_bytes);
 /* mrl_index_upload for records already in device memory (e.g. written by
  * mrl_encode_corpus_device); no host copy. */
 int mrl_index_from_device(mrl_ctx *ctx, const void *d_blocks, uint64_t n_blocks, mrl_index **out);

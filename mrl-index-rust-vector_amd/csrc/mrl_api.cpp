@@ -2828,6 +2828,18 @@ extern "C" void mrl_device_free(mrl_ctx* ctx, void* d_ptr) {
   (void)hipFree(d_ptr);
 }
 
+extern "C" int mrl_device_mem_info(mrl_ctx* ctx, uint64_t* free_bytes, uint64_t* total_bytes) {
+  if (!ctx || !free_bytes || !total_bytes) return fail(MRL_ERR_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  size_t f = 0, t = 0;
+  HIP_TRY(hipMemGetInfo(&f, &t));
+  *free_bytes = f;
+  *total_bytes = t;
+  return MRL_OK;
+}
+
 extern "C" int mrl_copy_to_device(mrl_ctx* ctx, void* d_dst, const void* src, size_t bytes) {
   if (!ctx || (bytes && (!d_dst || !src))) return fail(MRL_ERR_INVALID_ARG, "null argument");
   std::lock_guard<std::mutex> g(ctx->mu);

@@ -204,6 +204,7 @@ SIGNATURES = {
     "mrl_index_from_device": (C.c_int, [_P, _P, C.c_uint64, _PP]),
     "mrl_device_alloc": (C.c_int, [_P, C.c_size_t, _PP]),
     "mrl_device_free": (None, [_P, _P]),
+    "mrl_device_mem_info": (C.c_int, [_P, _U64, _U64]),
     "mrl_copy_to_device": (C.c_int, [_P, _P, _P, C.c_size_t]),
     "mrl_copy_to_host": (C.c_int, [_P, _P, _P, C.c_size_t]),
     "mrl_rerank_store_create": (C.c_int, [_P, _P, C.c_int, C.c_uint64, C.c_uint32, C.c_int, _PP]),

@@ -3,8 +3,10 @@ existing one (mrl_scan_async + mrl_results_fetch), through the C ABI.
 
 Two calls in a row on one context, the second with a smaller input (fewer
 queries and a smaller index), for the one-query kernel and for the MFMA
-path; a query re-run at the safe floor on the device; the batch limit.
-Results must be identical: ids, scores (bit for bit) and counts."""
+path; queries re-run at the safe floor on the device, alone and in an MFMA
+batch; the batch limit.  Results must be identical: ids, scores (bit for
+bit) and counts; and the device's free memory (hipMemGetInfo) is the same
+before and after the calls."""
 import ctypes as C
 
 import numpy as np
@@ -44,6 +46,12 @@ def noalloc(device, ix, plan, cfg, out):
                                   C.c_void_p(out.status.ptr)))
     device.synchronize()
     return out.fetch()
+
+
+def free_bytes(device):
+    f, t = C.c_uint64(), C.c_uint64()
+    _lib.check(L.mrl_device_mem_info(device.handle, C.byref(f), C.byref(t)))
+    return f.value
 
 
 def existing(device, ix, plan, cfg):
@@ -87,12 +95,15 @@ def test_noalloc_matches_existing_entry_point(device, data, n_first, n_second):
     cfg = m.ScanConfig(shortlist_cand=100)
     out = DevOut(device, n_first, 100)
     p1 = _plan(rows, pf, n_first, n_first, device)
-    assert_same(noalloc(device, ix_big, p1, cfg, out), existing(device, ix_big, p1, cfg), f"first {n_first}")
-    # second call: fewer queries, smaller index, the same array
     out2 = DevOut(device, n_second, 100)
     p2 = _plan(rows, pf, n_second, 1000 + n_second, device)
-    assert_same(noalloc(device, ix_small, p2, cfg, out2), existing(device, ix_small, p2, cfg),
-                f"second {n_second}")
+    free0 = free_bytes(device)
+    g1 = noalloc(device, ix_big, p1, cfg, out)
+    # second call: fewer queries, smaller index, the same array
+    g2 = noalloc(device, ix_small, p2, cfg, out2)
+    assert free_bytes(device) == free0, "the calls changed the device's free memory"
+    assert_same(g1, existing(device, ix_big, p1, cfg), f"first {n_first}")
+    assert_same(g2, existing(device, ix_small, p2, cfg), f"second {n_second}")
 
 
 def test_noalloc_safe_floor_rerun_on_device(device):
@@ -112,9 +123,37 @@ def test_noalloc_safe_floor_rerun_on_device(device):
     ref = existing(device, ix, plan, cfg)
     assert ref.stats.reruns_safe == 1
     out = DevOut(device, 1, k)
+    free0 = free_bytes(device)
     got = noalloc(device, ix, plan, cfg, out)
+    assert free_bytes(device) == free0
     assert_same(got, ref, "safe-floor re-run")
     assert int(got[2][0]) == k
+
+
+def test_noalloc_safe_floor_rerun_in_a_batch(device):
+    """Nine queries (the MFMA path), each with its near vectors only in
+    sampled blocks: every query is flagged and re-run on the device with the
+    one-query kernel, gated per query, inside the full candidate room."""
+    rng = np.random.default_rng(19)
+    n_blocks, dims, k, nq = 4096, 192, 64, 9
+    rows = normalized(rng, n_blocks * 64, dims)
+    qs = normalized(rng, nq, dims)
+    for qi in range(nq):
+        blks = 32 * (5 * qi + np.arange(40) // 8)
+        near = blks * 64 + np.arange(40) % 8
+        rows[near] = qs[qi][None, :] + np.float32(0.02) * normalized(rng, 40, dims)
+        rows[near] /= np.linalg.norm(rows[near], axis=1, keepdims=True).astype(np.float32)
+    ix = m.DeviceIndex.upload(m.encode_corpus(rows, 8), device)
+    plan = m.QueryPlan.from_query(qs, dims, device)
+    cfg = m.ScanConfig(shortlist_cand=k)
+    ref = existing(device, ix, plan, cfg)
+    assert ref.stats.reruns_safe >= 1
+    out = DevOut(device, nq, k)
+    free0 = free_bytes(device)
+    got = noalloc(device, ix, plan, cfg, out)
+    assert free_bytes(device) == free0
+    assert_same(got, ref, "batched safe-floor re-run")
+    assert np.all(got[2] == k)
 
 
 def test_noalloc_rejects_a_batch_beyond_its_scratch(device, data):
