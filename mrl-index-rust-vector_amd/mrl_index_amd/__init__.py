@@ -9,7 +9,7 @@ from .config import EngineConfig, MidCodec, PrefixCodec, ScanConfig, StrataDepth
 from .eden import EdenFit
 from .lowprec import RerankPrecision, RerankStore, rerank_batch, rerank_rows
 from .ring import PendingVector, RingBuffer
-from .pipeline import (IndexManifest, QueryPipeline, ScanPhase, live_slots, open_index, row_id_to_vector_id,
+from .pipeline import (IndexManifest, QueryPipeline, ScanPhase, live_slots, open_index, passage_count, row_id_to_vector_id,
                        scored_hits_to_row_ids)
 from .quantize import encode_block, encode_corpus, encode_corpus_clustered, encode_corpus_device
 from .scan import (Device, DeviceBuffer, DeviceIndex, DeviceResults, QueryPlan, ScanResult, ScanStats, ScoredHit, StageTrace, default_device,
@@ -26,5 +26,5 @@ __all__ = [
     "StageTrace", "default_device", "scan_batch", "scan_blocks", "scan_blocks_stats", "scan_fixed_tau", "scan_mma_bounds",
     "index_block_bounds",
     "SegmentWriter", "read_segment", "DeviceResults", "RerankPrecision", "RerankStore", "rerank_batch",
-    "rerank_rows", "PendingVector", "RingBuffer", "IndexManifest", "open_index", "live_slots", "Shortlist",
+    "rerank_rows", "PendingVector", "RingBuffer", "IndexManifest", "open_index", "passage_count", "live_slots", "Shortlist",
 ]

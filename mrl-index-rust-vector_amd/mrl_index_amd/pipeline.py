@@ -148,22 +148,45 @@ def live_slots(segment_path) -> int:
     return int(VECTORS_PER_BLOCK * tomb.size - int(np.unpackbits(tomb.view(np.uint8)).sum()))
 
 
+PASSAGE_INDEX_FILE = "passages.idx"
+PASSAGE_INDEX_ENTRY_BYTES = 24  # PassageIndexEntry (passage.rs:44)
+
+
+def passage_count(directory) -> Optional[int]:
+    """PassageStore::len() of an index directory (passage.rs:152-202): the
+    number of 24-byte entries in passages.idx; None when the file is absent."""
+    path = os.path.join(str(directory), PASSAGE_INDEX_FILE)
+    if not os.path.exists(path):
+        return None
+    size = os.path.getsize(path)
+    if size % PASSAGE_INDEX_ENTRY_BYTES:
+        raise ValueError(f"{path}: corrupt passage index (size {size} is not a multiple of 24)")
+    return size // PASSAGE_INDEX_ENTRY_BYTES
+
+
 def open_index(directory, device=None, verify_crc: bool = False) -> Tuple[QueryPipeline, DeviceIndex, IndexManifest]:
     """The scan path of IndexEngine::open (engine.rs:132-192) on an index
     directory: manifest.json's config (validated), segments/000001.pax
     streamed into HBM, and the prefix fit -- eden_prefix.json if present,
     else EdenFit::default_prefix(eden_seed) -- when the codec is EdenProd.
-    The reopen check compares the segment's live slots with the manifest's
-    next_passage_id (the passage count it was written with; the passage store
-    itself is not part of the scan path).  Errors raise ValueError (config,
-    JSON, reopen check) or MrlError (segment)."""
+    The reopen check compares the segment's live slots with
+    PassageStore::len(): the entries of passages.idx (24 bytes each, a size
+    that is not a multiple of 24 is PassageError::CorruptIndex;
+    passage.rs:152-202).  A directory without passages.idx (the passage
+    store is not on the scan path) is checked against the manifest's
+    next_passage_id, the passage count it was written with.  Errors raise
+    ValueError (config, JSON, passage index, reopen check) or MrlError
+    (segment)."""
     directory = str(directory)
     man = IndexManifest.load(os.path.join(directory, MANIFEST_FILE))
     man.config.validate()
     seg = os.path.join(directory, SEGMENT_PATH)
     live = live_slots(seg)
-    if live > man.next_passage_id:
-        raise ValueError(f"segment/passage mismatch: {live} live slots vs {man.next_passage_id} passages")
+    n_passages = passage_count(directory)
+    if n_passages is None:
+        n_passages = man.next_passage_id
+    if live > n_passages:
+        raise ValueError(f"segment/passage mismatch: {live} live slots vs {n_passages} passages")
     index = DeviceIndex.open_segment(seg, device or default_device(), verify_crc)
     fit = None
     if man.config.prefix_codec == PrefixCodec.EDEN_PROD:

@@ -131,3 +131,25 @@ def test_open_index_checks_before_the_device(tmp_path):
     m.IndexManifest("3.5.0", m.EngineConfig(shortlist_cand=8), 130, 3).save(tmp_path / "manifest.json")
     with pytest.raises(ValueError, match="shortlist_cand"):
         m.open_index(tmp_path)
+
+
+def test_open_index_reopen_check_uses_the_passage_store(tmp_path):
+    """IndexEngine::open (engine.rs:163-168) compares live slots with
+    PassageStore::len(), the 24-byte entries of passages.idx
+    (passage.rs:152-202); a size that is not a multiple of 24 is corrupt."""
+    rows = np.random.default_rng(3).standard_normal((130, 384)).astype(np.float32)
+    seg = m.SegmentWriter.create(tmp_path / "segments" / "000001.pax")
+    for b in m.encode_corpus(rows):
+        seg.append_block(b)
+    seg.close()
+    # the manifest alone would pass; the passage store holds 129 entries
+    m.IndexManifest("3.5.0", m.EngineConfig(), 130, 3).save(tmp_path / "manifest.json")
+    (tmp_path / "passages.idx").write_bytes(b"\0" * (24 * 129))
+    assert m.passage_count(tmp_path) == 129
+    with pytest.raises(ValueError, match="130 live slots vs 129 passages"):
+        m.open_index(tmp_path)
+    (tmp_path / "passages.idx").write_bytes(b"\0" * (24 * 130 + 5))
+    with pytest.raises(ValueError, match="corrupt passage index"):
+        m.open_index(tmp_path)
+    (tmp_path / "passages.idx").unlink()
+    assert m.passage_count(tmp_path) is None
