@@ -15,6 +15,7 @@
 #ifndef MRL_SCAN_AHEAD
 #define MRL_SCAN_AHEAD 2  // blocks in flight per wave, one-query scan
 #endif
+constexpr uint32_t kRerunWorkgroups = 2048;  // total workgroups of a gated re-run launch
 #ifndef MRL_SCAN_GRID1
 #define MRL_SCAN_GRID1 512u  // workgroups of the one-query scan
 #endif
@@ -3941,10 +3942,17 @@ uint32_t scan_grid(const ScanArgs& a, bool diag) {
   uint32_t grid = (a.n_pos + 4) / 4;  // 4 * grid - 1 >= n_pos waves carry positions
   uint32_t max_grid = res / tiles;
   // A gated re-run scans for the few flagged queries only (the other
-  // queries' workgroups exit at once): each query gets at least a quarter of
-  // the one-query grid, not 1/n_q of the GPU.
-  const uint32_t g_rerun = (res1 < MRL_SCAN_GRID1 ? res1 : MRL_SCAN_GRID1) / 4u;
-  if (a.gate && max_grid < g_rerun) max_grid = g_rerun;
+  // queries' workgroups exit at once): each query gets up to a quarter of
+  // the one-query grid, not 1/n_q of the GPU, within a total of
+  // kRerunWorkgroups so that the launch costs no more than an empty one
+  // when no query is flagged (a grid of 131,072 empty workgroups took 37 us).
+  if (a.gate) {
+    const uint32_t g_one = (res1 < MRL_SCAN_GRID1 ? res1 : MRL_SCAN_GRID1) / 4u;
+    const uint32_t g_budget = kRerunWorkgroups / tiles;
+    uint32_t g = g_one < g_budget ? g_one : g_budget;
+    if (g < 1u) g = 1u;
+    if (max_grid < g) max_grid = g;
+  }
   if (!tile && qt == 1 && !diag && !l0 && max_grid > MRL_SCAN_GRID1) max_grid = MRL_SCAN_GRID1;
   if (!a.excl && max_grid < a.nseg) max_grid = a.nseg;
   if (grid > max_grid) grid = max_grid;
