@@ -1152,9 +1152,27 @@ struct MmaStage {
   uint32_t shift;
   uint32_t n_pos;
 };
-static std::vector<MmaStage> mma_stages(uint64_t B, uint32_t n_q, uint32_t K) {
+// One sampling stage that stores every pair's lower bound serves an index
+// without block bounds when its stride is at least 1/16 and its block-query
+// pairs stay under kOneStageBudget (8.8M vectors x 64 queries: every 256th
+// block, 34,368 bounds per query); config 4: 0.406 -> 0.397 ms per step.  Over
+// block lists such a sample misses the queries' clusters and the floor is too
+// loose to skip blocks (0.165 -> 0.424 ms), so those keep two stages.
+static const uint64_t kOneStageBudget = 40000;
+
+// one_stage_room: the lower bounds a query's row holds (0: two stages).
+static std::vector<MmaStage> mma_stages(uint64_t B, uint32_t n_q, uint32_t K, uint32_t one_stage_room) {
   std::vector<MmaStage> st;
   if (B <= 256) return st;
+  if (one_stage_room) {
+    uint32_t s = 0;
+    while (((B + (1ull << s) - 1) >> s) * 64ull > one_stage_room) ++s;
+    const uint64_t n_pos = (B + (1ull << s) - 1) >> s;
+    if (s >= 4 && n_pos * n_q <= kOneStageBudget) {
+      st.push_back(MmaStage{s, (uint32_t)n_pos});
+      return st;
+    }
+  }
   // the first stage counts every pair: keep it near 4096 x 64 block-queries
   const uint64_t cap = std::min<uint64_t>(128, std::max<uint64_t>(16, 4096 / std::max<uint32_t>(n_q, 1)));
   uint32_t s1 = 0;
@@ -1274,7 +1292,8 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
                             bool rerun_safe, bool fuse_prep = false) {
   hipStream_t s = ctx->stream;
   const uint64_t B = ix->n_blocks;
-  const std::vector<MmaStage> stages = rerun_safe ? std::vector<MmaStage>() : mma_stages(B, n_q, K);
+  const std::vector<MmaStage> stages =
+      rerun_safe ? std::vector<MmaStage>() : mma_stages(B, n_q, K, bounds_ok(ix, plans, sp, pb) ? 0u : pb.nseg * pb.seg_cap);
   const bool sampled = !stages.empty();
   {
     MmaPrepArgs pa{};
@@ -1607,7 +1626,7 @@ extern "C" int mrl_scan_async(mrl_ctx* ctx, const mrl_index* index, const mrl_pl
   LevelPlan* lp;
   if ((rc = get_levels(ix, K, &lp))) return rc;
   const PassBuffers pb = results_buffers(res);
-  const bool sampled = mma_ok(plans, plans->n_q, sp, pb) ? !mma_stages(ix->n_blocks, plans->n_q, K).empty()
+  const bool sampled = mma_ok(plans, plans->n_q, sp, pb) ? !mma_stages(ix->n_blocks, plans->n_q, K, 0u).empty()
                                                          : lp->passes.size() > 1;
   res->floor_kind.assign(plans->n_q, sampled ? 1 : 0);
   if ((rc = enqueue_scan(ctx, ix, plans, 0, plans->n_q, sp, K, *lp, pb, res->d_stats))) return rc;
@@ -2037,7 +2056,7 @@ extern "C" int mrl_scan_noalloc(mrl_ctx* ctx, const mrl_index* index, const mrl_
   LevelPlan* lp;
   if ((rc = get_levels(ix, K, &lp))) return rc;
   const bool sampled =
-      mma_ok(plans, n_q, sp, pb) ? !mma_stages(ix->n_blocks, n_q, K).empty() : lp->passes.size() > 1;
+      mma_ok(plans, n_q, sp, pb) ? !mma_stages(ix->n_blocks, n_q, K, 0u).empty() : lp->passes.size() > 1;
   if ((rc = enqueue_scan(ctx, ix, plans, 0, n_q, sp, K, *lp, pb, nullptr))) return rc;
   // without a sampling pass no query can be flagged
   if (sampled && (rc = enqueue_gated_rerun(ctx, ix, plans, n_q, sp, K, pb))) return rc;

@@ -2734,30 +2734,40 @@ __device__ __forceinline__ void mma_wave_flush(ST& st, const ScanArgs& a, const 
 // query's histogram is built in LDS from its n_s values (the bins and the
 // values that count are those k_scan_mma's counting form would have added to
 // the global histogram), then the floors at `rank` and the safe rank K.
-__global__ __launch_bounds__(256) void k_mma_floors_lb(const float* lbuf, uint32_t lbuf_stride, uint32_t n_s,
-                                                      const float* luts, uint32_t rank, uint32_t safe_rank,
-                                                      float* floor_out, float* safe_out) {
-  __shared__ __align__(16) uint32_t s_h[kHistBins];
+constexpr int kFlbThreads = 1024;
+constexpr int kFlbCopies = 4;  // histogram copies (wave % 4): fewer LDS atomics on one address
+__global__ __launch_bounds__(kFlbThreads) void k_mma_floors_lb(const float* lbuf, uint32_t lbuf_stride, uint32_t n_s,
+                                                              const float* luts, uint32_t rank, uint32_t safe_rank,
+                                                              float* floor_out, float* safe_out) {
+  __shared__ __align__(16) uint32_t s_h[kFlbCopies][kHistBins];
   const uint32_t q = blockIdx.x, tid = threadIdx.x;
+  uint32_t* h = s_h[(tid >> 6) % kFlbCopies];
   const float hinv = luts[(uint64_t)q * kQData + kQdHistInv];
   const float sc = luts[(uint64_t)q * kQData + kQdHistScale];
-  for (uint32_t i = tid; i < (uint32_t)kHistBins; i += 256u) s_h[i] = 0u;
+  for (uint32_t i = tid; i < (uint32_t)(kFlbCopies * kHistBins); i += kFlbThreads) (&s_h[0][0])[i] = 0u;
   __syncthreads();
   const float* row = lbuf + (uint64_t)q * lbuf_stride;
-  for (uint32_t i0 = 0; i0 < n_s; i0 += 256u * 8u) {
+  for (uint32_t i0 = 0; i0 < n_s; i0 += kFlbThreads * 8u) {
     float v[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const uint32_t i = i0 + 256u * (uint32_t)u + tid;
+      const uint32_t i = i0 + kFlbThreads * (uint32_t)u + tid;
       v[u] = i < n_s ? row[i] : -INFINITY;
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u)
-      if (v[u] > -INFINITY) atomicAdd(&s_h[hist_bin(v[u], hinv)], 1u);
+      if (v[u] > -INFINITY) atomicAdd(&h[hist_bin(v[u], hinv)], 1u);
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < (uint32_t)kHistBins; i += kFlbThreads) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int k = 0; k < kFlbCopies; ++k) c += s_h[k][i];
+    s_h[0][i] = c;
   }
   __syncthreads();
   if (tid < 64) {
-    const HistRow r = hist_row(s_h);
+    const HistRow r = hist_row(s_h[0]);
     const float f = floor_of(r, rank) * sc;
     const float sf = floor_of(r, safe_rank) * sc;
     if (tid == 0) {
@@ -4091,7 +4101,7 @@ hipError_t launch_mma_floors_lb(const float* lbuf, uint32_t lbuf_stride, uint32_
                                 hipStream_t s, const LaunchEvents& ev) {
   if (n_q == 0) return hipSuccess;
   if (n_s > lbuf_stride) return hipErrorInvalidValue;
-  launch(k_mma_floors_lb, dim3(n_q), dim3(256), s, ev, lbuf, lbuf_stride, n_s, luts, rank, safe_rank, floor_out,
+  launch(k_mma_floors_lb, dim3(n_q), dim3(kFlbThreads), s, ev, lbuf, lbuf_stride, n_s, luts, rank, safe_rank, floor_out,
          safe_out);
   return hipGetLastError();
 }
