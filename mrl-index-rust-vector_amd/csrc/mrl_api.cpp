@@ -68,6 +68,7 @@ struct mrl_ctx {
   float* d_flag_tabs = nullptr;
   PlanConsts consts;
   bool profiling = false;
+  int s4_policy = MRL_S4_BOUND_AUTO;  // mrl_ctx_set_s4_bound
   std::vector<ProfRecord> prof;       // recorded, not yet collected
   std::vector<hipEvent_t> event_pool; // reusable events
   uint32_t* d_crc = nullptr;          // encoder CRC tables: [256] byte table, then [64][32] carry map
@@ -371,6 +372,15 @@ extern "C" int mrl_ctx_set_profiling(mrl_ctx* ctx, int enable) {
   if (!ctx) return fail(MRL_ERR_INVALID_ARG, "ctx is null");
   std::lock_guard<std::mutex> g(ctx->mu);
   ctx->profiling = enable != 0;
+  return MRL_OK;
+}
+
+extern "C" int mrl_ctx_set_s4_bound(mrl_ctx* ctx, int policy) {
+  if (!ctx) return fail(MRL_ERR_INVALID_ARG, "ctx is null");
+  if (policy != MRL_S4_BOUND_AUTO && policy != MRL_S4_BOUND_ALWAYS && policy != MRL_S4_BOUND_NEVER)
+    return fail(MRL_ERR_INVALID_ARG, "unknown S4 bound policy");
+  std::lock_guard<std::mutex> g(ctx->mu);
+  ctx->s4_policy = policy;
   return MRL_OK;
 }
 
@@ -1400,6 +1410,28 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
   a.blist = nullptr;
   a.bcount = nullptr;
   if (bounded && (rc = enqueue_block_select(ctx, ix, plans, n_q, sel, 1, floor, (uint32_t)B, 0u, &a))) return rc;
+  // The final pass bounds the S4 stage instead of running its four K-steps
+  // when it is expected to append few pairs.  The last sample's floor, at
+  // rank r of its n_pos blocks, leaves about r B / n_pos vectors per query
+  // with a lower bound above it, and about twice that many with an upper
+  // bound above it: 64 r / n_pos appends per 32-vector tile of 64 queries.
+  // The S4 bound lets more pairs through, and past about 2 appends per tile
+  // their epilogue and exact S4 sums cost more than the four K-steps save
+  // (config 4: 1.3, kept; config 3: 3.3, not kept).  On block lists (a
+  // cluster-grouped index) the listed blocks hold the pairs near the floor,
+  // and a re-run at the safe floor appends more: both keep the full tiles.
+  // A wide pass's wave whose appends pass 2 per 1024 pairs (4 per tile of
+  // 64 queries, plus kMmaWideSlack) runs the full tiles for the rest of it.
+  // (mrl_ctx_set_s4_bound: ALWAYS / NEVER override the estimate.)
+  {
+    const uint32_t n_last = stages.empty() ? 0u : stages.back().n_pos;
+    const double per_tile = n_last ? 64.0 * final_rank(K, n_last, B) / n_last : 1e30;
+    const bool cheap = !rerun_safe && !bounded && per_tile < 2.0;
+    const bool fits = sp.strata != MRL_STRATA_FULL64B || sp.w_s4 <= kMmaWideMaxWs4;
+    const int pol = ctx->s4_policy;
+    a.mma_wide = floor && fits && pol != MRL_S4_BOUND_NEVER && (cheap || pol == MRL_S4_BOUND_ALWAYS) ? 1u : 0u;
+    a.wide_lim = 2u;
+  }
   {
     ProfScope ps(ctx, MRL_KERNEL_SCAN, final_pass, (uint32_t)B, n_q);
     HIP_TRY(launch_scan_mma(a, floor ? 1 : 2, s, ps.ev()));
@@ -2204,10 +2236,11 @@ extern "C" int mrl_scan_mma_bounds(mrl_ctx* ctx, const mrl_index* index, const m
   std::lock_guard<std::mutex> g(ctx->mu);
   HIP_TRY(hipSetDevice(ctx->device));
   if (int rc = flush_plans(ctx, plans)) return rc;
-  float *d_u = nullptr, *d_l = nullptr, *d_consts = nullptr;
+  float *d_u = nullptr, *d_l = nullptr, *d_consts = nullptr, *d_tau = nullptr;
   uint32_t *d_row = nullptr, *d_cnt = nullptr, *d_work = nullptr;
   uint4* d_ops = nullptr;
   auto cleanup = [&]() {
+    dev_free(d_tau);
     dev_free(d_u);
     dev_free(d_l);
     dev_free(d_row);
@@ -2262,6 +2295,46 @@ extern "C" int mrl_scan_mma_bounds(mrl_ctx* ctx, const mrl_index* index, const m
   if (e == hipSuccess) e = hipMemcpyAsync(l.data(), d_l, nq * N * 4, hipMemcpyDeviceToHost, ctx->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(row.data(), d_row, nq * N * 4, hipMemcpyDeviceToHost, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  // ALWAYS: the S4-bounded final pass, at a floor one below every pair's
+  // lower bound so that every active pair passes it and is made exact.  At
+  // most 4 queries per launch: a 32-vector tile then appends at most 128
+  // pairs, which the wave's staging region holds (no pair is written out
+  // straight with the bound still in it).
+  const bool wide = ctx->s4_policy == MRL_S4_BOUND_ALWAYS &&
+                    (sp.strata != MRL_STRATA_FULL64B || sp.w_s4 <= kMmaWideMaxWs4);
+  if (wide && e == hipSuccess) {
+    std::vector<float> tau(nq);
+    for (uint64_t q = 0; q < nq; ++q) {
+      float mn = std::numeric_limits<float>::infinity();
+      for (uint64_t i = 0; i < std::min<uint64_t>(cnt[q], N); ++i)
+        if (std::isfinite(l[q * N + i])) mn = std::min(mn, l[q * N + i]);
+      tau[q] = std::isfinite(mn) ? mn - 1.0f : -1.0f;
+    }
+    e = hipMalloc(&d_tau, nq * 4);
+    if (e == hipSuccess) e = hipMemcpyAsync(d_tau, tau.data(), nq * 4, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(d_cnt, 0, nq * 4, ctx->stream);
+    for (uint64_t g0 = 0; g0 < nq && e == hipSuccess; g0 += 4) {
+      ScanArgs w = a;
+      w.plans = plans->d_plans + g0;
+      w.luts = plans->d_luts + g0 * kQData;
+      w.n_q = (uint32_t)std::min<uint64_t>(4, nq - g0);
+      w.mma_ops = d_ops + g0 * 2 * kMmaSteps;
+      w.mma_consts = d_consts + g0 * kMcCount;
+      w.tau = d_tau + g0;
+      w.cand_score = d_u + g0 * N;
+      w.cand_lower = d_l + g0 * N;
+      w.cand_row = d_row + g0 * N;
+      w.seg_count = d_cnt + g0;
+      w.mma_wide = 1u;
+      w.wide_lim = 1u << 20;  // no wave returns to the full tiles
+      e = launch_scan_mma(w, 1, ctx->stream);
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(cnt.data(), d_cnt, nq * 4, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(u.data(), d_u, nq * N * 4, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(l.data(), d_l, nq * N * 4, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(row.data(), d_row, nq * N * 4, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  }
   cleanup();
   if (e != hipSuccess) return fail(MRL_ERR_HIP, std::string("MFMA bounds: ") + hipGetErrorString(e));
   const float nan = std::numeric_limits<float>::quiet_NaN();

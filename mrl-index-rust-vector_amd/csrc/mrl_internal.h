@@ -175,6 +175,9 @@ enum {
   kMcCount = 16
 };
 constexpr float kMmaSafe = 4096.0f;  // larger |scale|, mid_n, high_n or |offset|: always a candidate
+// The final pass may replace the four S4 K-steps by a bound of the S4 score
+// (ScanArgs::mma_wide) for stratum weights up to this value.
+constexpr float kMmaWideMaxWs4 = 4.0f;
 
 struct MmaPrepArgs {
   const mrl_query_plan* plans;
@@ -250,7 +253,20 @@ struct ScanArgs {
   // query's histogram from the lists and a.hist.
   uint32_t* lcount;
   uint32_t lcap;
+  // Final MFMA pass (MODE 1) with mma_wide set (the kernel's WIDE
+  // instantiation): the tiles run 13 K-steps and
+  // the error step's K-half 1 carries a bound of the S4 stage score in place
+  // of the four S4 steps; each pair that passes is staged with the flag
+  // kMmaWideFlag and its S4 sum is taken from the query operands and the
+  // slot's S4 bits before it is written out.  A wave whose appends exceed
+  // wide_lim per 1024 pairs it scanned (plus kMmaWideSlack) runs the 17
+  // K-steps for the rest of the pass.
+  uint32_t mma_wide;
+  uint32_t wide_lim;
 };
+constexpr uint8_t kMmaWideFlag = 0x80;   // staged query index: the tile value holds the S4 bound
+constexpr uint8_t kMmaDropped = 0xff;    // staged entry dropped (upper bound below the floor)
+constexpr uint32_t kMmaWideSlack = 16;
 constexpr int kMaxListWg = 1024;  // workgroup lists per query a later sampling stage may keep
 
 // Exact finishing of the MFMA path.  k_finish, one workgroup per query: a

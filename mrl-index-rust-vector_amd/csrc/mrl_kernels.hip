@@ -2438,6 +2438,7 @@ __device__ __forceinline__ void mma_prep_body(const MmaPrepArgs& a, uint32_t q, 
   float* s_ex = sh.ex;
   const uint32_t lane = threadIdx.x;
   float s = 0.0f, psum = 0.0f;  // operand scale and prefix_sum, for the operand step below
+  float s4b = 0.0f;             // bound on |S4 stage score| per unit high_n (score units)
   if (lane < 64) {
     const mrl_query_plan* p = a.plans + q;
     const float* qd = a.luts + (uint64_t)q * kQData;
@@ -2479,6 +2480,10 @@ __device__ __forceinline__ void mma_prep_body(const MmaPrepArgs& a, uint32_t q, 
     const float eP = (cbm * l1w * (1.0f / 600.0f) + t25 * (64.0f * cbm + 1.0f) * inv_s) * up;
     const float e1 = s1on ? (l1w2 * (1.0f / 1800.0f) + t25 * 65.0f * inv_s) * up : 0.0f;
     const float e4 = tail ? (ws4 * l1w4 * (1.0f / 1800.0f) + t25 * (32.0f * ws4 + 1.0f) * inv_s) * up : 0.0f;
+    // |w_s4 * S4| <= w_s4 * sum|w4| / 2 (w4 = 2 pos, S4 = sum pos (2 b - 1)); raised by 2^-12 for the
+    // f32 sum over 64 terms above and the reference's own rounding of S4 (sequential, 65 terms)
+    // (the final pass bounds S4 only for w_s4 <= kMmaWideMaxWs4: then s * s4b / 64 < 2^15, a finite f16)
+    s4b = tail && ws4 <= kMmaWideMaxWs4 ? ws4 * l1w4 * 0.5f * (1.0f + 1.0f / 4096.0f) : 0.0f;
     const float eO = eden ? 0.0f : (fabsf(psum) * (1.0f / 1700.0f) + t25 * 2.0f * inv_s) * up;
     const float e0 =
         (fabsf(mean) * (1.0f / 16384.0f) + t25 * (l1w + l1w2 + l1w4 + fabsf(psum) + eP + e1 + e4 + eO)) * up +
@@ -2522,9 +2527,10 @@ __device__ __forceinline__ void mma_prep_body(const MmaPrepArgs& a, uint32_t q, 
       if (st < 16) v = src[mma_dim(st, kh, e)];
       else if (kh == 0 && e < 4) v = s_ex[e];   // error columns
       else if (kh == 0 && e == 4) v = psum;     // offset * prefix_sum
+      else if (kh == 1) v = s4b * (1.0f / 64.0f);  // S4 bound, 8 columns (f16 of 8 high_n, rounded up)
       const float x = s * v;
       uint32_t h = f32_to_f16(x);
-      if (st == 16 && e < 4 && h2f((uint16_t)h) < x) h += 1u;  // f16_up: magnitude no smaller than x
+      if (st == 16 && (e < 4 || kh == 1) && h2f((uint16_t)h) < x) h += 1u;  // f16_up: magnitude no smaller than x
       hv[e] = h;
     }
     a.ops[(uint64_t)q * (2 * kMmaSteps) + lane] =
@@ -2611,6 +2617,7 @@ struct MmaStaging {
   static constexpr int kWaves = W;
   static constexpr int kCap = CAP;  // entries per wave
   uint32_t n[W];
+  uint32_t drop;            // wide entries dropped once made exact (taken off the append count)
   uint32_t cnt[kMmaQ];      // final flush: entries per query of the workgroup
   uint32_t base[kMmaQ];
   uint32_t wcnt[W][kMmaQ];  // a wave's own flush: entries per query
@@ -2620,45 +2627,106 @@ struct MmaStaging {
   uint8_t q[W * CAP];
 };
 
-// Appends (u, l, row) of query q0 + qi (per lane) for the lanes in pm to this
-// wave's region at *fill (wave-uniform); past the region's room, straight
-// into the query's segment (one global atomic per lane).
-// Bounds (U, L) of a staged pair from its tile value acc = s (U' - tau): the
-// query's constants qk = {tau, 1/s, eP, e1, e4, eO, e0, ok} and the slot's
-// meta from its record.  A slot beyond the operand range gets (+inf, -inf).
-__device__ __forceinline__ void mma_bounds(float acc, const uint4* recs, uint32_t row, const float* qk,
-                                           const float* s_flag, float* U, float* L) {
-  const uint4 x = recs[(uint64_t)row * kRecWords + kRecS4Meta];
-  const float m_scale = h2f((uint16_t)(x.z & 0xffffu)), m_offset = h2f((uint16_t)(x.z >> 16));
+// The meta values of a slot's record word kRecS4Meta as the tiles use them.
+struct MmaMeta {
+  float m_scale, m_offset, mid_n, hn;
+  bool safe;  // every magnitude within the operand range
+};
+__device__ __forceinline__ MmaMeta mma_meta(const uint4 x, const float* s_flag) {
+  MmaMeta m;
+  m.m_scale = h2f((uint16_t)(x.z & 0xffffu));
+  m.m_offset = h2f((uint16_t)(x.z >> 16));
   const float tn = fmaxf(h2f((uint16_t)(x.w & 0xffffu)), 0.0f);
   const uint32_t fl = (x.w >> 16) & 0xffu;
-  const float mid_n = fmaxf(s_flag[256 + fl] * tn, 1e-6f);
-  const float hn = fmaxf(fmaxf(s_flag[fl] * tn, 0.0f), 1e-6f);
-  const bool safe = fabsf(m_scale) <= kMmaSafe && mid_n <= kMmaSafe && hn <= kMmaSafe && fabsf(m_offset) <= kMmaSafe;
+  m.mid_n = fmaxf(s_flag[256 + fl] * tn, 1e-6f);
+  m.hn = fmaxf(fmaxf(s_flag[fl] * tn, 0.0f), 1e-6f);
+  m.safe = fabsf(m.m_scale) <= kMmaSafe && m.mid_n <= kMmaSafe && m.hn <= kMmaSafe && fabsf(m.m_offset) <= kMmaSafe;
+  return m;
+}
+
+// Bounds (U, L) of a staged pair from its tile value acc = s (U' - tau): the
+// query's constants qk = {tau, 1/s, eP, e1, e4, eO, e0, ok} and the slot's
+// record word x = kRecS4Meta.  A slot beyond the operand range gets (+inf, -inf).
+// wpc != 0: the tile value still holds the S4 bound 8 h8 wpc (wpc = the
+// query's bound column, h8 = 8 high_n rounded up to f16): U stays, L drops by
+// twice the bound.
+__device__ __forceinline__ void mma_bounds_x(float acc, const uint4 x, const float* qk, const float* s_flag, float* U,
+                                             float* L, float wpc = 0.0f) {
+  const MmaMeta m = mma_meta(x, s_flag);
   float u = INFINITY, l = -INFINITY;
-  if (safe) {
+  if (m.safe) {
     const float4 k0 = *reinterpret_cast<const float4*>(qk);      // tau, 1/s, eP, e1
     const float4 k1 = *reinterpret_cast<const float4*>(qk + 4);  // e4, eO, e0, ok
     const float tau = k0.x;
     const float u0 = tau + acc * k0.y;
-    const float E = fabsf(m_scale) * k0.z + mid_n * k0.w + hn * k1.x + fabsf(m_offset) * k1.y + k1.z;
+    const float E = fabsf(m.m_scale) * k0.z + m.mid_n * k0.w + m.hn * k1.x + fabsf(m.m_offset) * k1.y + k1.z;
     const float mg = (fabsf(u0) + fabsf(tau)) * (1.0f / 4194304.0f);
+    const float W = wpc != 0.0f ? (8.0f * h2f((uint16_t)f16_up(8.0f * m.hn))) * wpc * k0.y : 0.0f;
     u = u0 + mg;
-    l = (u0 - 2.0f * E * (1.0f + 1.0f / 1048576.0f)) - mg;
+    l = (u0 - 2.0f * (E + W) * (1.0f + 1.0f / 1048576.0f)) - mg;
     if (!(u == u)) u = INFINITY;
     if (!(l == l)) l = -INFINITY;
   }
   *U = u;
   *L = l;
 }
+__device__ __forceinline__ void mma_bounds(float acc, const uint4* recs, uint32_t row, const float* qk,
+                                           const float* s_flag, float* U, float* L, float wpc = 0.0f) {
+  mma_bounds_x(acc, recs[(uint64_t)row * kRecWords + kRecS4Meta], qk, s_flag, U, L, wpc);
+}
+
+// The tile value of a pair from a final pass that bounded S4 (see
+// ScanArgs::mma_wide), made what the 17 K-steps would give with the e4
+// column counted twice (mma_bounds takes 2 e4 in such a pass): the eight
+// bound columns 8 h8 * piece (h8 = 8 high_n rounded up to f16, piece =
+// s * the query's S4 bound / 64 rounded up) are replaced by the S4 steps'
+// sum, V * sum_d A4[d] (2 b_d - 1) with V = f16(high_n * w_s4 / 2) and A4 the
+// query's S4 operands (in qa, steps 12..15, element order of mma_dim).
+// The products are exact and the few f32 roundings here are far inside the
+// second e4 column.  A slot beyond the operand range keeps its value.
+__device__ __forceinline__ float mma_tighten_x(float acc, const uint4 x, uint32_t qi, const uint4* qa,
+                                               const float* s_flag, float ws4) {
+  const MmaMeta m = mma_meta(x, s_flag);
+  if (!m.safe) return acc;
+  const float hn = m.hn;
+  const uint32_t ln = qi & 31u;
+  const uint4* qt = qa + (uint64_t)(qi >> 5) * (kMmaSteps * 64);
+  const float c4 = h2f((uint16_t)(qt[16 * 64 + ln].y & 0xffffu));        // e4 column (K-half 0, element 2)
+  const float pc = h2f((uint16_t)(qt[16 * 64 + 32 + ln].x & 0xffffu));   // bound column (K-half 1)
+  const float hn16 = h2f((uint16_t)f16_bits(hn));
+  const float h8 = h2f((uint16_t)f16_up(8.0f * hn));
+  const float V = h2f((uint16_t)f16_bits(0.5f * hn * ws4));
+  float S = 0.0f;
+#pragma unroll
+  for (int kh = 0; kh < 2; ++kh) {
+    const uint32_t bits = kh ? x.y : x.x;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const uint4 a4 = qt[(12 + st) * 64 + 32 * kh + ln];
+      const uint32_t w[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = h2f((uint16_t)(w[j] & 0xffffu)), hi = h2f((uint16_t)(w[j] >> 16));
+        S += ((bits >> (4 * st + j)) & 1u) ? lo : -lo;
+        S += ((bits >> (4 * st + j + 16)) & 1u) ? hi : -hi;
+      }
+    }
+  }
+  const float d = fmaf(hn16, c4, -((8.0f * h8) * pc));
+  return fmaf(V, S, acc + d);
+}
 
 // Stages the pairs of pm (one query per lane: qi) as (row, tile value, query)
 // in this wave's region; past its end they go straight to the query's
-// segment, bounds formed here.
+// segment, bounds formed here.  In a pass that bounded S4 (wide) a staged
+// pair's query index carries kMmaWideFlag (the flush makes it exact); a
+// wide pair written straight out keeps the bound, its lower bound widened
+// by twice the bound.
 template <typename ST>
 __device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, const float (*s_qk)[8], const float* s_flag,
                                            int wave, uint32_t* fill, uint32_t q0, uint32_t qi, uint32_t seg,
-                                           uint64_t pm, float acc, uint32_t row) {
+                                           uint64_t pm, float acc, uint32_t row, bool wide, const uint4* qa,
+                                           float ws4) {
   const uint32_t lane = __lane_id();
   const uint32_t base = *fill;
   *fill = base + (uint32_t)__popcll(pm);
@@ -2668,7 +2736,7 @@ __device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, const floa
     const uint32_t e = (uint32_t)wave * ST::kCap + slot;
     st.row[e] = row;
     st.acc[e] = acc;
-    st.q[e] = (uint8_t)qi;
+    st.q[e] = (uint8_t)(wide ? (qi | kMmaWideFlag) : qi);
   } else {
     // (the query index passes through an empty asm so the compiler cannot
     // hoist this rare path's addresses out of the scan loop into registers)
@@ -2678,7 +2746,11 @@ __device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, const floa
     const uint32_t g = atomicAdd(a.seg_count + sq, 1u);
     if (g < a.seg_cap) {
       float u, l;
-      mma_bounds(acc, a.recs, row, s_qk[qq - q0], s_flag, &u, &l);
+      // a wide pair keeps the S4 bound: its lower bound is widened by it twice
+      const float wpc = wide ? h2f((uint16_t)(qa[(uint64_t)((qq - q0) >> 5) * (kMmaSteps * 64) + 16 * 64 + 32 +
+                                                  ((qq - q0) & 31u)].x & 0xffffu))
+                             : 0.0f;
+      mma_bounds(acc, a.recs, row, s_qk[qq - q0], s_flag, &u, &l, wpc);
       const uint64_t i = sq * a.seg_cap + g;
       a.cand_score[i] = u;
       a.cand_lower[i] = l;
@@ -2687,23 +2759,50 @@ __device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, const floa
   }
 }
 
+// A staged entry of a pass that bounded S4 (flag kMmaWideFlag) is made
+// exact (mma_tighten_x, x = its record word); one whose upper bound is then
+// below the floor is marked kMmaDropped.
+template <typename ST>
+__device__ __forceinline__ void mma_stage_tighten(ST& st, const float* s_flag, uint32_t i, const uint4 x,
+                                                  const uint4* qa, float ws4) {
+  const uint32_t q8 = st.q[i];
+  if (!(q8 & kMmaWideFlag)) return;
+  const float t = mma_tighten_x(st.acc[i], x, q8 & 0x7fu, qa, s_flag, ws4);
+  st.acc[i] = t;
+  if (t < 0.0f) {
+    st.q[i] = kMmaDropped;
+    atomicAdd(&st.drop, 1u);
+  } else {
+    st.q[i] = (uint8_t)(q8 & 0x7fu);
+  }
+}
+
 // Writes out the n entries of this wave's region: a count per query in LDS,
-// one global reservation per query with entries, then each entry's bounds.
+// one global reservation per query with entries, then each entry's bounds
+// (wide entries made exact first).
 template <typename ST>
 __device__ __forceinline__ void mma_wave_flush(ST& st, const ScanArgs& a, const float (*s_qk)[8],
                                                const float* s_flag, int wave, uint32_t n, uint32_t q0,
-                                               uint32_t seg) {
+                                               uint32_t seg, bool wide, const uint4* qa, float ws4) {
   constexpr int kPer = ST::kCap / 64;
   const uint32_t lane = __lane_id();
   uint32_t* cnt = st.wcnt[wave];
   uint32_t* base = st.wbase[wave];
   cnt[lane] = 0u;
+  if (wide) {
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const uint32_t e = lane + 64u * (uint32_t)k, i = (uint32_t)wave * ST::kCap + e;
+      if (e < n) mma_stage_tighten(st, s_flag, i, a.recs[(uint64_t)st.row[i] * kRecWords + kRecS4Meta], qa, ws4);
+    }
+  }
   wave_lds_sync();
   uint32_t rk[kPer];
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const uint32_t e = lane + 64u * (uint32_t)k;
-    rk[k] = e < n ? atomicAdd(&cnt[st.q[(uint32_t)wave * ST::kCap + e]], 1u) : 0u;
+    const uint32_t q8 = e < n ? st.q[(uint32_t)wave * ST::kCap + e] : kMmaDropped;
+    rk[k] = q8 != kMmaDropped ? atomicAdd(&cnt[q8], 1u) : 0u;
   }
   wave_lds_sync();
   const uint32_t c = cnt[lane];
@@ -2712,8 +2811,8 @@ __device__ __forceinline__ void mma_wave_flush(ST& st, const ScanArgs& a, const 
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const uint32_t e = lane + 64u * (uint32_t)k;
-    if (e < n) {
-      const uint32_t i = (uint32_t)wave * ST::kCap + e;
+    const uint32_t i = (uint32_t)wave * ST::kCap + e;
+    if (e < n && st.q[i] != kMmaDropped) {
       const uint32_t qi = st.q[i];
       const uint32_t g = base[qi] + rk[k];
       if (g < a.seg_cap) {
@@ -2860,8 +2959,9 @@ __global__ __launch_bounds__(kSegThreads) void k_mma_floors_seg(const float* lbu
 // sampling pass listing the counted lower bounds per workgroup (a.lcount)
 // for k_mma_floors_seg; 1: final pass,
 // pairs with U >= the floor in a.tau are appended; 2: single pass, every
-// active pair is appended.
-template <int NQT, int MODE>
+// active pair is appended.  WIDE (MODE 1): the final pass that bounds the
+// S4 stage (ScanArgs::mma_wide).
+template <int NQT, int MODE, bool WIDE = false>
 __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   constexpr int WPG = kMmaWaves;  // waves per workgroup
   constexpr bool SAMPLE = MODE == 0 || MODE == 3 || MODE == 4;  // a sampling pass (lower bounds, no appends)
@@ -2914,6 +3014,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   }
   if (tid < kStatCount) s_stats[tid] = 0u;
   if (tid < WPG) s_st.n[tid] = 0u;
+  if (tid == 0) s_st.drop = 0u;
   if (tid < kMmaQ) {
     const int qi = tid;
     s_st.cnt[qi] = 0u;
@@ -2940,7 +3041,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
       qk[1] = mc[kMcInvS];
       qk[2] = mc[kMcEP];
       qk[3] = mc[kMcE1];
-      qk[4] = mc[kMcE4];
+      qk[4] = (MODE == 1 && WIDE) ? 2.0f * mc[kMcE4] : mc[kMcE4];  // mma_tighten's second e4 column
       qk[5] = mc[kMcEO];
       qk[6] = e0q;
       qk[7] = ok ? 1.0f : 0.0f;
@@ -2981,6 +3082,13 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   const float ws4 = a.sp.strata == MRL_STRATA_FULL64B ? a.sp.w_s4 : 0.0f;
   const uint32_t seg = blockIdx.x % a.nseg;
   uint32_t c_blocks = 0, c_active = 0, c_app = 0;
+  // final pass bounding S4 (wave-uniform; off for good once the wave's
+  // appends pass its allowance)
+  constexpr bool wide_pass = MODE == 1 && WIDE;
+  bool wide = wide_pass;
+  uint32_t w_items = 0, w_app = 0;
+  const uint32_t w_lim = (32u * (uint32_t)nq * a.wide_lim) >> 10;  // appends per item
+  const uint4* qa = &s_qa[0][0][0];
   uint32_t fill = 0;  // entries of this wave's staging region (wave-uniform)
   // bit 16 t + r: register r of tile t belongs to a query of the batch with
   // usable operands (read only on the rare paths that force candidates)
@@ -3084,29 +3192,40 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
             d[0] = (sc_b & 0x7fffu) | (f16_bits(mid_n) << 16);
             d[1] = f16_bits(hn) | ((of_b & 0x7fffu) << 16);
             d[2] = of_b;
+          } else if (MODE == 1 && wide) {
+            // the S4 bound columns: 8 high_n rounded up (as mma_tighten)
+            d[0] = d[1] = d[2] = d[3] = f16_up(8.0f * hn) * 0x10001u;
           }
         }
         return make_uint4(d[0], d[1], d[2], d[3]);
       };
-      // The query operands of step st + 1 are requested before step st's
+      // The query operands of step nst are requested before step st's
       // MFMAs, so their LDS latency overlaps the matrix work.
       uint4 an[NQT];
 #pragma unroll
       for (int t = 0; t < NQT; ++t) an[t] = qa_raw(t, 0);
-#pragma unroll
-      for (int st = 0; st < kMmaSteps; ++st) {
+      auto kstep = [&](int st, int nst) {
         uint4 ac[NQT];
 #pragma unroll
         for (int t = 0; t < NQT; ++t) ac[t] = an[t];
-        if (st + 1 < kMmaSteps) {
+        if (nst >= 0) {
 #pragma unroll
-          for (int t = 0; t < NQT; ++t) an[t] = qa_raw(t, st + 1);
+          for (int t = 0; t < NQT; ++t) an[t] = qa_raw(t, nst);
         }
         const uint4 bo = vec_op(st);
 #pragma unroll
         for (int t = 0; t < NQT; ++t)
           acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ac[t]), as_h8(bo), acc[t], 0, 0, 0);
+      };
+#pragma unroll
+      for (int st = 0; st < 11; ++st) kstep(st, st + 1);
+      kstep(11, MODE == 1 && wide ? 16 : 12);
+      if (!(MODE == 1 && wide)) {  // else the S4 steps' score is bounded in step 16
+#pragma unroll
+        for (int st = 12; st < 16; ++st) kstep(st, st + 1);
       }
+      kstep(16, -1);
+      static_assert(kMmaSteps == 17, "the step schedule above assumes prefix 4, S1 8, S4 4, error 1");
       // Register r of tile t holds query 32 t + 8 (r / 4) + 4 kh + r % 4.
       if constexpr (MODE == 3) {
         // store every pair's lower bound (sample 32 it + lane % 32 of the query)
@@ -3190,9 +3309,11 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
         // MODE 2 takes every present query's register as it is.
         // a region that may not hold this tile's pairs is written out first
         if (fill > (uint32_t)Staging::kCap - 128u) {
-          mma_wave_flush(s_st, a, s_qk, s_flag, wave, min(fill, (uint32_t)Staging::kCap), q0, seg);
+          mma_wave_flush(s_st, a, s_qk, s_flag, wave, min(fill, (uint32_t)Staging::kCap), q0, seg, wide_pass, qa,
+                         ws4);
           fill = 0u;
         }
+        const uint32_t c_app0 = c_app;
         const uint64_t actm = ballot(act);
         if (MODE == 1 && ballot(act && !safe) != 0) {
 #pragma unroll
@@ -3220,9 +3341,15 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
               if (pm == 0) continue;
               const int qi = 32 * t + 8 * (r >> 2) + 4 * (int)kh + (r & 3);
               c_app += (uint32_t)__popcll(pm);
-              mma_append(s_st, a, s_qk, s_flag, wave, &fill, q0, (uint32_t)qi, seg, pm, acc[t][r], row);
+              mma_append(s_st, a, s_qk, s_flag, wave, &fill, q0, (uint32_t)qi, seg, pm, acc[t][r], row,
+                         MODE == 1 && wide, qa, ws4);
             }
           }
+        if (MODE == 1 && wide) {
+          ++w_items;
+          w_app += c_app - c_app0;
+          if (w_app > w_items * w_lim + kMmaWideSlack) wide = false;
+        }
       }
     }
     cur = nxt;
@@ -3241,34 +3368,57 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   if constexpr (!SAMPLE) {
     if (lane == 0) s_st.n[wave] = min(fill, (uint32_t)Staging::kCap);
     __syncthreads();
-    for (int w = 0; w < WPG; ++w)
-      for (uint32_t i = tid; i < s_st.n[w]; i += 64 * WPG) atomicAdd(&s_st.cnt[s_st.q[w * Staging::kCap + i]], 1u);
+    // Every staged entry of the workgroup: entry tid + 64 WPG k of the
+    // regions laid end to end; the record words are loaded in one round.
+    constexpr int kFl = Staging::kCap / 64;
+    uint4 xr[kFl];
+    uint32_t ie[kFl];  // staging index, or ~0u past a region's fill
+#pragma unroll
+    for (int k = 0; k < kFl; ++k) {
+      const uint32_t j = (uint32_t)tid + 64u * WPG * (uint32_t)k;
+      const uint32_t w = j / (uint32_t)Staging::kCap, e = j % (uint32_t)Staging::kCap;
+      ie[k] = e < s_st.n[w] ? j : ~0u;
+      xr[k] = ie[k] != ~0u ? a.recs[(uint64_t)s_st.row[j] * kRecWords + kRecS4Meta] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (wide_pass) {
+#pragma unroll
+      for (int k = 0; k < kFl; ++k)
+        if (ie[k] != ~0u) mma_stage_tighten(s_st, s_flag, ie[k], xr[k], qa, ws4);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < kFl; ++k)
+      if (ie[k] != ~0u && s_st.q[ie[k]] != kMmaDropped) atomicAdd(&s_st.cnt[s_st.q[ie[k]]], 1u);
     __syncthreads();
     if (tid < nq) {
       const uint32_t c = s_st.cnt[tid];
       s_st.base[tid] = c ? atomicAdd(a.seg_count + (uint64_t)(q0 + tid) * a.nseg + seg, c) : 0u;
       s_st.cnt[tid] = 0u;
     }
-    if (a.stats && tid < kStatCount && s_stats[tid]) {
+    if (a.stats && tid < kStatCount) {
+      // appends count the pairs whose bound reached the floor: less those a wide pass dropped
+      const uint32_t v = s_stats[tid] - (tid == kStatPrefix ? s_st.drop : 0u);
       const uint32_t copy = (blockIdx.x + blockIdx.y * gridDim.x) % (uint32_t)kStatCopies;
-      atomicAdd(a.stats + copy * kStatCount + tid, (unsigned long long)s_stats[tid]);
+      if (v) atomicAdd(a.stats + copy * kStatCount + tid, (unsigned long long)v);
     }
     __syncthreads();
-    for (int w = 0; w < WPG; ++w)
-      for (uint32_t i0 = tid; i0 < s_st.n[w]; i0 += 64 * WPG) {
-        const uint32_t i = (uint32_t)w * Staging::kCap + i0;
-        const uint32_t qi = s_st.q[i];
-        const uint32_t g = s_st.base[qi] + atomicAdd(&s_st.cnt[qi], 1u);
-        if (g < a.seg_cap) {
-          const uint64_t e = ((uint64_t)(q0 + qi) * a.nseg + seg) * a.seg_cap + g;
-          const uint32_t row = s_st.row[i];
-          float u, l;
-          mma_bounds(s_st.acc[i], a.recs, row, s_qk[qi], s_flag, &u, &l);
-          a.cand_score[e] = u;
-          a.cand_lower[e] = l;
-          a.cand_row[e] = row;
-        }
+#pragma unroll
+    for (int k = 0; k < kFl; ++k) {
+      if (ie[k] == ~0u) continue;
+      const uint32_t i = ie[k];
+      const uint32_t qi = s_st.q[i];
+      if (qi == kMmaDropped) continue;
+      const uint32_t g = s_st.base[qi] + atomicAdd(&s_st.cnt[qi], 1u);
+      if (g < a.seg_cap) {
+        const uint64_t e = ((uint64_t)(q0 + qi) * a.nseg + seg) * a.seg_cap + g;
+        const uint32_t row = s_st.row[i];
+        float u, l;
+        mma_bounds_x(s_st.acc[i], xr[k], s_qk[qi], s_flag, &u, &l);
+        a.cand_score[e] = u;
+        a.cand_lower[e] = l;
+        a.cand_row[e] = row;
       }
+    }
   }
 }
 
@@ -4086,6 +4236,9 @@ hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const Lau
   } else if (mode == 0) {
     if (two) launch(k_scan_mma<2, 0>, g, b, s, ev, a);
     else launch(k_scan_mma<1, 0>, g, b, s, ev, a);
+  } else if (mode == 1 && a.mma_wide) {
+    if (two) launch(k_scan_mma<2, 1, true>, g, b, s, ev, a);
+    else launch(k_scan_mma<1, 1, true>, g, b, s, ev, a);
   } else if (mode == 1) {
     if (two) launch(k_scan_mma<2, 1>, g, b, s, ev, a);
     else launch(k_scan_mma<1, 1>, g, b, s, ev, a);

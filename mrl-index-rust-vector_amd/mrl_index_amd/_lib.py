@@ -190,6 +190,7 @@ SIGNATURES = {
     "mrl_ctx_set_profiling": (C.c_int, [_P, C.c_int]),
     "mrl_ctx_profile_collect": (C.c_int, [_P, C.POINTER(KernelTimeC), C.c_uint32, _U32]),
     "mrl_ctx_evict_caches": (C.c_int, [_P, C.c_uint64]),
+    "mrl_ctx_set_s4_bound": (C.c_int, [_P, C.c_int]),
     "mrl_encode_block": (C.c_int, [_F, C.c_uint32, C.c_uint32, _U32, _U32, C.POINTER(EdenFitC),
                                    C.POINTER(EdenFitC), _P]),
     "mrl_encode_corpus": (C.c_int, [_F, C.c_uint64, C.c_uint32, C.c_uint32, C.POINTER(EdenFitC),

@@ -41,6 +41,14 @@ class Device:
     def synchronize(self) -> None:
         _lib.check(_lib.lib.mrl_ctx_synchronize(self._h))
 
+    S4_BOUND_AUTO, S4_BOUND_ALWAYS, S4_BOUND_NEVER = 0, 1, 2
+
+    def set_s4_bound(self, policy: int) -> None:
+        """Cost policy of the MFMA final pass (mrl_ctx_set_s4_bound): AUTO,
+        ALWAYS or NEVER replace its four S4 K-steps by a bound of the S4
+        score; the results are the same under each."""
+        _lib.check(_lib.lib.mrl_ctx_set_s4_bound(self._h, int(policy)))
+
     def close(self) -> None:
         if self._h:
             _lib.lib.mrl_ctx_destroy(self._h)

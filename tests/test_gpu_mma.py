@@ -5,7 +5,11 @@ the Full64b and L1Rabitq depths, indexes with and without a sampling pass,
 one and two 32-query tiles per wave and a partial last query chunk, tombstones
 and the temporal filter, vectors whose meta is beyond the f16 operand range,
 near-duplicate clusters, K above the index size, and a non-finite query (an
-error, as on the exact path)."""
+error, as on the exact path).  Every case runs twice: under the library's own
+choice of final pass, and with the final pass forced to bound the S4 stage
+(mrl_ctx_set_s4_bound ALWAYS: its staged pairs are made exact before they
+are written out, a wave past its append allowance returns to the full
+tiles, and a pair beyond the staging room keeps the bound)."""
 import numpy as np
 import pytest
 
@@ -14,6 +18,13 @@ import ora
 from helpers import assert_topk_equal, normalized
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=["auto", "s4-bounded"], autouse=True)
+def s4_policy(request, device):
+    device.set_s4_bound(device.S4_BOUND_AUTO if request.param == "auto" else device.S4_BOUND_ALWAYS)
+    yield request.param
+    device.set_s4_bound(device.S4_BOUND_AUTO)
 
 
 def _rows(n, dims, seed, clusters=0):

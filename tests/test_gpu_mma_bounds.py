@@ -5,7 +5,10 @@ reference's order), and the bracket is narrow.  The top-K parity tests only
 see pairs near the K-th score; this checks all of them, over both prefix
 codecs, both depths with an S1 stage, two query chunks with a partial one,
 inactive slots, meta beyond the operand range, and queries equal to (or the
-negation of) corpus rows, which put scores at the ends of the range."""
+negation of) corpus rows, which put scores at the ends of the range.  Each
+case checks the full tiles' bounds and those of the final pass that bounds
+the S4 stage (mrl_ctx_set_s4_bound ALWAYS: every pair forced through that
+pass and made exact at its flush)."""
 import numpy as np
 import pytest
 
@@ -14,6 +17,13 @@ import ora
 from helpers import normalized
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=["full-tiles", "s4-bounded"], autouse=True)
+def s4_policy(request, device):
+    device.set_s4_bound(device.S4_BOUND_NEVER if request.param == "full-tiles" else device.S4_BOUND_ALWAYS)
+    yield request.param
+    device.set_s4_bound(device.S4_BOUND_AUTO)
 
 
 def _queries(rows, rng, n_q):

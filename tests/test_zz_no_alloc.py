@@ -7,7 +7,9 @@ path; queries re-run at the safe floor on the device, alone and in an MFMA
 batch; the batch limit.  Results must be identical: ids, scores (bit for
 bit) and counts; and the device's free memory (hipMemGetInfo) is the same
 before and after the calls."""
+import contextlib
 import ctypes as C
+import gc
 
 import numpy as np
 import pytest
@@ -54,6 +56,19 @@ def free_bytes(device):
     return f.value
 
 
+@contextlib.contextmanager
+def collector_paused():
+    """Python's cycle collector paused around a free-memory window: a
+    collection inside it could free an earlier test's device buffers and
+    change the figure for a reason other than the entry point."""
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        gc.enable()
+
+
 def existing(device, ix, plan, cfg):
     res = m.DeviceResults(plan.n_queries, max(cfg.shortlist_cand, 1), device)
     res.scan(ix, plan, cfg)
@@ -97,11 +112,13 @@ def test_noalloc_matches_existing_entry_point(device, data, n_first, n_second):
     p1 = _plan(rows, pf, n_first, n_first, device)
     out2 = DevOut(device, n_second, 100)
     p2 = _plan(rows, pf, n_second, 1000 + n_second, device)
-    free0 = free_bytes(device)
-    g1 = noalloc(device, ix_big, p1, cfg, out)
-    # second call: fewer queries, smaller index, the same array
-    g2 = noalloc(device, ix_small, p2, cfg, out2)
-    assert free_bytes(device) == free0, "the calls changed the device's free memory"
+    with collector_paused():
+        free0 = free_bytes(device)
+        g1 = noalloc(device, ix_big, p1, cfg, out)
+        # second call: fewer queries, smaller index, the same array
+        g2 = noalloc(device, ix_small, p2, cfg, out2)
+        free1 = free_bytes(device)
+    assert free1 == free0, "the calls changed the device's free memory"
     assert_same(g1, existing(device, ix_big, p1, cfg), f"first {n_first}")
     assert_same(g2, existing(device, ix_small, p2, cfg), f"second {n_second}")
 
@@ -123,9 +140,11 @@ def test_noalloc_safe_floor_rerun_on_device(device):
     ref = existing(device, ix, plan, cfg)
     assert ref.stats.reruns_safe == 1
     out = DevOut(device, 1, k)
-    free0 = free_bytes(device)
-    got = noalloc(device, ix, plan, cfg, out)
-    assert free_bytes(device) == free0
+    with collector_paused():
+        free0 = free_bytes(device)
+        got = noalloc(device, ix, plan, cfg, out)
+        free1 = free_bytes(device)
+    assert free1 == free0
     assert_same(got, ref, "safe-floor re-run")
     assert int(got[2][0]) == k
 
@@ -149,9 +168,11 @@ def test_noalloc_safe_floor_rerun_in_a_batch(device):
     ref = existing(device, ix, plan, cfg)
     assert ref.stats.reruns_safe >= 1
     out = DevOut(device, nq, k)
-    free0 = free_bytes(device)
-    got = noalloc(device, ix, plan, cfg, out)
-    assert free_bytes(device) == free0
+    with collector_paused():
+        free0 = free_bytes(device)
+        got = noalloc(device, ix, plan, cfg, out)
+        free1 = free_bytes(device)
+    assert free1 == free0
     assert_same(got, ref, "batched safe-floor re-run")
     assert np.all(got[2] == k)
 
