@@ -2415,15 +2415,17 @@ __device__ __forceinline__ int mma_dim(int st, int kh, int e) {
   return 32 * kh + 4 * (st - 12) + j + 16 * p;
 }
 
-// f16 bits of x >= 0 with a magnitude no smaller than x.
-__device__ __forceinline__ uint32_t f16_up(float x) {
-  uint32_t h = f32_to_f16(x);
-  if (h2f((uint16_t)h) < x) h += 1u;
-  return h;
-}
-
+// f16 bits of x, rounded to nearest (the hardware conversion).
 __device__ __forceinline__ uint32_t f16_bits(float x) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+// f16 bits of x >= 0 with a magnitude no smaller than x: the nearest f16,
+// one ulp up when that lies below x.
+__device__ __forceinline__ uint32_t f16_up(float x) {
+  uint32_t h = f16_bits(x);
+  if (h2f((uint16_t)h) < x) h += 1u;
+  return h;
 }
 
 // Query operands and error coefficients of query q, by the first wave of
