@@ -56,8 +56,12 @@ sys.path.insert(0, os.path.join(ROOT, "mrl-index-rust-vector_amd"))
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFS = 2500.0  # dense f16 MFMA, MI355X
 # MACs per (query, vector) pair of the MFMA bound: 64 prefix dims, 128 S1
-# bits, 64 S4 bits and the 5 meta / error columns of the last K-step
+# bits, 64 S4 bits and the 5 meta / error columns of the last K-step; a final
+# pass that bounds the S4 stage (profile flag MRL_KT_S4_BOUNDED) runs no S4
+# bits and 8 bound columns instead
 MMA_MACS_PER_PAIR = 64 + 128 + 64 + 5
+MMA_MACS_PER_PAIR_S4_BOUNDED = 64 + 128 + 5 + 8
+KT_S4_BOUNDED = 1
 EVICT_BYTES = 1 << 30  # cold-cache runs read this much between steps
 KIND_NAMES = {0: "plan", 1: "scan", 2: "select", 3: "thresh", 6: "finish", 7: "mma_prep", 8: "exact", 9: "bounds",
               10: "plan+scan", 11: "plan+mma_prep"}
@@ -144,16 +148,17 @@ def m_rows_fit(cfg_id):
 
 
 def kernel_groups(L, _lib, dev, cap):
-    """Collects the recorded launches: {(kind, pass): {"ms": [...], "blocks": [...]}}."""
+    """Collects the recorded launches: {(kind, pass): {"ms": [...], "blocks": [...], "flags": [...]}}."""
     kt = (_lib.KernelTimeC * cap)()
     nrec = C.c_uint32()
     _lib.check(L.mrl_ctx_profile_collect(dev.handle, kt, cap, C.byref(nrec)))
     groups = {}
     for i in range(min(nrec.value, cap)):
         r = kt[i]
-        g = groups.setdefault((KIND_NAMES.get(r.kind, str(r.kind)), r.pass_), {"ms": [], "blocks": []})
+        g = groups.setdefault((KIND_NAMES.get(r.kind, str(r.kind)), r.pass_), {"ms": [], "blocks": [], "flags": []})
         g["ms"].append(r.ms)
         g["blocks"].append(r.n_blocks)
+        g["flags"].append(r.flags)
     return groups
 
 
@@ -198,7 +203,10 @@ def roofline_of(groups, nq, prof_steps, w, cold=False, scanned=None):
         avg_ms = float(np.mean(g["ms"]))
         block_queries = float(scanned) if scanned is not None else float(np.mean(g["blocks"])) * nq
         pairs = 64.0 * block_queries
-        flops = 2.0 * MMA_MACS_PER_PAIR * pairs
+        # the MACs of the pass that ran: the S4-bounded pass needs fewer per pair
+        s4_bounded = float(np.mean([(f & KT_S4_BOUNDED) != 0 for f in g["flags"]]))
+        macs = s4_bounded * MMA_MACS_PER_PAIR_S4_BOUNDED + (1.0 - s4_bounded) * MMA_MACS_PER_PAIR
+        flops = 2.0 * macs * pairs
         achieved = flops / (avg_ms / 1000.0) / 1e12
         # the blocks one query scanned (a block shared by the batch is read once)
         bytes_per_launch = 4096.0 * block_queries / nq
@@ -210,6 +218,7 @@ def roofline_of(groups, nq, prof_steps, w, cold=False, scanned=None):
              "traffic": traffic["bytes_per_launch"] if traffic else None,
              "kernel": "k_scan_mma (final pass)", "launches_per_step": len(g["ms"]) / prof_steps,
              "kernel_avg_ms": round(avg_ms, 5), "algorithmic_flops_per_launch": flops,
+             "macs_per_pair": round(macs, 2), "s4_bounded_launches": round(s4_bounded, 4),
              "algorithmic_bytes_per_launch": bytes_per_launch, "hbm_achieved_gb_s": round(hbm, 1),
              "hbm_frac": round(hbm / HBM_PEAK_GBS, 4)}
     if traffic:

@@ -428,8 +428,9 @@ typedef struct mrl_kernel_time {
   uint32_t n_blocks; /* blocks this launch scanned */
   uint32_t n_queries;
   float ms;          /* kernel duration from events recorded by the dispatch itself */
-  uint32_t reserved;
+  uint32_t flags;    /* MRL_KT_S4_BOUNDED: an MFMA final pass that bounded the S4 stage (13 K-steps a tile) */
 } mrl_kernel_time;
+#define MRL_KT_S4_BOUNDED 1u
 
 /* While enabled, every plan / scan-pass / threshold / select / rerank launch on the
  * context records its kernel start and end (events written by the dispatch). */

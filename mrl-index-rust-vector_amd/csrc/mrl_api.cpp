@@ -1434,6 +1434,7 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
   }
   {
     ProfScope ps(ctx, MRL_KERNEL_SCAN, final_pass, (uint32_t)B, n_q);
+    ps.r.info.flags = a.mma_wide ? MRL_KT_S4_BOUNDED : 0u;
     HIP_TRY(launch_scan_mma(a, floor ? 1 : 2, s, ps.ev()));
     ps.commit(a.n_pos != 0 && n_q != 0);
   }

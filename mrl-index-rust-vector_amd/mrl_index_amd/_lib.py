@@ -127,7 +127,7 @@ class KernelTimeC(C.Structure):
         ("n_blocks", C.c_uint32),
         ("n_queries", C.c_uint32),
         ("ms", C.c_float),
-        ("reserved", C.c_uint32),
+        ("flags", C.c_uint32),  # MRL_KT_S4_BOUNDED = 1
     ]
 
 
