@@ -2708,9 +2708,9 @@ __device__ __forceinline__ float mma_tighten_x(float acc, const uint4 x, uint32_
       const uint32_t w[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float lo = h2f((uint16_t)(w[j] & 0xffffu)), hi = h2f((uint16_t)(w[j] >> 16));
-        S += ((bits >> (4 * st + j)) & 1u) ? lo : -lo;
-        S += ((bits >> (4 * st + j + 16)) & 1u) ? hi : -hi;
+        // the operand pair with each sign flipped where its bit is clear (as the tiles' vector operand)
+        const uint32_t sw = w[j] ^ ((~bits << (15 - 4 * st - j)) & 0x80008000u);
+        S += h2f((uint16_t)(sw & 0xffffu)) + h2f((uint16_t)(sw >> 16));
       }
     }
   }
@@ -3106,9 +3106,17 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
     asm volatile("" : "+v"(okbits));  // one register, not 32 hoisted masks
   }
 
+  // On block lists, a final pass reads the block of the item after next one
+  // item early, so the list read does not delay the record loads of the next
+  // item.  (The sampling passes keep the register.)
+  const bool pre = !SAMPLE && bl != nullptr;
+  uint64_t b_pre = 0;
+  if (pre && first + stride < n_it) b_pre = block_of((first + stride) >> 1);
   for (uint32_t it = first; it < n_it; it += stride) {
     const uint32_t it_nxt = it + stride < n_it ? it + stride : it_cur;
-    const uint64_t b_nxt = it + stride < n_it ? block_of(it_nxt >> 1) : b_cur;
+    uint64_t b_nxt = b_cur;
+    if (it + stride < n_it) b_nxt = pre ? b_pre : block_of(it_nxt >> 1);
+    if (pre && it + 2u * stride < n_it) b_pre = block_of((it + 2u * stride) >> 1);
     const MmaRaw nxt = mma_load(a.idx, a.recs, b_nxt, it_nxt & 1u);
     const uint32_t b = (uint32_t)b_cur, h = it_cur & 1u;
     const uint32_t min_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 0);
@@ -3219,15 +3227,20 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
         for (int t = 0; t < NQT; ++t)
           acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ac[t]), as_h8(bo), acc[t], 0, 0, 0);
       };
+      if constexpr (wide_pass) {
 #pragma unroll
-      for (int st = 0; st < 11; ++st) kstep(st, st + 1);
-      kstep(11, MODE == 1 && wide ? 16 : 12);
-      if (!(MODE == 1 && wide)) {  // else the S4 steps' score is bounded in step 16
+        for (int st = 0; st < 11; ++st) kstep(st, st + 1);
+        kstep(11, wide ? 16 : 12);
+        if (!wide) {  // else the S4 steps' score is bounded in step 16
 #pragma unroll
-        for (int st = 12; st < 16; ++st) kstep(st, st + 1);
+          for (int st = 12; st < 16; ++st) kstep(st, st + 1);
+        }
+        kstep(16, -1);
+        static_assert(kMmaSteps == 17, "the step schedule above assumes prefix 4, S1 8, S4 4, error 1");
+      } else {
+#pragma unroll
+        for (int st = 0; st < kMmaSteps; ++st) kstep(st, st + 1 < kMmaSteps ? st + 1 : -1);
       }
-      kstep(16, -1);
-      static_assert(kMmaSteps == 17, "the step schedule above assumes prefix 4, S1 8, S4 4, error 1");
       // Register r of tile t holds query 32 t + 8 (r / 4) + 4 kh + r % 4.
       if constexpr (MODE == 3) {
         // store every pair's lower bound (sample 32 it + lane % 32 of the query)
