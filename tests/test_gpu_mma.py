@@ -46,14 +46,15 @@ def _queries(rows, rng, n_q, noise=0.1):
 
 
 def _check(device, blocks, qs, dims, fit, k, depth=m.StrataDepth.FULL64B, lo=None, hi=None, temporal=True,
-           exhaustive=False, checked=None, what=""):
+           exhaustive=False, checked=None, what="", alpha=1.0, w_s4=0.2):
     eden = fit is not None
     codec = m.PrefixCodec.EDEN_PROD if eden else m.PrefixCodec.MIN_MAX4
     plan = m.QueryPlan.from_query_codec(qs, dims, codec, m.MidCodec.RABITQ, fit, None, device)
-    cfg = m.ScanConfig(shortlist_cand=k, strata_depth=depth, temporal_filter_enable=temporal, exhaustive=exhaustive)
+    cfg = m.ScanConfig(shortlist_cand=k, strata_depth=depth, temporal_filter_enable=temporal, exhaustive=exhaustive,
+                       cs_tolerance=alpha, stratum4_weight=w_s4)
     res = m.scan_batch(m.DeviceIndex.upload(blocks, device), plan, cfg, lo, hi)
     ofit = ora.Fit(fit.mean, 4, 1, fit.n_observed) if eden else None
-    ocfg = ora.scan_config(k, depth=int(depth), temporal=temporal, sharding=True, threads=8)
+    ocfg = ora.scan_config(k, alpha=alpha, w_s4=w_s4, depth=int(depth), temporal=temporal, sharding=True, threads=8)
     for qi in (range(len(qs)) if checked is None else checked):
         op = ora.plan_build(qs[qi], dims, int(codec), 0, ofit, None)
         rids, rsc = ora.scan_blocks(blocks, op, ocfg, lo, hi)
@@ -109,6 +110,32 @@ def test_tombstones_and_temporal_filter(device):
     _check(device, blocks, qs, 768, fit, 64, what="tombstones")
     # timestamps are row indices: keep rows 3000 .. 20000 (blocks 46 .. 312)
     _check(device, blocks, qs, 768, fit, 64, lo=3000, hi=20000, what="temporal")
+
+
+def test_dense_appends_past_the_staging_room(device):
+    """K 1024 over 300 blocks: the sampled floor passes ~9 % of the
+    vectors, about 170 pairs per 32-vector tile, more than a wave's staging
+    region takes in one tile.  Pairs go straight to their segments (with the
+    S4 bound still in them when the pass bounds S4), and every wave of an
+    S4-bounded pass returns to the full tiles after its first tiles."""
+    print("[mma] dense appends", flush=True)
+    rows, rng = _rows(300 * 64, 768, 29)
+    fit = m.EdenFit.fit_prefix(rows[:4096], 4, 1)
+    blocks = m.encode_corpus(rows, m.source.DOC, fit)
+    _check(device, blocks, _queries(rows, rng, 64), 768, fit, 1024, what="dense appends")
+
+
+@pytest.mark.parametrize("alpha,w_s4", [(10.0, 4.0), (12.0, 5.0)])
+def test_large_stratum_weights(device, alpha, w_s4):
+    """Admissible (2.4 w_s4 <= alpha) weights at and past the largest
+    stratum weight the S4 bound covers (4): past it the final pass keeps the
+    full tiles whatever the policy."""
+    print(f"[mma] alpha {alpha} w_s4 {w_s4}", flush=True)
+    rows, rng = _rows(400 * 64, 768, 30)
+    fit = m.EdenFit.fit_prefix(rows[:4096], 4, 1)
+    blocks = m.encode_corpus(rows, m.source.DOC, fit)
+    _check(device, blocks, _queries(rows, rng, 40), 768, fit, 64, alpha=alpha, w_s4=w_s4,
+           what=f"alpha {alpha} w_s4 {w_s4}")
 
 
 def test_exhaustive_flag_and_k_above_index(device):
