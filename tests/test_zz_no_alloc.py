@@ -104,9 +104,21 @@ def _plan(rows, pf, n, seed, device):
     return m.QueryPlan.from_query_eden(q, 768, pf, device)
 
 
-@pytest.mark.parametrize("n_first,n_second", [(5, 2), (40, 9), (64, 1)])
-def test_noalloc_matches_existing_entry_point(device, data, n_first, n_second):
+@pytest.fixture
+def s4_policy(device):
+    """Sets the device's S4-bound policy for one test and restores AUTO."""
+    def set_policy(p):
+        device.set_s4_bound(p)
+    yield set_policy
+    device.set_s4_bound(device.S4_BOUND_AUTO)
+
+
+@pytest.mark.parametrize("n_first,n_second,s4", [(5, 2, 0), (40, 9, 0), (64, 1, 0), (40, 9, 1)])
+def test_noalloc_matches_existing_entry_point(device, data, s4_policy, n_first, n_second, s4):
+    """s4 = 1: the MFMA final pass forced to bound the S4 stage
+    (mrl_ctx_set_s4_bound ALWAYS) for both entry points."""
     rows, pf, ix_big, ix_small = data
+    s4_policy(s4)
     cfg = m.ScanConfig(shortlist_cand=100)
     out = DevOut(device, n_first, 100)
     p1 = _plan(rows, pf, n_first, n_first, device)
