@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <map>
 #include <memory>
 #include <limits>
@@ -92,6 +93,27 @@ struct mrl_ctx {
 };
 
 static void ctx_free(mrl_ctx* ctx);
+
+// The context of the last MFMA final pass enqueued on each device, and when.
+// A final pass whose predecessor on the device came from another context
+// less than 2 ms earlier runs beside that context's work, and may leave room
+// for the other's small launches (ScanArgs::leave_room).  One context alone
+// keeps the whole GPU.
+struct RecentPass {
+  std::atomic<uintptr_t> ctx{0};
+  std::atomic<int64_t> t_ns{0};
+};
+static RecentPass g_recent_pass[64];
+static bool other_context_active(const mrl_ctx* ctx) {
+  if (ctx->device < 0 || ctx->device >= 64) return false;
+  RecentPass& r = g_recent_pass[ctx->device];
+  const int64_t now =
+      std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now().time_since_epoch())
+          .count();
+  const uintptr_t prev = r.ctx.exchange((uintptr_t)ctx);
+  const int64_t t_prev = r.t_ns.exchange(now);
+  return prev != 0 && prev != (uintptr_t)ctx && now - t_prev < 2000000;
+}
 static void ctx_retain(mrl_ctx* ctx) { ctx->refs.fetch_add(1, std::memory_order_relaxed); }
 static void ctx_release(mrl_ctx* ctx) {
   if (ctx->refs.fetch_sub(1, std::memory_order_acq_rel) == 1) ctx_free(ctx);
@@ -1432,6 +1454,13 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
     a.mma_wide = floor && fits && pol != MRL_S4_BOUND_NEVER && (cheap || pol == MRL_S4_BOUND_ALWAYS) ? 1u : 0u;
     a.wide_lim = 2u;
   }
+  // Room is left for batches of up to 256 queries, whose other launches are
+  // latency-bound (a few workgroups per query); a larger batch's exact
+  // scoring and selection fill the GPU themselves (config 4: 0.310 ->
+  // 0.303 ms per step over three contexts, config 3 0.189 -> 0.186;
+  // config 5, 1024 queries: 0.787 -> 0.812 with the room, so not there).
+  const bool other = other_context_active(ctx);
+  a.leave_room = other && n_q <= 256u ? 1u : 0u;
   {
     ProfScope ps(ctx, MRL_KERNEL_SCAN, final_pass, (uint32_t)B, n_q);
     ps.r.info.flags = a.mma_wide ? MRL_KT_S4_BOUNDED : 0u;

@@ -263,6 +263,9 @@ struct ScanArgs {
   // K-steps for the rest of the pass.
   uint32_t mma_wide;
   uint32_t wide_lim;
+  // MFMA final pass: leave 1/16 of the resident workgroup slots free (other
+  // contexts' launches on the device then start beside the pass).
+  uint32_t leave_room;
 };
 constexpr uint8_t kMmaWideFlag = 0x80;   // staged query index: the tile value holds the S4 bound
 constexpr uint8_t kMmaDropped = 0xff;    // staged entry dropped (upper bound below the floor)

@@ -3210,7 +3210,10 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
         return make_uint4(d[0], d[1], d[2], d[3]);
       };
       // The query operands of step nst are requested before step st's
-      // MFMAs, so their LDS latency overlaps the matrix work.
+      // MFMAs, so their LDS latency overlaps the matrix work.  A final pass
+      // raises the wave's issue priority while it feeds the matrix unit
+      // (the other waves' epilogues and operand builds take the slots left).
+      if constexpr (MODE == 1) __builtin_amdgcn_s_setprio(2);
       uint4 an[NQT];
 #pragma unroll
       for (int t = 0; t < NQT; ++t) an[t] = qa_raw(t, 0);
@@ -3241,6 +3244,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
 #pragma unroll
         for (int st = 0; st < kMmaSteps; ++st) kstep(st, st + 1 < kMmaSteps ? st + 1 : -1);
       }
+      if constexpr (MODE == 1) __builtin_amdgcn_s_setprio(0);
       // Register r of tile t holds query 32 t + 8 (r / 4) + 4 kh + r % 4.
       if constexpr (MODE == 3) {
         // store every pair's lower bound (sample 32 it + lane % 32 of the query)
@@ -4230,7 +4234,7 @@ uint32_t mma_scan_grid(const ScanArgs& a) {
   static const uint32_t res = resident_groups_n(k_scan_mma<2, 1>, kMmaWaves * 64);
   const uint32_t wpg = kMmaWaves;
   uint32_t grid = (2u * a.n_pos + wpg) / wpg;  // items: two 32-vector tiles per block
-  uint32_t max_grid = res / chunks;
+  uint32_t max_grid = (a.leave_room ? res - res / 16u : res) / chunks;
   if (max_grid < 1) max_grid = 1;
   if (grid > max_grid) grid = max_grid;
   return grid;
