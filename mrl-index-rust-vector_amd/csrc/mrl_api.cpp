@@ -1542,6 +1542,11 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
   hipStream_t s = ctx->stream;
   const size_t np = lp.passes.size();
   const bool sampled = np > 1 && !rerun_safe;
+  // Beside another context's scan, the one-query passes run 384 of their 512
+  // workgroups, leaving room for that context's launches (config 2 over three
+  // contexts 0.0224 -> 0.0211 ms per step; alone the final pass would take
+  // 19.6 -> 22.1 us, so only then).
+  const bool beside = other_context_active(ctx) && n_q < (uint32_t)kMmaMinQ;
   uint32_t nseg_final = pb.nseg, cap_final = pb.seg_cap;
   const uint32_t rank = np > 1 ? final_rank(K, lp.passes[0].n_pos, ix->n_blocks) : K;
   for (size_t pi = 0; pi < np; ++pi) {
@@ -1571,6 +1576,7 @@ static int enqueue_scan(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans, uin
     a.seg_count = pb.seg_count;
     a.nseg = pb.nseg;
     a.seg_cap = pb.seg_cap;
+    a.leave_room = beside ? 1u : 0u;
     if (last && excl_ok(pb, n_q, sp)) {
       // one segment per workgroup of the final pass, the same candidate room per query
       a.excl = 1;

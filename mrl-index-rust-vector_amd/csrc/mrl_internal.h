@@ -263,8 +263,9 @@ struct ScanArgs {
   // K-steps for the rest of the pass.
   uint32_t mma_wide;
   uint32_t wide_lim;
-  // MFMA final pass: leave 1/16 of the resident workgroup slots free (other
-  // contexts' launches on the device then start beside the pass).
+  // Final pass beside another context's scan: the MFMA pass leaves 1/16 of
+  // the resident workgroup slots free, the one-query pass a quarter of its
+  // workgroups (the other context's launches then start beside it).
   uint32_t leave_room;
 };
 constexpr uint8_t kMmaWideFlag = 0x80;   // staged query index: the tile value holds the S4 bound

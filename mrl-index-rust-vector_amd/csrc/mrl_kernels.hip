@@ -4132,7 +4132,10 @@ uint32_t scan_grid(const ScanArgs& a, bool diag) {
     if (g < 1u) g = 1u;
     if (max_grid < g) max_grid = g;
   }
-  if (!tile && qt == 1 && !diag && !l0 && max_grid > MRL_SCAN_GRID1) max_grid = MRL_SCAN_GRID1;
+  // (a one-query final pass beside another context's scan leaves a quarter
+  // of its workgroups to that context's launches)
+  const uint32_t grid1 = a.leave_room ? MRL_SCAN_GRID1 - MRL_SCAN_GRID1 / 4u : MRL_SCAN_GRID1;
+  if (!tile && qt == 1 && !diag && !l0 && max_grid > grid1) max_grid = grid1;
   if (!a.excl && max_grid < a.nseg) max_grid = a.nseg;
   if (grid > max_grid) grid = max_grid;
   return grid;
