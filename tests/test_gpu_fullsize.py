@@ -5,6 +5,7 @@ Full-size checks: for every query of every configuration the GPU top-K
 equals the oracle's scan_blocks top-K (exact ties excepted) with bit-identical
 scores; the first queries against the sharded scan (scan.rs:838-886), the
 rest against the serial one (scan.rs:822-836), run query-parallel."""
+import ctypes as C
 import os
 from concurrent.futures import ThreadPoolExecutor
 
@@ -12,7 +13,7 @@ import numpy as np
 import pytest
 
 import mrl_index_amd as m
-from mrl_index_amd import synth
+from mrl_index_amd import _lib, synth
 import ora
 from helpers import assert_topk_equal
 
@@ -38,7 +39,29 @@ def _oracle_all(blocks, qs, w, ofit, n_sharded):
     return out
 
 
-def _check_config(device, cfg_id, n_sharded, n_queries=None):
+def _check_config(device, cfg_id, n_sharded, n_queries=None, s4_policy=None, s4_bounded=None):
+    """s4_policy: the MFMA final pass's policy for this scan (mrl_ctx_set_s4_bound);
+    None keeps the library's own choice.  s4_bounded: whether the final pass
+    must have bounded the S4 stage (from its profile record's flag)."""
+    if s4_policy is not None:
+        device.set_s4_bound(s4_policy)
+    try:
+        return _check_config_now(device, cfg_id, n_sharded, n_queries, s4_bounded)
+    finally:
+        device.set_s4_bound(device.S4_BOUND_AUTO)
+
+
+def _final_pass_flags(device):
+    """The flags of the last scan's final pass (the scan record with the
+    highest pass index) from the context's profile records."""
+    kt = (_lib.KernelTimeC * 256)()
+    n = C.c_uint32()
+    _lib.check(_lib.lib.mrl_ctx_profile_collect(device.handle, kt, 256, C.byref(n)))
+    scans = [kt[i] for i in range(min(n.value, 256)) if kt[i].kind == _lib.KERNEL_SCAN]
+    return max(scans, key=lambda r: r.pass_).flags
+
+
+def _check_config_now(device, cfg_id, n_sharded, n_queries, s4_bounded):
     w = synth.CONFIGS[cfg_id]
     if n_queries:
         w = w.scaled(w.n_docs, n_queries)
@@ -49,7 +72,15 @@ def _check_config(device, cfg_id, n_sharded, n_queries=None):
     ix = m.DeviceIndex.upload(blocks, device)
     plan = m.QueryPlan.from_query_codec(qs, w.dims, w.prefix_codec, m.MidCodec.RABITQ, fit, None, device)
     cfg = m.ScanConfig(shortlist_cand=w.k, strata_depth=w.strata, exhaustive=w.exhaustive)
-    res = m.scan_batch(ix, plan, cfg)
+    if s4_bounded is not None:
+        _lib.check(_lib.lib.mrl_ctx_set_profiling(device.handle, 1))
+    try:
+        res = m.scan_batch(ix, plan, cfg)
+        if s4_bounded is not None:
+            assert bool(_final_pass_flags(device) & 1) == s4_bounded, "final pass variant"
+    finally:
+        if s4_bounded is not None:
+            _lib.check(_lib.lib.mrl_ctx_set_profiling(device.handle, 0))
     ofit = ora.Fit(fit.mean, 4, 1, fit.n_observed) if fit is not None else None
     refs = _oracle_all(blocks, qs, w, ofit, n_sharded)
     for qi in range(w.n_queries):
@@ -72,11 +103,23 @@ def test_config2_1m_batch1_k256(device):
 
 
 def test_config3_1m_batch256(device):
-    _check_config(device, 3, 8)
+    """(the library's rule keeps config 3's final pass on the full tiles)"""
+    _check_config(device, 3, 8, s4_bounded=False)
+
+
+def test_config3_s4_bounded_final_pass(device):
+    """Config 3 with its final pass forced to bound the S4 stage."""
+    _check_config(device, 3, 8, s4_policy=device.S4_BOUND_ALWAYS, s4_bounded=True)
 
 
 def test_config4_8_8m_clustered_batch64(device):
-    _check_config(device, 4, 4)
+    """(the library's rule gives config 4 the S4-bounded final pass)"""
+    _check_config(device, 4, 4, s4_bounded=True)
+
+
+def test_config4_full_tiles(device):
+    """Config 4 with its final pass on the full tiles."""
+    _check_config(device, 4, 4, s4_policy=device.S4_BOUND_NEVER, s4_bounded=False)
 
 
 def test_config5_minmax4_exhaustive_batch1024_k1024(device):
