@@ -4028,17 +4028,36 @@ __global__ __launch_bounds__(256) void k_block_select(BoundScanArgs a) {
     const float re = a.eden ? r.x : r.y;
     const float* trow = a.table + (uint64_t)cl * a.n_q + qc0;
     bool any = false;
-    constexpr int kB = 16;  // table loads in flight together
-    for (uint32_t i0 = 0; i0 < nq; i0 += kB) {
-      float t[kB];
+    if (nq == 64u && (a.n_q & 3u) == 0u) {
+      // a full chunk: its 64 table entries in one round of 16-byte loads
+      // (the row is 16-byte aligned when n_q is a multiple of 4)
+      const float4* tr4 = reinterpret_cast<const float4*>(trow);
+      float4 t4[16];
 #pragma unroll
-      for (int u = 0; u < kB; ++u) t[u] = i0 + u < nq ? trow[i0 + u] : -INFINITY;
+      for (int u = 0; u < 16; ++u) t4[u] = tr4[u];
 #pragma unroll
-      for (int u = 0; u < kB; ++u) {
-        const float4 qv = s_q[min(i0 + (uint32_t)u, 63u)];
-        const float bound = t[u] + (re * qv.x + r.z * qv.y + r.w * qv.z);
-        // NaN bounds keep the block; past the chunk t = -inf
-        any |= (i0 + u < nq) && !(bound < qv.w);
+      for (int u = 0; u < 16; ++u) {
+        const float tv[4] = {t4[u].x, t4[u].y, t4[u].z, t4[u].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float4 qv = s_q[4 * u + c];
+          const float bound = tv[c] + (re * qv.x + r.z * qv.y + r.w * qv.z);
+          any |= !(bound < qv.w);  // NaN bounds keep the block
+        }
+      }
+    } else {
+      constexpr int kB = 16;  // table loads in flight together
+      for (uint32_t i0 = 0; i0 < nq; i0 += kB) {
+        float t[kB];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) t[u] = i0 + u < nq ? trow[i0 + u] : -INFINITY;
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+          const float4 qv = s_q[min(i0 + (uint32_t)u, 63u)];
+          const float bound = t[u] + (re * qv.x + r.z * qv.y + r.w * qv.z);
+          // NaN bounds keep the block; past the chunk t = -inf
+          any |= (i0 + u < nq) && !(bound < qv.w);
+        }
       }
     }
     need = any;
