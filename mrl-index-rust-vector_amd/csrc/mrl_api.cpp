@@ -1461,6 +1461,7 @@ static int enqueue_scan_mma(mrl_ctx* ctx, mrl_index* ix, const mrl_plans* plans,
   // config 5, 1024 queries: 0.787 -> 0.812 with the room, so not there).
   const bool other = other_context_active(ctx);
   a.leave_room = other && n_q <= 256u ? 1u : 0u;
+  a.lmax = reinterpret_cast<uint32_t*>(pb.mma_consts) + kMcLMax;
   {
     ProfScope ps(ctx, MRL_KERNEL_SCAN, final_pass, (uint32_t)B, n_q);
     ps.r.info.flags = a.mma_wide ? MRL_KT_S4_BOUNDED : 0u;

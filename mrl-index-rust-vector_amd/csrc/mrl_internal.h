@@ -172,6 +172,7 @@ enum {
   kMcE0,      //   and constant
   kMcR,       // bound on |score| + error for vectors whose meta magnitudes are <= kMmaSafe
   kMcOk,      // 1: operands finite; 0: the query is re-run by the exact kernels
+  kMcLMax,    // (u32 bits, cleared here) the final pass's largest written lower-bound key, for k_finish
   kMcCount = 16
 };
 constexpr float kMmaSafe = 4096.0f;  // larger |scale|, mid_n, high_n or |offset|: always a candidate
@@ -231,6 +232,10 @@ struct ScanArgs {
   const uint4* mma_ops;
   const float* mma_consts;
   float* cand_lower;
+  // MFMA final pass: the largest score_key of the lower bounds it writes, per
+  // query, raised with atomicMax at lmax[q * kMcCount] (mma_consts' kMcLMax
+  // slot; null: not kept)
+  uint32_t* lmax;
   // Gated re-run (one-query kernel only): a workgroup of query q exits at
   // once unless bit 2 of gate[q] (a final floor left the query short of K) is set.
   const uint32_t* gate;

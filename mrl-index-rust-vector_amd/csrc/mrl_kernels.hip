@@ -2620,6 +2620,7 @@ struct MmaStaging {
   static constexpr int kCap = CAP;  // entries per wave
   uint32_t n[W];
   uint32_t drop;            // wide entries dropped once made exact (taken off the append count)
+  uint32_t lmax[kMmaQ];     // largest lower-bound key written per query (ScanArgs::lmax)
   uint32_t cnt[kMmaQ];      // final flush: entries per query of the workgroup
   uint32_t base[kMmaQ];
   uint32_t wcnt[W][kMmaQ];  // a wave's own flush: entries per query
@@ -2753,6 +2754,7 @@ __device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, const floa
                                                   ((qq - q0) & 31u)].x & 0xffffu))
                              : 0.0f;
       mma_bounds(acc, a.recs, row, s_qk[qq - q0], s_flag, &u, &l, wpc);
+      if (a.lmax) atomicMax(a.lmax + (uint64_t)qq * kMcCount, score_key(l));
       const uint64_t i = sq * a.seg_cap + g;
       a.cand_score[i] = u;
       a.cand_lower[i] = l;
@@ -2821,6 +2823,7 @@ __device__ __forceinline__ void mma_wave_flush(ST& st, const ScanArgs& a, const 
         const uint32_t row = st.row[i];
         float u, l;
         mma_bounds(st.acc[i], a.recs, row, s_qk[qi], s_flag, &u, &l);
+        atomicMax(&st.lmax[qi], score_key(l));
         const uint64_t o = ((uint64_t)(q0 + qi) * a.nseg + seg) * a.seg_cap + g;
         a.cand_score[o] = u;
         a.cand_lower[o] = l;
@@ -3017,6 +3020,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   if (tid < kStatCount) s_stats[tid] = 0u;
   if (tid < WPG) s_st.n[tid] = 0u;
   if (tid == 0) s_st.drop = 0u;
+  if (tid < kMmaQ) s_st.lmax[tid] = 0u;
   if (tid < kMmaQ) {
     const int qi = tid;
     s_st.cnt[qi] = 0u;
@@ -3433,10 +3437,15 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
         const uint32_t row = s_st.row[i];
         float u, l;
         mma_bounds_x(s_st.acc[i], xr[k], s_qk[qi], s_flag, &u, &l);
+        atomicMax(&s_st.lmax[qi], score_key(l));
         a.cand_score[e] = u;
         a.cand_lower[e] = l;
         a.cand_row[e] = row;
       }
+    }
+    if (a.lmax) {
+      __syncthreads();
+      if (tid < nq && s_st.lmax[tid]) atomicMax(a.lmax + (uint64_t)(q0 + tid) * kMcCount, s_st.lmax[tid]);
     }
   }
 }
@@ -3556,15 +3565,16 @@ __global__ __launch_bounds__(kFinThreads, 8) void k_finish(FinishArgs a) {
   uint32_t tkey = 0u;
   if (total > K) {
     const CandView vl{a.cand_lower + qbase, a.cand_row + qbase, a.seg_cap, a.nseg, s_off, s_coff};
-    uint32_t mk = 0u;
-    for_each_cand<16>(vl, [&](float sc, uint32_t) { mk = max(mk, score_key(sc)); });
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mk = max(mk, (uint32_t)__shfl_xor((int)mk, o));
+    // the largest key: the final pass kept it (kMcLMax), so no walk finds it
+    // here.  A key above it (which the pass's own bookkeeping rules out)
+    // would count at distance 0, which keeps the boundary below the K-th key.
+    const uint32_t kmax = reinterpret_cast<const uint32_t*>(a.mma_consts)[(uint64_t)q * kMcCount + kMcLMax];
     for (int i = tid; i < 2048; i += kFinThreads) s_hist[i] = 0u;
-    if ((tid & 63) == 0) atomicMax(&s_misc[6], mk);
     __syncthreads();
-    const uint32_t kmax = s_misc[6];
-    for_each_cand<16>(vl, [&](float sc, uint32_t) { atomicAdd(&s_hist[dist_bin(kmax - score_key(sc))], 1u); });
+    for_each_cand<16>(vl, [&](float sc, uint32_t) {
+      const uint32_t k = score_key(sc);
+      atomicAdd(&s_hist[dist_bin(k < kmax ? kmax - k : 0u)], 1u);
+    });
     __syncthreads();
     find_boundary(s_hist, 2048, K, false, &s_misc[3], &s_misc[4], s_ws);
     __syncthreads();
