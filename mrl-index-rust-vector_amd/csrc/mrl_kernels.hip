@@ -3351,10 +3351,15 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             // MODE 1: one compare per group of four registers (four queries)
-            // first; fmaxf passes a group whenever a register of it passes
+            // first.  The IEEE maximum (v_maximum3_f32, no quieting of its
+            // inputs) is NaN where a register is: such a group is checked
+            // register by register, so a group passes whenever a register
+            // of it passes.
             if (MODE == 1) {
-              const float m4 = fmaxf(fmaxf(acc[t][4 * g], acc[t][4 * g + 1]), fmaxf(acc[t][4 * g + 2], acc[t][4 * g + 3]));
-              if ((ballot(m4 >= 0.0f) & actm) == 0) continue;
+              const float m4 =
+                  __builtin_elementwise_maximum(__builtin_elementwise_maximum(acc[t][4 * g], acc[t][4 * g + 1]),
+                                                __builtin_elementwise_maximum(acc[t][4 * g + 2], acc[t][4 * g + 3]));
+              if ((ballot(!(m4 < 0.0f)) & actm) == 0) continue;
             }
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
