@@ -3229,6 +3229,11 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
 #pragma unroll
           for (int t = 0; t < NQT; ++t) an[t] = qa_raw(t, nst);
         }
+        // In the final passes the next step's reads stay ahead of this
+        // step's MFMAs (left to itself the scheduler sinks each read to just
+        // before its MFMA, which then waits out the LDS latency; the
+        // sampling passes keep that order, which spills less there).
+        if constexpr (!SAMPLE) __builtin_amdgcn_sched_barrier(0);
         const uint4 bo = vec_op(st);
 #pragma unroll
         for (int t = 0; t < NQT; ++t)
