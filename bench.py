@@ -33,6 +33,15 @@ floor needed a re-run (safe: done on the device inside the step, by two
 launches every sampled scan enqueues) or whose list overflowed (dense: done
 at fetch time, outside the timed step, so a non-zero count would mean the
 timed step left work out).
+Before each workload's warmup, `clock_settle` reads a 1 GiB device buffer
+(mrl_ctx_evict_caches, the library's k_read_sweep) for about 200 ms: the
+corpus is generated on the host for seconds with the GPU idle, and after
+such an idle the first steps run up to ~15 % slower until the GPU has seen
+some 100 ms of memory traffic (measured after a 13 s idle, config 4 over
+three streams: 0.341 ms per step with no settle, 0.311 after 30 ms of
+reads, 0.298 after 165 ms; VALU-bound work did not help), which the few
+warmup steps of a short run do not give.  It runs no step and leaves
+nothing the steps use (it evicts the caches instead).
 `cpu_baseline` times the C restatement of the reference's scan_blocks
 (oracle/, Rayon-equivalent sharding on host threads) on query 0 of the same
 index, on the host's cores and on one thread; the batch figure is the time
@@ -63,6 +72,7 @@ MMA_MACS_PER_PAIR = 64 + 128 + 64 + 5
 MMA_MACS_PER_PAIR_S4_BOUNDED = 64 + 128 + 5 + 8
 KT_S4_BOUNDED = 1
 EVICT_BYTES = 1 << 30  # cold-cache runs read this much between steps
+SETTLE_MS = 200.0  # clock settle before each workload's warmup (device reads, no steps)
 KIND_NAMES = {0: "plan", 1: "scan", 2: "select", 3: "thresh", 6: "finish", 7: "mma_prep", 8: "exact", 9: "bounds",
               10: "plan+scan", 11: "plan+mma_prep"}
 
@@ -110,6 +120,8 @@ def main():
     ap.add_argument("--no-cluster-layout", action="store_true",
                     help="default run: skip config 4 in the cluster-grouped layout")
     ap.add_argument("--rerank-reps", type=int, default=100)
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="device reads before each workload's warmup, in ms (0: none)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run the library's fill and read-sweep kernels over MIB MiB (PMC byte-counter calibration) and exit")
     args = ap.parse_args()
@@ -301,6 +313,8 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
         _lib.check(L.mrl_results_fetch(lanes[i][0].handle, lanes[i][2], None, None, None, C.byref(s_i)))
         return {f: getattr(s_i, f) for f, _ in _lib.ScanStatsC._fields_}
 
+    settle = settle_clocks(L, _lib, dev, args.settle_ms)
+    log(f"clock settle: {settle['reads']} reads of {EVICT_BYTES >> 20} MiB in {settle['ms']} ms")
     log(f"warmup {args.warmup} steps on each of {len(lanes)} streams")
     for _ in range(args.warmup):
         for i in range(len(lanes)):
@@ -382,6 +396,7 @@ def run_workload(cfg_id, args, m, dev, n_threads, legs, layout="standard", cpu_s
         "scan_stats_per_step": {f: v / args.steps for f, v in timed_stats.items()},
         "reruns_per_step": {"safe": timed_stats["reruns_safe"] / args.steps,
                             "dense": timed_stats["reruns_dense"] / args.steps},
+        "clock_settle": settle,
     }
     if layout == "clustered":
         # blocks the final pass scanned per query, against the index's
@@ -554,6 +569,22 @@ def cpu_rerank_us(prec, q, rows, cand, gpu_rows, gpu_scores, budget_s=2.0):
     ok = ref is not None and np.array_equal(ref[0], gpu_rows) and \
         np.array_equal(ref[1].view(np.uint32), np.asarray(gpu_scores, dtype=np.float32).view(np.uint32))
     return us, "identical" if ok else "MISMATCH"
+
+
+def settle_clocks(L, _lib, dev, ms=SETTLE_MS):
+    """Device reads of a 1 GiB buffer (k_read_sweep through
+    mrl_ctx_evict_caches) for about `ms` milliseconds before a workload's
+    warmup, so that the GPU's clocks have come up from the idle of the
+    host-side corpus generation.  No scan step runs here."""
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1000.0 < ms:  # (ms <= 0: none)
+        for _ in range(10):
+            _lib.check(L.mrl_ctx_evict_caches(dev.handle, EVICT_BYTES))
+        n += 10
+        dev.synchronize()
+    return {"method": f"{EVICT_BYTES >> 20} MiB device reads (k_read_sweep) before the warmup; no scan step",
+            "reads": n, "ms": round((time.perf_counter() - t0) * 1000.0, 1)}
 
 
 def host_boundary_rate(L, _lib, dev, ix, queries, fit, w, ccfg, tr, reps=20):
