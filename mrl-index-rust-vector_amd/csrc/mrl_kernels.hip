@@ -2441,6 +2441,7 @@ __device__ __forceinline__ void mma_prep_body(const MmaPrepArgs& a, uint32_t q, 
   const uint32_t lane = threadIdx.x;
   float s = 0.0f, psum = 0.0f;  // operand scale and prefix_sum, for the operand step below
   float s4b = 0.0f;             // bound on |S4 stage score| per unit high_n (score units)
+  float s1b = 0.0f;             // bound on |S1| (the S1 stage's score per unit mid_n)
   if (lane < 64) {
     const mrl_query_plan* p = a.plans + q;
     const float* qd = a.luts + (uint64_t)q * kQData;
@@ -2486,6 +2487,10 @@ __device__ __forceinline__ void mma_prep_body(const MmaPrepArgs& a, uint32_t q, 
     // f32 sum over 64 terms above and the reference's own rounding of S4 (sequential, 65 terms)
     // (the final pass bounds S4 only for w_s4 <= kMmaWideMaxWs4: then s * s4b / 64 < 2^15, a finite f16)
     s4b = tail && ws4 <= kMmaWideMaxWs4 ? ws4 * l1w4 * 0.5f * (1.0f + 1.0f / 4096.0f) : 0.0f;
+    // |S1| <= sum |w1| / 2 (w1 = 2 pos, S1 = sum pos (2 b - 1)), raised by 2^-12 for the f32 sum above and
+    // the reference's own rounding of S1 (sequential, 129 terms); s * s1b < 2^20 (every s |w1| < 2^14), so
+    // s * s1b / 24 is a finite f16
+    s1b = s1on ? l1w2 * 0.5f * (1.0f + 1.0f / 4096.0f) : 0.0f;
     const float eO = eden ? 0.0f : (fabsf(psum) * (1.0f / 1700.0f) + t25 * 2.0f * inv_s) * up;
     const float e0 =
         (fabsf(mean) * (1.0f / 16384.0f) + t25 * (l1w + l1w2 + l1w4 + fabsf(psum) + eP + e1 + e4 + eO)) * up +
@@ -2529,10 +2534,11 @@ __device__ __forceinline__ void mma_prep_body(const MmaPrepArgs& a, uint32_t q, 
       if (st < 16) v = src[mma_dim(st, kh, e)];
       else if (kh == 0 && e < 4) v = s_ex[e];   // error columns
       else if (kh == 0 && e == 4) v = psum;     // offset * prefix_sum
+      else if (kh == 0) v = s1b * (1.0f / 24.0f);  // S1 bound, 3 columns (f16 of 8 mid_n, rounded up)
       else if (kh == 1) v = s4b * (1.0f / 64.0f);  // S4 bound, 8 columns (f16 of 8 high_n, rounded up)
       const float x = s * v;
       uint32_t h = f32_to_f16(x);
-      if (st == 16 && (e < 4 || kh == 1) && h2f((uint16_t)h) < x) h += 1u;  // f16_up: magnitude no smaller than x
+      if (st == 16 && (e != 4 || kh == 1) && h2f((uint16_t)h) < x) h += 1u;  // f16_up: magnitude no smaller than x
       hv[e] = h;
     }
     a.ops[(uint64_t)q * (2 * kMmaSteps) + lane] =
@@ -2650,11 +2656,12 @@ __device__ __forceinline__ MmaMeta mma_meta(const uint4 x, const float* s_flag) 
 // Bounds (U, L) of a staged pair from its tile value acc = s (U' - tau): the
 // query's constants qk = {tau, 1/s, eP, e1, e4, eO, e0, ok} and the slot's
 // record word x = kRecS4Meta.  A slot beyond the operand range gets (+inf, -inf).
-// wpc != 0: the tile value still holds the S4 bound 8 h8 wpc (wpc = the
-// query's bound column, h8 = 8 high_n rounded up to f16): U stays, L drops by
-// twice the bound.
+// wpc != 0: the tile value still holds the stage bounds of a bounded final
+// pass: 8 h8 wpc for S4 (wpc = the query's S4 bound column, h8 = 8 high_n
+// rounded up to f16) and 3 m8 wpc1 for S1 (wpc1 = its S1 bound column, m8 =
+// 8 mid_n rounded up): U stays, L drops by twice the bounds.
 __device__ __forceinline__ void mma_bounds_x(float acc, const uint4 x, const float* qk, const float* s_flag, float* U,
-                                             float* L, float wpc = 0.0f) {
+                                             float* L, float wpc = 0.0f, float wpc1 = 0.0f) {
   const MmaMeta m = mma_meta(x, s_flag);
   float u = INFINITY, l = -INFINITY;
   if (m.safe) {
@@ -2664,7 +2671,8 @@ __device__ __forceinline__ void mma_bounds_x(float acc, const uint4 x, const flo
     const float u0 = tau + acc * k0.y;
     const float E = fabsf(m.m_scale) * k0.z + m.mid_n * k0.w + m.hn * k1.x + fabsf(m.m_offset) * k1.y + k1.z;
     const float mg = (fabsf(u0) + fabsf(tau)) * (1.0f / 4194304.0f);
-    const float W = wpc != 0.0f ? (8.0f * h2f((uint16_t)f16_up(8.0f * m.hn))) * wpc * k0.y : 0.0f;
+    const float W = (wpc != 0.0f ? (8.0f * h2f((uint16_t)f16_up(8.0f * m.hn))) * wpc * k0.y : 0.0f) +
+                    (wpc1 != 0.0f ? (3.0f * h2f((uint16_t)f16_up(8.0f * m.mid_n))) * wpc1 * k0.y : 0.0f);
     u = u0 + mg;
     l = (u0 - 2.0f * (E + W) * (1.0f + 1.0f / 1048576.0f)) - mg;
     if (!(u == u)) u = INFINITY;
@@ -2674,36 +2682,49 @@ __device__ __forceinline__ void mma_bounds_x(float acc, const uint4 x, const flo
   *L = l;
 }
 __device__ __forceinline__ void mma_bounds(float acc, const uint4* recs, uint32_t row, const float* qk,
-                                           const float* s_flag, float* U, float* L, float wpc = 0.0f) {
-  mma_bounds_x(acc, recs[(uint64_t)row * kRecWords + kRecS4Meta], qk, s_flag, U, L, wpc);
+                                           const float* s_flag, float* U, float* L, float wpc = 0.0f,
+                                           float wpc1 = 0.0f) {
+  mma_bounds_x(acc, recs[(uint64_t)row * kRecWords + kRecS4Meta], qk, s_flag, U, L, wpc, wpc1);
 }
 
-// The tile value of a pair from a final pass that bounded S4 (see
-// ScanArgs::mma_wide), made what the 17 K-steps would give with the e4
-// column counted twice (mma_bounds takes 2 e4 in such a pass): the eight
-// bound columns 8 h8 * piece (h8 = 8 high_n rounded up to f16, piece =
-// s * the query's S4 bound / 64 rounded up) are replaced by the S4 steps'
-// sum, V * sum_d A4[d] (2 b_d - 1) with V = f16(high_n * w_s4 / 2) and A4 the
-// query's S4 operands (in qa, steps 12..15, element order of mma_dim).
-// The products are exact and the few f32 roundings here are far inside the
-// second e4 column.  A slot beyond the operand range keeps its value.
-__device__ __forceinline__ float mma_tighten_x(float acc, const uint4 x, uint32_t qi, const uint4* qa,
-                                               const float* s_flag, float ws4) {
+// The tile value of a pair from a bounded final pass (see ScanArgs::mma_wide),
+// made what the 17 K-steps would give with the e1 and e4 columns counted
+// twice (mma_bounds takes 2 e1 and 2 e4 in such a pass).  The eight S4 bound
+// columns 8 h8 * piece (h8 = 8 high_n rounded up to f16, piece = s * the
+// query's S4 bound / 64 rounded up) are replaced by the S4 steps' sum,
+// V4 * sum_d A4[d] (2 b_d - 1) with V4 = f16(high_n * w_s4 / 2) and A4 the
+// query's S4 operands (in qa, steps 12..15, element order of mma_dim, bits b
+// from the record word x); the three S1 bound columns 8 m8 * piece1 (m8 =
+// 8 mid_n rounded up, piece1 = s * the query's S1 bound / 24 rounded up) by
+// the S1 steps' sum, V1 * sum_d A1[d] (2 b_d - 1) with V1 = f16(mid_n / 2), A1
+// the query's S1 operands (steps 4..11) and b the slot's S1 bits (record word
+// x1).  The products are exact and the f32 roundings here (a few 2^-24 of the
+// summed magnitudes) are far inside the second e1 / e4 columns.  A slot beyond
+// the operand range keeps its value.
+__device__ __forceinline__ float mma_tighten_x(float acc, const uint4 x, const uint4 x1, uint32_t qi,
+                                               const uint4* qa, const float* s_flag, float ws4) {
   const MmaMeta m = mma_meta(x, s_flag);
   if (!m.safe) return acc;
   const float hn = m.hn;
   const uint32_t ln = qi & 31u;
   const uint4* qt = qa + (uint64_t)(qi >> 5) * (kMmaSteps * 64);
-  const float c4 = h2f((uint16_t)(qt[16 * 64 + ln].y & 0xffffu));        // e4 column (K-half 0, element 2)
-  const float pc = h2f((uint16_t)(qt[16 * 64 + 32 + ln].x & 0xffffu));   // bound column (K-half 1)
+  const uint4 e0 = qt[16 * 64 + ln];  // the error step's query operand, K-half 0
+  const float c1 = h2f((uint16_t)(e0.x >> 16));                          // e1 column (element 1)
+  const float c4 = h2f((uint16_t)(e0.y & 0xffffu));                      // e4 column (element 2)
+  const float pc1 = h2f((uint16_t)(e0.z >> 16));                         // S1 bound column (element 5)
+  const float pc = h2f((uint16_t)(qt[16 * 64 + 32 + ln].x & 0xffffu));   // S4 bound column (K-half 1)
   const float hn16 = h2f((uint16_t)f16_bits(hn));
   const float h8 = h2f((uint16_t)f16_up(8.0f * hn));
   const float V = h2f((uint16_t)f16_bits(0.5f * hn * ws4));
-  float S = 0.0f;
-#pragma unroll
+  const float mid16 = h2f((uint16_t)f16_bits(m.mid_n));
+  const float m8 = h2f((uint16_t)f16_up(8.0f * m.mid_n));
+  const float V1 = h2f((uint16_t)f16_bits(0.5f * m.mid_n));
+  float S = 0.0f, S1 = 0.0f;
+  // (the loops are not unrolled: a wave's flush runs inside the scan loop, which has no registers to spare)
+#pragma unroll 1
   for (int kh = 0; kh < 2; ++kh) {
     const uint32_t bits = kh ? x.y : x.x;
-#pragma unroll
+#pragma unroll 1
     for (int st = 0; st < 4; ++st) {
       const uint4 a4 = qt[(12 + st) * 64 + 32 * kh + ln];
       const uint32_t w[4] = {a4.x, a4.y, a4.z, a4.w};
@@ -2714,9 +2735,20 @@ __device__ __forceinline__ float mma_tighten_x(float acc, const uint4 x, uint32_
         S += h2f((uint16_t)(sw & 0xffffu)) + h2f((uint16_t)(sw >> 16));
       }
     }
+#pragma unroll 1
+    for (int t = 0; t < 8; ++t) {
+      const uint32_t b1 = t < 4 ? (kh ? x1.z : x1.x) : (kh ? x1.w : x1.y);  // dword 2 kh + t / 4
+      const uint4 a1 = qt[(4 + t) * 64 + 32 * kh + ln];
+      const uint32_t w[4] = {a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t sw = w[j] ^ ((~b1 << (15 - 4 * (t & 3) - j)) & 0x80008000u);
+        S1 += h2f((uint16_t)(sw & 0xffffu)) + h2f((uint16_t)(sw >> 16));
+      }
+    }
   }
-  const float d = fmaf(hn16, c4, -((8.0f * h8) * pc));
-  return fmaf(V, S, acc + d);
+  const float d = fmaf(hn16, c4, -((8.0f * h8) * pc)) + fmaf(mid16, c1, -((3.0f * m8) * pc1));
+  return fmaf(V1, S1, fmaf(V, S, acc + d));
 }
 
 // Stages the pairs of pm (one query per lane: qi) as (row, tile value, query)
@@ -2749,11 +2781,11 @@ __device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, const floa
     const uint32_t g = atomicAdd(a.seg_count + sq, 1u);
     if (g < a.seg_cap) {
       float u, l;
-      // a wide pair keeps the S4 bound: its lower bound is widened by it twice
-      const float wpc = wide ? h2f((uint16_t)(qa[(uint64_t)((qq - q0) >> 5) * (kMmaSteps * 64) + 16 * 64 + 32 +
-                                                  ((qq - q0) & 31u)].x & 0xffffu))
-                             : 0.0f;
-      mma_bounds(acc, a.recs, row, s_qk[qq - q0], s_flag, &u, &l, wpc);
+      // a wide pair keeps the stage bounds: its lower bound is widened by them twice
+      const uint4* qe = qa + (uint64_t)((qq - q0) >> 5) * (kMmaSteps * 64) + 16 * 64 + ((qq - q0) & 31u);
+      const float wpc = wide ? h2f((uint16_t)(qe[32].x & 0xffffu)) : 0.0f;
+      const float wpc1 = wide ? h2f((uint16_t)(qe[0].z >> 16)) : 0.0f;
+      mma_bounds(acc, a.recs, row, s_qk[qq - q0], s_flag, &u, &l, wpc, wpc1);
       if (a.lmax) atomicMax(a.lmax + (uint64_t)qq * kMcCount, score_key(l));
       const uint64_t i = sq * a.seg_cap + g;
       a.cand_score[i] = u;
@@ -2768,10 +2800,10 @@ __device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, const floa
 // below the floor is marked kMmaDropped.
 template <typename ST>
 __device__ __forceinline__ void mma_stage_tighten(ST& st, const float* s_flag, uint32_t i, const uint4 x,
-                                                  const uint4* qa, float ws4) {
+                                                  const uint4 x1, const uint4* qa, float ws4) {
   const uint32_t q8 = st.q[i];
   if (!(q8 & kMmaWideFlag)) return;
-  const float t = mma_tighten_x(st.acc[i], x, q8 & 0x7fu, qa, s_flag, ws4);
+  const float t = mma_tighten_x(st.acc[i], x, x1, q8 & 0x7fu, qa, s_flag, ws4);
   st.acc[i] = t;
   if (t < 0.0f) {
     st.q[i] = kMmaDropped;
@@ -2794,10 +2826,14 @@ __device__ __forceinline__ void mma_wave_flush(ST& st, const ScanArgs& a, const 
   uint32_t* base = st.wbase[wave];
   cnt[lane] = 0u;
   if (wide) {
-#pragma unroll
+    // one entry at a time: this flush runs inside the scan loop, which has no registers to spare
+#pragma unroll 1
     for (int k = 0; k < kPer; ++k) {
       const uint32_t e = lane + 64u * (uint32_t)k, i = (uint32_t)wave * ST::kCap + e;
-      if (e < n) mma_stage_tighten(st, s_flag, i, a.recs[(uint64_t)st.row[i] * kRecWords + kRecS4Meta], qa, ws4);
+      if (e < n) {
+        const uint4* rec = a.recs + (uint64_t)st.row[i] * kRecWords;
+        mma_stage_tighten(st, s_flag, i, rec[kRecS4Meta], rec[kRecS1], qa, ws4);
+      }
     }
   }
   wave_lds_sync();
@@ -3046,8 +3082,8 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
       qk[0] = tau;
       qk[1] = mc[kMcInvS];
       qk[2] = mc[kMcEP];
-      qk[3] = mc[kMcE1];
-      qk[4] = (MODE == 1 && WIDE) ? 2.0f * mc[kMcE4] : mc[kMcE4];  // mma_tighten's second e4 column
+      qk[3] = (MODE == 1 && WIDE) ? 2.0f * mc[kMcE1] : mc[kMcE1];  // mma_tighten's second e1 column
+      qk[4] = (MODE == 1 && WIDE) ? 2.0f * mc[kMcE4] : mc[kMcE4];  // and second e4 column
       qk[5] = mc[kMcEO];
       qk[6] = e0q;
       qk[7] = ok ? 1.0f : 0.0f;
@@ -3206,6 +3242,12 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
             d[0] = (sc_b & 0x7fffu) | (f16_bits(mid_n) << 16);
             d[1] = f16_bits(hn) | ((of_b & 0x7fffu) << 16);
             d[2] = of_b;
+            if (MODE == 1 && wide) {
+              // the S1 bound columns (elements 5..7): 8 mid_n rounded up, 3 times (as mma_tighten)
+              const uint32_t m8 = f16_up(8.0f * mid_n);
+              d[2] |= m8 << 16;
+              d[3] = m8 * 0x10001u;
+            }
           } else if (MODE == 1 && wide) {
             // the S4 bound columns: 8 high_n rounded up (as mma_tighten)
             d[0] = d[1] = d[2] = d[3] = f16_up(8.0f * hn) * 0x10001u;
@@ -3241,11 +3283,11 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
       };
       if constexpr (wide_pass) {
 #pragma unroll
-        for (int st = 0; st < 11; ++st) kstep(st, st + 1);
-        kstep(11, wide ? 16 : 12);
-        if (!wide) {  // else the S4 steps' score is bounded in step 16
+        for (int st = 0; st < 3; ++st) kstep(st, st + 1);
+        kstep(3, wide ? 16 : 4);
+        if (!wide) {  // else the S1 and S4 stages' scores are bounded in step 16
 #pragma unroll
-          for (int st = 12; st < 16; ++st) kstep(st, st + 1);
+          for (int st = 4; st < 16; ++st) kstep(st, st + 1);
         }
         kstep(16, -1);
         static_assert(kMmaSteps == 17, "the step schedule above assumes prefix 4, S1 8, S4 4, error 1");
@@ -3404,19 +3446,21 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
     // Every staged entry of the workgroup: entry tid + 64 WPG k of the
     // regions laid end to end; the record words are loaded in one round.
     constexpr int kFl = Staging::kCap / 64;
-    uint4 xr[kFl];
+    uint4 xr[kFl], x1r[kFl];  // the record words with the meta / S4 bits and (bounded pass) the S1 bits
     uint32_t ie[kFl];  // staging index, or ~0u past a region's fill
 #pragma unroll
     for (int k = 0; k < kFl; ++k) {
       const uint32_t j = (uint32_t)tid + 64u * WPG * (uint32_t)k;
       const uint32_t w = j / (uint32_t)Staging::kCap, e = j % (uint32_t)Staging::kCap;
       ie[k] = e < s_st.n[w] ? j : ~0u;
-      xr[k] = ie[k] != ~0u ? a.recs[(uint64_t)s_st.row[j] * kRecWords + kRecS4Meta] : make_uint4(0u, 0u, 0u, 0u);
+      const uint4* rec = a.recs + (uint64_t)(ie[k] != ~0u ? s_st.row[j] : 0u) * kRecWords;
+      xr[k] = ie[k] != ~0u ? rec[kRecS4Meta] : make_uint4(0u, 0u, 0u, 0u);
+      x1r[k] = wide_pass && ie[k] != ~0u ? rec[kRecS1] : make_uint4(0u, 0u, 0u, 0u);
     }
     if (wide_pass) {
 #pragma unroll
       for (int k = 0; k < kFl; ++k)
-        if (ie[k] != ~0u) mma_stage_tighten(s_st, s_flag, ie[k], xr[k], qa, ws4);
+        if (ie[k] != ~0u) mma_stage_tighten(s_st, s_flag, ie[k], xr[k], x1r[k], qa, ws4);
       __syncthreads();
     }
 #pragma unroll
