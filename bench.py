@@ -25,8 +25,10 @@ timed region), on the library's stream; `traffic` is the committed rocprofv3
 FETCH_SIZE + WRITE_SIZE reading for the same workload.  Batches under 8 run
 the one-query k_scan, HBM-bound: 4096 B per block scanned.  Batches of 8+
 run the MFMA-bounded scan, whose final pass (k_scan_mma over every block)
-dominates: 2 x 261 f16 MACs per (query, vector) pair against the dense f16
-MFMA peak, with that launch's HBM rate beside it.  `cold_cache` repeats the
+dominates: 2 x 261 f16 MACs per (query, vector) pair with full tiles, 2 x 80
+in a bounded pass (no S1 / S4 bits, their bound columns instead), and 4096 B
+per block; the roof that binds is the larger floor (MACs at the dense f16
+MFMA peak or bytes at the HBM peak), and both fractions are reported.  `cold_cache` repeats the
 profiled steps with a 1 GiB read before each (the L2s and the 256 MB
 Infinity Cache evicted).  `reruns_per_step` counts the queries whose final
 floor needed a re-run (safe: done on the device inside the step, by two
@@ -65,11 +67,11 @@ sys.path.insert(0, os.path.join(ROOT, "mrl-index-rust-vector_amd"))
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFS = 2500.0  # dense f16 MFMA, MI355X
 # MACs per (query, vector) pair of the MFMA bound: 64 prefix dims, 128 S1
-# bits, 64 S4 bits and the 5 meta / error columns of the last K-step; a final
-# pass that bounds the S4 stage (profile flag MRL_KT_S4_BOUNDED) runs no S4
-# bits and 8 bound columns instead
+# bits, 64 S4 bits and the 5 meta / error columns of the last K-step; a
+# bounded final pass (profile flag MRL_KT_S4_BOUNDED) runs no S1 or S4 bits,
+# and 3 S1 and 8 S4 bound columns instead
 MMA_MACS_PER_PAIR = 64 + 128 + 64 + 5
-MMA_MACS_PER_PAIR_S4_BOUNDED = 64 + 128 + 5 + 8
+MMA_MACS_PER_PAIR_BOUNDED = 64 + 5 + 3 + 8
 KT_S4_BOUNDED = 1
 EVICT_BYTES = 1 << 30  # cold-cache runs read this much between steps
 SETTLE_MS = 200.0  # clock settle before each workload's warmup (device reads, no steps)
@@ -217,22 +219,29 @@ def roofline_of(groups, nq, prof_steps, w, cold=False, scanned=None):
         pairs = 64.0 * block_queries
         # the MACs of the pass that ran: the S4-bounded pass needs fewer per pair
         s4_bounded = float(np.mean([(f & KT_S4_BOUNDED) != 0 for f in g["flags"]]))
-        macs = s4_bounded * MMA_MACS_PER_PAIR_S4_BOUNDED + (1.0 - s4_bounded) * MMA_MACS_PER_PAIR
+        macs = s4_bounded * MMA_MACS_PER_PAIR_BOUNDED + (1.0 - s4_bounded) * MMA_MACS_PER_PAIR
         flops = 2.0 * macs * pairs
-        achieved = flops / (avg_ms / 1000.0) / 1e12
+        tflops = flops / (avg_ms / 1000.0) / 1e12
         # the blocks one query scanned (a block shared by the batch is read once)
         bytes_per_launch = 4096.0 * block_queries / nq
         hbm = bytes_per_launch / (avg_ms / 1000.0) / 1e9
+        # the roof that binds is the larger floor: the MACs at the dense f16 MFMA peak, or the bytes at
+        # the HBM peak (a bounded final pass runs so few MACs that its bytes bind)
+        hbm_bound = bytes_per_launch / (HBM_PEAK_GBS * 1e9) >= flops / (MFMA_F16_PEAK_TFS * 1e12)
         # (the committed counters cover the standard layout; a block-listed pass reads other bytes)
         traffic = None if cold or scanned is not None else committed_traffic("k_scan_mma", w.name)
-        r = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
-             "frac": round(achieved / MFMA_F16_PEAK_TFS, 4),
+        r = {"bound": "hbm" if hbm_bound else "mfma",
+             "achieved": round(hbm if hbm_bound else tflops, 1),
+             "peak": HBM_PEAK_GBS if hbm_bound else MFMA_F16_PEAK_TFS,
+             "unit": "GB/s" if hbm_bound else "TFLOP/s",
+             "frac": round(hbm / HBM_PEAK_GBS if hbm_bound else tflops / MFMA_F16_PEAK_TFS, 4),
              "traffic": traffic["bytes_per_launch"] if traffic else None,
              "kernel": "k_scan_mma (final pass)", "launches_per_step": len(g["ms"]) / prof_steps,
              "kernel_avg_ms": round(avg_ms, 5), "algorithmic_flops_per_launch": flops,
              "macs_per_pair": round(macs, 2), "s4_bounded_launches": round(s4_bounded, 4),
-             "algorithmic_bytes_per_launch": bytes_per_launch, "hbm_achieved_gb_s": round(hbm, 1),
-             "hbm_frac": round(hbm / HBM_PEAK_GBS, 4)}
+             "algorithmic_bytes_per_launch": bytes_per_launch,
+             "mfma_achieved_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_F16_PEAK_TFS, 4),
+             "hbm_achieved_gb_s": round(hbm, 1), "hbm_frac": round(hbm / HBM_PEAK_GBS, 4)}
     if traffic:
         r["traffic_source"] = traffic["source"]
     return r

@@ -53,16 +53,26 @@ def test_mfma_roofline_by_hand():
     }
     r = bench.roofline_of(groups, 64, 2, w)
     pairs = 64.0 * n_blocks * 64
-    macs = 0.5 * (64 + 128 + 5 + 8) + 0.5 * (64 + 128 + 64 + 5)
+    macs = 0.5 * (64 + 5 + 3 + 8) + 0.5 * (64 + 128 + 64 + 5)
     flops = 2.0 * macs * pairs
+    # MFMA floor 2 x 170.5 x 563.2M / 2.5 PFLOP/s = 76.8 us against the HBM floor 563.2 MB / 8 TB/s = 70.4 us
     assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s" and r["peak"] == 2500.0
     assert r["kernel_avg_ms"] == pytest.approx(0.275)
     assert r["algorithmic_flops_per_launch"] == pytest.approx(flops)
     assert r["achieved"] == pytest.approx(flops / 0.275e-3 / 1e12, rel=1e-4)
     assert r["frac"] == pytest.approx(r["achieved"] / 2500.0, abs=1e-4)
+    assert r["mfma_frac"] == r["frac"]
     assert r["launches_per_step"] == 1.0
     # the same launch's HBM figure: 4096 B per block, each block read once for the whole batch
     assert r["hbm_achieved_gb_s"] == pytest.approx(4096.0 * n_blocks / 0.275e-3 / 1e9, rel=1e-4)
+    # every launch bounded: 80 MACs per pair, the bytes bind (MFMA floor 36.0 us < HBM floor 70.4 us)
+    gb = dict(groups)
+    gb[("scan", 1)] = {"ms": [0.2, 0.2], "blocks": [n_blocks, n_blocks], "flags": [bench.KT_S4_BOUNDED] * 2}
+    rb = bench.roofline_of(gb, 64, 2, w)
+    assert rb["bound"] == "hbm" and rb["unit"] == "GB/s" and rb["peak"] == 8000.0 and rb["macs_per_pair"] == 80
+    assert rb["achieved"] == pytest.approx(4096.0 * n_blocks / 0.2e-3 / 1e9, rel=1e-4)
+    assert rb["frac"] == rb["hbm_frac"]
+    assert rb["mfma_achieved_tflops"] == pytest.approx(2.0 * 80 * pairs / 0.2e-3 / 1e12, rel=1e-4)
     assert r["traffic"] == bench.committed_traffic("k_scan_mma", w.name)["bytes_per_launch"]
     # cold-cache runs quote no traffic; block-listed passes count the pairs they scanned
     assert bench.roofline_of(groups, 64, 2, w, cold=True)["traffic"] is None
