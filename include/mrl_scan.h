@@ -428,7 +428,7 @@ typedef struct mrl_kernel_time {
   uint32_t n_blocks; /* blocks this launch scanned */
   uint32_t n_queries;
   float ms;          /* kernel duration from events recorded by the dispatch itself */
-  uint32_t flags;    /* MRL_KT_S4_BOUNDED: an MFMA final pass that bounded the S4 stage (13 K-steps a tile) */
+  uint32_t flags;    /* MRL_KT_S4_BOUNDED: an MFMA final pass that bounded the S1 and S4 stages (5 K-steps a tile) */
 } mrl_kernel_time;
 #define MRL_KT_S4_BOUNDED 1u
 
@@ -444,14 +444,14 @@ int mrl_ctx_profile_collect(mrl_ctx *ctx, mrl_kernel_time *out, uint32_t max, ui
  * cold-cache measurement.  Not timed as a scan kernel. */
 int mrl_ctx_evict_caches(mrl_ctx *ctx, uint64_t bytes);
 /* Cost policy of the MFMA final pass (no reference counterpart: the
- * reference's scan has no tiles).  The pass may replace its four S4
- * K-steps by a bound of the S4 stage score; each pair that passes is then
- * given its S4 sum from the query operands and the slot's S4 bits before it
- * is written out, so the results are the same either way.  AUTO takes the
- * bound when the pass is expected to append few pairs (from the sample's
- * floor rank); ALWAYS takes it wherever it applies (w_s4 <= 4); NEVER
- * runs the full tiles.  mrl_scan_mma_bounds reports the bounds of the
- * S4-bounded pass under ALWAYS and of the full tiles otherwise. */
+ * reference's scan has no tiles).  The pass may replace its eight S1 and
+ * four S4 K-steps by bounds of the two stages' scores; each pair that passes
+ * is then given its S1 and S4 sums from the query operands and the slot's
+ * bits before it is written out, so the results are the same either way.
+ * AUTO takes the bounds when the pass is expected to append few pairs (from
+ * the sample's floor rank); ALWAYS takes them wherever they apply
+ * (w_s4 <= 4); NEVER runs the full tiles.  mrl_scan_mma_bounds reports the
+ * bounds of the bounded pass under ALWAYS and of the full tiles otherwise. */
 typedef enum { MRL_S4_BOUND_AUTO = 0, MRL_S4_BOUND_ALWAYS = 1, MRL_S4_BOUND_NEVER = 2 } mrl_s4_bound_policy;
 int mrl_ctx_set_s4_bound(mrl_ctx *ctx, int policy);
 
