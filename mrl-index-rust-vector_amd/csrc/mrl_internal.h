@@ -276,6 +276,10 @@ struct ScanArgs {
 constexpr uint8_t kMmaWideFlag = 0x80;   // staged query index: the tile value holds the S4 bound
 constexpr uint8_t kMmaDropped = 0xff;    // staged entry dropped (upper bound below the floor)
 constexpr uint32_t kMmaWideSlack = 16;
+// A final-pass wave writes out its staging region once fewer than this many
+// of its entries are free (the next tile's appends, on clustered data
+// rarely more; those past the end go straight to their segments).
+constexpr uint32_t kMmaFlushRoom = 64;
 constexpr int kMaxListWg = 1024;  // workgroup lists per query a later sampling stage may keep
 
 // Exact finishing of the MFMA path.  k_finish, one workgroup per query: a

@@ -2700,7 +2700,8 @@ __device__ __forceinline__ void mma_bounds(float acc, const uint4* recs, uint32_
 // the query's S1 operands (steps 4..11) and b the slot's S1 bits (record word
 // x1).  The products are exact and the f32 roundings here (a few 2^-24 of the
 // summed magnitudes) are far inside the second e1 / e4 columns.  A slot beyond
-// the operand range keeps its value.
+// the operand range keeps its value.  U: unroll factor of the operand loops.
+template <int U>
 __device__ __forceinline__ float mma_tighten_x(float acc, const uint4 x, const uint4 x1, uint32_t qi,
                                                const uint4* qa, const float* s_flag, float ws4) {
   const MmaMeta m = mma_meta(x, s_flag);
@@ -2720,11 +2721,10 @@ __device__ __forceinline__ float mma_tighten_x(float acc, const uint4 x, const u
   const float m8 = h2f((uint16_t)f16_up(8.0f * m.mid_n));
   const float V1 = h2f((uint16_t)f16_bits(0.5f * m.mid_n));
   float S = 0.0f, S1 = 0.0f;
-  // (the loops are not unrolled: a wave's flush runs inside the scan loop, which has no registers to spare)
 #pragma unroll 1
   for (int kh = 0; kh < 2; ++kh) {
     const uint32_t bits = kh ? x.y : x.x;
-#pragma unroll 1
+#pragma unroll U
     for (int st = 0; st < 4; ++st) {
       const uint4 a4 = qt[(12 + st) * 64 + 32 * kh + ln];
       const uint32_t w[4] = {a4.x, a4.y, a4.z, a4.w};
@@ -2735,7 +2735,7 @@ __device__ __forceinline__ float mma_tighten_x(float acc, const uint4 x, const u
         S += h2f((uint16_t)(sw & 0xffffu)) + h2f((uint16_t)(sw >> 16));
       }
     }
-#pragma unroll 1
+#pragma unroll U
     for (int t = 0; t < 8; ++t) {
       const uint32_t b1 = t < 4 ? (kh ? x1.z : x1.x) : (kh ? x1.w : x1.y);  // dword 2 kh + t / 4
       const uint4 a1 = qt[(4 + t) * 64 + 32 * kh + ln];
@@ -2798,12 +2798,12 @@ __device__ __forceinline__ void mma_append(ST& st, const ScanArgs& a, const floa
 // A staged entry of a pass that bounded S4 (flag kMmaWideFlag) is made
 // exact (mma_tighten_x, x = its record word); one whose upper bound is then
 // below the floor is marked kMmaDropped.
-template <typename ST>
+template <int U, typename ST>
 __device__ __forceinline__ void mma_stage_tighten(ST& st, const float* s_flag, uint32_t i, const uint4 x,
                                                   const uint4 x1, const uint4* qa, float ws4) {
   const uint32_t q8 = st.q[i];
   if (!(q8 & kMmaWideFlag)) return;
-  const float t = mma_tighten_x(st.acc[i], x, x1, q8 & 0x7fu, qa, s_flag, ws4);
+  const float t = mma_tighten_x<U>(st.acc[i], x, x1, q8 & 0x7fu, qa, s_flag, ws4);
   st.acc[i] = t;
   if (t < 0.0f) {
     st.q[i] = kMmaDropped;
@@ -2815,7 +2815,8 @@ __device__ __forceinline__ void mma_stage_tighten(ST& st, const float* s_flag, u
 
 // Writes out the n entries of this wave's region: a count per query in LDS,
 // one global reservation per query with entries, then each entry's bounds
-// (wide entries made exact first).
+// (wide entries made exact first).  Every entry's record words are requested
+// at once, and the bounds use the same words.
 template <typename ST>
 __device__ __forceinline__ void mma_wave_flush(ST& st, const ScanArgs& a, const float (*s_qk)[8],
                                                const float* s_flag, int wave, uint32_t n, uint32_t q0,
@@ -2825,15 +2826,19 @@ __device__ __forceinline__ void mma_wave_flush(ST& st, const ScanArgs& a, const 
   uint32_t* cnt = st.wcnt[wave];
   uint32_t* base = st.wbase[wave];
   cnt[lane] = 0u;
+  uint4 xr[kPer], x1r[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t e = lane + 64u * (uint32_t)k;
+    const uint4* rec = a.recs + (uint64_t)(e < n ? st.row[(uint32_t)wave * ST::kCap + e] : 0u) * kRecWords;
+    xr[k] = e < n ? rec[kRecS4Meta] : make_uint4(0u, 0u, 0u, 0u);
+    x1r[k] = wide && e < n ? rec[kRecS1] : make_uint4(0u, 0u, 0u, 0u);
+  }
   if (wide) {
-    // one entry at a time: this flush runs inside the scan loop, which has no registers to spare
-#pragma unroll 1
+#pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const uint32_t e = lane + 64u * (uint32_t)k, i = (uint32_t)wave * ST::kCap + e;
-      if (e < n) {
-        const uint4* rec = a.recs + (uint64_t)st.row[i] * kRecWords;
-        mma_stage_tighten(st, s_flag, i, rec[kRecS4Meta], rec[kRecS1], qa, ws4);
-      }
+      const uint32_t e = lane + 64u * (uint32_t)k;
+      if (e < n) mma_stage_tighten<4>(st, s_flag, (uint32_t)wave * ST::kCap + e, xr[k], x1r[k], qa, ws4);
     }
   }
   wave_lds_sync();
@@ -2858,7 +2863,7 @@ __device__ __forceinline__ void mma_wave_flush(ST& st, const ScanArgs& a, const 
       if (g < a.seg_cap) {
         const uint32_t row = st.row[i];
         float u, l;
-        mma_bounds(st.acc[i], a.recs, row, s_qk[qi], s_flag, &u, &l);
+        mma_bounds_x(st.acc[i], xr[k], s_qk[qi], s_flag, &u, &l);
         atomicMax(&st.lmax[qi], score_key(l));
         const uint64_t o = ((uint64_t)(q0 + qi) * a.nseg + seg) * a.seg_cap + g;
         a.cand_score[o] = u;
@@ -3015,6 +3020,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   __shared__ float s_hinv[kMmaQ];                 // histogram scale of each query (2^-e, sampling passes)
   __shared__ unsigned int s_stats[kStatCount];
   __shared__ uint32_t s_anyall;  // sampling: some query counts every lower bound
+  __shared__ uint32_t s_next;    // final passes: the workgroup's next item number
   __shared__ Staging s_st;
 
   const int tid = threadIdx.x;
@@ -3022,7 +3028,10 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   const uint32_t lane = lane_id(), kh = lane >> 5, vl = lane & 31u;
   const uint32_t q0 = blockIdx.y * kMmaQ;
   const int nq = (int)min((uint32_t)kMmaQ, a.n_q - q0);
-  if (tid == 0) s_anyall = 0u;
+  if (tid == 0) {
+    s_anyall = 0u;
+    s_next = 0u;
+  }
   __syncthreads();
 
   // item i: half i % 2 of the block at position i / 2 (pos << shift, or
@@ -3031,8 +3040,29 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   const uint32_t n_items = 2u * (bl ? a.bcount[blockIdx.y] : a.n_pos);
   auto block_of = [&](uint32_t pos) -> uint64_t { return bl ? (uint64_t)bl[pos] : (uint64_t)pos << a.shift; };
   const uint32_t stride = gridDim.x * WPG - 1;  // odd: see k_scan
-  const uint32_t first = blockIdx.x * WPG + wave;
-  const uint32_t n_it = first < stride ? n_items : 0u;
+  // The final passes share a workgroup's items among its waves: items
+  // blockIdx.x + gridDim.x k, each wave taking k from an LDS counter two
+  // items ahead (a wave slowed by its appends then takes fewer).  The
+  // sampling passes keep the fixed stride.
+  constexpr bool dyn = !SAMPLE;
+  auto grab = [&]() -> uint32_t {  // the next k (lane 0's value)
+    uint32_t k = 0u;
+    if (lane == 0u) k = atomicAdd(&s_next, 1u);
+    return k;
+  };
+  auto item_of = [&](uint32_t k) -> uint32_t {  // n_items or more past the end
+    const uint32_t kk = (uint32_t)__builtin_amdgcn_readfirstlane((int)k);
+    return kk < n_items ? blockIdx.x + gridDim.x * kk : n_items;
+  };
+  uint32_t first = blockIdx.x * WPG + wave;
+  uint32_t after = first + stride;  // the item after the current one (n_it or more: none)
+  uint32_t pend = 0u;               // (dyn) the k of the item after that, requested one item early
+  const uint32_t n_it = dyn || first < stride ? n_items : 0u;
+  if (dyn) {
+    first = item_of(grab());
+    after = item_of(grab());
+    pend = grab();
+  }
   uint32_t it_cur = first;
   uint64_t b_cur = 0;
   MmaRaw cur{};
@@ -3151,12 +3181,19 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   // item.  (The sampling passes keep the register.)
   const bool pre = !SAMPLE && bl != nullptr;
   uint64_t b_pre = 0;
-  if (pre && first + stride < n_it) b_pre = block_of((first + stride) >> 1);
-  for (uint32_t it = first; it < n_it; it += stride) {
-    const uint32_t it_nxt = it + stride < n_it ? it + stride : it_cur;
+  if (pre && after < n_it) b_pre = block_of(after >> 1);
+  for (uint32_t it = first; it < n_it;) {
+    const uint32_t it_adv = after;  // the next item
+    if (dyn) {
+      after = item_of(pend);
+      pend = grab();
+    } else {
+      after = it_adv + stride;
+    }
+    const uint32_t it_nxt = it_adv < n_it ? it_adv : it_cur;
     uint64_t b_nxt = b_cur;
-    if (it + stride < n_it) b_nxt = pre ? b_pre : block_of(it_nxt >> 1);
-    if (pre && it + 2u * stride < n_it) b_pre = block_of((it + 2u * stride) >> 1);
+    if (it_adv < n_it) b_nxt = pre ? b_pre : block_of(it_nxt >> 1);
+    if (pre && after < n_it) b_pre = block_of(after >> 1);
     const MmaRaw nxt = mma_load(a.idx, a.recs, b_nxt, it_nxt & 1u);
     const uint32_t b = (uint32_t)b_cur, h = it_cur & 1u;
     const uint32_t min_ts = (uint32_t)__builtin_amdgcn_readlane(cur.hdr, 0);
@@ -3377,12 +3414,6 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
         // beyond the operand range is a candidate of every present query: its
         // registers are raised to +inf (its bounds are then taken as +-inf);
         // MODE 2 takes every present query's register as it is.
-        // a region that may not hold this tile's pairs is written out first
-        if (fill > (uint32_t)Staging::kCap - 128u) {
-          mma_wave_flush(s_st, a, s_qk, s_flag, wave, min(fill, (uint32_t)Staging::kCap), q0, seg, wide_pass, qa,
-                         ws4);
-          fill = 0u;
-        }
         const uint32_t c_app0 = c_app;
         const uint64_t actm = ballot(act);
         if (MODE == 1 && ballot(act && !safe) != 0) {
@@ -3425,11 +3456,20 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
           w_app += c_app - c_app0;
           if (w_app > w_items * w_lim + kMmaWideSlack) wide = false;
         }
+        // A region that may not hold the next tile's pairs is written out
+        // now, while this tile's registers are free.  (Pairs past a region's
+        // end go straight to their segments.)
+        if (fill > (uint32_t)Staging::kCap - kMmaFlushRoom) {
+          mma_wave_flush(s_st, a, s_qk, s_flag, wave, min(fill, (uint32_t)Staging::kCap), q0, seg, wide_pass, qa,
+                         ws4);
+          fill = 0u;
+        }
       }
     }
     cur = nxt;
     it_cur = it_nxt;
     b_cur = b_nxt;
+    it = it_adv;
   }
   if (a.stats && lane == 0) {
     atomicAdd(&s_stats[kStatBlocks], c_blocks);
@@ -3460,7 +3500,7 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
     if (wide_pass) {
 #pragma unroll
       for (int k = 0; k < kFl; ++k)
-        if (ie[k] != ~0u) mma_stage_tighten(s_st, s_flag, ie[k], xr[k], x1r[k], qa, ws4);
+        if (ie[k] != ~0u) mma_stage_tighten<8>(s_st, s_flag, ie[k], xr[k], x1r[k], qa, ws4);
       __syncthreads();
     }
 #pragma unroll
