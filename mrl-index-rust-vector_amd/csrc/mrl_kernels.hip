@@ -3274,21 +3274,23 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) d[j] = hp4 | ((nx << (15 - 4 * tt - j)) & 0x80008000u);
         } else {
-          d[0] = d[1] = d[2] = d[3] = 0u;
-          if (kh == 0) {
-            d[0] = (sc_b & 0x7fffu) | (f16_bits(mid_n) << 16);
-            d[1] = f16_bits(hn) | ((of_b & 0x7fffu) << 16);
-            d[2] = of_b;
-            if (MODE == 1 && wide) {
-              // the S1 bound columns (elements 5..7): 8 mid_n rounded up, 3 times (as mma_tighten)
-              const uint32_t m8 = f16_up(8.0f * mid_n);
-              d[2] |= m8 << 16;
-              d[3] = m8 * 0x10001u;
-            }
-          } else if (MODE == 1 && wide) {
-            // the S4 bound columns: 8 high_n rounded up (as mma_tighten)
-            d[0] = d[1] = d[2] = d[3] = f16_up(8.0f * hn) * 0x10001u;
+          // K-half 0: the error columns and the offset; K-half 1: zero.  In a
+          // bounded pass K-half 0 also carries the S1 bound columns (elements
+          // 5..7: 8 mid_n rounded up, 3 times) and K-half 1 the S4 bound
+          // columns (8 high_n rounded up), as mma_tighten takes them.  Both
+          // halves' words are formed and each lane takes its own (no branch
+          // on the lane's half).
+          uint32_t e2 = of_b, e3 = 0u, k1 = 0u;
+          if (MODE == 1 && wide) {
+            const uint32_t m8 = f16_up(8.0f * mid_n);
+            e2 |= m8 << 16;
+            e3 = m8 * 0x10001u;
+            k1 = f16_up(8.0f * hn) * 0x10001u;
           }
+          d[0] = kh ? k1 : (sc_b & 0x7fffu) | (f16_bits(mid_n) << 16);
+          d[1] = kh ? k1 : f16_bits(hn) | ((of_b & 0x7fffu) << 16);
+          d[2] = kh ? k1 : e2;
+          d[3] = kh ? k1 : e3;
         }
         return make_uint4(d[0], d[1], d[2], d[3]);
       };
