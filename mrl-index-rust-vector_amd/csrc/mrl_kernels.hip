@@ -2616,15 +2616,15 @@ __device__ __forceinline__ MmaRaw mma_load(const uint8_t* idx, const uint4* recs
   return r;
 }
 
-// Candidate appends of one workgroup, staged in LDS and flushed at its end
-// with one global atomic per (workgroup, query).  Each wave owns a region of
-// kMmaWaveCap entries and keeps its fill count in a scalar register, so an
-// append needs no atomic.
+// Candidate appends of one workgroup, staged in LDS.  Each wave owns a
+// region of CAP entries and keeps its fill count in a scalar register, so an
+// append needs no atomic; a region is written out when nearly full
+// (mma_wave_flush) and at the kernel's end (one global reservation per query
+// for the workgroup).
 template <int W, int CAP>
 struct MmaStaging {
   static constexpr int kWaves = W;
   static constexpr int kCap = CAP;  // entries per wave
-  uint32_t n[W];
   uint32_t drop;            // wide entries dropped once made exact (taken off the append count)
   uint32_t lmax[kMmaQ];     // largest lower-bound key written per query (ScanArgs::lmax)
   uint32_t cnt[kMmaQ];      // final flush: entries per query of the workgroup
@@ -3084,7 +3084,6 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
     s_flag[256 + tid] = a.flag_tabs[256 + tid];
   }
   if (tid < kStatCount) s_stats[tid] = 0u;
-  if (tid < WPG) s_st.n[tid] = 0u;
   if (tid == 0) s_st.drop = 0u;
   if (tid < kMmaQ) s_st.lmax[tid] = 0u;
   if (tid < kMmaQ) {
@@ -3483,31 +3482,37 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
     if (tid < nq) a.lcount[(uint64_t)(q0 + tid) * a.lbuf_stride + blockIdx.x] = min(s_st.cnt[tid], a.lcap);
   }
   if constexpr (!SAMPLE) {
-    if (lane == 0) s_st.n[wave] = min(fill, (uint32_t)Staging::kCap);
-    __syncthreads();
-    // Every staged entry of the workgroup: entry tid + 64 WPG k of the
-    // regions laid end to end; the record words are loaded in one round.
+    // Each wave writes out its own region (entry lane + 64 k, as its flushes
+    // in the loop): its record words requested at once, then (bounded pass)
+    // the entries made exact and the survivors counted per query, without
+    // waiting for the other waves; then one reservation per query for the
+    // workgroup and each entry's bounds from the same record words.
     constexpr int kFl = Staging::kCap / 64;
-    uint4 xr[kFl], x1r[kFl];  // the record words with the meta / S4 bits and (bounded pass) the S1 bits
-    uint32_t ie[kFl];  // staging index, or ~0u past a region's fill
+    const uint32_t nf = min(fill, (uint32_t)Staging::kCap);
+    const uint32_t r0 = (uint32_t)wave * Staging::kCap;
+    uint4 xr[kFl];  // the record words with the meta / S4 bits
+    {
+      uint4 x1r[kFl];  // (bounded pass) the S1 bits
+#pragma unroll
+      for (int k = 0; k < kFl; ++k) {
+        const uint32_t e = lane + 64u * (uint32_t)k;
+        const uint4* rec = a.recs + (uint64_t)(e < nf ? s_st.row[r0 + e] : 0u) * kRecWords;
+        xr[k] = e < nf ? rec[kRecS4Meta] : make_uint4(0u, 0u, 0u, 0u);
+        x1r[k] = wide_pass && e < nf ? rec[kRecS1] : make_uint4(0u, 0u, 0u, 0u);
+      }
+      if (wide_pass) {
+#pragma unroll
+        for (int k = 0; k < kFl; ++k) {
+          const uint32_t e = lane + 64u * (uint32_t)k;
+          if (e < nf) mma_stage_tighten<8>(s_st, s_flag, r0 + e, xr[k], x1r[k], qa, ws4);
+        }
+      }
+    }
 #pragma unroll
     for (int k = 0; k < kFl; ++k) {
-      const uint32_t j = (uint32_t)tid + 64u * WPG * (uint32_t)k;
-      const uint32_t w = j / (uint32_t)Staging::kCap, e = j % (uint32_t)Staging::kCap;
-      ie[k] = e < s_st.n[w] ? j : ~0u;
-      const uint4* rec = a.recs + (uint64_t)(ie[k] != ~0u ? s_st.row[j] : 0u) * kRecWords;
-      xr[k] = ie[k] != ~0u ? rec[kRecS4Meta] : make_uint4(0u, 0u, 0u, 0u);
-      x1r[k] = wide_pass && ie[k] != ~0u ? rec[kRecS1] : make_uint4(0u, 0u, 0u, 0u);
+      const uint32_t e = lane + 64u * (uint32_t)k;
+      if (e < nf && s_st.q[r0 + e] != kMmaDropped) atomicAdd(&s_st.cnt[s_st.q[r0 + e]], 1u);
     }
-    if (wide_pass) {
-#pragma unroll
-      for (int k = 0; k < kFl; ++k)
-        if (ie[k] != ~0u) mma_stage_tighten<8>(s_st, s_flag, ie[k], xr[k], x1r[k], qa, ws4);
-      __syncthreads();
-    }
-#pragma unroll
-    for (int k = 0; k < kFl; ++k)
-      if (ie[k] != ~0u && s_st.q[ie[k]] != kMmaDropped) atomicAdd(&s_st.cnt[s_st.q[ie[k]]], 1u);
     __syncthreads();
     if (tid < nq) {
       const uint32_t c = s_st.cnt[tid];
@@ -3523,20 +3528,20 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < kFl; ++k) {
-      if (ie[k] == ~0u) continue;
-      const uint32_t i = ie[k];
+      const uint32_t e = lane + 64u * (uint32_t)k, i = r0 + e;
+      if (e >= nf) continue;
       const uint32_t qi = s_st.q[i];
       if (qi == kMmaDropped) continue;
       const uint32_t g = s_st.base[qi] + atomicAdd(&s_st.cnt[qi], 1u);
       if (g < a.seg_cap) {
-        const uint64_t e = ((uint64_t)(q0 + qi) * a.nseg + seg) * a.seg_cap + g;
+        const uint64_t o = ((uint64_t)(q0 + qi) * a.nseg + seg) * a.seg_cap + g;
         const uint32_t row = s_st.row[i];
         float u, l;
         mma_bounds_x(s_st.acc[i], xr[k], s_qk[qi], s_flag, &u, &l);
         atomicMax(&s_st.lmax[qi], score_key(l));
-        a.cand_score[e] = u;
-        a.cand_lower[e] = l;
-        a.cand_row[e] = row;
+        a.cand_score[o] = u;
+        a.cand_lower[o] = l;
+        a.cand_row[o] = row;
       }
     }
     if (a.lmax) {
