@@ -272,6 +272,13 @@ struct ScanArgs {
   // the resident workgroup slots free, the one-query pass a quarter of its
   // workgroups (the other context's launches then start beside it).
   uint32_t leave_room;
+  // MFMA final pass without leave_room: the device's CU count (set by
+  // launch_scan_mma; 0: none).
+  // The hardware gives workgroup w the first slot of CU w and workgroup
+  // w + pair_cols the second slot of the same CU, whose waves then lose the
+  // CU's issue arbitration to the first's: the two split the items of column
+  // w (w + pair_cols k), the first taking kMmaFirstShare / 256 of them.
+  uint32_t pair_cols;
 };
 constexpr uint8_t kMmaWideFlag = 0x80;   // staged query index: the tile value holds the S4 bound
 constexpr uint8_t kMmaDropped = 0xff;    // staged entry dropped (upper bound below the floor)
@@ -280,6 +287,8 @@ constexpr uint32_t kMmaWideSlack = 16;
 // of its entries are free (the next tile's appends, on clustered data
 // rarely more; those past the end go straight to their segments).
 constexpr uint32_t kMmaFlushRoom = 64;
+// The first workgroup's share of a CU's column of items (ScanArgs::pair_cols), in 256ths.
+constexpr uint32_t kMmaFirstShare = 141;
 constexpr int kMaxListWg = 1024;  // workgroup lists per query a later sampling stage may keep
 
 // Exact finishing of the MFMA path.  k_finish, one workgroup per query: a

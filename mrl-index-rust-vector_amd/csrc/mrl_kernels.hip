@@ -3040,19 +3040,33 @@ __global__ __launch_bounds__(kMmaWaves * 64, 4) void k_scan_mma(ScanArgs a) {
   const uint32_t n_items = 2u * (bl ? a.bcount[blockIdx.y] : a.n_pos);
   auto block_of = [&](uint32_t pos) -> uint64_t { return bl ? (uint64_t)bl[pos] : (uint64_t)pos << a.shift; };
   const uint32_t stride = gridDim.x * WPG - 1;  // odd: see k_scan
-  // The final passes share a workgroup's items among its waves: items
-  // blockIdx.x + gridDim.x k, each wave taking k from an LDS counter two
-  // items ahead (a wave slowed by its appends then takes fewer).  The
+  // The final passes share a workgroup's items among its waves, each wave
+  // taking the next from an LDS counter two items ahead (a wave slowed by
+  // its appends then takes fewer).  The items: column col = blockIdx.x % n_col
+  // (col + n_col j), j in this workgroup's part of the column: all of it,
+  // or with ScanArgs::pair_cols (n_col = the CU count) the first
+  // kMmaFirstShare / 256 of it for the CU's first workgroup and the rest for
+  // its second (a third or later workgroup of a column: equal parts).  The
   // sampling passes keep the fixed stride.
   constexpr bool dyn = !SAMPLE;
+  const uint32_t n_col = a.pair_cols ? min(a.pair_cols, gridDim.x) : gridDim.x;
+  const uint32_t col = blockIdx.x % n_col, slot = blockIdx.x / n_col;
+  const uint32_t n_slot = (gridDim.x - col + n_col - 1u) / n_col;  // workgroups of this column
+  const uint32_t col_n = n_items > col ? (n_items - col - 1u) / n_col + 1u : 0u;  // items of this column
+  auto cut = [&](uint32_t s) -> uint32_t {  // the column's items before slot s
+    if (s >= n_slot) return col_n;
+    if (n_slot == 2u) return s ? (uint32_t)(((uint64_t)col_n * kMmaFirstShare) >> 8) : 0u;
+    return (uint32_t)((uint64_t)col_n * s / n_slot);
+  };
+  const uint32_t j_lo = cut(slot), j_n = cut(slot + 1u) - j_lo;
   auto grab = [&]() -> uint32_t {  // the next k (lane 0's value)
     uint32_t k = 0u;
     if (lane == 0u) k = atomicAdd(&s_next, 1u);
     return k;
   };
-  auto item_of = [&](uint32_t k) -> uint32_t {  // n_items or more past the end
+  auto item_of = [&](uint32_t k) -> uint32_t {  // n_items past the end
     const uint32_t kk = (uint32_t)__builtin_amdgcn_readfirstlane((int)k);
-    return kk < n_items ? blockIdx.x + gridDim.x * kk : n_items;
+    return kk < j_n ? col + n_col * (j_lo + kk) : n_items;
   };
   uint32_t first = blockIdx.x * WPG + wave;
   uint32_t after = first + stride;  // the item after the current one (n_it or more: none)
@@ -4373,8 +4387,21 @@ uint32_t mma_scan_grid(const ScanArgs& a) {
   return grid;
 }
 
-hipError_t launch_scan_mma(const ScanArgs& a, int mode, hipStream_t s, const LaunchEvents& ev) {
-  if (a.n_pos == 0 || a.n_q == 0) return hipSuccess;
+hipError_t launch_scan_mma(const ScanArgs& args, int mode, hipStream_t s, const LaunchEvents& ev) {
+  if (args.n_pos == 0 || args.n_q == 0) return hipSuccess;
+  static const uint32_t cus = [] {
+    int dev = 0, n = 0;
+    return hipGetDevice(&dev) == hipSuccess &&
+                   hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
+               ? (uint32_t)n
+               : 0u;
+  }();
+  // A final pass that has the device to itself splits a CU's items between
+  // its two workgroups.  (Beside another context's launches the
+  // workgroups' placement is not known: config 4 over three contexts went
+  // 0.1972 -> 0.2009 ms per step with the split, same box.)
+  ScanArgs a = args;
+  a.pair_cols = mode != 0 && !a.leave_room ? cus : 0u;
   const dim3 g(mma_scan_grid(a), (a.n_q + kMmaQ - 1) / kMmaQ), b(kMmaWaves * 64);
   const bool two = a.n_q > 32;  // one 32-query tile per wave suffices up to 32 queries
   if (mode == 0 && a.lbuf && a.lcount) {
