@@ -2701,6 +2701,14 @@ __device__ __forceinline__ void mma_bounds(float acc, const uint4* recs, uint32_
 // x1).  The products are exact and the f32 roundings here (a few 2^-24 of the
 // summed magnitudes) are far inside the second e1 / e4 columns.  A slot beyond
 // the operand range keeps its value.  U: unroll factor of the operand loops.
+// (float)lo + (float)hi of the two f16 halves of w, in one mixed-precision
+// FMA (lo * 1 + hi, one rounding to f32: the same value bit for bit).
+__device__ __forceinline__ float f16_pair_sum(uint32_t w) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %1 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(w));
+  return r;
+}
+
 template <int U>
 __device__ __forceinline__ float mma_tighten_x(float acc, const uint4 x, const uint4 x1, uint32_t qi,
                                                const uint4* qa, const float* s_flag, float ws4) {
@@ -2732,7 +2740,7 @@ __device__ __forceinline__ float mma_tighten_x(float acc, const uint4 x, const u
       for (int j = 0; j < 4; ++j) {
         // the operand pair with each sign flipped where its bit is clear (as the tiles' vector operand)
         const uint32_t sw = w[j] ^ ((~bits << (15 - 4 * st - j)) & 0x80008000u);
-        S += h2f((uint16_t)(sw & 0xffffu)) + h2f((uint16_t)(sw >> 16));
+        S += f16_pair_sum(sw);
       }
     }
 #pragma unroll U
@@ -2743,7 +2751,7 @@ __device__ __forceinline__ float mma_tighten_x(float acc, const uint4 x, const u
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t sw = w[j] ^ ((~b1 << (15 - 4 * (t & 3) - j)) & 0x80008000u);
-        S1 += h2f((uint16_t)(sw & 0xffffu)) + h2f((uint16_t)(sw >> 16));
+        S1 += f16_pair_sum(sw);
       }
     }
   }
