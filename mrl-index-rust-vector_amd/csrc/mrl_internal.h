@@ -286,7 +286,7 @@ constexpr uint32_t kMmaWideSlack = 16;
 // A final-pass wave writes out its staging region once fewer than this many
 // of its entries are free (the next tile's appends, on clustered data
 // rarely more; those past the end go straight to their segments).
-constexpr uint32_t kMmaFlushRoom = 64;
+constexpr uint32_t kMmaFlushRoom = 40;
 // The first workgroup's share of a CU's column of items (ScanArgs::pair_cols), in 256ths.
 constexpr uint32_t kMmaFirstShare = 141;
 constexpr int kMaxListWg = 1024;  // workgroup lists per query a later sampling stage may keep
