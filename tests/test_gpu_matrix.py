@@ -6,7 +6,8 @@ query operands are built in one launch, and the first that takes two), K
 from 1 to 4096, indexes with a partial last block, at and just above the
 256 blocks below which no sampling pass runs, dims 384 / 512 / 768 / 1024,
 both prefix codecs, the L0Only / L1Rabitq / Full64b depths and the
-exhaustive flag.  Every query's top K must equal the oracle's sharded
+exhaustive flag, and indexes of 1,500 and 2,100 blocks (a final-pass grid
+between one and two workgroups per CU, and the full two).  Every query's top K must equal the oracle's sharded
 scan_blocks (scan.rs:802-886) with bit-identical scores (exact ties at the
 K-th score excepted), under the library's own choice of MFMA final pass and
 with the S4-bounded pass forced."""
@@ -39,6 +40,10 @@ CASES = [
     (768, 257 * 64, 9, 256, True, FULL, False, 0),
     (768, 40 * 64 + 5, 16, 1000, True, FULL, False, 0),
     (768, 500 * 64, 12, 128, True, L0, False, 0),
+    # grids between one and two workgroups per CU (the final pass's CU pairs split their columns) and
+    # at the full two (a partial last block, clustered rows)
+    (768, 1500 * 64 - 7, 64, 256, True, FULL, False, 50),
+    (512, 2100 * 64, 40, 100, True, FULL, False, 0),
 ]
 
 
